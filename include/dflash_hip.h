@@ -1,0 +1,136 @@
+/*
+ * dflash_hip.h -- C ABI of libdflash_hip.so, the MI355X (gfx950) implementation of the
+ * DFlash block-diffusion draft forward (W8A16) of 0xClandestine/mirror-sd.
+ *
+ * The library replaces the reference's native draft back-end, the PyO3 module
+ * `mirror_sd_ane` (ane/src/lib.rs:6-16, ane/src/wrapper.rs) and the MLX draft
+ * (mirror_sd/dflash.py), behind the same Python draft-model interface.  Every entry
+ * point below names the reference interface it stands in for.
+ *
+ * Conventions
+ *  - All tensor pointers are DEVICE pointers (hipMalloc / torch CUDA tensors).
+ *    fp16 tensors are passed as uint16_t*.  Shapes are row-major.
+ *  - `stream` is a hipStream_t (NULL = default stream).  Every call only enqueues
+ *    work on `stream`; results are valid after the stream is synchronised.
+ *  - Return value: DFL_OK (0) or an error code; dfl_last_error() returns the message
+ *    of the last failed call on the calling thread (wrapper.rs:204-209, 334-339 raise
+ *    RuntimeError / ValueError with the kernel name; the Python layer does the same).
+ *  - Threading: a context is used from one host thread / one stream at a time; calls
+ *    on different contexts are independent.  Weights are copied into context-owned
+ *    device memory at load (wrapper.rs:88-92, 451-465 copy into Rust-owned memory).
+ */
+#ifndef DFLASH_HIP_H
+#define DFLASH_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DFL_OK 0
+#define DFL_EINVAL 1   /* bad argument / shape (reference: ValueError) */
+#define DFL_ERANGE 2   /* capacity exceeded (ane_model.py:389-393, 620-624) */
+#define DFL_EHIP 3     /* HIP runtime error */
+#define DFL_ESTATE 4   /* weights not loaded / wrong call order */
+
+typedef struct dfl_ctx dfl_ctx;
+
+/* Model dimensions; field meaning follows DFlashConfig (mirror_sd/dflash.py:34-50). */
+typedef struct dfl_config {
+  int32_t hidden;          /* hidden_size                                  */
+  int32_t n_heads;         /* num_attention_heads                          */
+  int32_t n_kv_heads;      /* num_key_value_heads (n_heads % n_kv_heads == 0) */
+  int32_t head_dim;        /* head_dim; must be 128                        */
+  int32_t intermediate;    /* intermediate_size                            */
+  int32_t n_layers;        /* num_hidden_layers (draft layers)             */
+  int32_t n_target_feat;   /* len(target_layer_ids); fc input = n_target_feat*hidden; 0 = no fc */
+  int32_t vocab;           /* vocab_size of embedding / lm_head; 0 = none  */
+  int32_t max_block;       /* largest block (query rows) per draft call    */
+  int32_t max_ctx;         /* KV-cache capacity in context rows            */
+  float rms_eps;           /* rms_norm_eps                                 */
+  double rope_theta;       /* rope_theta (neox / split-half RoPE)          */
+} dfl_config;
+
+/* Create / destroy a draft context (replaces ANEDraftModel.__init__ kernel compile
+ * + buffer allocation, ane_model.py:47-150; compile_dflash_kernels*, wrapper.rs:308-361). */
+int dfl_create(const dfl_config* cfg, dfl_ctx** out);
+int dfl_destroy(dfl_ctx* ctx);
+const char* dfl_last_error(void);
+
+/* W8A16 quantiser on device (ane_model.py:265-279 `_quantize_weight_q8`):
+ * w fp32 [oc][ic] -> q int8 [oc][ic], scale fp16 [oc]; scale = max|w_row|/127 (0 -> 1/127),
+ * q = clamp(round_half_even(w/scale), -127, 127).  Bit-identical to the numpy quantiser. */
+int dfl_quantize_w8(const float* w, int64_t oc, int64_t ic, int8_t* q, uint16_t* scale,
+                    void* stream);
+
+/* Load one layer (replaces Q8LayerWeights, wrapper.rs:363-428, + _load_layer_norm_weights,
+ * ane_model.py:281-292).  q[i]/scale[i] in the order q,k,v,o,gate,up,down, reference byte
+ * layout: int8 [oc][ic] row-major + fp16 [oc].  Norm gains fp16: input_layernorm [H],
+ * post_attention_layernorm [H], q_norm [128], k_norm [128].  Data are copied. */
+int dfl_load_layer_w8(dfl_ctx* ctx, int layer, const int8_t* const q[7],
+                      const uint16_t* const scale[7], const uint16_t* in_norm,
+                      const uint16_t* post_norm, const uint16_t* q_norm, const uint16_t* k_norm,
+                      void* stream);
+
+/* fc [H][n_target_feat*H] fp16 and hidden_norm [H] fp16 (dflash.py:373-378; the
+ * reference never quantises fc, ane_model.py:319-322).  Copied. */
+int dfl_load_fc(dfl_ctx* ctx, const uint16_t* fc_weight, const uint16_t* hidden_norm,
+                void* stream);
+
+/* Final norm [H] (dflash.py:379), the target's embedding table [V][H] (kept as a
+ * caller-owned pointer; must outlive the context) and lm_head [V][H] (copied into the
+ * context's layout) -- target.py:188-197; compile_lm_head_kernel, wrapper.rs:507-523.
+ * embed / lm_head may be NULL. */
+int dfl_load_head(dfl_ctx* ctx, const uint16_t* final_norm, const uint16_t* embed,
+                  const uint16_t* lm_head, void* stream);
+
+/* Context ingest (dflash.py:392 `hidden_norm(fc(target_hidden))` then, per layer,
+ * k_norm(k_proj(ctx)) + RoPE and v_proj(ctx), appended to the KV cache at positions
+ * offset .. offset+C-1 -- the context half of Qwen3DFlashAttention, dflash.py:287-308;
+ * `_compute_context`, ane_model.py:632-637).  target_hidden [C][n_target_feat*H] fp16. */
+int dfl_ingest_context(dfl_ctx* ctx, const uint16_t* target_hidden, int32_t C, void* stream);
+/* Same for context rows that are already fused ([C][H] fp16): skips fc + hidden_norm. */
+int dfl_ingest_fused(dfl_ctx* ctx, const uint16_t* ctx_hidden, int32_t C, void* stream);
+
+/* Draft one block (DFlashDraftModel.__call__, dflash.py:384-403, with the block K/V
+ * appended and trimmed again as generate.py:599-609 does; ANEDraftModel.run_kernels +
+ * read_output + read_draft_tokens, ane_model.py:564-604; read_argmax, wrapper.rs:108-140).
+ * Input: exactly one of noise_emb [B][H] fp16 or ids [B] int32 (rows of the loaded
+ * embedding).  Outputs (each may be NULL): out_hidden [B][H] fp16 (final-normed),
+ * out_prenorm [B][H] fp16 (residual stream before the final norm), out_logits [B][V]
+ * fp32, out_ids [B] int32 (argmax, lowest index on ties).  Block rows use positions
+ * offset .. offset+B-1 and attend to all cached context rows plus the block. */
+int dfl_draft_block(dfl_ctx* ctx, const uint16_t* noise_emb, const int32_t* ids, int32_t B,
+                    uint16_t* out_hidden, uint16_t* out_prenorm, float* out_logits,
+                    int32_t* out_ids, void* stream);
+
+/* Run only the first n draft layers (DFlashDraftModel.num_draft_layers, dflash.py:382,
+ * 394, lowered by generate.py:423-426); 1 <= n <= n_layers.  Ingest then fills only
+ * those layers' caches. */
+int dfl_set_num_layers(dfl_ctx* ctx, int32_t n);
+
+/* KV-cache bookkeeping (DFlashKVCache, dflash.py:139-212). */
+/* Drop the last n cached context rows; offset -= n (trim, dflash.py:195-207). */
+int dfl_cache_trim(dfl_ctx* ctx, int32_t n);
+/* Keep the first n block rows of the last dfl_draft_block as cached context
+ * (what update_and_fetch did before the caller's trim). */
+int dfl_cache_commit(dfl_ctx* ctx, int32_t n);
+int dfl_cache_reset(dfl_ctx* ctx);
+/* Set the absolute position of the next context row without touching cached rows
+ * (the ANE caller assigns cache.offset directly, generate.py:1409-1417). */
+int dfl_cache_set_offset(dfl_ctx* ctx, int64_t offset);
+/* Current cached rows and absolute position offset. */
+int dfl_cache_state(const dfl_ctx* ctx, int32_t* len, int64_t* offset);
+/* Device pointers of layer `layer`'s cache: K [NKV][cap][128], Vt [NKV][128][cap]. */
+int dfl_cache_kv(const dfl_ctx* ctx, int32_t layer, uint16_t** k, uint16_t** vt, int32_t* cap);
+
+/* Sticky device-side error flags (bit 0: a token id outside [0, vocab)); reading clears. */
+int dfl_device_errors(dfl_ctx* ctx, int32_t* flags, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DFLASH_HIP_H */

@@ -1,0 +1,572 @@
+// C ABI of libdflash_hip.so: context management, weight loading, context ingest and the
+// draft-block sequence.  See include/dflash_hip.h for the contract of each entry point.
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "dflash_hip.h"
+#include "dfl_kernels.h"
+
+using namespace dfl;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+#define DFL_HIP(x)                                                                   \
+  do {                                                                               \
+    hipError_t e_ = (x);                                                             \
+    if (e_ != hipSuccess) return fail(DFL_EHIP, std::string(#x) + ": " + hipGetErrorString(e_)); \
+  } while (0)
+
+constexpr int ING_ROWS = 1024;     // context rows per ingest pass
+constexpr int MAX_CHUNKS = 64;     // attention key splits
+constexpr int TARGET_WAVES = 2048; // ~8 waves per CU on 256 CUs
+
+struct GemmPlan {
+  int SK = 4;
+  int S_x = 1;
+};
+
+GemmPlan plan_for(int N, int KB, int epi) {
+  GemmPlan p;
+  const int n_wt = N / 64;
+  p.SK = (n_wt >= TARGET_WAVES) ? 1 : (2 * n_wt >= TARGET_WAVES ? 2 : 4);
+  if (epi != EPI_PARTIAL) return p;
+  const int waves = n_wt * p.SK;
+  int sx = (TARGET_WAVES + waves - 1) / waves;
+  const int maxsx = std::max(1, KB / (p.SK * 2));
+  p.S_x = std::max(1, std::min(std::min(sx, maxsx), 16));
+  return p;
+}
+
+struct Layer {
+  uint4 *w_qkv = nullptr, *w_o = nullptr, *w_gu = nullptr, *w_down = nullptr;
+  half_t *s_qkv = nullptr, *s_o = nullptr, *s_gu = nullptr, *s_down = nullptr;
+  half_t *in_norm = nullptr, *post_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+  half_t *Kc = nullptr, *Vt = nullptr;
+  bool loaded = false;
+};
+
+}  // namespace
+
+struct dfl_ctx {
+  dfl_config cfg;
+  int H, NH, NKV, F, NL, NQKV, Bmax, cap, V, NF;
+  std::vector<Layer> layers;
+  uint4* w_fc = nullptr;
+  half_t* hidden_norm = nullptr;
+  bool fc_loaded = false;
+  half_t* final_norm = nullptr;
+  uint4* w_lm = nullptr;
+  const half_t* embed = nullptr;
+  bool head_loaded = false;
+  int active = 0;   // layers run per call (num_draft_layers)
+  int len = 0;
+  long long offset = 0;
+  int last_block = 0;
+  half_t *x = nullptr, *h = nullptr, *Q = nullptr, *attn = nullptr, *act = nullptr,
+         *ctxbuf = nullptr;
+  float* ws = nullptr;
+  float *Op = nullptr, *Ml = nullptr;
+  unsigned long long* keys = nullptr;
+  int* err = nullptr;
+  GemmPlan p_qkv, p_o, p_gu, p_down, p_lm;
+  std::vector<void*> allocs;
+
+  ~dfl_ctx() {
+    for (void* p : allocs) (void)hipFree(p);
+  }
+  template <class T>
+  int alloc(T** p, size_t n, bool zero = false) {
+    void* v = nullptr;
+    hipError_t e = hipMalloc(&v, std::max<size_t>(n, 1) * sizeof(T));
+    if (e != hipSuccess)
+      return fail(DFL_EHIP, std::string("hipMalloc(") + std::to_string(n * sizeof(T)) +
+                                " bytes): " + hipGetErrorString(e));
+    allocs.push_back(v);
+    *p = static_cast<T*>(v);
+    if (zero) {
+      e = hipMemset(v, 0, std::max<size_t>(n, 1) * sizeof(T));
+      if (e != hipSuccess) return fail(DFL_EHIP, std::string("hipMemset: ") + hipGetErrorString(e));
+    }
+    return DFL_OK;
+  }
+};
+
+#define DFL_TRY(x)              \
+  do {                          \
+    int r_ = (x);               \
+    if (r_ != DFL_OK) return r_; \
+  } while (0)
+
+static int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(DFL_EHIP, std::string(what) + ": " + hipGetErrorString(e));
+  return DFL_OK;
+}
+
+extern "C" {
+
+const char* dfl_last_error(void) { return g_err.c_str(); }
+
+int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
+  if (!cfg || !out) return fail(DFL_EINVAL, "dfl_create: null argument");
+  *out = nullptr;
+  const dfl_config& c = *cfg;
+  if (c.head_dim != 128) return fail(DFL_EINVAL, "dfl_create: head_dim must be 128");
+  if (c.hidden <= 0 || c.hidden % 64 || c.hidden > 8192)
+    return fail(DFL_EINVAL, "dfl_create: hidden must be a positive multiple of 64, <= 8192");
+  if (c.n_heads <= 0 || c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads)
+    return fail(DFL_EINVAL, "dfl_create: n_heads must be a positive multiple of n_kv_heads");
+  if (c.intermediate <= 0 || c.intermediate % 32 || c.intermediate > 8192 * 8)
+    return fail(DFL_EINVAL, "dfl_create: intermediate must be a positive multiple of 32");
+  if (c.n_layers <= 0) return fail(DFL_EINVAL, "dfl_create: n_layers must be positive");
+  if (c.vocab < 0 || c.vocab % 64) return fail(DFL_EINVAL, "dfl_create: vocab must be a multiple of 64");
+  if (c.max_block <= 0 || c.max_block > 256)
+    return fail(DFL_EINVAL, "dfl_create: max_block must be in [1, 256]");
+  if (c.max_ctx < 0) return fail(DFL_EINVAL, "dfl_create: max_ctx must be >= 0");
+  if (c.n_target_feat < 0) return fail(DFL_EINVAL, "dfl_create: n_target_feat must be >= 0");
+  if (!(c.rms_eps > 0.f) || !(c.rope_theta > 0.0))
+    return fail(DFL_EINVAL, "dfl_create: rms_eps and rope_theta must be positive");
+
+  dfl_ctx* x = new dfl_ctx();
+  x->cfg = c;
+  x->H = c.hidden;
+  x->NH = c.n_heads;
+  x->NKV = c.n_kv_heads;
+  x->F = c.intermediate;
+  x->NL = c.n_layers;
+  x->NQKV = (c.n_heads + 2 * c.n_kv_heads) * 128;
+  x->Bmax = c.max_block;
+  x->V = c.vocab;
+  x->NF = c.n_target_feat;
+  x->cap = ((c.max_ctx + c.max_block + 63) / 64) * 64;
+  x->layers.resize(c.n_layers);
+  x->active = c.n_layers;
+  x->p_qkv = plan_for(x->NQKV, x->H / 32, EPI_PARTIAL);
+  x->p_o = plan_for(x->H, x->NH * 128 / 32, EPI_PARTIAL);
+  x->p_gu = plan_for(2 * x->F, x->H / 32, EPI_SWIGLU);
+  x->p_down = plan_for(x->H, x->F / 32, EPI_PARTIAL);
+  x->p_lm = plan_for(std::max(x->V, 64), x->H / 16, EPI_ARGMAX);
+
+  const size_t Bm = x->Bmax;
+  size_t ws = std::max({(size_t)x->p_qkv.S_x * Bm * x->NQKV, (size_t)x->p_o.S_x * Bm * x->H,
+                        (size_t)x->p_down.S_x * Bm * x->H});
+  ws = std::max(ws, (size_t)ING_ROWS * std::max(x->H, 2 * x->NKV * 128));
+  int r = DFL_OK;
+  if ((r = x->alloc(&x->x, Bm * x->H)) || (r = x->alloc(&x->h, Bm * x->H)) ||
+      (r = x->alloc(&x->Q, (size_t)x->NH * Bm * 128)) ||
+      (r = x->alloc(&x->attn, Bm * x->NH * 128)) || (r = x->alloc(&x->act, Bm * x->F)) ||
+      (r = x->alloc(&x->ctxbuf, (size_t)ING_ROWS * x->H)) || (r = x->alloc(&x->ws, ws)) ||
+      (r = x->alloc(&x->Op, (size_t)MAX_CHUNKS * x->NH * Bm * 128)) ||
+      (r = x->alloc(&x->Ml, (size_t)MAX_CHUNKS * x->NH * Bm * 2)) ||
+      (r = x->alloc(&x->keys, Bm, true)) || (r = x->alloc(&x->err, 1, true))) {
+    delete x;
+    return r;
+  }
+  for (auto& L : x->layers) {
+    const size_t kv = (size_t)x->NKV * x->cap * 128;
+    if ((r = x->alloc(&L.Kc, kv, true)) || (r = x->alloc(&L.Vt, kv, true))) {
+      delete x;
+      return r;
+    }
+  }
+  *out = x;
+  return DFL_OK;
+}
+
+int dfl_destroy(dfl_ctx* ctx) {
+  if (!ctx) return fail(DFL_EINVAL, "dfl_destroy: null context");
+  (void)hipDeviceSynchronize();
+  delete ctx;
+  return DFL_OK;
+}
+
+int dfl_quantize_w8(const float* w, int64_t oc, int64_t ic, int8_t* q, uint16_t* scale,
+                    void* stream) {
+  if (!w || !q || !scale) return fail(DFL_EINVAL, "dfl_quantize_w8: null pointer");
+  if (oc <= 0 || ic <= 0 || oc > (1ll << 31) - 1)
+    return fail(DFL_EINVAL, "dfl_quantize_w8: bad shape");
+  launch_quantize_w8(w, oc, ic, q, reinterpret_cast<half_t*>(scale), (hipStream_t)stream);
+  return check_launch("quantize_w8");
+}
+
+int dfl_load_layer_w8(dfl_ctx* ctx, int layer, const int8_t* const q[7],
+                      const uint16_t* const scale[7], const uint16_t* in_norm,
+                      const uint16_t* post_norm, const uint16_t* q_norm, const uint16_t* k_norm,
+                      void* stream) {
+  if (!ctx || !q || !scale) return fail(DFL_EINVAL, "dfl_load_layer_w8: null argument");
+  if (layer < 0 || layer >= ctx->NL)
+    return fail(DFL_ERANGE, "dfl_load_layer_w8: layer index out of range");
+  for (int i = 0; i < 7; ++i)
+    if (!q[i] || !scale[i]) return fail(DFL_EINVAL, "dfl_load_layer_w8: null weight pointer");
+  if (!in_norm || !post_norm || !q_norm || !k_norm)
+    return fail(DFL_EINVAL, "dfl_load_layer_w8: null norm pointer");
+  hipStream_t st = (hipStream_t)stream;
+  Layer& L = ctx->layers[layer];
+  const int H = ctx->H, NH = ctx->NH, NKV = ctx->NKV, F = ctx->F, NQ = NH * 128;
+  if (!L.w_qkv) {
+    DFL_TRY(ctx->alloc(&L.w_qkv, (size_t)ctx->NQKV * H / 16));
+    DFL_TRY(ctx->alloc(&L.s_qkv, (size_t)ctx->NQKV));
+    DFL_TRY(ctx->alloc(&L.w_o, (size_t)H * NQ / 16));
+    DFL_TRY(ctx->alloc(&L.s_o, (size_t)H));
+    DFL_TRY(ctx->alloc(&L.w_gu, (size_t)2 * F * H / 16));
+    DFL_TRY(ctx->alloc(&L.s_gu, (size_t)2 * F));
+    DFL_TRY(ctx->alloc(&L.w_down, (size_t)H * F / 16));
+    DFL_TRY(ctx->alloc(&L.s_down, (size_t)H));
+    DFL_TRY(ctx->alloc(&L.in_norm, (size_t)H));
+    DFL_TRY(ctx->alloc(&L.post_norm, (size_t)H));
+    DFL_TRY(ctx->alloc(&L.q_norm, (size_t)128));
+    DFL_TRY(ctx->alloc(&L.k_norm, (size_t)128));
+  }
+  auto S = [&](int i) { return reinterpret_cast<const half_t*>(scale[i]); };
+  // fused QKV: row-blocks [0, NH*4) = q_proj, then k_proj, then v_proj
+  launch_pack_i8(q[0], S(0), NQ, H, L.w_qkv, L.s_qkv, 0, 1, st);
+  launch_pack_i8(q[1], S(1), NKV * 128, H, L.w_qkv, L.s_qkv, NH * 4, 1, st);
+  launch_pack_i8(q[2], S(2), NKV * 128, H, L.w_qkv, L.s_qkv, (NH + NKV) * 4, 1, st);
+  launch_pack_i8(q[3], S(3), H, NQ, L.w_o, L.s_o, 0, 1, st);
+  // gate|up interleaved by row-block: 2j = gate rows [32j, 32j+32), 2j+1 = up rows
+  launch_pack_i8(q[4], S(4), F, H, L.w_gu, L.s_gu, 0, 2, st);
+  launch_pack_i8(q[5], S(5), F, H, L.w_gu, L.s_gu, 1, 2, st);
+  launch_pack_i8(q[6], S(6), H, F, L.w_down, L.s_down, 0, 1, st);
+  DFL_HIP(hipMemcpyAsync(L.in_norm, in_norm, H * 2, hipMemcpyDeviceToDevice, st));
+  DFL_HIP(hipMemcpyAsync(L.post_norm, post_norm, H * 2, hipMemcpyDeviceToDevice, st));
+  DFL_HIP(hipMemcpyAsync(L.q_norm, q_norm, 256, hipMemcpyDeviceToDevice, st));
+  DFL_HIP(hipMemcpyAsync(L.k_norm, k_norm, 256, hipMemcpyDeviceToDevice, st));
+  DFL_TRY(check_launch("pack layer weights"));
+  L.loaded = true;
+  return DFL_OK;
+}
+
+int dfl_load_fc(dfl_ctx* ctx, const uint16_t* fc_weight, const uint16_t* hidden_norm,
+                void* stream) {
+  if (!ctx || !fc_weight || !hidden_norm) return fail(DFL_EINVAL, "dfl_load_fc: null argument");
+  if (ctx->NF <= 0) return fail(DFL_ESTATE, "dfl_load_fc: context created with n_target_feat = 0");
+  hipStream_t st = (hipStream_t)stream;
+  const int K = ctx->NF * ctx->H;
+  if (!ctx->w_fc) {
+    DFL_TRY(ctx->alloc(&ctx->w_fc, (size_t)ctx->H * K / 8));
+    DFL_TRY(ctx->alloc(&ctx->hidden_norm, (size_t)ctx->H));
+  }
+  launch_pack_f16(reinterpret_cast<const half_t*>(fc_weight), ctx->H, K, ctx->w_fc, st);
+  DFL_HIP(hipMemcpyAsync(ctx->hidden_norm, hidden_norm, ctx->H * 2, hipMemcpyDeviceToDevice, st));
+  DFL_TRY(check_launch("pack fc"));
+  ctx->fc_loaded = true;
+  return DFL_OK;
+}
+
+int dfl_load_head(dfl_ctx* ctx, const uint16_t* final_norm, const uint16_t* embed,
+                  const uint16_t* lm_head, void* stream) {
+  if (!ctx || !final_norm) return fail(DFL_EINVAL, "dfl_load_head: null argument");
+  if ((embed || lm_head) && ctx->V <= 0)
+    return fail(DFL_ESTATE, "dfl_load_head: context created with vocab = 0");
+  hipStream_t st = (hipStream_t)stream;
+  if (!ctx->final_norm) DFL_TRY(ctx->alloc(&ctx->final_norm, (size_t)ctx->H));
+  DFL_HIP(hipMemcpyAsync(ctx->final_norm, final_norm, ctx->H * 2, hipMemcpyDeviceToDevice, st));
+  ctx->embed = reinterpret_cast<const half_t*>(embed);
+  if (lm_head) {
+    if (!ctx->w_lm) DFL_TRY(ctx->alloc(&ctx->w_lm, (size_t)ctx->V * ctx->H / 8));
+    launch_pack_f16(reinterpret_cast<const half_t*>(lm_head), ctx->V, ctx->H, ctx->w_lm, st);
+    DFL_TRY(check_launch("pack lm_head"));
+  }
+  ctx->head_loaded = true;
+  return DFL_OK;
+}
+
+static void gemm(dfl_ctx* ctx, int wt, int epi, const uint4* W, const half_t* scale,
+                 const half_t* X, int ldx, int M, int N, int KB, GemmPlan p, half_t* out,
+                 int ldo, float* logits, unsigned long long* keys, hipStream_t st) {
+  SkinnyArgs a;
+  a.W = W;
+  a.scale = scale;
+  a.X = X;
+  a.ldx = ldx;
+  a.M = M;
+  a.N = N;
+  a.KB = KB;
+  a.S_x = p.S_x;
+  a.ws = ctx->ws;
+  a.out = out;
+  a.ldo = ldo;
+  a.logits = logits;
+  a.ldl = N;
+  a.keys = keys;
+  launch_skinny_gemm(wt, epi, a, p.SK, (M + 31) / 32, st);
+}
+
+static int layers_ready(dfl_ctx* ctx, const char* who) {
+  for (int l = 0; l < ctx->active; ++l)
+    if (!ctx->layers[l].loaded)
+      return fail(DFL_ESTATE, std::string(who) + ": layer " + std::to_string(l) + " not loaded");
+  return DFL_OK;
+}
+
+// Per-layer K/V of `rows` fused context rows in ctx->ctxbuf, appended at cache row
+// len + r0 with absolute position offset + r0.
+static void ingest_kv_rows(dfl_ctx* ctx, const half_t* ctxrows, int rows, int r0, hipStream_t st) {
+  const int H = ctx->H, NH = ctx->NH, NKV = ctx->NKV;
+  const int KB = H / 32;
+  const int Nkv = 2 * NKV * 128;
+  GemmPlan p;
+  p.SK = 4;
+  p.S_x = 1;
+  for (int l = 0; l < ctx->active; ++l) {
+    Layer& L = ctx->layers[l];
+    const uint4* Wkv = L.w_qkv + (size_t)(NH * 4) * KB * 64;
+    gemm(ctx, WT_INT8, EPI_PARTIAL, Wkv, nullptr, ctxrows, H, rows, Nkv, KB, p, nullptr, 0,
+         nullptr, nullptr, st);
+    QKRopeArgs q;
+    q.ws = ctx->ws;
+    q.S_x = 1;
+    q.M = rows;
+    q.N = Nkv;
+    q.col_slot0 = NH;
+    q.scale = L.s_qkv;
+    q.slot0 = NH;
+    q.n_slots = 2 * NKV;
+    q.NH = NH;
+    q.NKV = NKV;
+    q.q_norm = L.q_norm;
+    q.k_norm = L.k_norm;
+    q.eps = ctx->cfg.rms_eps;
+    q.pos0 = ctx->offset + r0;
+    q.log2_theta = std::log2(ctx->cfg.rope_theta);
+    q.Q = nullptr;
+    q.q_rows = 0;
+    q.Kc = L.Kc;
+    q.Vt = L.Vt;
+    q.cap = ctx->cap;
+    q.cache_row0 = ctx->len + r0;
+    launch_qk_rope(q, st);
+  }
+}
+
+static int ingest(dfl_ctx* ctx, const uint16_t* src, int C, bool fused, void* stream) {
+  if (!ctx || (!src && C > 0)) return fail(DFL_EINVAL, "dfl_ingest: null argument");
+  if (C < 0) return fail(DFL_EINVAL, "dfl_ingest: negative row count");
+  if ((long long)ctx->len + C > ctx->cfg.max_ctx)
+    return fail(DFL_ERANGE, "dfl_ingest: context rows " + std::to_string(ctx->len + C) +
+                                " exceed max_ctx " + std::to_string(ctx->cfg.max_ctx));
+  DFL_TRY(layers_ready(ctx, "dfl_ingest"));
+  if (!fused && !ctx->fc_loaded) return fail(DFL_ESTATE, "dfl_ingest_context: fc not loaded");
+  hipStream_t st = (hipStream_t)stream;
+  const int H = ctx->H;
+  const int K = ctx->NF * H;
+  ctx->last_block = 0;
+  for (int r0 = 0; r0 < C; r0 += ING_ROWS) {
+    const int rows = std::min(ING_ROWS, C - r0);
+    const half_t* ctxrows;
+    if (fused) {
+      ctxrows = reinterpret_cast<const half_t*>(src) + (size_t)r0 * H;
+    } else {
+      GemmPlan p;
+      p.SK = 4;
+      p.S_x = 1;
+      gemm(ctx, WT_F16, EPI_PARTIAL, ctx->w_fc, nullptr,
+           reinterpret_cast<const half_t*>(src) + (size_t)r0 * K, K, rows, H, K / 16, p, nullptr,
+           0, nullptr, nullptr, st);
+      launch_reduce_resid_norm(ctx->ws, 1, rows, H, nullptr, nullptr, false, ctx->hidden_norm,
+                               ctx->cfg.rms_eps, ctx->ctxbuf, H, st);
+      ctxrows = ctx->ctxbuf;
+    }
+    ingest_kv_rows(ctx, ctxrows, rows, r0, st);
+  }
+  DFL_TRY(check_launch("ingest"));
+  ctx->len += C;
+  ctx->offset += C;
+  return DFL_OK;
+}
+
+int dfl_ingest_context(dfl_ctx* ctx, const uint16_t* target_hidden, int32_t C, void* stream) {
+  return ingest(ctx, target_hidden, C, false, stream);
+}
+
+int dfl_ingest_fused(dfl_ctx* ctx, const uint16_t* ctx_hidden, int32_t C, void* stream) {
+  return ingest(ctx, ctx_hidden, C, true, stream);
+}
+
+int dfl_draft_block(dfl_ctx* ctx, const uint16_t* noise_emb, const int32_t* ids, int32_t B,
+                    uint16_t* out_hidden, uint16_t* out_prenorm, float* out_logits,
+                    int32_t* out_ids, void* stream) {
+  if (!ctx) return fail(DFL_EINVAL, "dfl_draft_block: null context");
+  if (B <= 0 || B > ctx->Bmax)
+    return fail(DFL_ERANGE, "dfl_draft_block: block size " + std::to_string(B) +
+                                " outside [1, max_block=" + std::to_string(ctx->Bmax) + "]");
+  if ((noise_emb == nullptr) == (ids == nullptr))
+    return fail(DFL_EINVAL, "dfl_draft_block: pass exactly one of noise_emb / ids");
+  if (ids && !ctx->embed) return fail(DFL_ESTATE, "dfl_draft_block: embedding not loaded");
+  if (!ctx->head_loaded) return fail(DFL_ESTATE, "dfl_draft_block: final norm not loaded");
+  if ((out_logits || out_ids) && !ctx->w_lm)
+    return fail(DFL_ESTATE, "dfl_draft_block: lm_head not loaded");
+  if (ctx->len + B > ctx->cap) return fail(DFL_ERANGE, "dfl_draft_block: cache capacity exceeded");
+  DFL_TRY(layers_ready(ctx, "dfl_draft_block"));
+
+  hipStream_t st = (hipStream_t)stream;
+  const int H = ctx->H, NH = ctx->NH, NKV = ctx->NKV, F = ctx->F, NQ = NH * 128;
+  const float eps = ctx->cfg.rms_eps;
+  launch_embed_norm(ids, ctx->embed, reinterpret_cast<const half_t*>(noise_emb), B, H, ctx->V,
+                    ctx->layers[0].in_norm, eps, ctx->x, ctx->h, ctx->err, st);
+
+  const int L = ctx->len + B;
+  const int ratio = NH / NKV;
+  const int n_qt = (ratio * B + 31) / 32;
+  int n_chunks = std::max(1, 1024 / (NKV * n_qt));
+  n_chunks = std::min(n_chunks, std::min(MAX_CHUNKS, (L + 63) / 64));
+  n_chunks = std::max(n_chunks, 1);
+  int chunk = (L + n_chunks - 1) / n_chunks;
+  chunk = ((chunk + 31) / 32) * 32;
+  n_chunks = (L + chunk - 1) / chunk;
+
+  for (int l = 0; l < ctx->active; ++l) {
+    Layer& Ly = ctx->layers[l];
+    gemm(ctx, WT_INT8, EPI_PARTIAL, Ly.w_qkv, nullptr, ctx->h, H, B, ctx->NQKV, H / 32,
+         ctx->p_qkv, nullptr, 0, nullptr, nullptr, st);
+    QKRopeArgs q;
+    q.ws = ctx->ws;
+    q.S_x = ctx->p_qkv.S_x;
+    q.M = B;
+    q.N = ctx->NQKV;
+    q.col_slot0 = 0;
+    q.scale = Ly.s_qkv;
+    q.slot0 = 0;
+    q.n_slots = NH + 2 * NKV;
+    q.NH = NH;
+    q.NKV = NKV;
+    q.q_norm = Ly.q_norm;
+    q.k_norm = Ly.k_norm;
+    q.eps = eps;
+    q.pos0 = ctx->offset;
+    q.log2_theta = std::log2(ctx->cfg.rope_theta);
+    q.Q = ctx->Q;
+    q.q_rows = B;
+    q.Kc = Ly.Kc;
+    q.Vt = Ly.Vt;
+    q.cap = ctx->cap;
+    q.cache_row0 = ctx->len;
+    launch_qk_rope(q, st);
+
+    AttnArgs at;
+    at.Q = ctx->Q;
+    at.Kc = Ly.Kc;
+    at.Vt = Ly.Vt;
+    at.B = B;
+    at.NH = NH;
+    at.NKV = NKV;
+    at.cap = ctx->cap;
+    at.L = L;
+    at.chunk = chunk;
+    at.n_chunks = n_chunks;
+    at.scale_log2 = (float)(1.4426950408889634 / std::sqrt(128.0));
+    at.Op = ctx->Op;
+    at.Ml = ctx->Ml;
+    at.O = ctx->attn;
+    launch_block_attention(at, st);
+
+    gemm(ctx, WT_INT8, EPI_PARTIAL, Ly.w_o, nullptr, ctx->attn, NQ, B, H, NQ / 32, ctx->p_o,
+         nullptr, 0, nullptr, nullptr, st);
+    launch_reduce_resid_norm(ctx->ws, ctx->p_o.S_x, B, H, Ly.s_o, ctx->x, true, Ly.post_norm, eps,
+                             ctx->h, H, st);
+    gemm(ctx, WT_INT8, EPI_SWIGLU, Ly.w_gu, Ly.s_gu, ctx->h, H, B, 2 * F, H / 32, ctx->p_gu,
+         ctx->act, F, nullptr, nullptr, st);
+    gemm(ctx, WT_INT8, EPI_PARTIAL, Ly.w_down, nullptr, ctx->act, F, B, H, F / 32, ctx->p_down,
+         nullptr, 0, nullptr, nullptr, st);
+    const half_t* gnext = (l + 1 < ctx->active) ? ctx->layers[l + 1].in_norm : ctx->final_norm;
+    launch_reduce_resid_norm(ctx->ws, ctx->p_down.S_x, B, H, Ly.s_down, ctx->x, true, gnext, eps,
+                             ctx->h, H, st);
+  }
+  if (out_logits || out_ids) {
+    gemm(ctx, WT_F16, EPI_ARGMAX, ctx->w_lm, nullptr, ctx->h, H, B, ctx->V, H / 16, ctx->p_lm,
+         nullptr, 0, out_logits, out_ids ? ctx->keys : nullptr, st);
+    if (out_ids) launch_argmax_finalize(ctx->keys, B, out_ids, st);
+  }
+  if (out_hidden)
+    DFL_HIP(hipMemcpyAsync(out_hidden, ctx->h, (size_t)B * H * 2, hipMemcpyDeviceToDevice, st));
+  if (out_prenorm)
+    DFL_HIP(hipMemcpyAsync(out_prenorm, ctx->x, (size_t)B * H * 2, hipMemcpyDeviceToDevice, st));
+  DFL_TRY(check_launch("dfl_draft_block"));
+  ctx->last_block = B;
+  return DFL_OK;
+}
+
+int dfl_set_num_layers(dfl_ctx* ctx, int32_t n) {
+  if (!ctx) return fail(DFL_EINVAL, "dfl_set_num_layers: null context");
+  if (n < 1 || n > ctx->NL)
+    return fail(DFL_ERANGE, "dfl_set_num_layers: n must be in [1, " + std::to_string(ctx->NL) + "]");
+  ctx->active = n;
+  return DFL_OK;
+}
+
+int dfl_cache_trim(dfl_ctx* ctx, int32_t n) {
+  if (!ctx) return fail(DFL_EINVAL, "dfl_cache_trim: null context");
+  if (n < 0) return fail(DFL_EINVAL, "dfl_cache_trim: negative count");
+  const int k = std::min(n, ctx->len);   // DFlashKVCache.trim clamps the length at 0
+  ctx->len -= k;
+  ctx->offset -= n;
+  ctx->last_block = 0;
+  return DFL_OK;
+}
+
+int dfl_cache_commit(dfl_ctx* ctx, int32_t n) {
+  if (!ctx) return fail(DFL_EINVAL, "dfl_cache_commit: null context");
+  if (n < 0 || n > ctx->last_block)
+    return fail(DFL_EINVAL, "dfl_cache_commit: n must be in [0, rows of the last block]");
+  if (ctx->len + n > ctx->cfg.max_ctx) return fail(DFL_ERANGE, "dfl_cache_commit: max_ctx exceeded");
+  ctx->len += n;
+  ctx->offset += n;
+  ctx->last_block = 0;
+  return DFL_OK;
+}
+
+int dfl_cache_reset(dfl_ctx* ctx) {
+  if (!ctx) return fail(DFL_EINVAL, "dfl_cache_reset: null context");
+  ctx->len = 0;
+  ctx->offset = 0;
+  ctx->last_block = 0;
+  return DFL_OK;
+}
+
+int dfl_cache_set_offset(dfl_ctx* ctx, int64_t offset) {
+  if (!ctx) return fail(DFL_EINVAL, "dfl_cache_set_offset: null context");
+  if (offset < 0) return fail(DFL_EINVAL, "dfl_cache_set_offset: negative offset");
+  ctx->offset = offset;
+  ctx->last_block = 0;
+  return DFL_OK;
+}
+
+int dfl_cache_state(const dfl_ctx* ctx, int32_t* len, int64_t* offset) {
+  if (!ctx) return fail(DFL_EINVAL, "dfl_cache_state: null context");
+  if (len) *len = ctx->len;
+  if (offset) *offset = ctx->offset;
+  return DFL_OK;
+}
+
+int dfl_cache_kv(const dfl_ctx* ctx, int32_t layer, uint16_t** k, uint16_t** vt, int32_t* cap) {
+  if (!ctx) return fail(DFL_EINVAL, "dfl_cache_kv: null context");
+  if (layer < 0 || layer >= ctx->NL) return fail(DFL_ERANGE, "dfl_cache_kv: layer out of range");
+  if (k) *k = reinterpret_cast<uint16_t*>(ctx->layers[layer].Kc);
+  if (vt) *vt = reinterpret_cast<uint16_t*>(ctx->layers[layer].Vt);
+  if (cap) *cap = ctx->cap;
+  return DFL_OK;
+}
+
+int dfl_device_errors(dfl_ctx* ctx, int32_t* flags, void* stream) {
+  if (!ctx || !flags) return fail(DFL_EINVAL, "dfl_device_errors: null argument");
+  hipStream_t st = (hipStream_t)stream;
+  int v = 0;
+  DFL_HIP(hipMemcpyAsync(&v, ctx->err, sizeof(int), hipMemcpyDeviceToHost, st));
+  DFL_HIP(hipStreamSynchronize(st));
+  DFL_HIP(hipMemsetAsync(ctx->err, 0, sizeof(int), st));
+  *flags = v;
+  return DFL_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,89 @@
+// Shared device helpers for the DFlash draft kernels (gfx950 / CDNA4).
+//
+// Conventions used by every kernel in this library:
+//  * fp16 tensors are passed as uint16_t* at the C ABI and used as _Float16 here.
+//  * A "row-block" is 32 consecutive output rows of a projection; MFMA tiles are
+//    v_mfma_f32_32x32x16_f16 (wave64).  For that instruction lane l supplies
+//    A[i = l%32][k = 8*(l/32) + 0..7] and B[k = 8*(l/32) + 0..7][j = l%32], and
+//    receives D[i = 8*(r/4) + 4*(l/32) + (r%4)][j = l%32] in accumulator r.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+#define DFL_DEV __device__ __forceinline__
+
+// D += A(32x16) * B(16x32), fp16 inputs, fp32 accumulate.
+DFL_DEV floatx16 mfma32x32x16(half8_t a, half8_t b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+DFL_DEV half8_t as_half8(uint4 v) { return __builtin_bit_cast(half8_t, v); }
+DFL_DEV uint4 as_uint4(half8_t v) { return __builtin_bit_cast(uint4, v); }
+
+// 128-bit streaming load (nontemporal hint: weights are read once per block).
+DFL_DEV uint4 load_stream(const uint4* p) {
+  return __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p)));
+}
+
+// Exact int8 -> fp16 conversion of 16 packed bytes (bytes 0..7 -> lo, 8..15 -> hi).
+// For q in [-127, 127]: u = q ^ 0x80 = q + 128 in [1, 255]; the fp16 bit pattern
+// 0x6400 | u encodes 1024 + u exactly, so (0x6400 | u) - 1152 = q exactly.
+DFL_DEV void dequant_i8x16(uint4 w, half8_t& lo, half8_t& hi) {
+  const uint32_t k64 = 0x64646464u;
+  uint32_t d[4] = {w.x ^ 0x80808080u, w.y ^ 0x80808080u, w.z ^ 0x80808080u, w.w ^ 0x80808080u};
+  uint32_t o[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o[2 * i] = __builtin_amdgcn_perm(k64, d[i], 0x04010400u);      // [b0, 64, b1, 64]
+    o[2 * i + 1] = __builtin_amdgcn_perm(k64, d[i], 0x04030402u);  // [b2, 64, b3, 64]
+  }
+  const half2_t bias = {(half_t)1152.0f, (half_t)1152.0f};
+  half2_t h[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) h[i] = __builtin_bit_cast(half2_t, o[i]) - bias;
+  lo = (half8_t){h[0].x, h[0].y, h[1].x, h[1].y, h[2].x, h[2].y, h[3].x, h[3].y};
+  hi = (half8_t){h[4].x, h[4].y, h[5].x, h[5].y, h[6].x, h[6].y, h[7].x, h[7].y};
+}
+
+DFL_DEV float h2f(half_t h) { return (float)h; }
+DFL_DEV half_t f2h(float f) { return (half_t)f; }   // round-to-nearest-even
+
+// Wave64 reductions via cross-lane shuffles.
+DFL_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+DFL_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Block-wide sum over all threads (blockDim.x a multiple of 64, <= 1024).
+DFL_DEV float block_sum(float v, float* smem /* >= 16 floats */) {
+  v = wave_sum(v);
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  __syncthreads();
+  if (l == 0) smem[w] = v;
+  __syncthreads();
+  float t = 0.f;
+  const int nw = blockDim.x >> 6;
+  for (int i = 0; i < nw; ++i) t += smem[i];   // fixed order: deterministic
+  return t;
+}
+
+// Monotone map of a float onto uint32 so that unsigned comparison orders floats.
+DFL_DEV uint32_t float_order_key(float f) {
+  uint32_t b = __float_as_uint(f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}

@@ -1,0 +1,92 @@
+// Internal kernel launch interface shared by the .hip translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dfl_common.h"
+
+namespace dfl {
+
+enum { WT_INT8 = 0, WT_F16 = 1 };
+enum { EPI_PARTIAL = 0, EPI_SWIGLU = 1, EPI_ARGMAX = 2 };
+
+struct SkinnyArgs {
+  const uint4* W;        // packed weight blocks
+  const half_t* scale;   // [N] per packed row (int8 weights) or nullptr
+  const half_t* X;       // activations, row-major, leading dimension ldx
+  int ldx;
+  int M;                 // activation rows
+  int N;                 // packed weight rows (multiple of 64)
+  int KB;                // k-blocks: K/32 (int8) or K/16 (fp16)
+  int S_x;               // k-splits across workgroups
+  float* ws;             // EPI_PARTIAL: [S_x][M][N] fp32
+  half_t* out;           // EPI_SWIGLU: [M][ldo] fp16, N/2 columns
+  int ldo;
+  float* logits;         // EPI_ARGMAX: optional [M][ldl] fp32
+  int ldl;
+  unsigned long long* keys;  // EPI_ARGMAX: optional [M] packed (order(value) << 32 | ~index)
+};
+
+void launch_skinny_gemm(int wt, int epi, const SkinnyArgs& a, int SK, int n_mtiles,
+                        hipStream_t st);
+
+// ---- pack / quantise (dfl_pack.hip) ----
+// Symmetric per-row int8 quantisation of w [oc][ic] fp32.
+void launch_quantize_w8(const float* w, int64_t oc, int64_t ic, int8_t* q, half_t* s,
+                        hipStream_t st);
+// int8 [rows][K] row-major (+ fp16 scales) -> packed blocks. Source row-block i goes to
+// destination row-block rb0 + i*rb_step of a matrix with KB = K/32 k-blocks.
+void launch_pack_i8(const int8_t* q, const half_t* s, int rows, int K, uint4* dst,
+                    half_t* dst_scale, int rb0, int rb_step, hipStream_t st);
+// fp16 [rows][K] row-major -> packed blocks (KB = K/16).
+void launch_pack_f16(const half_t* w, int rows, int K, uint4* dst, hipStream_t st);
+
+// ---- row kernels (dfl_rows.hip) ----
+// x[b] = ids ? embed[ids[b]] : noise[b];  h[b] = RMSNorm(x[b]) * g.  An id outside
+// [0, V) yields a zero row and sets *err |= 1.
+void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* noise, int B,
+                       int H, int V, const half_t* g, float eps, half_t* x, half_t* h, int* err,
+                       hipStream_t st);
+// v = sum_s ws[s][m][n] (fixed order) * scale[n] -> fp16; optional residual:
+// x[m][n] = fp16(x[m][n] + v) (else x[m][n] = v); then, if h != nullptr,
+// h[m][n] = RMSNorm(x[m]) * g.  One workgroup per row.
+void launch_reduce_resid_norm(const float* ws, int S_x, int M, int N, const half_t* scale,
+                              half_t* x, bool residual, const half_t* g, float eps, half_t* h,
+                              int ldh, hipStream_t st);
+// QKV reduce + per-head RMSNorm + neox RoPE + scatter.  Rows m use position pos0 + m.
+// Head slots [0, NH) -> Q[h][m][d] (q_rows rows per head); slots [NH, NH+NKV) -> K
+// cache rows (cache_row0 + m); [NH+NKV, NH+2NKV) -> Vt cache columns.  The partial sums
+// hold head slots col_slot0 .. col_slot0 + N/128 - 1 (so the ingest path can project
+// only K and V); scale is indexed by the absolute slot.
+struct QKRopeArgs {
+  const float* ws; int S_x; int M; int N;   // partial sums [S_x][M][N]
+  int col_slot0;                             // head slot of ws column 0
+  const half_t* scale;                       // [(NH+2NKV)*128]
+  int slot0, n_slots;                        // head slots handled (q,k,v numbering)
+  int NH, NKV;
+  const half_t* q_norm; const half_t* k_norm; float eps;
+  long long pos0; double log2_theta;
+  half_t* Q; int q_rows;                     // [NH][q_rows][128]
+  half_t* Kc; half_t* Vt; int cap; int cache_row0;  // K [NKV][cap][128], Vt [NKV][128][cap]
+};
+void launch_qk_rope(const QKRopeArgs& a, hipStream_t st);
+// ids[m] = ~low32(keys[m]); keys[m] = 0.
+void launch_argmax_finalize(unsigned long long* keys, int M, int32_t* ids, hipStream_t st);
+
+// ---- attention (dfl_attn.hip) ----
+struct AttnArgs {
+  const half_t* Q;        // [NH][B][128]
+  const half_t* Kc;       // [NKV][cap][128]
+  const half_t* Vt;       // [NKV][128][cap]
+  int B, NH, NKV, cap, L; // L = number of valid keys
+  int chunk;              // keys per split (multiple of 32)
+  int n_chunks;
+  float scale_log2;       // head_dim^-0.5 * log2(e)
+  float* Op;              // [n_chunks][NH*B][128] unnormalised partial outputs
+  float* Ml;              // [n_chunks][NH*B][2] running (max, sum) in log2 domain
+  half_t* O;              // [B][NH*128] final output
+};
+void launch_block_attention(const AttnArgs& a, hipStream_t st);
+
+}  // namespace dfl

@@ -1,0 +1,70 @@
+// Weight preparation kernels: the W8A16 quantiser and the HBM block packers.
+#include "dfl_common.h"
+#include "dfl_kernels.h"
+
+namespace dfl {
+
+// Symmetric per-output-channel int8 quantisation (ane_model.py:265-279):
+//   max = max_k |w[n][k]| (0 -> 1),  scale = max / 127 (fp32, correctly rounded),
+//   q = clamp(rint(w / scale), -127, 127),  stored scale = fp16(scale).
+// Same fp32 operation sequence as the numpy reference, so results are bit-identical.
+__global__ __launch_bounds__(256) void quantize_w8_kernel(const float* __restrict__ w, int64_t ic,
+                                                          int8_t* __restrict__ q,
+                                                          half_t* __restrict__ s) {
+  __shared__ float smax[4];
+  const int64_t rowi = blockIdx.x;
+  const float* wr = w + rowi * ic;
+  float mx = 0.f;
+  for (int64_t k = threadIdx.x; k < ic; k += blockDim.x) mx = fmaxf(mx, fabsf(wr[k]));
+  mx = wave_max(mx);
+  if ((threadIdx.x & 63) == 0) smax[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
+  if (mx == 0.f) mx = 1.0f;
+  const float scale = __fdiv_rn(mx, 127.0f);
+  int8_t* qr = q + rowi * ic;
+  for (int64_t k = threadIdx.x; k < ic; k += blockDim.x) {
+    float v = rintf(__fdiv_rn(wr[k], scale));
+    v = fminf(fmaxf(v, -127.f), 127.f);
+    qr[k] = (int8_t)(int)v;
+  }
+  if (threadIdx.x == 0) s[rowi] = f2h(scale);
+}
+
+void launch_quantize_w8(const float* w, int64_t oc, int64_t ic, int8_t* q, half_t* s,
+                        hipStream_t st) {
+  hipLaunchKernelGGL(quantize_w8_kernel, dim3((unsigned)oc), dim3(256), 0, st, w, ic, q, s);
+}
+
+__global__ __launch_bounds__(64) void pack_i8_kernel(const int8_t* __restrict__ q,
+                                                     const half_t* __restrict__ s, int K,
+                                                     uint4* __restrict__ dst,
+                                                     half_t* __restrict__ dscale, int rb0,
+                                                     int rb_step) {
+  const int kb = blockIdx.x, rb = blockIdx.y, l = threadIdx.x;
+  const int KB = K / 32;
+  const int drb = rb0 + rb * rb_step;
+  const int8_t* src = q + (size_t)(rb * 32 + (l & 31)) * K + (size_t)kb * 32 + 16 * (l >> 5);
+  dst[((size_t)drb * KB + kb) * 64 + l] = *reinterpret_cast<const uint4*>(src);
+  if (kb == 0 && l < 32) dscale[(size_t)drb * 32 + l] = s[(size_t)rb * 32 + l];
+}
+
+void launch_pack_i8(const int8_t* q, const half_t* s, int rows, int K, uint4* dst,
+                    half_t* dst_scale, int rb0, int rb_step, hipStream_t st) {
+  hipLaunchKernelGGL(pack_i8_kernel, dim3(K / 32, rows / 32), dim3(64), 0, st, q, s, K, dst,
+                     dst_scale, rb0, rb_step);
+}
+
+__global__ __launch_bounds__(64) void pack_f16_kernel(const half_t* __restrict__ w, int K,
+                                                      uint4* __restrict__ dst) {
+  const int kb = blockIdx.x, rb = blockIdx.y, l = threadIdx.x;
+  const int KB = K / 16;
+  const half_t* src = w + (size_t)(rb * 32 + (l & 31)) * K + (size_t)kb * 16 + 8 * (l >> 5);
+  dst[((size_t)rb * KB + kb) * 64 + l] = *reinterpret_cast<const uint4*>(src);
+}
+
+void launch_pack_f16(const half_t* w, int rows, int K, uint4* dst, hipStream_t st) {
+  hipLaunchKernelGGL(pack_f16_kernel, dim3(K / 16, rows / 32), dim3(64), 0, st, w, K, dst);
+}
+
+}  // namespace dfl

@@ -1,0 +1,170 @@
+// Row-wise kernels of the draft block: embedding + RMSNorm, split-K reduction with
+// residual add and the following RMSNorm, per-head Q/K RMSNorm + neox RoPE with the
+// KV-cache scatter, and the argmax finaliser.
+//
+// fp16 rounding points follow the MLX graph of mirror_sd/dflash.py: every Linear,
+// RMSNorm, RoPE and residual add produces an fp16 tensor; internal math is fp32.
+#include "dfl_common.h"
+#include "dfl_kernels.h"
+
+namespace dfl {
+
+constexpr int ROW_THREADS = 512;
+constexpr int ROW_MAXV = 16;   // hidden sizes up to 8192
+
+// RMSNorm output expression: fp16(fp16(x * r) * g)  (nn.RMSNorm, dflash.py:338-339).
+DFL_DEV half_t rms_out(float x, float r, half_t g) { return f2h(h2f(f2h(x * r)) * h2f(g)); }
+
+__global__ __launch_bounds__(ROW_THREADS) void embed_norm_kernel(
+    const int32_t* __restrict__ ids, const half_t* __restrict__ embed,
+    const half_t* __restrict__ noise, int H, int V, const half_t* __restrict__ g, float eps,
+    half_t* __restrict__ x, half_t* __restrict__ h, int* __restrict__ err) {
+  __shared__ float sm[16];
+  const int b = blockIdx.x;
+  const half_t* src = noise + (size_t)b * H;
+  bool bad = false;
+  if (ids) {
+    const int id = ids[b];
+    bad = id < 0 || id >= V;   // out-of-range token id: flag it, use a zero row
+    src = embed + (size_t)(bad ? 0 : id) * H;
+    if (bad && threadIdx.x == 0) atomicOr(err, 1);
+  }
+  float v[ROW_MAXV];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < ROW_MAXV; ++i) {
+    const int k = threadIdx.x + i * ROW_THREADS;
+    v[i] = 0.f;
+    if (k < H) {
+      const half_t t = bad ? (half_t)0.0f : src[k];
+      x[(size_t)b * H + k] = t;
+      v[i] = h2f(t);
+      ss += v[i] * v[i];
+    }
+  }
+  ss = block_sum(ss, sm);
+  const float r = 1.0f / sqrtf(ss / (float)H + eps);
+#pragma unroll
+  for (int i = 0; i < ROW_MAXV; ++i) {
+    const int k = threadIdx.x + i * ROW_THREADS;
+    if (k < H) h[(size_t)b * H + k] = rms_out(v[i], r, g[k]);
+  }
+}
+
+void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* noise, int B,
+                       int H, int V, const half_t* g, float eps, half_t* x, half_t* h, int* err,
+                       hipStream_t st) {
+  hipLaunchKernelGGL(embed_norm_kernel, dim3(B), dim3(ROW_THREADS), 0, st, ids, embed, noise, H,
+                     V, g, eps, x, h, err);
+}
+
+__global__ __launch_bounds__(ROW_THREADS) void reduce_resid_norm_kernel(
+    const float* __restrict__ ws, int S_x, int M, int N, const half_t* __restrict__ scale,
+    half_t* __restrict__ x, int residual, const half_t* __restrict__ g, float eps,
+    half_t* __restrict__ h, int ldh) {
+  __shared__ float sm[16];
+  const int m = blockIdx.x;
+  float v[ROW_MAXV];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < ROW_MAXV; ++i) {
+    const int n = threadIdx.x + i * ROW_THREADS;
+    v[i] = 0.f;
+    if (n < N) {
+      float acc = 0.f;
+      for (int s = 0; s < S_x; ++s) acc += ws[((size_t)s * M + m) * N + n];
+      float y = h2f(f2h(scale ? acc * h2f(scale[n]) : acc));
+      if (residual) y = h2f(f2h(h2f(x[(size_t)m * N + n]) + y));
+      if (x) x[(size_t)m * N + n] = f2h(y);
+      v[i] = y;
+      ss += y * y;
+    }
+  }
+  if (!h) return;
+  ss = block_sum(ss, sm);
+  const float r = 1.0f / sqrtf(ss / (float)N + eps);
+#pragma unroll
+  for (int i = 0; i < ROW_MAXV; ++i) {
+    const int n = threadIdx.x + i * ROW_THREADS;
+    if (n < N) h[(size_t)m * ldh + n] = rms_out(v[i], r, g[n]);
+  }
+}
+
+void launch_reduce_resid_norm(const float* ws, int S_x, int M, int N, const half_t* scale,
+                              half_t* x, bool residual, const half_t* g, float eps, half_t* h,
+                              int ldh, hipStream_t st) {
+  hipLaunchKernelGGL(reduce_resid_norm_kernel, dim3(M), dim3(ROW_THREADS), 0, st, ws, S_x, M, N,
+                     scale, x, residual ? 1 : 0, g, eps, h, ldh);
+}
+
+// One wave per (row m, head slot); lane j holds head elements j and j + 64, which are
+// exactly the neox RoPE pair (dflash.py:263-275, split-half rotation), so the
+// rotation is lane-local.  Angles are computed in fp64 (pos * theta^(-j/64)).
+__global__ __launch_bounds__(256) void qk_rope_kernel(QKRopeArgs a) {
+  const int lane = threadIdx.x & 63;
+  const long long p = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (p >= (long long)a.M * a.n_slots) return;
+  const int m = (int)(p / a.n_slots);
+  const int slot = a.slot0 + (int)(p - (long long)m * a.n_slots);
+  const int n0 = slot * 128 + lane, n1 = n0 + 64;
+  const int c0 = (slot - a.col_slot0) * 128 + lane;
+  float v0 = 0.f, v1 = 0.f;
+  for (int s = 0; s < a.S_x; ++s) {
+    const float* wsr = a.ws + ((size_t)s * a.M + m) * a.N;
+    v0 += wsr[c0];
+    v1 += wsr[c0 + 64];
+  }
+  v0 = h2f(f2h(v0 * h2f(a.scale[n0])));   // Linear output is fp16
+  v1 = h2f(f2h(v1 * h2f(a.scale[n1])));
+  const int kv_slot0 = a.NH + a.NKV;
+  if (slot >= kv_slot0) {   // V head: no norm, no rotation
+    const int gk = slot - kv_slot0;
+    half_t* vt = a.Vt + (size_t)gk * 128 * a.cap + a.cache_row0 + m;
+    vt[(size_t)lane * a.cap] = f2h(v0);
+    vt[(size_t)(lane + 64) * a.cap] = f2h(v1);
+    return;
+  }
+  const bool is_q = slot < a.NH;
+  const half_t* gn = is_q ? a.q_norm : a.k_norm;
+  const float ss = wave_sum(v0 * v0 + v1 * v1);
+  const float r = 1.0f / sqrtf(ss * (1.0f / 128.0f) + a.eps);
+  const float y0 = h2f(rms_out(v0, r, gn[lane]));
+  const float y1 = h2f(rms_out(v1, r, gn[lane + 64]));
+  const double inv_freq = exp2(-(double)lane * (1.0 / 64.0) * a.log2_theta);
+  const double ang = (double)(a.pos0 + m) * inv_freq;
+  double sd, cd;
+  sincos(ang, &sd, &cd);
+  const float c = (float)cd, sn = (float)sd;
+  const half_t o0 = f2h(y0 * c - y1 * sn);
+  const half_t o1 = f2h(y1 * c + y0 * sn);
+  half_t* dst;
+  if (is_q) {
+    dst = a.Q + ((size_t)slot * a.q_rows + m) * 128;
+  } else {
+    const int gk = slot - a.NH;
+    dst = a.Kc + ((size_t)gk * a.cap + a.cache_row0 + m) * 128;
+  }
+  dst[lane] = o0;
+  dst[lane + 64] = o1;
+}
+
+void launch_qk_rope(const QKRopeArgs& a, hipStream_t st) {
+  const long long waves = (long long)a.M * a.n_slots;
+  hipLaunchKernelGGL(qk_rope_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, a);
+}
+
+__global__ void argmax_finalize_kernel(unsigned long long* keys, int M, int32_t* ids) {
+  const int m = threadIdx.x;
+  if (m < M) {
+    const unsigned long long k = keys[m];
+    ids[m] = k ? (int32_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull)) : -1;
+    keys[m] = 0ull;
+  }
+}
+
+void launch_argmax_finalize(unsigned long long* keys, int M, int32_t* ids, hipStream_t st) {
+  hipLaunchKernelGGL(argmax_finalize_kernel, dim3(1), dim3(64 * ((M + 63) / 64)), 0, st, keys,
+                     M, ids);
+}
+
+}  // namespace dfl

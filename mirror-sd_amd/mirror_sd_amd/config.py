@@ -1,0 +1,182 @@
+"""Draft-model configuration: the schema of the reference's ``DFlashConfig``.
+
+Field names, defaults and the two construction paths (class defaults versus
+``from_dict`` defaults) follow mirror_sd/dflash.py:34-105 exactly, including the
+places where the two disagree (rope_theta 1e6 vs 1e4, mask id 151669 vs 151667,
+intermediate 12288 vs 10944, kv heads 8 vs 2), because checkpoints loaded through
+``from_dict`` rely on the latter.  ``build_target_layer_ids`` follows
+dflash.py:108-119 and ``extract_context_feature`` dflash.py:122-130.
+
+The named workloads at the bottom are the benchmark shapes this library is
+measured and tested on (hidden/heads/FFN/block/context/vocab per workload).
+"""
+
+from __future__ import annotations
+
+import copy
+from dataclasses import dataclass, field, asdict
+from typing import List, Optional, Sequence
+
+
+@dataclass
+class DFlashConfig:
+    """Mirror of ``DFlashConfig`` (mirror_sd/dflash.py:34-50)."""
+
+    hidden_size: int = 4096
+    num_hidden_layers: int = 5
+    intermediate_size: int = 12288
+    num_attention_heads: int = 32
+    num_key_value_heads: int = 8
+    head_dim: int = 128
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 1000000.0
+    max_position_embeddings: int = 40960
+    vocab_size: int = 151936
+    block_size: int = 16
+    mask_token_id: int = 151669
+    target_layer_ids: List[int] = field(default_factory=lambda: [4, 12, 19, 26, 33])
+    num_target_layers: int = 36
+    rope_scaling: Optional[dict] = None
+
+    # dflash.py:52-58
+    @classmethod
+    def qwen3_8b(cls, num_target_layers: int = 36) -> "DFlashConfig":
+        cfg = cls(num_target_layers=num_target_layers)
+        cfg.target_layer_ids = build_target_layer_ids(num_target_layers, cfg.num_hidden_layers)
+        return cfg
+
+    # dflash.py:60-75
+    @classmethod
+    def qwen3_4b(cls, num_target_layers: int = 36) -> "DFlashConfig":
+        cfg = cls(hidden_size=2560, num_hidden_layers=5, intermediate_size=6912,
+                  num_attention_heads=20, num_key_value_heads=4, head_dim=128,
+                  vocab_size=151936)
+        cfg.num_target_layers = num_target_layers
+        cfg.target_layer_ids = build_target_layer_ids(num_target_layers, cfg.num_hidden_layers)
+        return cfg
+
+    # dflash.py:77-105
+    @classmethod
+    def from_dict(cls, d: dict) -> "DFlashConfig":
+        dcfg = d.get("dflash_config", {})
+        num_hidden_layers = d.get("num_hidden_layers", dcfg.get("num_hidden_layers", 5))
+        num_target_layers = dcfg.get("num_target_layers", d.get("num_target_layers", 36))
+        cfg = cls(
+            hidden_size=d.get("hidden_size", 4096),
+            num_hidden_layers=num_hidden_layers,
+            intermediate_size=d.get("intermediate_size", 10944),
+            num_attention_heads=d.get("num_attention_heads", 32),
+            num_key_value_heads=d.get("num_key_value_heads", 2),
+            head_dim=d.get("head_dim", 128),
+            rms_norm_eps=d.get("rms_norm_eps", 1e-6),
+            rope_theta=d.get("rope_theta", 10000.0),
+            max_position_embeddings=d.get("max_position_embeddings", 4096),
+            vocab_size=d.get("vocab_size", 151936),
+            block_size=dcfg.get("block_size", d.get("block_size", 16)),
+            mask_token_id=dcfg.get("mask_token_id", d.get("mask_token_id", 151667)),
+            num_target_layers=num_target_layers,
+        )
+        if "target_layer_ids" in dcfg:
+            cfg.target_layer_ids = list(dcfg["target_layer_ids"])
+        else:
+            cfg.target_layer_ids = build_target_layer_ids(cfg.num_target_layers,
+                                                           cfg.num_hidden_layers)
+        if "rope_scaling" in d:
+            cfg.rope_scaling = d["rope_scaling"]
+        return cfg
+
+    @property
+    def num_target_features(self) -> int:
+        """Number of tapped target layers concatenated into target_hidden (dflash.py:373-377)."""
+        return len(self.target_layer_ids)
+
+    def to_dict(self) -> dict:
+        return asdict(self)
+
+    def copy(self) -> "DFlashConfig":
+        return copy.deepcopy(self)
+
+
+def build_target_layer_ids(num_target_layers: int, num_draft_layers: int) -> List[int]:
+    """dflash.py:108-119: evenly spaced taps over target layers [1, L-3]."""
+    if num_draft_layers == 1:
+        return [num_target_layers // 2]
+    start = 1
+    end = num_target_layers - 3
+    span = end - start
+    return [int(round(start + (i * span) / (num_draft_layers - 1)))
+            for i in range(num_draft_layers)]
+
+
+def extract_context_feature(hidden_states: Sequence, layer_ids: Sequence[int]):
+    """dflash.py:122-130: concatenate tapped layer outputs along the feature axis.
+
+    Works on torch tensors or numpy arrays.  When ``hidden_states`` holds every
+    layer output (embedding at index 0), layer ``lid`` is read at ``lid + 1``.
+    """
+    if len(hidden_states) == len(layer_ids):
+        sel = list(hidden_states)
+    else:
+        sel = [hidden_states[lid + 1] for lid in layer_ids]
+    first = sel[0]
+    if hasattr(first, "detach"):  # torch
+        import torch
+        return torch.cat(sel, dim=-1)
+    import numpy as np
+    return np.concatenate(sel, axis=-1)
+
+
+# ---------------------------------------------------------------------------
+# Named benchmark / test workloads.
+# ---------------------------------------------------------------------------
+
+@dataclass
+class Workload:
+    """One benchmark shape: a draft config plus block/context sizes."""
+
+    name: str
+    cfg: DFlashConfig
+    block: int
+    ctx: int
+    description: str = ""
+    with_lm_head: bool = True
+    n_feat: int = 5
+
+
+def _draft_cfg(hidden, heads, kv_heads, ffn, layers, vocab=151936, theta=1e6,
+               block=16, mask_id=151669, n_feat=5):
+    cfg = DFlashConfig(hidden_size=hidden, num_hidden_layers=layers,
+                       intermediate_size=ffn, num_attention_heads=heads,
+                       num_key_value_heads=kv_heads, head_dim=128, rms_norm_eps=1e-6,
+                       rope_theta=theta, vocab_size=vocab, block_size=block,
+                       mask_token_id=mask_id)
+    # n_feat tapped layers -> fc input is n_feat*hidden.
+    cfg.target_layer_ids = build_target_layer_ids(36, n_feat)
+    return cfg
+
+
+def workload(name: str) -> Workload:
+    """Return a named workload.
+
+    qwen3_4b_layer  : 1 layer, H2560, 32/8 heads, FFN 9728, block 16, ctx 64 (no lm_head).
+    qwen3_8b_draft  : 5 layers, H4096, 32/8, FFN 12288, block 16, ctx 2048, V151936.
+    dflash_27b      : 5 layers, H5120, 40/8, FFN 17408, block 32, ctx 4096, V151936.
+    dflash_27b_ctxN : dflash_27b at context N (64, 2048, 4096, 16384, 32768).
+    """
+    if name == "qwen3_4b_layer":
+        cfg = _draft_cfg(2560, 32, 8, 9728, 1, block=16)
+        return Workload(name, cfg, block=16, ctx=64, with_lm_head=False,
+                        description="1 layer, H2560, 32/8 heads, FFN 9728, block 16, ctx 64")
+    if name == "qwen3_8b_draft":
+        cfg = _draft_cfg(4096, 32, 8, 12288, 5, block=16)
+        return Workload(name, cfg, block=16, ctx=2048,
+                        description="5 layers, H4096, 32/8 heads, FFN 12288, block 16, ctx 2048, V151936")
+    if name == "dflash_27b" or name.startswith("dflash_27b_ctx"):
+        ctx = 4096 if name == "dflash_27b" else int(name[len("dflash_27b_ctx"):])
+        cfg = _draft_cfg(5120, 40, 8, 17408, 5, block=32)
+        return Workload(name, cfg, block=32, ctx=ctx,
+                        description=f"5 layers, H5120, 40/8 heads, FFN 17408, block 32, ctx {ctx}, V151936")
+    if name == "tiny":
+        cfg = _draft_cfg(256, 4, 2, 512, 2, vocab=1024, block=8)
+        return Workload(name, cfg, block=8, ctx=24, description="test shape")
+    raise KeyError(name)

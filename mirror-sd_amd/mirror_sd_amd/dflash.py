@@ -1,0 +1,519 @@
+"""DFlash draft model on MI355X: drop-in for mirror_sd/dflash.py's ``DFlashDraftModel``.
+
+The public surface mirrors the reference:
+
+* ``DFlashDraftModel(config)`` with ``.config``, ``.block_size``, ``.mask_token_id``,
+  ``.num_draft_layers`` (mutable) and ``__call__(noise_embedding, target_hidden,
+  mask=None, cache=None)`` returning the final-normed hidden states
+  (dflash.py:365-403);
+* ``make_cache()`` returning per-layer ``DFlashKVCache`` handles with ``.offset``,
+  ``.keys`` / ``.values`` and ``.trim(n)`` (dflash.py:139-212, 405-406);
+* the split API of the ANE draft that ``_spec_generate_parallel`` drives from a worker
+  thread: ``prepare_forward`` / ``run_kernels`` / ``read_output`` /
+  ``read_draft_tokens`` / ``set_block_size`` / ``max_ctx_len`` / ``_compute_context``
+  (ane_model.py:384-430, 538-637);
+* the north-star entry point ``draft(ids, target_hidden)`` -> per-position logits and
+  argmax ids (generate.py:594-606 in one call).
+
+All arithmetic runs in libdflash_hip.so on the GPU.  Tensors are torch CUDA tensors;
+batch size 1 per model instance (the reference draft is single-sequence).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Dict, List, Optional
+
+from . import _lib
+from .config import DFlashConfig
+from .synth import PROJ_NAMES, proj_key
+
+__all__ = ["DFlashDraftModel", "DFlashKVCache", "sample"]
+
+
+def sample(logits, temperature: float = 0.0):
+    """dflash.py:133-136: greedy argmax below 1e-5, else categorical."""
+    import torch
+    if temperature < 1e-5:
+        return torch.argmax(logits, dim=-1)
+    probs = torch.softmax(logits.float() / temperature, dim=-1)
+    flat = probs.reshape(-1, probs.shape[-1])
+    return torch.multinomial(flat, 1).reshape(probs.shape[:-1])
+
+
+class DFlashKVCache:
+    """Per-layer handle onto the model's device-resident KV cache (dflash.py:139-212).
+
+    ``offset`` counts absolute positions, ``trim(n)`` drops the last n rows exactly as
+    the reference does; the device cache is reconciled with these handles at the next
+    forward call.  ``keys`` / ``values`` are device views ``[1, NKV, L, 128]`` (keys
+    after k_norm and RoPE, as the reference stores them).
+    """
+
+    def __init__(self, model: "DFlashDraftModel", layer: int, generation: int,
+                 sink_size: int = 0, window_size: int = 0):
+        self._model = model
+        self.layer = layer
+        self._gen = generation
+        self.sink_size = int(sink_size)
+        self.window_size = int(window_size)
+        self.offset = 0
+        self._len = 0
+        self._has_keys = False
+
+    def trim(self, n: int):
+        if self._has_keys and n > 0:
+            self._len = max(self._len - n, 0)
+            self.offset -= n
+
+    @property
+    def keys(self):
+        if not self._has_keys:
+            return None
+        k, vt = self._model._cache_tensors[self.layer]
+        return k[:, :self._len].unsqueeze(0)
+
+    @property
+    def values(self):
+        if not self._has_keys:
+            return None
+        k, vt = self._model._cache_tensors[self.layer]
+        return vt[:, :, :self._len].transpose(1, 2).unsqueeze(0)
+
+    def update_and_fetch(self, keys, values):
+        raise NotImplementedError(
+            "the device cache is filled by DFlashDraftModel.__call__; update_and_fetch is "
+            "not callable directly")
+
+    def state(self):
+        if not self._has_keys:
+            return []
+        return [self.keys, self.values]
+
+
+class DFlashDraftModel:
+    """MI355X draft model behind the reference ``DFlashDraftModel`` interface."""
+
+    def __init__(self, config: DFlashConfig, max_ctx: int = 8192, max_block: Optional[int] = None,
+                 device=None, n_target_feat: Optional[int] = None):
+        import torch
+        self.config = config
+        self.block_size = config.block_size
+        self.mask_token_id = config.mask_token_id
+        self.num_draft_layers = config.num_hidden_layers
+        self.device = torch.device(device if device is not None else "cuda")
+        self.max_ctx_len = int(max_ctx)
+        self.max_block = int(max_block if max_block is not None else max(config.block_size, 32))
+        self.n_feat = config.num_target_features if n_target_feat is None else int(n_target_feat)
+        self._L = _lib.load()
+        cfg = _lib.DflConfig(
+            hidden=config.hidden_size, n_heads=config.num_attention_heads,
+            n_kv_heads=config.num_key_value_heads, head_dim=config.head_dim,
+            intermediate=config.intermediate_size, n_layers=config.num_hidden_layers,
+            n_target_feat=self.n_feat, vocab=config.vocab_size, max_block=self.max_block,
+            max_ctx=self.max_ctx_len, rms_eps=config.rms_norm_eps,
+            rope_theta=float(config.rope_theta))
+        h = ctypes.c_void_p()
+        with torch.cuda.device(self.device):
+            _lib.check(self._L.dfl_create(ctypes.byref(cfg), ctypes.byref(h)), "dfl_create")
+        self._ctx = h
+        self._keep: Dict[str, object] = {}   # caller-owned buffers the library points at
+        self._gen = 0
+        self._cache_tensors = self._make_cache_views()
+        self._layers_loaded = [False] * config.num_hidden_layers
+        self._has_fc = False
+        self._has_head = False
+        self._has_lm = False
+        self._has_embed = False
+        # split-API state
+        self._prepared = None
+        self._out_hidden = None
+        self._out_ids = None
+
+    # ------------------------------------------------------------------ lifecycle
+    def close(self):
+        if getattr(self, "_ctx", None):
+            self._L.dfl_destroy(self._ctx)
+            self._ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _stream(self):
+        return _lib.stream_handle()
+
+    def _make_cache_views(self):
+        import torch
+        views = []
+        for layer in range(self.config.num_hidden_layers):
+            k_ptr, vt_ptr = ctypes.c_void_p(), ctypes.c_void_p()
+            cap = ctypes.c_int32()
+            _lib.check(self._L.dfl_cache_kv(self._ctx, layer, ctypes.byref(k_ptr),
+                                            ctypes.byref(vt_ptr), ctypes.byref(cap)),
+                       "dfl_cache_kv")
+            nkv, c = self.config.num_key_value_heads, cap.value
+            views.append((_wrap_device(k_ptr.value, (nkv, c, 128), self.device),
+                          _wrap_device(vt_ptr.value, (nkv, 128, c), self.device)))
+        return views
+
+    # ------------------------------------------------------------------ weights
+    def load_weights(self, tensors: Dict[str, "torch.Tensor"], quantized: Optional[Dict] = None):
+        """Load draft weights named as the reference module attributes.
+
+        Projection weights (``layers.{i}.self_attn.q_proj.weight`` ...) are quantised
+        on the GPU with the W8A16 quantiser of ane_model.py:265-279 unless
+        ``quantized[name] = (q int8 [oc, ic], scale fp16 [oc])`` is supplied.
+        ``fc.weight`` / ``hidden_norm.weight`` / ``norm.weight`` and norm gains are
+        fp16; ``embed_tokens.weight`` / ``lm_head.weight`` are optional fp16 [V, H].
+        """
+        import torch
+        dev = self.device
+        st = self._stream()
+        quantized = quantized or {}
+        for i in range(self.config.num_hidden_layers):
+            qs, ss = [], []
+            for p in PROJ_NAMES:
+                key = proj_key(i, p)
+                if key in quantized:
+                    q, s = quantized[key]
+                    q = q.to(dev, torch.int8).contiguous()
+                    s = s.to(dev, torch.float16).contiguous()
+                else:
+                    q, s = self.quantize_w8(tensors[key])
+                qs.append(q)
+                ss.append(s)
+            norms = [tensors[f"layers.{i}.input_layernorm.weight"],
+                     tensors[f"layers.{i}.post_attention_layernorm.weight"],
+                     tensors[f"layers.{i}.self_attn.q_norm.weight"],
+                     tensors[f"layers.{i}.self_attn.k_norm.weight"]]
+            norms = [n.to(dev, torch.float16).contiguous() for n in norms]
+            self.load_layer_q8(i, qs, ss, *norms)
+            del qs, ss
+        if "fc.weight" in tensors and self.n_feat > 0:
+            self.load_fc(tensors["fc.weight"], tensors["hidden_norm.weight"])
+        self.load_head(tensors["norm.weight"], tensors.get("embed_tokens.weight"),
+                       tensors.get("lm_head.weight"))
+        torch.cuda.current_stream().synchronize()
+
+    def quantize_w8(self, w):
+        """W8A16 quantiser on the GPU: returns (q int8 [oc, ic], scale fp16 [oc])."""
+        import torch
+        w32 = w.to(self.device, torch.float32).contiguous()
+        oc, ic = w32.shape
+        q = torch.empty((oc, ic), dtype=torch.int8, device=self.device)
+        s = torch.empty((oc,), dtype=torch.float16, device=self.device)
+        _lib.check(self._L.dfl_quantize_w8(w32.data_ptr(), oc, ic, q.data_ptr(), s.data_ptr(),
+                                           self._stream()), "dfl_quantize_w8")
+        return q, s
+
+    def load_layer_q8(self, layer, qs, ss, in_norm, post_norm, q_norm, k_norm):
+        """Load one layer from W8A16 tensors in the order q,k,v,o,gate,up,down
+        (the Q8LayerWeights order, wrapper.rs:363-428)."""
+        shapes = self._proj_shapes()
+        for (name, shp), q, s in zip(shapes, qs, ss):
+            if tuple(q.shape) != shp or tuple(s.shape) != (shp[0],):
+                raise ValueError(f"layer {layer} {name}: expected int8 {shp} + fp16 [{shp[0]}], "
+                                 f"got {tuple(q.shape)} / {tuple(s.shape)}")
+        H, D = self.config.hidden_size, self.config.head_dim
+        for n, exp in zip((in_norm, post_norm, q_norm, k_norm), (H, H, D, D)):
+            if n.numel() != exp:
+                raise ValueError(f"layer {layer}: norm gain of {n.numel()} elements, expected {exp}")
+        qa = _lib.PtrArray7(*[q.data_ptr() for q in qs])
+        sa = _lib.PtrArray7(*[s.data_ptr() for s in ss])
+        _lib.check(self._L.dfl_load_layer_w8(self._ctx, layer, qa, sa, in_norm.data_ptr(),
+                                             post_norm.data_ptr(), q_norm.data_ptr(),
+                                             k_norm.data_ptr(), self._stream()),
+                   "dfl_load_layer_w8")
+        # the pack kernels read the inputs asynchronously: keep them alive until done
+        import torch
+        torch.cuda.current_stream().synchronize()
+        self._layers_loaded[layer] = True
+
+    def load_fc(self, fc_weight, hidden_norm):
+        import torch
+        H = self.config.hidden_size
+        w = fc_weight.to(self.device, torch.float16).contiguous()
+        g = hidden_norm.to(self.device, torch.float16).contiguous()
+        if tuple(w.shape) != (H, self.n_feat * H):
+            raise ValueError(f"fc.weight: expected {(H, self.n_feat * H)}, got {tuple(w.shape)}")
+        _lib.check(self._L.dfl_load_fc(self._ctx, w.data_ptr(), g.data_ptr(), self._stream()),
+                   "dfl_load_fc")
+        torch.cuda.current_stream().synchronize()
+        self._has_fc = True
+
+    def load_head(self, final_norm, embed=None, lm_head=None):
+        """Final norm gain, the target's embedding (kept by reference) and lm_head
+        (target.py:188-197)."""
+        import torch
+        H, V = self.config.hidden_size, self.config.vocab_size
+        g = final_norm.to(self.device, torch.float16).contiguous()
+        e = None
+        if embed is not None:
+            e = embed.to(self.device, torch.float16).contiguous()
+            if tuple(e.shape) != (V, H):
+                raise ValueError(f"embed_tokens: expected {(V, H)}, got {tuple(e.shape)}")
+            self._keep["embed"] = e
+        lm = None
+        if lm_head is not None:
+            lm = lm_head.to(self.device, torch.float16).contiguous()
+            if tuple(lm.shape) != (V, H):
+                raise ValueError(f"lm_head: expected {(V, H)}, got {tuple(lm.shape)}")
+        _lib.check(self._L.dfl_load_head(self._ctx, g.data_ptr(), _lib.ptr(e), _lib.ptr(lm),
+                                         self._stream()), "dfl_load_head")
+        torch.cuda.current_stream().synchronize()
+        self._has_head = True
+        self._has_embed = e is not None
+        self._has_lm = lm is not None
+
+    def _proj_shapes(self):
+        from .synth import proj_shapes
+        shp = proj_shapes(self.config)
+        return [(p, shp[p]) for p in PROJ_NAMES]
+
+    # ------------------------------------------------------------------ cache
+    def make_cache(self, sink_size: int = 64, window_size: int = 1024) -> List[DFlashKVCache]:
+        """dflash.py:405-406.  One live cache per model: a new cache resets the device
+        cache and invalidates older handles.  Sink/window eviction (dflash.py:179-193)
+        is not performed on the device; a cache that would evict raises."""
+        self._gen += 1
+        _lib.check(self._L.dfl_cache_reset(self._ctx), "dfl_cache_reset")
+        return [DFlashKVCache(self, i, self._gen, sink_size, window_size)
+                for i in range(self.num_draft_layers)]
+
+    def _device_state(self):
+        n = ctypes.c_int32()
+        off = ctypes.c_int64()
+        _lib.check(self._L.dfl_cache_state(self._ctx, ctypes.byref(n), ctypes.byref(off)),
+                   "dfl_cache_state")
+        return n.value, off.value
+
+    def _sync_cache(self, cache: List[DFlashKVCache], check_only: bool = False):
+        """Bring the device cache to the state the per-layer handles describe."""
+        if any(c._gen != self._gen or c._model is not self for c in cache):
+            raise ValueError("stale cache: create caches with this model's make_cache()")
+        lens = {c._len for c in cache}
+        offs = {c.offset for c in cache}
+        if len(lens) != 1 or len(offs) != 1:
+            raise ValueError("per-layer caches diverged (different length/offset per layer)")
+        want_len, want_off = lens.pop(), offs.pop()
+        if check_only:
+            return
+        dev_len, dev_off = self._device_state()
+        if want_len > dev_len:
+            _lib.check(self._L.dfl_cache_commit(self._ctx, want_len - dev_len), "dfl_cache_commit")
+        elif want_len < dev_len:
+            _lib.check(self._L.dfl_cache_trim(self._ctx, dev_len - want_len), "dfl_cache_trim")
+        _lib.check(self._L.dfl_cache_set_offset(self._ctx, want_off), "dfl_cache_set_offset")
+
+    def _check_window(self, cache, new_rows):
+        for c in cache:
+            if c.sink_size > 0 and c.window_size > 0 and \
+                    c._len + new_rows > c.sink_size + c.window_size:
+                raise NotImplementedError(
+                    "sink/window eviction of the draft cache is not implemented on the GPU; "
+                    "use make_cache(0, 0) or a context below sink+window rows")
+
+    # ------------------------------------------------------------------ forward
+    def _apply_num_layers(self):
+        n = int(self.num_draft_layers)
+        _lib.check(self._L.dfl_set_num_layers(self._ctx, n), "dfl_set_num_layers")
+
+    def _ingest(self, target_hidden, fused: bool = False):
+        import torch
+        th = target_hidden
+        if th.dim() == 3:
+            if th.shape[0] != 1:
+                raise ValueError("batch size must be 1")
+            th = th[0]
+        th = th.to(self.device, torch.float16).contiguous()
+        C = th.shape[0]
+        if C == 0:
+            return
+        if fused:
+            if th.shape[1] != self.config.hidden_size:
+                raise ValueError(f"fused context must be [C, {self.config.hidden_size}]")
+            _lib.check(self._L.dfl_ingest_fused(self._ctx, th.data_ptr(), C, self._stream()),
+                       "dfl_ingest_fused")
+        else:
+            if th.shape[1] != self.n_feat * self.config.hidden_size:
+                raise ValueError(f"target_hidden must be [C, {self.n_feat * self.config.hidden_size}],"
+                                 f" got {tuple(th.shape)}")
+            _lib.check(self._L.dfl_ingest_context(self._ctx, th.data_ptr(), C, self._stream()),
+                       "dfl_ingest_context")
+        self._keep["ingest_src"] = th   # keep alive until the stream passes it
+
+    def _draft(self, noise=None, ids=None, want_hidden=True, want_prenorm=False,
+               want_logits=False, want_ids=False):
+        import torch
+        H, V = self.config.hidden_size, self.config.vocab_size
+        if noise is not None:
+            if noise.dim() == 3:
+                if noise.shape[0] != 1:
+                    raise ValueError("batch size must be 1")
+                noise = noise[0]
+            noise = noise.to(self.device, torch.float16).contiguous()
+            B = noise.shape[0]
+            if noise.shape[1] != H:
+                raise ValueError(f"noise_embedding must be [B, {H}]")
+        else:
+            ids = torch.as_tensor(ids, dtype=torch.int32).reshape(-1)
+            if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= V):
+                raise ValueError(f"token id outside [0, {V})")
+            ids = ids.to(self.device).contiguous()
+            B = ids.numel()
+        if not all(self._layers_loaded[:self.num_draft_layers]) or not self._has_head:
+            raise RuntimeError("weights not loaded")
+        out_h = torch.empty((B, H), dtype=torch.float16, device=self.device) if want_hidden else None
+        out_p = torch.empty((B, H), dtype=torch.float16, device=self.device) if want_prenorm else None
+        out_l = torch.empty((B, V), dtype=torch.float32, device=self.device) if want_logits else None
+        out_i = torch.empty((B,), dtype=torch.int32, device=self.device) if want_ids else None
+        _lib.check(self._L.dfl_draft_block(
+            self._ctx, _lib.ptr(noise), _lib.ptr(ids), B, _lib.ptr(out_h), _lib.ptr(out_p),
+            _lib.ptr(out_l), _lib.ptr(out_i), self._stream()), "dfl_draft_block")
+        self._keep["draft_src"] = (noise, ids)
+        return out_h, out_p, out_l, out_i
+
+    def __call__(self, noise_embedding, target_hidden, mask=None, cache=None, **kwargs):
+        """dflash.py:384-403.  noise_embedding [1, q, H], target_hidden [1, C, nf*H];
+        returns final-normed hidden [1, q, H] (fp16).  With ``cache`` the context rows
+        are appended to the cache and the block rows are left in it (offset += C + q)
+        until the caller's ``trim(q)``, exactly as update_and_fetch + trim behave."""
+        if mask is not None:
+            raise ValueError("DFlash drafting is non-causal; mask must be None (dflash.py:215-233)")
+        self._apply_num_layers()
+        q = noise_embedding.shape[-2]
+        C = target_hidden.shape[-2]
+        if cache is None:
+            _lib.check(self._L.dfl_cache_reset(self._ctx), "dfl_cache_reset")
+            self._gen += 1
+            self._ingest(target_hidden)
+            out_h, _, _, _ = self._draft(noise=noise_embedding)
+            _lib.check(self._L.dfl_cache_reset(self._ctx), "dfl_cache_reset")
+            return out_h.unsqueeze(0)
+        cache = list(cache)[:self.num_draft_layers]
+        self._check_window(cache, C + q)
+        self._sync_cache(cache)
+        self._ingest(target_hidden)
+        out_h, _, _, _ = self._draft(noise=noise_embedding)
+        for c in cache:
+            c._len += C + q
+            c.offset += C + q
+            c._has_keys = True
+        return out_h.unsqueeze(0)
+
+    def draft(self, ids, target_hidden=None, cache=None, return_logits=False,
+              return_hidden=False, fused_context=False):
+        """North-star entry point: block token ids [B] (+ new target_hidden rows) in,
+        per-position argmax ids [B] (and fp32 logits [B, V]) out.
+
+        Equivalent to the serial caller's embed -> draft -> lm_head -> argmax ->
+        trim sequence (generate.py:594-609) for all B positions; position 0 (the
+        anchor) is included, callers use 1..B-1.
+        """
+        self._apply_num_layers()
+        if cache is None:
+            _lib.check(self._L.dfl_cache_reset(self._ctx), "dfl_cache_reset")
+            self._gen += 1
+        else:
+            cache = list(cache)[:self.num_draft_layers]
+            self._sync_cache(cache)
+        if target_hidden is not None:
+            self._ingest(target_hidden, fused=fused_context)
+            if cache is not None:
+                C = target_hidden.shape[-2]
+                for c in cache:
+                    c._len += C
+                    c.offset += C
+                    c._has_keys = True
+        out_h, _, out_l, out_i = self._draft(ids=ids, want_hidden=return_hidden,
+                                             want_logits=return_logits, want_ids=True)
+        res = [out_i]
+        if return_logits:
+            res.append(out_l)
+        if return_hidden:
+            res.append(out_h)
+        return res[0] if len(res) == 1 else tuple(res)
+
+    # ------------------------------------------------------------------ split API
+    @property
+    def ane(self):
+        """Dispatch marker used by generate.py:401-408 to select the threaded caller."""
+        return self
+
+    @property
+    def seq_q(self):
+        return self.block_size
+
+    def set_block_size(self, new_seq_q: int):
+        """ane_model.py:611-630."""
+        if new_seq_q < 1 or new_seq_q > self.max_block:
+            raise ValueError(f"new_seq_q={new_seq_q} must be in [1, {self.max_block}]")
+        self.block_size = int(new_seq_q)
+        self.config.block_size = int(new_seq_q)
+
+    def _compute_context(self, target_hidden):
+        """Return the raw target_hidden; fc + hidden_norm run inside the ingest kernel."""
+        return target_hidden
+
+    def prepare_forward(self, noise_embedding, precomputed_context, cache, target_hidden):
+        """ane_model.py:538-562: stage inputs on the calling thread."""
+        import torch
+        self._apply_num_layers()
+        rope_offset = 0
+        if cache is not None and len(cache) > 0 and cache[0].offset > 0:
+            rope_offset = cache[0].offset
+        ctx_len = target_hidden.shape[-2]
+        if ctx_len > self.max_ctx_len:
+            raise ValueError(f"ctx_len={ctx_len} exceeds max_ctx_len={self.max_ctx_len}")
+        ne = noise_embedding.to(self.device, torch.float16).contiguous()
+        th = target_hidden.to(self.device, torch.float16).contiguous()
+        self._prepared = (ne, th, rope_offset)
+
+    def run_kernels(self):
+        """ane_model.py:564-589: the ANE path keeps no K/V and re-ingests the current
+        target_hidden with RoPE positions starting at cache.offset."""
+        if self._prepared is None:
+            raise RuntimeError("prepare_forward() must be called first")
+        ne, th, rope_offset = self._prepared
+        _lib.check(self._L.dfl_cache_reset(self._ctx), "dfl_cache_reset")
+        _lib.check(self._L.dfl_cache_set_offset(self._ctx, int(rope_offset)),
+                   "dfl_cache_set_offset")
+        self._gen += 1
+        self._ingest(th)
+        h, _, _, ids = self._draft(noise=ne, want_hidden=True, want_ids=self._has_lm)
+        self._out_hidden, self._out_ids = h, ids
+
+    def read_output(self):
+        if self._out_hidden is None:
+            raise RuntimeError("run_kernels() has not produced an output")
+        return self._out_hidden.unsqueeze(0)
+
+    def read_draft_tokens(self):
+        if self._out_ids is None:
+            raise RuntimeError("lm_head not loaded -- no draft tokens")
+        return self._out_ids.reshape(1, -1)
+
+    def run_prepared(self):
+        self.run_kernels()
+        return self.read_output()
+
+
+def _wrap_device(ptr: int, shape, device):
+    """Non-owning torch view of fp16 device memory owned by the library."""
+    import torch
+
+    class _Holder:
+        def __init__(self, p, shp):
+            strides, acc = [], 1
+            for d in reversed(shp):
+                strides.insert(0, acc)
+                acc *= d
+            self.__cuda_array_interface__ = {
+                "shape": tuple(shp), "typestr": "<f2", "data": (p, False),
+                "version": 2, "strides": tuple(s * 2 for s in strides),
+            }
+
+    return torch.as_tensor(_Holder(ptr, shape), device=device)

@@ -1,0 +1,124 @@
+"""Host-side tests that need no GPU: the C ABI library loads and exports every
+symbol the header declares, argument validation runs before any device work,
+and the config / synthetic-input helpers behave like the reference's."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from mirror_sd_amd import _lib
+from mirror_sd_amd.config import DFlashConfig, build_target_layer_ids, extract_context_feature, workload
+from mirror_sd_amd import synth
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "dflash_hip.h")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dfl_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_symbols_exported():
+    syms = _declared_symbols()
+    assert len(syms) >= 15
+    lib = _lib.load()
+    for s in syms:
+        assert hasattr(lib, s), f"{s} declared in dflash_hip.h but not exported"
+        assert s in _lib.SIGNATURES, f"{s} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(syms)
+
+
+def _cfg(**over):
+    c = dict(hidden=256, n_heads=4, n_kv_heads=2, head_dim=128, intermediate=512, n_layers=2,
+             n_target_feat=5, vocab=1024, max_block=16, max_ctx=64, rms_eps=1e-6,
+             rope_theta=1e6)
+    c.update(over)
+    return _lib.DflConfig(**c)
+
+
+@pytest.mark.parametrize("over,needle", [
+    (dict(head_dim=64), "head_dim"),
+    (dict(hidden=100), "hidden"),
+    (dict(n_heads=5, n_kv_heads=2), "n_heads"),
+    (dict(intermediate=100), "intermediate"),
+    (dict(vocab=1000), "vocab"),
+    (dict(max_block=0), "max_block"),
+    (dict(max_block=1000), "max_block"),
+    (dict(rms_eps=0.0), "rms_eps"),
+    (dict(n_layers=0), "n_layers"),
+])
+def test_create_validates_config(over, needle):
+    lib = _lib.load()
+    h = ctypes.c_void_p()
+    rc = lib.dfl_create(ctypes.byref(_cfg(**over)), ctypes.byref(h))
+    assert rc == _lib.DFL_EINVAL and not h.value
+    assert needle in lib.dfl_last_error().decode()
+    with pytest.raises(ValueError):
+        _lib.check(rc, "dfl_create")
+
+
+def test_null_context_errors():
+    lib = _lib.load()
+    assert lib.dfl_cache_trim(None, 1) == _lib.DFL_EINVAL
+    assert lib.dfl_draft_block(None, None, None, 1, None, None, None, None, None) == _lib.DFL_EINVAL
+    assert lib.dfl_quantize_w8(None, 1, 1, None, None, None) == _lib.DFL_EINVAL
+    assert lib.dfl_create(None, None) == _lib.DFL_EINVAL
+    assert "null" in lib.dfl_last_error().decode()
+
+
+def test_build_target_layer_ids():
+    assert build_target_layer_ids(36, 5) == [1, 9, 17, 25, 33]
+    assert build_target_layer_ids(36, 1) == [18]
+    assert build_target_layer_ids(64, 5) == [1, 16, 31, 46, 61]
+    assert build_target_layer_ids(35, 5) == [1, 9, 16, 24, 32]   # round(16.5) == 16 (half-even)
+
+
+def test_from_dict_defaults_follow_reference():
+    c = DFlashConfig.from_dict({})
+    assert c.rope_theta == 10000.0 and c.mask_token_id == 151667 and c.num_key_value_heads == 2
+    assert c.intermediate_size == 10944 and c.max_position_embeddings == 4096
+    d = DFlashConfig()
+    assert d.rope_theta == 1e6 and d.mask_token_id == 151669
+    c = DFlashConfig.from_dict({"dflash_config": {"target_layer_ids": [2, 3], "block_size": 32,
+                                                   "mask_token_id": 7}, "hidden_size": 5120})
+    assert c.target_layer_ids == [2, 3] and c.block_size == 32 and c.mask_token_id == 7
+    assert c.num_target_features == 2 and c.hidden_size == 5120
+
+
+def test_extract_context_feature():
+    hs = [np.full((1, 2, 3), i, dtype=np.float32) for i in range(6)]
+    out = extract_context_feature(hs, [0, 2, 4])
+    assert out.shape == (1, 2, 9) and list(out[0, 0, ::3]) == [1, 3, 5]
+    out = extract_context_feature(hs[:3], [0, 2, 4])
+    assert list(out[0, 0, ::3]) == [0, 1, 2]
+
+
+def test_synth_deterministic_and_order_independent():
+    cfg = workload("tiny").cfg
+    a = synth.make_weights_numpy(cfg, seed=0)
+    b = synth.make_weights_numpy(cfg, seed=0)
+    for k in a:
+        np.testing.assert_array_equal(a[k], b[k])
+    # a tensor generated on its own equals the same tensor generated among all others
+    name = "layers.1.mlp.up_proj.weight"
+    x = synth.np_normal(0, name, a[name].shape, 0.02)
+    np.testing.assert_array_equal(x, a[name])
+    c = synth.make_weights_numpy(cfg, seed=1)
+    assert not np.array_equal(a["fc.weight"], c["fc.weight"])
+    inp = synth.make_inputs_numpy(cfg, 8, 24, seed=0)
+    assert inp["ids"][0] < cfg.vocab_size and np.all(inp["ids"][1:] == cfg.mask_token_id)
+    assert inp["target_hidden"].shape == (24, 5 * 256) and inp["target_hidden"].dtype == np.float16
+
+
+def test_workload_shapes():
+    w = workload("dflash_27b")
+    assert (w.cfg.hidden_size, w.cfg.num_attention_heads, w.cfg.num_key_value_heads,
+            w.cfg.intermediate_size, w.block, w.ctx) == (5120, 40, 8, 17408, 32, 4096)
+    assert workload("dflash_27b_ctx32768").ctx == 32768
+    w = workload("qwen3_4b_layer")
+    assert (w.cfg.hidden_size, w.cfg.intermediate_size, w.cfg.num_hidden_layers) == (2560, 9728, 1)
