@@ -1,0 +1,284 @@
+#!/usr/bin/env python3
+"""Benchmark: DFlash draft-block latency + achieved HBM bandwidth on one MI355X.
+
+Default workload (the headline): 27B-class draft, 5 layers, H5120, 40/8 heads,
+FFN 17408, W8A16 projections, fp16 lm_head [151936, 5120], block 32, context 4096.
+
+A step is one draft block: embedding of the block ids -> 5 decoder layers attending to
+the resident context K/V plus the block -> final norm -> lm_head -> argmax ids.  The
+context (fc fusion + per-layer K/V of 4096 rows) is ingested once before timing and
+reported as its own phase.  Weights and inputs are synthetic (seeded, random-init).
+
+Prints ONE JSON line.  ``value`` is the mean draft-block latency in microseconds over
+the timed steps (inputs resident in HBM).  ``roofline`` describes the W8A16 projection
+GEMM kernel, timed live with HIP events on the library's stream in a separate pass of
+``--profile-steps`` blocks.  ``cpu_baseline`` times the CPU oracle (numpy fp32,
+dequantised weights) on a bounded number of the same blocks on this host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "mirror-sd_amd"))
+
+METRIC = ("draft-block latency (us) + achieved HBM GB/s, 27B-class W8A16 block=32 ctx=4096")
+HBM_PEAK_GBS = 8000.0
+
+
+def algorithmic_bytes(cfg, block, ctx):
+    """Bytes a draft block must move from HBM: int8 projection weights + fp16 scales,
+    context+block K/V read by attention, fp16 lm_head."""
+    H, NH, NKV, F, D = (cfg.hidden_size, cfg.num_attention_heads, cfg.num_key_value_heads,
+                        cfg.intermediate_size, cfg.head_dim)
+    NQKV = (NH + 2 * NKV) * D
+    per_layer_w = NQKV * H + H * NH * D + 2 * F * H + H * F
+    per_layer_s = 2 * (NQKV + H + 2 * F + H)
+    L = ctx + block
+    kv = 2 * NKV * L * D * 2
+    nl = cfg.num_hidden_layers
+    lm = cfg.vocab_size * H * 2
+    return {"proj_weights": nl * per_layer_w, "proj_scales": nl * per_layer_s,
+            "kv_read": nl * kv, "lm_head": lm,
+            "total": nl * (per_layer_w + per_layer_s + kv) + lm}
+
+
+def build_model(wl, seed, keep_host: bool):
+    """Synthetic weights generated on the GPU, quantised by the library's W8A16
+    quantiser and loaded.  Optionally keeps host copies for the CPU baseline."""
+    import torch
+    from mirror_sd_amd.dflash import DFlashDraftModel
+    from mirror_sd_amd import synth
+    cfg = wl.cfg
+    m = DFlashDraftModel(cfg, max_ctx=wl.ctx, max_block=max(wl.block, 32))
+    host = {}
+    names = [n for n, _, _ in synth.weight_specs(cfg)]
+    gen = dict(synth.make_weights_torch(cfg, seed=seed, device="cuda",
+                                        only=[n for n in names if "layers." not in n]))
+    for i in range(cfg.num_hidden_layers):
+        lt = dict(synth.make_weights_torch(cfg, seed=seed, device="cuda",
+                                           only=[n for n in names if n.startswith(f"layers.{i}.")]))
+        qs, ss = [], []
+        for p in synth.PROJ_NAMES:
+            key = synth.proj_key(i, p)
+            q, s = m.quantize_w8(lt.pop(key))
+            qs.append(q)
+            ss.append(s)
+            if keep_host:
+                host[key] = (q.cpu().numpy(), s.cpu().numpy())
+        norms = [lt[f"layers.{i}.input_layernorm.weight"],
+                 lt[f"layers.{i}.post_attention_layernorm.weight"],
+                 lt[f"layers.{i}.self_attn.q_norm.weight"], lt[f"layers.{i}.self_attn.k_norm.weight"]]
+        m.load_layer_q8(i, qs, ss, *norms)
+        if keep_host:
+            for k, v in lt.items():
+                host[k] = v.cpu().numpy()
+        del lt, qs, ss
+    m.load_fc(gen["fc.weight"], gen["hidden_norm.weight"])
+    m.load_head(gen["norm.weight"], gen["embed_tokens.weight"], gen["lm_head.weight"])
+    if keep_host:
+        for k in ("norm.weight", "embed_tokens.weight", "lm_head.weight"):
+            host[k] = gen[k].cpu().numpy()
+    del gen["fc.weight"]
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return m, host
+
+
+def cpu_baseline(wl, model, host, ids, max_seconds=12.0, max_blocks=8):
+    """Time the CPU oracle (numpy fp32, dequantised weights, fp16 materialisation) on
+    the same block step: context K/V taken from the GPU cache, block of ``wl.block``
+    ids, 5 layers + final norm + lm_head + argmax."""
+    import numpy as np
+    import torch
+    from oracle import dflash_oracle as O
+    cfg = wl.cfg
+    f32 = np.float32
+    W = O.OracleWeights.__new__(O.OracleWeights)
+    W.cfg, W.fc = cfg, None
+    W.hidden_norm = None
+    W.norm = host["norm.weight"]
+    W.embed = host["embed_tokens.weight"]
+    W.lm_head = host["lm_head.weight"].astype(f32)
+    W.layers = []
+    for i in range(cfg.num_hidden_layers):
+        lw = {p: O.dequantize_w8(*host[f"layers.{i}.{'mlp' if p in ('gate_proj', 'up_proj', 'down_proj') else 'self_attn'}.{p}.weight"], dtype=f32)
+              for p in O.OracleWeights.PROJ}
+        lw["input_layernorm"] = host[f"layers.{i}.input_layernorm.weight"]
+        lw["post_attention_layernorm"] = host[f"layers.{i}.post_attention_layernorm.weight"]
+        lw["q_norm"] = host[f"layers.{i}.self_attn.q_norm.weight"]
+        lw["k_norm"] = host[f"layers.{i}.self_attn.k_norm.weight"]
+        W.layers.append(lw)
+    caches = []
+    C = wl.ctx
+    for i in range(cfg.num_hidden_layers):
+        k, vt = model._cache_tensors[i]
+        c = O.OracleKVCache()
+        c.keys = k[:, :C].float().cpu().numpy()
+        c.values = vt[:, :, :C].transpose(1, 2).float().cpu().numpy()
+        c.offset = C
+        caches.append(c)
+    empty = np.zeros((0, cfg.hidden_size), dtype=np.float16)   # no new context rows
+    ids_np = ids.cpu().numpy()
+    times = []
+    t_all = time.perf_counter()
+    while len(times) < max_blocks and (len(times) < 2 or time.perf_counter() - t_all < max_seconds):
+        t0 = time.perf_counter()
+        noise = O.embed(W, ids_np)
+        h = O.draft_forward(W, noise, empty, cache=caches, fp16=True, fused_context=True,
+                            dtype=f32)
+        logits = O.lm_head_logits(h, W.lm_head, dtype=f32)
+        O.argmax_first(logits)
+        times.append(time.perf_counter() - t0)
+        for c in caches:
+            c.trim(wl.block)
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max([p.get("num_threads", 1) for p in threadpool_info()] + [1])
+    except Exception:
+        cores = len(os.sched_getaffinity(0))
+    return {"value": float(np.mean(times) * 1e6), "unit": "us", "cores": int(cores),
+            "kind": "port",
+            "sample": f"{len(times)} full draft blocks of the same workload (numpy fp32 oracle, "
+                      f"dequantised W8A16 weights, context K/V precomputed)"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="dflash_27b")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--profile-steps", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-profile", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on exactly one GPU; --gpus {args.gpus} is not "
+              f"supported (the multi-GPU sharding is described, not implemented)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    from mirror_sd_amd.config import workload
+    from mirror_sd_amd import synth, _lib
+
+    wl = workload(args.workload)
+    cfg = wl.cfg
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    torch.manual_seed(args.seed)
+    want_cpu = not args.no_cpu_baseline
+    t_setup = time.perf_counter()
+    model, host = build_model(wl, args.seed, keep_host=want_cpu)
+    inp = synth.make_inputs_torch(cfg, wl.block, wl.ctx, seed=args.seed, device="cuda")
+    th, ids = inp["target_hidden"], inp["ids"]
+    setup_s = time.perf_counter() - t_setup
+
+    L = model._L
+    ctx = model._ctx
+    stream = torch.cuda.current_stream()
+    sh = stream.cuda_stream
+    out_ids = torch.empty((wl.block,), dtype=torch.int32, device="cuda")
+
+    # context ingest (fc fusion + per-layer K/V), timed as its own phase
+    model.make_cache(0, 0)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    ev0.record(stream)
+    _lib.check(L.dfl_ingest_context(ctx, th.data_ptr(), wl.ctx, sh), "dfl_ingest_context")
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ingest_ms = ev0.elapsed_time(ev1)
+
+    def step():
+        rc = L.dfl_draft_block(ctx, None, ids.data_ptr(), wl.block, None, None, None,
+                               out_ids.data_ptr(), sh)
+        if rc:
+            _lib.check(rc, "dfl_draft_block")
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0.record(stream)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - t0
+    ms_per_step = ev0.elapsed_time(ev1) / args.steps
+    first_ids = out_ids.cpu().tolist()
+
+    nbytes = algorithmic_bytes(cfg, wl.block, wl.ctx)
+    lat_us = ms_per_step * 1e3
+    gbs = nbytes["total"] / (ms_per_step * 1e-3) / 1e9
+
+    roofline, kernels = None, None
+    if not args.no_profile and args.profile_steps > 0:
+        model.profile(True)
+        model.profile_read()
+        for _ in range(args.profile_steps):
+            step()
+        torch.cuda.synchronize()
+        prof = model.profile_read()
+        model.profile(False)
+        kernels = {}
+        for name, r in prof.items():
+            if r["launches"] == 0:
+                continue
+            ent = {"ms_per_block": r["ms"] / args.profile_steps,
+                   "launches_per_block": r["launches"] / args.profile_steps}
+            if r["bytes"]:
+                ent["gbs"] = r["bytes"] / (r["ms"] * 1e-3) / 1e9
+                ent["bytes_per_launch"] = r["bytes"] / r["launches"]
+            kernels[name] = ent
+        g = prof.get("gemm_w8a16")
+        if g and g["launches"]:
+            avg_s = g["ms"] * 1e-3 / g["launches"]
+            per_launch = g["bytes"] / g["launches"]
+            ach = per_launch / avg_s / 1e9
+            roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                        "kernel": "skinny_gemm_kernel<int8> (W8A16 projections)",
+                        "bytes_per_launch": per_launch, "avg_launch_us": avg_s * 1e6}
+
+    cpu = None
+    if want_cpu:
+        try:
+            cpu = cpu_baseline(wl, model, host, ids)
+        except Exception as e:  # report, never lose the GPU line
+            cpu = {"value": None, "error": f"{type(e).__name__}: {e}"}
+
+    out = {
+        "metric": METRIC, "value": round(lat_us, 2), "unit": "us", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic (seeded random-init weights, N(0,1) target_hidden)",
+        "config": {"workload": wl.name, "hidden": cfg.hidden_size, "layers": cfg.num_hidden_layers,
+                   "heads": cfg.num_attention_heads, "kv_heads": cfg.num_key_value_heads,
+                   "ffn": cfg.intermediate_size, "vocab": cfg.vocab_size, "block": wl.block,
+                   "ctx": wl.ctx, "weights": "W8A16 (int8 + fp16 per-row scale), fp16 lm_head"},
+        "hbm_gbps": round(gbs, 1),
+        "algorithmic_bytes_per_block": nbytes["total"],
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "phases": {"context_ingest_ms": round(ingest_ms, 3), "setup_s": round(setup_s, 1),
+                   "wall_ms_per_step": round(wall_s * 1e3 / args.steps, 4)},
+        "kernels": kernels,
+        "draft_ids_head": first_ids[:4],
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

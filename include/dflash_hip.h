@@ -126,6 +126,17 @@ int dfl_cache_state(const dfl_ctx* ctx, int32_t* len, int64_t* offset);
 /* Device pointers of layer `layer`'s cache: K [NKV][cap][128], Vt [NKV][128][cap]. */
 int dfl_cache_kv(const dfl_ctx* ctx, int32_t layer, uint16_t** k, uint16_t** vt, int32_t* cap);
 
+/* Kernel timing with HIP events (the reference times phases and kernels with
+ * time.perf_counter wrappers: bench_ane_profile.py:41-245, ANEKernel.run_timed
+ * wrapper.rs:284-301).  While enabled, each kernel group launched by dfl_draft_block /
+ * dfl_ingest_* is bracketed by events on its stream.  dfl_profile_read synchronises,
+ * returns per-category totals (name <= 31 chars each, in names[i*32]), launch counts
+ * and algorithmic bytes (weights + scales for GEMMs, K/V read for attention), then
+ * clears the records. */
+int dfl_profile_enable(dfl_ctx* ctx, int32_t on);
+int dfl_profile_read(dfl_ctx* ctx, int32_t max_cat, char* names, double* total_ms,
+                     int64_t* launches, int64_t* bytes, int32_t* n_cat);
+
 /* Sticky device-side error flags (bit 0: a token id outside [0, vocab)); reading clears. */
 int dfl_device_errors(dfl_ctx* ctx, int32_t* flags, void* stream);
 

@@ -48,6 +48,17 @@ GemmPlan plan_for(int N, int KB, int epi) {
   return p;
 }
 
+enum ProfCat { P_GEMM_W8 = 0, P_LM_HEAD, P_ATTN, P_QK_ROPE, P_ROWS, P_INGEST_FC, P_INGEST_KV, P_N };
+const char* const kProfNames[P_N] = {"gemm_w8a16",   "lm_head_argmax", "attention",
+                                     "qk_norm_rope", "row_reduce_norm", "ingest_fc",
+                                     "ingest_kv"};
+
+struct ProfRec {
+  int cat;
+  hipEvent_t a, b;
+  long long bytes;
+};
+
 struct Layer {
   uint4 *w_qkv = nullptr, *w_o = nullptr, *w_gu = nullptr, *w_down = nullptr;
   half_t *s_qkv = nullptr, *s_o = nullptr, *s_gu = nullptr, *s_down = nullptr;
@@ -81,8 +92,14 @@ struct dfl_ctx {
   int* err = nullptr;
   GemmPlan p_qkv, p_o, p_gu, p_down, p_lm;
   std::vector<void*> allocs;
+  bool prof = false;
+  std::vector<ProfRec> recs;
 
   ~dfl_ctx() {
+    for (auto& r : recs) {
+      (void)hipEventDestroy(r.a);
+      (void)hipEventDestroy(r.b);
+    }
     for (void* p : allocs) (void)hipFree(p);
   }
   template <class T>
@@ -99,6 +116,26 @@ struct dfl_ctx {
       if (e != hipSuccess) return fail(DFL_EHIP, std::string("hipMemset: ") + hipGetErrorString(e));
     }
     return DFL_OK;
+  }
+};
+
+// Brackets the kernels launched in its scope with events when profiling is on.
+struct ProfScope {
+  dfl_ctx* c;
+  int cat;
+  long long bytes;
+  hipStream_t st;
+  hipEvent_t a = nullptr, b = nullptr;
+  ProfScope(dfl_ctx* c_, int cat_, long long bytes_, hipStream_t st_)
+      : c(c_), cat(cat_), bytes(bytes_), st(st_) {
+    if (c->prof && hipEventCreate(&a) == hipSuccess && hipEventCreate(&b) == hipSuccess)
+      (void)hipEventRecord(a, st);
+  }
+  ~ProfScope() {
+    if (c->prof && a && b) {
+      (void)hipEventRecord(b, st);
+      c->recs.push_back({cat, a, b, bytes});
+    }
   }
 };
 
@@ -282,9 +319,13 @@ int dfl_load_head(dfl_ctx* ctx, const uint16_t* final_norm, const uint16_t* embe
   return DFL_OK;
 }
 
-static void gemm(dfl_ctx* ctx, int wt, int epi, const uint4* W, const half_t* scale,
+static void gemm(dfl_ctx* ctx, int cat, int wt, int epi, const uint4* W, const half_t* scale,
                  const half_t* X, int ldx, int M, int N, int KB, GemmPlan p, half_t* out,
                  int ldo, float* logits, unsigned long long* keys, hipStream_t st) {
+  // algorithmic bytes: the weight matrix (+ int8 scales), streamed once per m-tile
+  const long long wbytes = (wt == WT_INT8) ? (long long)N * KB * 32 + 2LL * N
+                                           : (long long)N * KB * 16 * 2;
+  ProfScope ps(ctx, cat, wbytes * ((M + 31) / 32), st);
   SkinnyArgs a;
   a.W = W;
   a.scale = scale;
@@ -322,7 +363,7 @@ static void ingest_kv_rows(dfl_ctx* ctx, const half_t* ctxrows, int rows, int r0
   for (int l = 0; l < ctx->active; ++l) {
     Layer& L = ctx->layers[l];
     const uint4* Wkv = L.w_qkv + (size_t)(NH * 4) * KB * 64;
-    gemm(ctx, WT_INT8, EPI_PARTIAL, Wkv, nullptr, ctxrows, H, rows, Nkv, KB, p, nullptr, 0,
+    gemm(ctx, P_INGEST_KV, WT_INT8, EPI_PARTIAL, Wkv, nullptr, ctxrows, H, rows, Nkv, KB, p, nullptr, 0,
          nullptr, nullptr, st);
     QKRopeArgs q;
     q.ws = ctx->ws;
@@ -346,6 +387,7 @@ static void ingest_kv_rows(dfl_ctx* ctx, const half_t* ctxrows, int rows, int r0
     q.Vt = L.Vt;
     q.cap = ctx->cap;
     q.cache_row0 = ctx->len + r0;
+    ProfScope ps(ctx, P_INGEST_KV, 0, st);
     launch_qk_rope(q, st);
   }
 }
@@ -371,9 +413,10 @@ static int ingest(dfl_ctx* ctx, const uint16_t* src, int C, bool fused, void* st
       GemmPlan p;
       p.SK = 4;
       p.S_x = 1;
-      gemm(ctx, WT_F16, EPI_PARTIAL, ctx->w_fc, nullptr,
+      gemm(ctx, P_INGEST_FC, WT_F16, EPI_PARTIAL, ctx->w_fc, nullptr,
            reinterpret_cast<const half_t*>(src) + (size_t)r0 * K, K, rows, H, K / 16, p, nullptr,
            0, nullptr, nullptr, st);
+      ProfScope ps(ctx, P_INGEST_FC, 0, st);
       launch_reduce_resid_norm(ctx->ws, 1, rows, H, nullptr, nullptr, false, ctx->hidden_norm,
                                ctx->cfg.rms_eps, ctx->ctxbuf, H, st);
       ctxrows = ctx->ctxbuf;
@@ -413,8 +456,11 @@ int dfl_draft_block(dfl_ctx* ctx, const uint16_t* noise_emb, const int32_t* ids,
   hipStream_t st = (hipStream_t)stream;
   const int H = ctx->H, NH = ctx->NH, NKV = ctx->NKV, F = ctx->F, NQ = NH * 128;
   const float eps = ctx->cfg.rms_eps;
-  launch_embed_norm(ids, ctx->embed, reinterpret_cast<const half_t*>(noise_emb), B, H, ctx->V,
+  {
+    ProfScope ps(ctx, P_ROWS, 0, st);
+    launch_embed_norm(ids, ctx->embed, reinterpret_cast<const half_t*>(noise_emb), B, H, ctx->V,
                     ctx->layers[0].in_norm, eps, ctx->x, ctx->h, ctx->err, st);
+  }
 
   const int L = ctx->len + B;
   const int ratio = NH / NKV;
@@ -428,7 +474,7 @@ int dfl_draft_block(dfl_ctx* ctx, const uint16_t* noise_emb, const int32_t* ids,
 
   for (int l = 0; l < ctx->active; ++l) {
     Layer& Ly = ctx->layers[l];
-    gemm(ctx, WT_INT8, EPI_PARTIAL, Ly.w_qkv, nullptr, ctx->h, H, B, ctx->NQKV, H / 32,
+    gemm(ctx, P_GEMM_W8, WT_INT8, EPI_PARTIAL, Ly.w_qkv, nullptr, ctx->h, H, B, ctx->NQKV, H / 32,
          ctx->p_qkv, nullptr, 0, nullptr, nullptr, st);
     QKRopeArgs q;
     q.ws = ctx->ws;
@@ -452,7 +498,10 @@ int dfl_draft_block(dfl_ctx* ctx, const uint16_t* noise_emb, const int32_t* ids,
     q.Vt = Ly.Vt;
     q.cap = ctx->cap;
     q.cache_row0 = ctx->len;
-    launch_qk_rope(q, st);
+    {
+      ProfScope ps(ctx, P_QK_ROPE, 0, st);
+      launch_qk_rope(q, st);
+    }
 
     AttnArgs at;
     at.Q = ctx->Q;
@@ -469,24 +518,36 @@ int dfl_draft_block(dfl_ctx* ctx, const uint16_t* noise_emb, const int32_t* ids,
     at.Op = ctx->Op;
     at.Ml = ctx->Ml;
     at.O = ctx->attn;
-    launch_block_attention(at, st);
+    {
+      ProfScope ps(ctx, P_ATTN, 2LL * NKV * L * 128 * 2, st);
+      launch_block_attention(at, st);
+    }
 
-    gemm(ctx, WT_INT8, EPI_PARTIAL, Ly.w_o, nullptr, ctx->attn, NQ, B, H, NQ / 32, ctx->p_o,
+    gemm(ctx, P_GEMM_W8, WT_INT8, EPI_PARTIAL, Ly.w_o, nullptr, ctx->attn, NQ, B, H, NQ / 32, ctx->p_o,
          nullptr, 0, nullptr, nullptr, st);
-    launch_reduce_resid_norm(ctx->ws, ctx->p_o.S_x, B, H, Ly.s_o, ctx->x, true, Ly.post_norm, eps,
-                             ctx->h, H, st);
-    gemm(ctx, WT_INT8, EPI_SWIGLU, Ly.w_gu, Ly.s_gu, ctx->h, H, B, 2 * F, H / 32, ctx->p_gu,
+    {
+      ProfScope ps(ctx, P_ROWS, 0, st);
+      launch_reduce_resid_norm(ctx->ws, ctx->p_o.S_x, B, H, Ly.s_o, ctx->x, true, Ly.post_norm,
+                               eps, ctx->h, H, st);
+    }
+    gemm(ctx, P_GEMM_W8, WT_INT8, EPI_SWIGLU, Ly.w_gu, Ly.s_gu, ctx->h, H, B, 2 * F, H / 32, ctx->p_gu,
          ctx->act, F, nullptr, nullptr, st);
-    gemm(ctx, WT_INT8, EPI_PARTIAL, Ly.w_down, nullptr, ctx->act, F, B, H, F / 32, ctx->p_down,
+    gemm(ctx, P_GEMM_W8, WT_INT8, EPI_PARTIAL, Ly.w_down, nullptr, ctx->act, F, B, H, F / 32, ctx->p_down,
          nullptr, 0, nullptr, nullptr, st);
     const half_t* gnext = (l + 1 < ctx->active) ? ctx->layers[l + 1].in_norm : ctx->final_norm;
-    launch_reduce_resid_norm(ctx->ws, ctx->p_down.S_x, B, H, Ly.s_down, ctx->x, true, gnext, eps,
-                             ctx->h, H, st);
+    {
+      ProfScope ps(ctx, P_ROWS, 0, st);
+      launch_reduce_resid_norm(ctx->ws, ctx->p_down.S_x, B, H, Ly.s_down, ctx->x, true, gnext,
+                               eps, ctx->h, H, st);
+    }
   }
   if (out_logits || out_ids) {
-    gemm(ctx, WT_F16, EPI_ARGMAX, ctx->w_lm, nullptr, ctx->h, H, B, ctx->V, H / 16, ctx->p_lm,
+    gemm(ctx, P_LM_HEAD, WT_F16, EPI_ARGMAX, ctx->w_lm, nullptr, ctx->h, H, B, ctx->V, H / 16, ctx->p_lm,
          nullptr, 0, out_logits, out_ids ? ctx->keys : nullptr, st);
-    if (out_ids) launch_argmax_finalize(ctx->keys, B, out_ids, st);
+    if (out_ids) {
+      ProfScope ps(ctx, P_ROWS, 0, st);
+      launch_argmax_finalize(ctx->keys, B, out_ids, st);
+    }
   }
   if (out_hidden)
     DFL_HIP(hipMemcpyAsync(out_hidden, ctx->h, (size_t)B * H * 2, hipMemcpyDeviceToDevice, st));
@@ -556,6 +617,43 @@ int dfl_cache_kv(const dfl_ctx* ctx, int32_t layer, uint16_t** k, uint16_t** vt,
   if (vt) *vt = reinterpret_cast<uint16_t*>(ctx->layers[layer].Vt);
   if (cap) *cap = ctx->cap;
   return DFL_OK;
+}
+
+int dfl_profile_enable(dfl_ctx* ctx, int32_t on) {
+  if (!ctx) return fail(DFL_EINVAL, "dfl_profile_enable: null context");
+  ctx->prof = on != 0;
+  return DFL_OK;
+}
+
+int dfl_profile_read(dfl_ctx* ctx, int32_t max_cat, char* names, double* total_ms,
+                     int64_t* launches, int64_t* bytes, int32_t* n_cat) {
+  if (!ctx || !n_cat) return fail(DFL_EINVAL, "dfl_profile_read: null argument");
+  const int nc = std::min<int>(max_cat, P_N);
+  std::vector<double> ms(P_N, 0.0);
+  std::vector<long long> cnt(P_N, 0), by(P_N, 0);
+  int rc = DFL_OK;
+  for (auto& r : ctx->recs) {
+    float t = 0.f;
+    if (hipEventSynchronize(r.b) != hipSuccess || hipEventElapsedTime(&t, r.a, r.b) != hipSuccess)
+      rc = fail(DFL_EHIP, "dfl_profile_read: event timing failed");
+    ms[r.cat] += t;
+    cnt[r.cat] += 1;
+    by[r.cat] += r.bytes;
+    (void)hipEventDestroy(r.a);
+    (void)hipEventDestroy(r.b);
+  }
+  ctx->recs.clear();
+  for (int i = 0; i < nc; ++i) {
+    if (names) {
+      std::strncpy(names + 32 * i, kProfNames[i], 31);
+      names[32 * i + 31] = 0;
+    }
+    if (total_ms) total_ms[i] = ms[i];
+    if (launches) launches[i] = cnt[i];
+    if (bytes) bytes[i] = by[i];
+  }
+  *n_cat = nc;
+  return rc;
 }
 
 int dfl_device_errors(dfl_ctx* ctx, int32_t* flags, void* stream) {

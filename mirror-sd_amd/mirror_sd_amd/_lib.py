@@ -57,6 +57,10 @@ SIGNATURES = {
     "dfl_cache_state": (c_int32, [c_void_p, ctypes.POINTER(c_int32), ctypes.POINTER(c_int64)]),
     "dfl_cache_kv": (c_int32, [c_void_p, c_int32, ctypes.POINTER(c_void_p),
                                ctypes.POINTER(c_void_p), ctypes.POINTER(c_int32)]),
+    "dfl_profile_enable": (c_int32, [c_void_p, c_int32]),
+    "dfl_profile_read": (c_int32, [c_void_p, c_int32, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
+                                   ctypes.POINTER(c_int64), ctypes.POINTER(c_int64),
+                                   ctypes.POINTER(c_int32)]),
     "dfl_device_errors": (c_int32, [c_void_p, ctypes.POINTER(c_int32), c_void_p]),
 }
 

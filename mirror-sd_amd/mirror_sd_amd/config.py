@@ -145,6 +145,8 @@ class Workload:
 
 def _draft_cfg(hidden, heads, kv_heads, ffn, layers, vocab=151936, theta=1e6,
                block=16, mask_id=151669, n_feat=5):
+    if mask_id >= vocab:     # a reduced test vocabulary: use its last id as the mask
+        mask_id = vocab - 1
     cfg = DFlashConfig(hidden_size=hidden, num_hidden_layers=layers,
                        intermediate_size=ffn, num_attention_heads=heads,
                        num_key_value_heads=kv_heads, head_dim=128, rms_norm_eps=1e-6,

@@ -437,6 +437,27 @@ class DFlashDraftModel:
             res.append(out_h)
         return res[0] if len(res) == 1 else tuple(res)
 
+    # ------------------------------------------------------------------ profiling
+    def profile(self, enable: bool = True):
+        """Bracket every kernel group with HIP events (see dfl_profile_enable)."""
+        _lib.check(self._L.dfl_profile_enable(self._ctx, 1 if enable else 0), "dfl_profile_enable")
+
+    def profile_read(self) -> Dict[str, dict]:
+        """Per-category {ms, launches, bytes} since the last read (synchronises)."""
+        n = 16
+        names = ctypes.create_string_buffer(32 * n)
+        ms = (ctypes.c_double * n)()
+        cnt = (ctypes.c_int64 * n)()
+        by = (ctypes.c_int64 * n)()
+        nc = ctypes.c_int32()
+        _lib.check(self._L.dfl_profile_read(self._ctx, n, names, ms, cnt, by, ctypes.byref(nc)),
+                   "dfl_profile_read")
+        out = {}
+        for i in range(nc.value):
+            name = names.raw[32 * i:32 * i + 32].split(b"\0", 1)[0].decode()
+            out[name] = {"ms": ms[i], "launches": cnt[i], "bytes": by[i]}
+        return out
+
     # ------------------------------------------------------------------ split API
     @property
     def ane(self):

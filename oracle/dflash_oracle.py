@@ -341,7 +341,7 @@ def lm_head_logits(h: np.ndarray, w_lm: np.ndarray, dtype=F64, chunk: int = 1638
     h = h.astype(dtype)
     out = np.empty((h.shape[0], w_lm.shape[0]), dtype=dtype)
     for i in range(0, w_lm.shape[0], chunk):
-        out[:, i:i + chunk] = h @ w_lm[i:i + chunk].astype(dtype).T
+        out[:, i:i + chunk] = h @ w_lm[i:i + chunk].astype(dtype, copy=False).T
     return out
 
 

@@ -163,6 +163,7 @@ def test_qwen3_8b_shape_one_layer_matches_oracle():
     cfg = workload("qwen3_8b_draft").cfg.copy()
     cfg.num_hidden_layers = 1
     cfg.vocab_size = 4096
+    cfg.mask_token_id = 4095
     block, ctx = 16, 256
     t = synth.make_weights_numpy(cfg, seed=0)
     inp = synth.make_inputs_numpy(cfg, block, ctx, seed=0)
