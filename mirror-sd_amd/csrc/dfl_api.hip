@@ -90,6 +90,18 @@ struct dfl_ctx {
   float *Op = nullptr, *Ml = nullptr;
   unsigned long long* keys = nullptr;
   int* err = nullptr;
+  // stream-K GEMM state (block step)
+  int n_cu = 256;
+  half_t* qkvbuf = nullptr;      // [Bmax][NQKV] fp16 projections
+  float* rnorm = nullptr;        // [Bmax] 1/rms of the residual rows
+  float* sk_ws = nullptr;        // split-tile partials
+  int* sk_tile_cnt = nullptr;    // [max tiles]
+  float* sk_ss = nullptr;        // [max tiles][32]
+  int* sk_done = nullptr;        // [1]
+  struct SKPlan { int G = 1, seg_cap = 1; } sk_qkv, sk_o, sk_gu, sk_down, sk_lm;
+  float* ss_part = nullptr;   // [rows][ceil(H/1024)] per-chunk sums of squares
+  int* row_cnt = nullptr;     // [rows] arrival counters of the reduce kernel
+  half_t* fc_out = nullptr;   // [ING_ROWS][H] rounded fc output (ingest)
   GemmPlan p_qkv, p_o, p_gu, p_down, p_lm;
   std::vector<void*> allocs;
   bool prof = false;
@@ -206,9 +218,44 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
       (r = x->alloc(&x->ctxbuf, (size_t)ING_ROWS * x->H)) || (r = x->alloc(&x->ws, ws)) ||
       (r = x->alloc(&x->Op, (size_t)MAX_CHUNKS * x->NH * Bm * 128)) ||
       (r = x->alloc(&x->Ml, (size_t)MAX_CHUNKS * x->NH * Bm * 2)) ||
-      (r = x->alloc(&x->keys, Bm, true)) || (r = x->alloc(&x->err, 1, true))) {
+      (r = x->alloc(&x->keys, Bm, true)) || (r = x->alloc(&x->err, 1, true)) ||
+      (r = x->alloc(&x->ss_part, std::max<size_t>(Bm, ING_ROWS) * 8)) ||
+      (r = x->alloc(&x->row_cnt, std::max<size_t>(Bm, ING_ROWS), true)) ||
+      (r = x->alloc(&x->fc_out, (size_t)ING_ROWS * x->H))) {
     delete x;
     return r;
+  }
+  {
+    int dev = 0, ncu = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        ncu > 0)
+      x->n_cu = ncu;
+    auto plan = [&](int N, int KB) {
+      dfl_ctx::SKPlan p;
+      p.G = streamk_grid(N, KB, x->n_cu);
+      p.seg_cap = streamk_seg_cap(N, KB, p.G);
+      return p;
+    };
+    x->sk_qkv = plan(x->NQKV, x->H / 32);
+    x->sk_o = plan(x->H, x->NH * 128 / 32);
+    x->sk_gu = plan(2 * x->F, x->H / 32);
+    x->sk_down = plan(x->H, x->F / 32);
+    x->sk_lm = plan(std::max(x->V, 64), x->H / 16);
+    size_t wsn = 0, tiles = 0;
+    for (auto pr : {std::make_pair(x->sk_qkv, x->NQKV), std::make_pair(x->sk_o, x->H),
+                    std::make_pair(x->sk_gu, 2 * x->F), std::make_pair(x->sk_down, x->H),
+                    std::make_pair(x->sk_lm, std::max(x->V, 64))}) {
+      wsn = std::max(wsn, (size_t)(pr.second / 64) * pr.first.seg_cap * 2048);
+      tiles = std::max(tiles, (size_t)(pr.second / 64));
+    }
+    const size_t bm32 = ((Bm + 31) / 32) * 32;
+    if ((r = x->alloc(&x->qkvbuf, Bm * x->NQKV)) || (r = x->alloc(&x->rnorm, bm32)) ||
+        (r = x->alloc(&x->sk_ws, wsn)) || (r = x->alloc(&x->sk_tile_cnt, tiles, true)) ||
+        (r = x->alloc(&x->sk_ss, tiles * 32)) || (r = x->alloc(&x->sk_done, 1, true))) {
+      delete x;
+      return r;
+    }
   }
   for (auto& L : x->layers) {
     const size_t kv = (size_t)x->NKV * x->cap * 128;
@@ -326,7 +373,7 @@ static void gemm(dfl_ctx* ctx, int cat, int wt, int epi, const uint4* W, const h
   const long long wbytes = (wt == WT_INT8) ? (long long)N * KB * 32 + 2LL * N
                                            : (long long)N * KB * 16 * 2;
   ProfScope ps(ctx, cat, wbytes * ((M + 31) / 32), st);
-  SkinnyArgs a;
+  SkinnyArgs a{};
   a.W = W;
   a.scale = scale;
   a.X = X;
@@ -342,6 +389,42 @@ static void gemm(dfl_ctx* ctx, int cat, int wt, int epi, const uint4* W, const h
   a.ldl = N;
   a.keys = keys;
   launch_skinny_gemm(wt, epi, a, p.SK, (M + 31) / 32, st);
+}
+
+// Stream-K GEMM over the M rows of a block, in 32-row m-tiles.
+static void skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const dfl_ctx::SKPlan& p,
+                   const uint4* W, const half_t* scale, int N, int KB, const half_t* X, int ldx,
+                   int M, const half_t* gnorm, half_t* out, int ldo, half_t* xres,
+                   float* logits, unsigned long long* keys, hipStream_t st) {
+  const long long wbytes = (wt == WT_INT8) ? (long long)N * KB * 32 + 2LL * N
+                                           : (long long)N * KB * 16 * 2;
+  for (int m0 = 0; m0 < M; m0 += 32) {
+    ProfScope ps(ctx, cat, wbytes, st);
+    StreamArgs a{};
+    a.W = W;
+    a.scale = scale;
+    a.N = N;
+    a.KB = KB;
+    a.X = X + (size_t)m0 * ldx;
+    a.ldx = ldx;
+    a.M = std::min(32, M - m0);
+    a.rnorm = ctx->rnorm + m0;
+    a.gnorm = gnorm;
+    a.ws = ctx->sk_ws;
+    a.seg_cap = p.seg_cap;
+    a.tile_cnt = ctx->sk_tile_cnt;
+    a.out = out ? out + (size_t)m0 * ldo : nullptr;
+    a.ldo = ldo;
+    a.x = xres ? xres + (size_t)m0 * ldo : nullptr;
+    a.ss_part = ctx->sk_ss;
+    a.done_cnt = ctx->sk_done;
+    a.rnorm_out = ctx->rnorm + m0;
+    a.eps = ctx->cfg.rms_eps;
+    a.logits = logits ? logits + (size_t)m0 * N : nullptr;
+    a.ldl = N;
+    a.keys = keys ? keys + m0 : nullptr;
+    launch_streamk_gemm(wt, epi, gnorm != nullptr, a, p.G, st);
+  }
 }
 
 static int layers_ready(dfl_ctx* ctx, const char* who) {
@@ -365,7 +448,8 @@ static void ingest_kv_rows(dfl_ctx* ctx, const half_t* ctxrows, int rows, int r0
     const uint4* Wkv = L.w_qkv + (size_t)(NH * 4) * KB * 64;
     gemm(ctx, P_INGEST_KV, WT_INT8, EPI_PARTIAL, Wkv, nullptr, ctxrows, H, rows, Nkv, KB, p, nullptr, 0,
          nullptr, nullptr, st);
-    QKRopeArgs q;
+    QKRopeArgs q{};   // value-initialised: qkv16 must stay null on this path
+    q.qkv16 = nullptr;
     q.ws = ctx->ws;
     q.S_x = 1;
     q.M = rows;
@@ -418,7 +502,8 @@ static int ingest(dfl_ctx* ctx, const uint16_t* src, int C, bool fused, void* st
            0, nullptr, nullptr, st);
       ProfScope ps(ctx, P_INGEST_FC, 0, st);
       launch_reduce_resid_norm(ctx->ws, 1, rows, H, nullptr, nullptr, false, ctx->hidden_norm,
-                               ctx->cfg.rms_eps, ctx->ctxbuf, H, st);
+                               ctx->cfg.rms_eps, ctx->ctxbuf, H, ctx->fc_out, ctx->ss_part,
+                               ctx->row_cnt, st);
       ctxrows = ctx->ctxbuf;
     }
     ingest_kv_rows(ctx, ctxrows, rows, r0, st);
@@ -456,10 +541,12 @@ int dfl_draft_block(dfl_ctx* ctx, const uint16_t* noise_emb, const int32_t* ids,
   hipStream_t st = (hipStream_t)stream;
   const int H = ctx->H, NH = ctx->NH, NKV = ctx->NKV, F = ctx->F, NQ = NH * 128;
   const float eps = ctx->cfg.rms_eps;
+  // x = embedding rows (residual stream); rnorm = 1/rms(x).  Every projection whose input
+  // is an RMSNorm output applies the norm on its activation load.
   {
     ProfScope ps(ctx, P_ROWS, 0, st);
     launch_embed_norm(ids, ctx->embed, reinterpret_cast<const half_t*>(noise_emb), B, H, ctx->V,
-                    ctx->layers[0].in_norm, eps, ctx->x, ctx->h, ctx->err, st);
+                      ctx->layers[0].in_norm, eps, ctx->x, nullptr, ctx->rnorm, ctx->err, st);
   }
 
   const int L = ctx->len + B;
@@ -474,11 +561,13 @@ int dfl_draft_block(dfl_ctx* ctx, const uint16_t* noise_emb, const int32_t* ids,
 
   for (int l = 0; l < ctx->active; ++l) {
     Layer& Ly = ctx->layers[l];
-    gemm(ctx, P_GEMM_W8, WT_INT8, EPI_PARTIAL, Ly.w_qkv, nullptr, ctx->h, H, B, ctx->NQKV, H / 32,
-         ctx->p_qkv, nullptr, 0, nullptr, nullptr, st);
-    QKRopeArgs q;
-    q.ws = ctx->ws;
-    q.S_x = ctx->p_qkv.S_x;
+    // q|k|v = input_layernorm(x) @ [Wq; Wk; Wv]^T  (fp16 out)
+    skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_STORE, ctx->sk_qkv, Ly.w_qkv, Ly.s_qkv, ctx->NQKV, H / 32,
+           ctx->x, H, B, Ly.in_norm, ctx->qkvbuf, ctx->NQKV, nullptr, nullptr, nullptr, st);
+    QKRopeArgs q{};
+    q.qkv16 = ctx->qkvbuf;
+    q.ws = nullptr;
+    q.S_x = 0;
     q.M = B;
     q.N = ctx->NQKV;
     q.col_slot0 = 0;
@@ -503,7 +592,7 @@ int dfl_draft_block(dfl_ctx* ctx, const uint16_t* noise_emb, const int32_t* ids,
       launch_qk_rope(q, st);
     }
 
-    AttnArgs at;
+    AttnArgs at{};
     at.Q = ctx->Q;
     at.Kc = Ly.Kc;
     at.Vt = Ly.Vt;
@@ -522,35 +611,30 @@ int dfl_draft_block(dfl_ctx* ctx, const uint16_t* noise_emb, const int32_t* ids,
       ProfScope ps(ctx, P_ATTN, 2LL * NKV * L * 128 * 2, st);
       launch_block_attention(at, st);
     }
-
-    gemm(ctx, P_GEMM_W8, WT_INT8, EPI_PARTIAL, Ly.w_o, nullptr, ctx->attn, NQ, B, H, NQ / 32, ctx->p_o,
-         nullptr, 0, nullptr, nullptr, st);
-    {
-      ProfScope ps(ctx, P_ROWS, 0, st);
-      launch_reduce_resid_norm(ctx->ws, ctx->p_o.S_x, B, H, Ly.s_o, ctx->x, true, Ly.post_norm,
-                               eps, ctx->h, H, st);
-    }
-    gemm(ctx, P_GEMM_W8, WT_INT8, EPI_SWIGLU, Ly.w_gu, Ly.s_gu, ctx->h, H, B, 2 * F, H / 32, ctx->p_gu,
-         ctx->act, F, nullptr, nullptr, st);
-    gemm(ctx, P_GEMM_W8, WT_INT8, EPI_PARTIAL, Ly.w_down, nullptr, ctx->act, F, B, H, F / 32, ctx->p_down,
-         nullptr, 0, nullptr, nullptr, st);
-    const half_t* gnext = (l + 1 < ctx->active) ? ctx->layers[l + 1].in_norm : ctx->final_norm;
-    {
-      ProfScope ps(ctx, P_ROWS, 0, st);
-      launch_reduce_resid_norm(ctx->ws, ctx->p_down.S_x, B, H, Ly.s_down, ctx->x, true, gnext,
-                               eps, ctx->h, H, st);
-    }
+    // x += attn @ Wo^T ; rnorm = 1/rms(x)
+    skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_RESID, ctx->sk_o, Ly.w_o, Ly.s_o, H, NQ / 32, ctx->attn,
+           NQ, B, nullptr, nullptr, H, ctx->x, nullptr, nullptr, st);
+    // act = silu(gate(post_norm(x))) * up(post_norm(x))
+    skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_SWIGLU, ctx->sk_gu, Ly.w_gu, Ly.s_gu, 2 * F, H / 32,
+           ctx->x, H, B, Ly.post_norm, ctx->act, F, nullptr, nullptr, nullptr, st);
+    // x += act @ Wdown^T ; rnorm = 1/rms(x)
+    skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_RESID, ctx->sk_down, Ly.w_down, Ly.s_down, H, F / 32,
+           ctx->act, F, B, nullptr, nullptr, H, ctx->x, nullptr, nullptr, st);
   }
   if (out_logits || out_ids) {
-    gemm(ctx, P_LM_HEAD, WT_F16, EPI_ARGMAX, ctx->w_lm, nullptr, ctx->h, H, B, ctx->V, H / 16, ctx->p_lm,
-         nullptr, 0, out_logits, out_ids ? ctx->keys : nullptr, st);
+    skgemm(ctx, P_LM_HEAD, WT_F16, EPI_ARGMAX, ctx->sk_lm, ctx->w_lm, nullptr, ctx->V, H / 16,
+           ctx->x, H, B, ctx->final_norm, nullptr, 0, nullptr, out_logits,
+           out_ids ? ctx->keys : nullptr, st);
     if (out_ids) {
       ProfScope ps(ctx, P_ROWS, 0, st);
       launch_argmax_finalize(ctx->keys, B, out_ids, st);
     }
   }
-  if (out_hidden)
-    DFL_HIP(hipMemcpyAsync(out_hidden, ctx->h, (size_t)B * H * 2, hipMemcpyDeviceToDevice, st));
+  if (out_hidden) {
+    ProfScope ps(ctx, P_ROWS, 0, st);
+    launch_apply_norm(ctx->x, ctx->rnorm, ctx->final_norm, B, H,
+                      reinterpret_cast<half_t*>(out_hidden), st);
+  }
   if (out_prenorm)
     DFL_HIP(hipMemcpyAsync(out_prenorm, ctx->x, (size_t)B * H * 2, hipMemcpyDeviceToDevice, st));
   DFL_TRY(check_launch("dfl_draft_block"));

@@ -33,10 +33,7 @@ __global__ __launch_bounds__(64) void block_attn_kernel(AttnArgs a) {
     const uint4* qp = reinterpret_cast<const uint4*>(a.Q + ((size_t)g * R + (row_ok ? rq : 0)) * 128 +
                                                      64 * gg);
 #pragma unroll
-    for (int st = 0; st < 8; ++st) {
-      const half8_t v = as_half8(qp[st]);
-      qf[st] = row_ok ? v : (half8_t){};
-    }
+    for (int st = 0; st < 8; ++st) qf[st] = as_half8(qp[st]);   // rows >= R: never stored
   }
 
   const int k_begin = c * a.chunk;
@@ -52,19 +49,35 @@ __global__ __launch_bounds__(64) void block_attn_kernel(AttnArgs a) {
   for (int dt = 0; dt < 4; ++dt) o[dt] = (floatx16){};
 
   const half_t* kbase = a.Kc + (size_t)g * a.cap * 128 + 64 * gg;
-  const half_t* vbase = a.Vt + (size_t)g * 128 * a.cap + 8 * gg;
+  const half_t* vbase = a.Vt + (size_t)g * 128 * a.cap + 8 * gg + (size_t)(lane & 31) * a.cap;
 
+  // K fragment of a 32-key block: this lane's key row (clamped into the chunk so the
+  // address is valid; out-of-chunk keys are masked to -inf after the MFMA).
+  auto load_k = [&](u32x4 (&kf)[8], int kb) {
+    const int key = min(kb + koff, k_end - 1);
+    const half_t* kp = kbase + (size_t)key * 128;
+    static_for<0, 8>([&](auto st) { kf[st] = load_vec(kp + 8 * st); });
+  };
+  // V fragments (transposed cache): rows d = dt*32 + lane%32, keys kb + 8*gg + 0..7 and
+  // kb + 16 + 8*gg + 0..7.  Keys past L hold finite data (zero-initialised cache) and
+  // meet p = 0.
+  auto load_v = [&](u32x4 (&vf)[8], int kb) {
+    static_for<0, 4>([&](auto dt) {
+      const half_t* vp = vbase + (size_t)dt * 32 * a.cap + kb;
+      vf[2 * dt] = load_vec(vp);
+      vf[2 * dt + 1] = load_vec(vp + 16);
+    });
+  };
+
+  u32x4 kcur[8], knext[8], vcur[8];
+  load_k(kcur, k_begin);
   for (int kb = k_begin; kb < k_end; kb += 32) {
-    const int key = kb + koff;
-    const bool key_ok = key < k_end;
-    const uint4* kp = reinterpret_cast<const uint4*>(kbase + (size_t)(key_ok ? key : kb) * 128);
+    load_v(vcur, kb);
+    const bool more = kb + 32 < k_end;
+    load_k(knext, more ? kb + 32 : kb);
+    __builtin_amdgcn_sched_barrier(0);
     floatx16 s = {};
-#pragma unroll
-    for (int st = 0; st < 8; ++st) {
-      const half8_t kv = as_half8(kp[st]);
-      const half8_t kf = key_ok ? kv : (half8_t){};
-      s = mfma32x32x16(kf, qf[st], s);
-    }
+    static_for<0, 8>([&](auto st) { s = mfma32x32x16(as_half8(kcur[st]), qf[st], s); });
     // Accumulator r holds key kb + (r < 8 ? 8*gg + r : 16 + 8*gg + r - 8).
     float v[16];
     float bmax = -INFINITY;
@@ -89,15 +102,12 @@ __global__ __launch_bounds__(64) void block_attn_kernel(AttnArgs a) {
     psum += __shfl_xor(psum, 32, 64);
     lrun = lrun * alpha + psum;
     mrun = mnew;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
+    static_for<0, 4>([&](auto dt) {
       o[dt] *= alpha;
-      const half_t* vp = vbase + (size_t)(dt * 32 + (lane & 31)) * a.cap + kb;
-      const half8_t v1 = as_half8(*reinterpret_cast<const uint4*>(vp));
-      const half8_t v2 = as_half8(*reinterpret_cast<const uint4*>(vp + 16));
-      o[dt] = mfma32x32x16(v1, p1, o[dt]);
-      o[dt] = mfma32x32x16(v2, p2, o[dt]);
-    }
+      o[dt] = mfma32x32x16(as_half8(vcur[2 * dt]), p1, o[dt]);
+      o[dt] = mfma32x32x16(as_half8(vcur[2 * dt + 1]), p2, o[dt]);
+    });
+    static_for<0, 8>([&](auto st) { kcur[st] = knext[st]; });
   }
 
   if (!row_ok) return;
@@ -117,20 +127,38 @@ __global__ __launch_bounds__(64) void block_attn_kernel(AttnArgs a) {
 }
 
 // out[b][h*128 + d] = sum_c Op_c * 2^(m_c - M) / sum_c l_c * 2^(m_c - M), fp16.
+// The per-chunk (max, sum) pairs are staged in LDS first so the Op loads of all chunks
+// are independent of each other.
 __global__ __launch_bounds__(128) void attn_merge_kernel(AttnArgs a) {
+  __shared__ float wts[64];
+  __shared__ float den_s;
   const int rowg = blockIdx.x;   // h * B + b
   const int d = threadIdx.x;
   const size_t NB = (size_t)a.NH * a.B;
-  float M = -INFINITY;
-  for (int c = 0; c < a.n_chunks; ++c) M = fmaxf(M, a.Ml[((size_t)c * NB + rowg) * 2]);
-  float num = 0.f, den = 0.f;
-  for (int c = 0; c < a.n_chunks; ++c) {
-    const float w = exp2f(a.Ml[((size_t)c * NB + rowg) * 2] - M);
-    den += a.Ml[((size_t)c * NB + rowg) * 2 + 1] * w;
-    num += a.Op[((size_t)c * NB + rowg) * 128 + d] * w;
+  const int nc = a.n_chunks;
+  float mc = -INFINITY, lc = 0.f;
+  if (d < nc) {
+    mc = a.Ml[((size_t)d * NB + rowg) * 2];
+    lc = a.Ml[((size_t)d * NB + rowg) * 2 + 1];
   }
+  float M = mc;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+  if (d < 64) {
+    const float w = (d < nc) ? exp2f(mc - M) : 0.f;
+    wts[d] = w;
+    float dl = w * lc;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) dl += __shfl_xor(dl, o, 64);
+    if (d == 0) den_s = dl;
+  }
+  __syncthreads();
+  float num = 0.f;
+  const float* op = a.Op + (size_t)rowg * 128 + d;
+#pragma unroll 8
+  for (int c = 0; c < nc; ++c) num += op[(size_t)c * NB * 128] * wts[c];
   const int h = rowg / a.B, b = rowg - h * a.B;
-  a.O[(size_t)b * a.NH * 128 + h * 128 + d] = f2h(num / den);
+  a.O[(size_t)b * a.NH * 128 + h * 128 + d] = f2h(num / den_s);
 }
 
 void launch_block_attention(const AttnArgs& a, hipStream_t st) {

@@ -11,6 +11,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 typedef _Float16 half_t;
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
@@ -21,6 +23,16 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 #define DFL_DEV __device__ __forceinline__
 
+// Compile-time loop: calls f(std::integral_constant<int, I>) for I in [B, E), so array
+// indices derived from I are constants and register arrays are never demoted to scratch.
+template <int B, int E, class F>
+DFL_DEV void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
 // D += A(32x16) * B(16x32), fp16 inputs, fp32 accumulate.
 DFL_DEV floatx16 mfma32x32x16(half8_t a, half8_t b, floatx16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -29,17 +41,21 @@ DFL_DEV floatx16 mfma32x32x16(half8_t a, half8_t b, floatx16 c) {
 DFL_DEV half8_t as_half8(uint4 v) { return __builtin_bit_cast(half8_t, v); }
 DFL_DEV uint4 as_uint4(half8_t v) { return __builtin_bit_cast(uint4, v); }
 
-// 128-bit streaming load (nontemporal hint: weights are read once per block).
-DFL_DEV uint4 load_stream(const uint4* p) {
-  return __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p)));
+// 128-bit loads into native vector registers (u32x4 is a first-class vector, so selects
+// and copies stay in VGPRs).  load_stream adds the nontemporal hint for data read once.
+DFL_DEV u32x4 load_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
+DFL_DEV u32x4 load_vec(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+DFL_DEV half8_t as_half8(u32x4 v) { return __builtin_bit_cast(half8_t, v); }
 
 // Exact int8 -> fp16 conversion of 16 packed bytes (bytes 0..7 -> lo, 8..15 -> hi).
 // For q in [-127, 127]: u = q ^ 0x80 = q + 128 in [1, 255]; the fp16 bit pattern
 // 0x6400 | u encodes 1024 + u exactly, so (0x6400 | u) - 1152 = q exactly.
-DFL_DEV void dequant_i8x16(uint4 w, half8_t& lo, half8_t& hi) {
+DFL_DEV void dequant_i8x16(u32x4 w, half8_t& lo, half8_t& hi) {
   const uint32_t k64 = 0x64646464u;
-  uint32_t d[4] = {w.x ^ 0x80808080u, w.y ^ 0x80808080u, w.z ^ 0x80808080u, w.w ^ 0x80808080u};
+  const u32x4 x = w ^ 0x80808080u;
+  uint32_t d[4] = {x.x, x.y, x.z, x.w};
   uint32_t o[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {

@@ -40,14 +40,16 @@ struct WTraits<WT_F16> {
 };
 
 template <int WT, int EPI, int SK, int P>
-__global__ __launch_bounds__(256) void skinny_gemm_kernel(SkinnyArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void skinny_gemm_kernel(SkinnyArgs a) {
   constexpr int TN = 4 / SK;
   constexpr int KBK = WTraits<WT>::KBK;
   constexpr int NX = WTraits<WT>::NX;
   __shared__ float red[(SK > 1) ? 4 * 2 * 16 * 64 : 1];
 
   const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
+  // wave-uniform values (readfirstlane lets the compiler use scalar branches)
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int group = blockIdx.x / a.S_x;
   const int split = blockIdx.x - group * a.S_x;
   const int wt = group * TN + w / SK;          // wave-tile (64 packed rows)
@@ -67,6 +69,9 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(SkinnyArgs a) {
   const int row = mt * 32 + m;
   const bool row_ok = row < a.M;
 
+  // Rows past M read row 0: an activation row only feeds its own output column
+  // (D[n][m] = sum_k W[n][k] X[m][k]), which is never stored, so no masking is needed
+  // and every load stays unconditional.
   const uint4* w0 = a.W + ((size_t)(2 * wt) * a.KB + kb0) * 64 + lane;
   const uint4* w1 = w0 + (size_t)a.KB * 64;
   const half_t* xrow = a.X + (size_t)(row_ok ? row : 0) * a.ldx + (size_t)kb0 * KBK +
@@ -74,50 +79,60 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(SkinnyArgs a) {
 
   floatx16 acc0 = {}, acc1 = {};
 
-  uint4 sw0[P], sw1[P], sx[P][NX];
-  const uint4 zero4 = {0u, 0u, 0u, 0u};
-
-  auto issue = [&](int s, int i) {
-    sw0[s] = load_stream(w0 + (size_t)i * 64);
-    sw1[s] = load_stream(w1 + (size_t)i * 64);
-    // Rows past M read row 0 (always valid) and are zeroed by a select, so the loads
-    // stay unconditional.
-    const uint4* xp = reinterpret_cast<const uint4*>(xrow + (size_t)i * KBK);
-#pragma unroll
-    for (int x = 0; x < NX; ++x) {
-      const uint4 v = xp[x];
-      sx[s][x] = row_ok ? v : zero4;
-    }
+  // One pipeline stage holds P consecutive k-blocks: two 1 KiB weight fragments per
+  // k-block and NX activation fragments.
+  struct Stage {
+    u32x4 w0[P], w1[P], x[P][NX];
+  };
+  // Loads are unconditional: block indices past the wave's range are clamped to its
+  // last block (a cache hit) and contribute nothing (zero activation at use).
+  auto issue = [&](Stage& st, int base, int last) {
+    static_for<0, P>([&](auto s) {
+      const int i = min(base + (int)s, last);
+      st.w0[s] = load_stream(w0 + (size_t)i * 64);
+      st.w1[s] = load_stream(w1 + (size_t)i * 64);
+      const half_t* xp = xrow + (size_t)i * KBK;
+      static_for<0, NX>([&](auto x) { st.x[s][x] = load_vec(xp + 8 * x); });
+    });
+  };
+  auto consume = [&](const Stage& st, int base, int nkb_) {
+    static_for<0, P>([&](auto s) {
+      const bool valid = base + (int)s < nkb_;
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      const u32x4 xa = valid ? st.x[s][0] : z;
+      const u32x4 xb = valid ? st.x[s][NX - 1] : z;
+      if constexpr (WT == WT_INT8) {
+        half8_t lo0, hi0, lo1, hi1;
+        dequant_i8x16(st.w0[s], lo0, hi0);
+        dequant_i8x16(st.w1[s], lo1, hi1);
+        const half8_t xl = as_half8(xa), xh = as_half8(xb);
+        acc0 = mfma32x32x16(lo0, xl, acc0);
+        acc1 = mfma32x32x16(lo1, xl, acc1);
+        acc0 = mfma32x32x16(hi0, xh, acc0);
+        acc1 = mfma32x32x16(hi1, xh, acc1);
+      } else {
+        const half8_t xv = as_half8(xa);
+        acc0 = mfma32x32x16(as_half8(st.w0[s]), xv, acc0);
+        acc1 = mfma32x32x16(as_half8(st.w1[s]), xv, acc1);
+      }
+    });
   };
 
-#pragma unroll
-  for (int s = 0; s < P; ++s)
-    if (s < nkb) issue(s, s);
-
-  for (int it = 0; it < nkb; it += P) {
-#pragma unroll
-    for (int s = 0; s < P; ++s) {
-      if (it + s < nkb) {
-        const uint4 cw0 = sw0[s], cw1 = sw1[s];
-        uint4 cx[NX];
-#pragma unroll
-        for (int x = 0; x < NX; ++x) cx[x] = sx[s][x];
-        if (it + s + P < nkb) issue(s, it + s + P);
-        if constexpr (WT == WT_INT8) {
-          half8_t lo0, hi0, lo1, hi1;
-          dequant_i8x16(cw0, lo0, hi0);
-          dequant_i8x16(cw1, lo1, hi1);
-          const half8_t xl = as_half8(cx[0]), xh = as_half8(cx[NX - 1]);
-          acc0 = mfma32x32x16(lo0, xl, acc0);
-          acc1 = mfma32x32x16(lo1, xl, acc1);
-          acc0 = mfma32x32x16(hi0, xh, acc0);
-          acc1 = mfma32x32x16(hi1, xh, acc1);
-        } else {
-          const half8_t xv = as_half8(cx[0]);
-          acc0 = mfma32x32x16(as_half8(cw0), xv, acc0);
-          acc1 = mfma32x32x16(as_half8(cw1), xv, acc1);
-        }
-      }
+  // Ping-pong between two register stages: the loads of one stage stay in flight
+  // while the other is consumed (no register copies, so no forced waits).
+  // sched_barrier keeps the scheduler from sinking a stage's loads down to their uses.
+  if (nkb > 0) {
+    const int last = nkb - 1;
+    Stage A, B;
+    issue(A, 0, last);
+    for (int base = 0; base < nkb; base += 2 * P) {
+      issue(B, base + P, last);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(A, base, nkb);
+      if (base + P >= nkb) break;
+      issue(A, base + 2 * P, last);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(B, base + P, nkb);
     }
   }
 
@@ -221,7 +236,7 @@ static void launch_sk(const SkinnyArgs& a, int n_mtiles, hipStream_t st) {
   const int n_wt = a.N / 64;
   const int n_groups = (n_wt + TN - 1) / TN;
   dim3 grid(n_groups * a.S_x, n_mtiles);
-  hipLaunchKernelGGL((skinny_gemm_kernel<WT, EPI, SK, 8>), grid, dim3(256), 0, st, a);
+  hipLaunchKernelGGL((skinny_gemm_kernel<WT, EPI, SK, 4>), grid, dim3(256), 0, st, a);
 }
 
 template <int WT, int EPI>

@@ -9,7 +9,7 @@
 namespace dfl {
 
 enum { WT_INT8 = 0, WT_F16 = 1 };
-enum { EPI_PARTIAL = 0, EPI_SWIGLU = 1, EPI_ARGMAX = 2 };
+enum { EPI_PARTIAL = 0, EPI_SWIGLU = 1, EPI_ARGMAX = 2, EPI_STORE = 3, EPI_RESID = 4 };
 
 struct SkinnyArgs {
   const uint4* W;        // packed weight blocks
@@ -31,6 +31,33 @@ struct SkinnyArgs {
 void launch_skinny_gemm(int wt, int epi, const SkinnyArgs& a, int SK, int n_mtiles,
                         hipStream_t st);
 
+// ---- stream-K weight-streaming GEMM for M <= 32 rows (dfl_stream.hip) ----
+struct StreamArgs {
+  const uint4* W;           // packed weight blocks, N rows (multiple of 64)
+  const half_t* scale;      // [N] per packed row (int8) or nullptr
+  int N, KB;                // KB = K/32 (int8) or K/16 (fp16)
+  const half_t* X;          // activations [M][ldx], M <= 32
+  int ldx, M;
+  const float* rnorm;       // NORM: per-row 1/rms of X
+  const half_t* gnorm;      // NORM: [K] gain (K <= 8192)
+  float* ws;                // [N/64][seg_cap][2048] partials of tiles split across workgroups
+  int seg_cap;
+  int* tile_cnt;            // [N/64] arrival counters (zero-initialised, self-resetting)
+  half_t* out;              // STORE: [M][ldo] fp16; SWIGLU: [M][ldo] (N/2 columns)
+  int ldo;                  // also the row stride of x for RESID
+  half_t* x;                // RESID: residual stream [M][ldo], updated in place
+  float* ss_part;           // RESID: [N/64][32] per-tile row sums of squares
+  int* done_cnt;            // RESID: launch-wide tile counter (zero-initialised)
+  float* rnorm_out;         // RESID: [M] 1/rms of the updated rows
+  float eps;
+  float* logits;            // ARGMAX: optional [M][ldl] fp32
+  int ldl;
+  unsigned long long* keys; // ARGMAX: optional [M] packed (order(value) << 32 | ~index)
+};
+int streamk_grid(int N, int KB, int n_cu);
+int streamk_seg_cap(int N, int KB, int G);
+void launch_streamk_gemm(int wt, int epi, bool norm, const StreamArgs& a, int G, hipStream_t st);
+
 // ---- pack / quantise (dfl_pack.hip) ----
 // Symmetric per-row int8 quantisation of w [oc][ic] fp32.
 void launch_quantize_w8(const float* w, int64_t oc, int64_t ic, int8_t* q, half_t* s,
@@ -43,24 +70,29 @@ void launch_pack_i8(const int8_t* q, const half_t* s, int rows, int K, uint4* ds
 void launch_pack_f16(const half_t* w, int rows, int K, uint4* dst, hipStream_t st);
 
 // ---- row kernels (dfl_rows.hip) ----
-// x[b] = ids ? embed[ids[b]] : noise[b];  h[b] = RMSNorm(x[b]) * g.  An id outside
-// [0, V) yields a zero row and sets *err |= 1.
+// x[b] = ids ? embed[ids[b]] : noise[b];  rnorm[b] = 1/rms(x[b]); optionally
+// h[b] = RMSNorm(x[b]) * g.  An id outside [0, V) yields a zero row and sets *err |= 1.
 void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* noise, int B,
-                       int H, int V, const half_t* g, float eps, half_t* x, half_t* h, int* err,
+                       int H, int V, const half_t* g, float eps, half_t* x, half_t* h,
+                       float* rnorm, int* err, hipStream_t st);
+// h[m][n] = fp16(fp16(x[m][n] * r[m]) * g[n]).
+void launch_apply_norm(const half_t* x, const float* r, const half_t* g, int M, int N, half_t* h,
                        hipStream_t st);
-// v = sum_s ws[s][m][n] (fixed order) * scale[n] -> fp16; optional residual:
-// x[m][n] = fp16(x[m][n] + v) (else x[m][n] = v); then, if h != nullptr,
-// h[m][n] = RMSNorm(x[m]) * g.  One workgroup per row.
+// v = sum_s ws[s][m][n] (fixed order) * scale[n] -> fp16; with residual:
+// x[m][n] = fp16(x[m][n] + v), else the rounded v goes to x (or to xs when x is null);
+// then, if h != nullptr, h[m][n] = RMSNorm(row m) * g.  Grid: (ceil(N/1024), M);
+// ss_part [M][ceil(N/1024)] and cnt [M] (zero-initialised, self-resetting) are scratch.
 void launch_reduce_resid_norm(const float* ws, int S_x, int M, int N, const half_t* scale,
                               half_t* x, bool residual, const half_t* g, float eps, half_t* h,
-                              int ldh, hipStream_t st);
+                              int ldh, half_t* xs, float* ss_part, int* cnt, hipStream_t st);
 // QKV reduce + per-head RMSNorm + neox RoPE + scatter.  Rows m use position pos0 + m.
 // Head slots [0, NH) -> Q[h][m][d] (q_rows rows per head); slots [NH, NH+NKV) -> K
 // cache rows (cache_row0 + m); [NH+NKV, NH+2NKV) -> Vt cache columns.  The partial sums
 // hold head slots col_slot0 .. col_slot0 + N/128 - 1 (so the ingest path can project
 // only K and V); scale is indexed by the absolute slot.
 struct QKRopeArgs {
-  const float* ws; int S_x; int M; int N;   // partial sums [S_x][M][N]
+  const half_t* qkv16;                       // if set: fp16 projections [M][N] (scaled)
+  const float* ws; int S_x; int M; int N;   // else partial sums [S_x][M][N]
   int col_slot0;                             // head slot of ws column 0
   const half_t* scale;                       // [(NH+2NKV)*128]
   int slot0, n_slots;                        // head slots handled (q,k,v numbering)

@@ -18,7 +18,8 @@ DFL_DEV half_t rms_out(float x, float r, half_t g) { return f2h(h2f(f2h(x * r)) 
 __global__ __launch_bounds__(ROW_THREADS) void embed_norm_kernel(
     const int32_t* __restrict__ ids, const half_t* __restrict__ embed,
     const half_t* __restrict__ noise, int H, int V, const half_t* __restrict__ g, float eps,
-    half_t* __restrict__ x, half_t* __restrict__ h, int* __restrict__ err) {
+    half_t* __restrict__ x, half_t* __restrict__ h, float* __restrict__ rnorm,
+    int* __restrict__ err) {
   __shared__ float sm[16];
   const int b = blockIdx.x;
   const half_t* src = noise + (size_t)b * H;
@@ -44,6 +45,8 @@ __global__ __launch_bounds__(ROW_THREADS) void embed_norm_kernel(
   }
   ss = block_sum(ss, sm);
   const float r = 1.0f / sqrtf(ss / (float)H + eps);
+  if (rnorm && threadIdx.x == 0) rnorm[b] = r;
+  if (!h) return;
 #pragma unroll
   for (int i = 0; i < ROW_MAXV; ++i) {
     const int k = threadIdx.x + i * ROW_THREADS;
@@ -52,49 +55,97 @@ __global__ __launch_bounds__(ROW_THREADS) void embed_norm_kernel(
 }
 
 void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* noise, int B,
-                       int H, int V, const half_t* g, float eps, half_t* x, half_t* h, int* err,
-                       hipStream_t st) {
+                       int H, int V, const half_t* g, float eps, half_t* x, half_t* h,
+                       float* rnorm, int* err, hipStream_t st) {
   hipLaunchKernelGGL(embed_norm_kernel, dim3(B), dim3(ROW_THREADS), 0, st, ids, embed, noise, H,
-                     V, g, eps, x, h, err);
+                     V, g, eps, x, h, rnorm, err);
 }
 
-__global__ __launch_bounds__(ROW_THREADS) void reduce_resid_norm_kernel(
-    const float* __restrict__ ws, int S_x, int M, int N, const half_t* __restrict__ scale,
-    half_t* __restrict__ x, int residual, const half_t* __restrict__ g, float eps,
-    half_t* __restrict__ h, int ldh) {
-  __shared__ float sm[16];
-  const int m = blockIdx.x;
-  float v[ROW_MAXV];
-  float ss = 0.f;
+__global__ __launch_bounds__(256) void apply_norm_kernel(const half_t* __restrict__ x,
+                                                         const float* __restrict__ r,
+                                                         const half_t* __restrict__ g, int N,
+                                                         half_t* __restrict__ h) {
+  const int m = blockIdx.y;
+  const int n = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (n >= N) return;
+  const float rr = r[m];
+  const half4_t xv = *reinterpret_cast<const half4_t*>(x + (size_t)m * N + n);
+  half4_t o;
 #pragma unroll
-  for (int i = 0; i < ROW_MAXV; ++i) {
-    const int n = threadIdx.x + i * ROW_THREADS;
-    v[i] = 0.f;
-    if (n < N) {
-      float acc = 0.f;
-      for (int s = 0; s < S_x; ++s) acc += ws[((size_t)s * M + m) * N + n];
-      float y = h2f(f2h(scale ? acc * h2f(scale[n]) : acc));
-      if (residual) y = h2f(f2h(h2f(x[(size_t)m * N + n]) + y));
-      if (x) x[(size_t)m * N + n] = f2h(y);
-      v[i] = y;
+  for (int j = 0; j < 4; ++j) o[j] = rms_out(h2f(xv[j]), rr, g[n + j]);
+  *reinterpret_cast<half4_t*>(h + (size_t)m * N + n) = o;
+}
+
+void launch_apply_norm(const half_t* x, const float* r, const half_t* g, int M, int N, half_t* h,
+                       hipStream_t st) {
+  hipLaunchKernelGGL(apply_norm_kernel, dim3((N / 4 + 255) / 256, M), dim3(256), 0, st, x, r, g,
+                     N, h);
+}
+
+// Split-K reduction + residual + RMSNorm, parallel over (column chunk, row).
+// Each workgroup handles RED_COLS columns of one row: sums the S_x partials in a fixed
+// order, applies the per-row weight scale, rounds to fp16 (Linear output), adds the
+// residual (fp16 add), stores x and its chunk's sum of squares.  The last chunk of a
+// row to finish (device-scope counter; every chunk fences its stores before counting)
+// sums the chunk partials in a fixed order and writes h = RMSNorm(x) * g for the whole
+// row, then re-arms the counter for the next launch.
+constexpr int RED_THREADS = 256;
+constexpr int RED_COLS = 4 * RED_THREADS;
+
+__global__ __launch_bounds__(RED_THREADS) void reduce_resid_norm_kernel(
+    const float* __restrict__ ws, int S_x, int M, int N, const half_t* __restrict__ scale,
+    half_t* x, int residual, const half_t* __restrict__ g, float eps, half_t* __restrict__ h,
+    int ldh, half_t* __restrict__ xs_out, float* __restrict__ ss_part, int* __restrict__ cnt) {
+  __shared__ float sm[16];
+  __shared__ int last_flag;
+  const int chunk = blockIdx.x, m = blockIdx.y, NC = gridDim.x;
+  const int n0 = chunk * RED_COLS + threadIdx.x * 4;
+  // x may be null (no residual stream): then the rounded projection goes to xs_out.
+  half_t* xrow = (x ? x : xs_out) + (size_t)m * N;
+  float ss = 0.f;
+  if (n0 < N) {   // N is a multiple of 64, so a 4-column group is all in or all out
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < S_x; ++s)
+      acc += *reinterpret_cast<const floatx4*>(ws + ((size_t)s * M + m) * N + n0);
+    half4_t out;
+    const half4_t xo = residual ? *reinterpret_cast<const half4_t*>(xrow + n0) : (half4_t){};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float y = h2f(f2h(scale ? acc[j] * h2f(scale[n0 + j]) : acc[j]));
+      if (residual) y = h2f(f2h(h2f(xo[j]) + y));
+      out[j] = f2h(y);
       ss += y * y;
     }
+    *reinterpret_cast<half4_t*>(xrow + n0) = out;
   }
   if (!h) return;
   ss = block_sum(ss, sm);
-  const float r = 1.0f / sqrtf(ss / (float)N + eps);
+  if (threadIdx.x == 0) ss_part[(size_t)m * NC + chunk] = ss;
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) last_flag = (atomicAdd(cnt + m, 1) == NC - 1);
+  __syncthreads();
+  if (!last_flag) return;
+  __threadfence();
+  float tot = 0.f;
+  for (int c = 0; c < NC; ++c) tot += __builtin_nontemporal_load(ss_part + (size_t)m * NC + c);
+  const float r = 1.0f / sqrtf(tot / (float)N + eps);
+  for (int n = threadIdx.x * 4; n < N; n += RED_COLS) {
+    const half4_t xv = __builtin_nontemporal_load(reinterpret_cast<const half4_t*>(xrow + n));
+    half4_t o;
 #pragma unroll
-  for (int i = 0; i < ROW_MAXV; ++i) {
-    const int n = threadIdx.x + i * ROW_THREADS;
-    if (n < N) h[(size_t)m * ldh + n] = rms_out(v[i], r, g[n]);
+    for (int j = 0; j < 4; ++j) o[j] = rms_out(h2f(xv[j]), r, g[n + j]);
+    *reinterpret_cast<half4_t*>(h + (size_t)m * ldh + n) = o;
   }
+  if (threadIdx.x == 0) cnt[m] = 0;
 }
 
 void launch_reduce_resid_norm(const float* ws, int S_x, int M, int N, const half_t* scale,
                               half_t* x, bool residual, const half_t* g, float eps, half_t* h,
-                              int ldh, hipStream_t st) {
-  hipLaunchKernelGGL(reduce_resid_norm_kernel, dim3(M), dim3(ROW_THREADS), 0, st, ws, S_x, M, N,
-                     scale, x, residual ? 1 : 0, g, eps, h, ldh);
+                              int ldh, half_t* xs, float* ss_part, int* cnt, hipStream_t st) {
+  dim3 grid((N + RED_COLS - 1) / RED_COLS, M);
+  hipLaunchKernelGGL(reduce_resid_norm_kernel, grid, dim3(RED_THREADS), 0, st, ws, S_x, M, N,
+                     scale, x, residual ? 1 : 0, g, eps, h, ldh, xs, ss_part, cnt);
 }
 
 // One wave per (row m, head slot); lane j holds head elements j and j + 64, which are
@@ -109,13 +160,18 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(QKRopeArgs a) {
   const int n0 = slot * 128 + lane, n1 = n0 + 64;
   const int c0 = (slot - a.col_slot0) * 128 + lane;
   float v0 = 0.f, v1 = 0.f;
-  for (int s = 0; s < a.S_x; ++s) {
-    const float* wsr = a.ws + ((size_t)s * a.M + m) * a.N;
-    v0 += wsr[c0];
-    v1 += wsr[c0 + 64];
+  if (a.qkv16) {   // already scaled and rounded by the GEMM epilogue
+    v0 = h2f(a.qkv16[(size_t)m * a.N + c0]);
+    v1 = h2f(a.qkv16[(size_t)m * a.N + c0 + 64]);
+  } else {
+    for (int s = 0; s < a.S_x; ++s) {
+      const float* wsr = a.ws + ((size_t)s * a.M + m) * a.N;
+      v0 += wsr[c0];
+      v1 += wsr[c0 + 64];
+    }
+    v0 = h2f(f2h(v0 * h2f(a.scale[n0])));   // Linear output is fp16
+    v1 = h2f(f2h(v1 * h2f(a.scale[n1])));
   }
-  v0 = h2f(f2h(v0 * h2f(a.scale[n0])));   // Linear output is fp16
-  v1 = h2f(f2h(v1 * h2f(a.scale[n1])));
   const int kv_slot0 = a.NH + a.NKV;
   if (slot >= kv_slot0) {   // V head: no norm, no rotation
     const int gk = slot - kv_slot0;
