@@ -249,7 +249,7 @@ def main():
             ach = per_launch / avg_s / 1e9
             roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
                         "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-                        "kernel": "skinny_gemm_kernel<int8> (W8A16 projections)",
+                        "kernel": "gsk_gemm_kernel<int8,*> (stream-K W8A16 projections qkv/o/gate_up/down)",
                         "bytes_per_launch": per_launch, "avg_launch_us": avg_s * 1e6}
 
     cpu = None

@@ -98,7 +98,7 @@ struct dfl_ctx {
   int* sk_tile_cnt = nullptr;    // [max tiles]
   float* sk_ss = nullptr;        // [max tiles][32]
   int* sk_done = nullptr;        // [1]
-  struct SKPlan { int G = 1, seg_cap = 1; } sk_qkv, sk_o, sk_gu, sk_down, sk_lm;
+  SKPlan sk_qkv, sk_o, sk_gu, sk_down, sk_lm;
   float* ss_part = nullptr;   // [rows][ceil(H/1024)] per-chunk sums of squares
   int* row_cnt = nullptr;     // [rows] arrival counters of the reduce kernel
   half_t* fc_out = nullptr;   // [ING_ROWS][H] rounded fc output (ingest)
@@ -212,9 +212,11 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
                         (size_t)x->p_down.S_x * Bm * x->H});
   ws = std::max(ws, (size_t)ING_ROWS * std::max(x->H, 2 * x->NKV * 128));
   int r = DFL_OK;
-  if ((r = x->alloc(&x->x, Bm * x->H)) || (r = x->alloc(&x->h, Bm * x->H)) ||
+  // x / attn / act are 32-row tiles in the activation fragment layout (zero padded rows)
+  const size_t Bt = ((Bm + 31) / 32) * 32;
+  if ((r = x->alloc(&x->x, Bt * x->H, true)) || (r = x->alloc(&x->h, Bm * x->H)) ||
       (r = x->alloc(&x->Q, (size_t)x->NH * Bm * 128)) ||
-      (r = x->alloc(&x->attn, Bm * x->NH * 128)) || (r = x->alloc(&x->act, Bm * x->F)) ||
+      (r = x->alloc(&x->attn, Bt * x->NH * 128, true)) || (r = x->alloc(&x->act, Bt * x->F, true)) ||
       (r = x->alloc(&x->ctxbuf, (size_t)ING_ROWS * x->H)) || (r = x->alloc(&x->ws, ws)) ||
       (r = x->alloc(&x->Op, (size_t)MAX_CHUNKS * x->NH * Bm * 128)) ||
       (r = x->alloc(&x->Ml, (size_t)MAX_CHUNKS * x->NH * Bm * 2)) ||
@@ -231,12 +233,7 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
         ncu > 0)
       x->n_cu = ncu;
-    auto plan = [&](int N, int KB) {
-      dfl_ctx::SKPlan p;
-      p.G = streamk_grid(N, KB, x->n_cu);
-      p.seg_cap = streamk_seg_cap(N, KB, p.G);
-      return p;
-    };
+    auto plan = [&](int N, int KB) { return streamk_plan(N, KB, x->n_cu); };
     x->sk_qkv = plan(x->NQKV, x->H / 32);
     x->sk_o = plan(x->H, x->NH * 128 / 32);
     x->sk_gu = plan(2 * x->F, x->H / 32);
@@ -392,7 +389,7 @@ static void gemm(dfl_ctx* ctx, int cat, int wt, int epi, const uint4* W, const h
 }
 
 // Stream-K GEMM over the M rows of a block, in 32-row m-tiles.
-static void skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const dfl_ctx::SKPlan& p,
+static void skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const SKPlan& p,
                    const uint4* W, const half_t* scale, int N, int KB, const half_t* X, int ldx,
                    int M, const half_t* gnorm, half_t* out, int ldo, half_t* xres,
                    float* logits, unsigned long long* keys, hipStream_t st) {
@@ -423,7 +420,7 @@ static void skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const dfl_ctx::SKPlan
     a.logits = logits ? logits + (size_t)m0 * N : nullptr;
     a.ldl = N;
     a.keys = keys ? keys + m0 : nullptr;
-    launch_streamk_gemm(wt, epi, gnorm != nullptr, a, p.G, st);
+    launch_streamk_gemm(wt, epi, gnorm != nullptr, a, p, st);
   }
 }
 
@@ -635,8 +632,10 @@ int dfl_draft_block(dfl_ctx* ctx, const uint16_t* noise_emb, const int32_t* ids,
     launch_apply_norm(ctx->x, ctx->rnorm, ctx->final_norm, B, H,
                       reinterpret_cast<half_t*>(out_hidden), st);
   }
-  if (out_prenorm)
-    DFL_HIP(hipMemcpyAsync(out_prenorm, ctx->x, (size_t)B * H * 2, hipMemcpyDeviceToDevice, st));
+  if (out_prenorm) {
+    ProfScope ps(ctx, P_ROWS, 0, st);
+    launch_afl_to_rows(ctx->x, B, H, reinterpret_cast<half_t*>(out_prenorm), st);
+  }
   DFL_TRY(check_launch("dfl_draft_block"));
   ctx->last_block = B;
   return DFL_OK;

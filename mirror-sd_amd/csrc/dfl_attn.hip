@@ -158,7 +158,7 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(AttnArgs a) {
 #pragma unroll 8
   for (int c = 0; c < nc; ++c) num += op[(size_t)c * NB * 128] * wts[c];
   const int h = rowg / a.B, b = rowg - h * a.B;
-  a.O[(size_t)b * a.NH * 128 + h * 128 + d] = f2h(num / den_s);
+  a.O[afl_index(b, h * 128 + d, a.NH * 128)] = f2h(num / den_s);
 }
 
 void launch_block_attention(const AttnArgs& a, hipStream_t st) {

@@ -70,6 +70,19 @@ DFL_DEV void dequant_i8x16(u32x4 w, half8_t& lo, half8_t& hi) {
   hi = (half8_t){h[4].x, h[4].y, h[5].x, h[5].y, h[6].x, h[6].y, h[7].x, h[7].y};
 }
 
+// Activation fragment layout ("AFL") of a 32-row activation tile X[32][K], K % 32 == 0,
+// the operand order of the W8A16 MFMA loop: 1 KiB records, record (kb, h) holding for lane
+// l the 8 halves X[l % 32][32*kb + 16*(l/32) + 8*h + 0..7].  One wave-wide 128-bit load of a
+// record is a contiguous 1 KiB read (a row-major fragment load touches 32 cache lines).
+// Offset in halves of element (m, k), m in [0, 32):
+DFL_DEV size_t afl_offset(int m, int k) {
+  return ((size_t)((k >> 5) * 2 + ((k >> 3) & 1)) * 64 + m + 32 * ((k >> 4) & 1)) * 8 + (k & 7);
+}
+// Element (row, k) of a multi-tile AFL buffer (tiles of 32 rows, each 32*K halves).
+DFL_DEV size_t afl_index(int row, int k, int K) {
+  return (size_t)(row >> 5) * 32 * K + afl_offset(row & 31, k);
+}
+
 DFL_DEV float h2f(half_t h) { return (float)h; }
 DFL_DEV half_t f2h(float f) { return (half_t)f; }   // round-to-nearest-even
 

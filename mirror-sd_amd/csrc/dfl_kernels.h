@@ -36,16 +36,16 @@ struct StreamArgs {
   const uint4* W;           // packed weight blocks, N rows (multiple of 64)
   const half_t* scale;      // [N] per packed row (int8) or nullptr
   int N, KB;                // KB = K/32 (int8) or K/16 (fp16)
-  const half_t* X;          // activations [M][ldx], M <= 32
+  const half_t* X;          // activations: one 32-row tile in the fragment layout (afl_offset)
   int ldx, M;
   const float* rnorm;       // NORM: per-row 1/rms of X
   const half_t* gnorm;      // NORM: [K] gain (K <= 8192)
   float* ws;                // [N/64][seg_cap][2048] partials of tiles split across workgroups
   int seg_cap;
   int* tile_cnt;            // [N/64] arrival counters (zero-initialised, self-resetting)
-  half_t* out;              // STORE: [M][ldo] fp16; SWIGLU: [M][ldo] (N/2 columns)
-  int ldo;                  // also the row stride of x for RESID
-  half_t* x;                // RESID: residual stream [M][ldo], updated in place
+  half_t* out;              // STORE: row-major [M][ldo] fp16; SWIGLU: fragment-layout tile [32][N/2]
+  int ldo;
+  half_t* x;                // RESID: residual stream, fragment-layout tile [32][N], updated in place
   float* ss_part;           // RESID: [N/64][32] per-tile row sums of squares
   int* done_cnt;            // RESID: launch-wide tile counter (zero-initialised)
   float* rnorm_out;         // RESID: [M] 1/rms of the updated rows
@@ -54,9 +54,14 @@ struct StreamArgs {
   int ldl;
   unsigned long long* keys; // ARGMAX: optional [M] packed (order(value) << 32 | ~index)
 };
-int streamk_grid(int N, int KB, int n_cu);
-int streamk_seg_cap(int N, int KB, int G);
-void launch_streamk_gemm(int wt, int epi, bool norm, const StreamArgs& a, int G, hipStream_t st);
+struct SKPlan {
+  bool wave_level = false;  // independent waves (4 per 256-thread workgroup) or 8-wave workgroups
+  int workers = 1;          // waves (wave-level) or workgroups (workgroup-level)
+  int seg_cap = 1;          // workspace slots per tile
+};
+SKPlan streamk_plan(int N, int KB, int n_cu);
+void launch_streamk_gemm(int wt, int epi, bool norm, const StreamArgs& a, const SKPlan& p,
+                         hipStream_t st);
 
 // ---- pack / quantise (dfl_pack.hip) ----
 // Symmetric per-row int8 quantisation of w [oc][ic] fp32.
@@ -70,14 +75,17 @@ void launch_pack_i8(const int8_t* q, const half_t* s, int rows, int K, uint4* ds
 void launch_pack_f16(const half_t* w, int rows, int K, uint4* dst, hipStream_t st);
 
 // ---- row kernels (dfl_rows.hip) ----
-// x[b] = ids ? embed[ids[b]] : noise[b];  rnorm[b] = 1/rms(x[b]); optionally
+// x[b] = ids ? embed[ids[b]] : noise[b] (x in the activation fragment layout, K = H);
+// rnorm[b] = 1/rms(x[b]); optionally
 // h[b] = RMSNorm(x[b]) * g.  An id outside [0, V) yields a zero row and sets *err |= 1.
 void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* noise, int B,
                        int H, int V, const half_t* g, float eps, half_t* x, half_t* h,
                        float* rnorm, int* err, hipStream_t st);
-// h[m][n] = fp16(fp16(x[m][n] * r[m]) * g[n]).
+// x in the activation fragment layout (afl_index) [M][N] -> row-major h [M][N]:
+// h = fp16(fp16(x * r[m]) * g[n])  (apply_norm), or a plain copy (afl_to_rows).
 void launch_apply_norm(const half_t* x, const float* r, const half_t* g, int M, int N, half_t* h,
                        hipStream_t st);
+void launch_afl_to_rows(const half_t* x, int M, int N, half_t* h, hipStream_t st);
 // v = sum_s ws[s][m][n] (fixed order) * scale[n] -> fp16; with residual:
 // x[m][n] = fp16(x[m][n] + v), else the rounded v goes to x (or to xs when x is null);
 // then, if h != nullptr, h[m][n] = RMSNorm(row m) * g.  Grid: (ceil(N/1024), M);
@@ -117,7 +125,7 @@ struct AttnArgs {
   float scale_log2;       // head_dim^-0.5 * log2(e)
   float* Op;              // [n_chunks][NH*B][128] unnormalised partial outputs
   float* Ml;              // [n_chunks][NH*B][2] running (max, sum) in log2 domain
-  half_t* O;              // [B][NH*128] final output
+  half_t* O;              // [B][NH*128] final output, activation fragment layout
 };
 void launch_block_attention(const AttnArgs& a, hipStream_t st);
 

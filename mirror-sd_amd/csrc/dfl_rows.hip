@@ -38,7 +38,7 @@ __global__ __launch_bounds__(ROW_THREADS) void embed_norm_kernel(
     v[i] = 0.f;
     if (k < H) {
       const half_t t = bad ? (half_t)0.0f : src[k];
-      x[(size_t)b * H + k] = t;
+      x[afl_index(b, k, H)] = t;   // residual stream in the activation fragment layout
       v[i] = h2f(t);
       ss += v[i] * v[i];
     }
@@ -61,25 +61,34 @@ void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* no
                      V, g, eps, x, h, rnorm, err);
 }
 
-__global__ __launch_bounds__(256) void apply_norm_kernel(const half_t* __restrict__ x,
-                                                         const float* __restrict__ r,
-                                                         const half_t* __restrict__ g, int N,
-                                                         half_t* __restrict__ h) {
+// x (activation fragment layout, [M][N]) -> row-major h; with r/g set, h = RMSNorm(x) * g.
+__global__ __launch_bounds__(256) void afl_rows_kernel(const half_t* __restrict__ x,
+                                                       const float* __restrict__ r,
+                                                       const half_t* __restrict__ g, int N,
+                                                       half_t* __restrict__ h) {
   const int m = blockIdx.y;
   const int n = (blockIdx.x * 256 + threadIdx.x) * 4;
   if (n >= N) return;
-  const float rr = r[m];
-  const half4_t xv = *reinterpret_cast<const half4_t*>(x + (size_t)m * N + n);
-  half4_t o;
+  // 4 consecutive columns (n % 4 == 0) are 4 consecutive halves of one record
+  const half4_t xv = *reinterpret_cast<const half4_t*>(x + afl_index(m, n, N));
+  half4_t o = xv;
+  if (r) {
+    const float rr = r[m];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) o[j] = rms_out(h2f(xv[j]), rr, g[n + j]);
+    for (int j = 0; j < 4; ++j) o[j] = rms_out(h2f(xv[j]), rr, g[n + j]);
+  }
   *reinterpret_cast<half4_t*>(h + (size_t)m * N + n) = o;
 }
 
 void launch_apply_norm(const half_t* x, const float* r, const half_t* g, int M, int N, half_t* h,
                        hipStream_t st) {
-  hipLaunchKernelGGL(apply_norm_kernel, dim3((N / 4 + 255) / 256, M), dim3(256), 0, st, x, r, g,
-                     N, h);
+  hipLaunchKernelGGL(afl_rows_kernel, dim3((N / 4 + 255) / 256, M), dim3(256), 0, st, x, r, g, N,
+                     h);
+}
+
+void launch_afl_to_rows(const half_t* x, int M, int N, half_t* h, hipStream_t st) {
+  hipLaunchKernelGGL(afl_rows_kernel, dim3((N / 4 + 255) / 256, M), dim3(256), 0, st, x, nullptr,
+                     nullptr, N, h);
 }
 
 // Split-K reduction + residual + RMSNorm, parallel over (column chunk, row).

@@ -1,25 +1,34 @@
 // Stream-K weight-streaming GEMM for the draft block (M <= 32 activation rows):
 //   Y[m, n] = sum_k Xn[m, k] * W[n, k]  (* scale[n] for int8 weights)
 // with an optional RMSNorm applied to X on load (Xn = fp16(fp16(X * r[m]) * g[k])).
+// X is a 32-row tile in the activation fragment layout (afl_offset in dfl_common.h), so
+// activation fragments, like weight fragments, arrive as contiguous 1 KiB wave loads; the
+// residual and SwiGLU epilogues write their outputs in the same layout.
 //
-// Partition.  The packed weight matrix (see dfl_gemm.hip for the block layout) is a
-// sequence of U = (N/64) * KB work units (64-row wave-tile x one 1 KiB k-block pair),
-// tile-major.  The grid is exactly one 512-thread workgroup per CU; workgroup b takes
-// the contiguous unit range [b*U/G, (b+1)*U/G), so every CU streams the same number of
-// bytes and there is no second-round tail.  A range is cut into segments at tile
-// boundaries; the 8 waves split each segment's k-blocks, stream them with a two-stage
-// register pipeline, and reduce through LDS in a fixed order.
+// Partition.  The packed weight matrix (block layout: see dfl_gemm.hip) is a sequence of
+// U = (N/64) * KB work units (one 64-row wave-tile x one k-block), tile-major.  Workers
+// take equal contiguous unit ranges, so every CU streams the same number of bytes and
+// there is no second-round tail.  Two granularities:
+//   * wave-level (256-thread workgroups, 2 per CU, every wave an independent worker):
+//     for matrices with many tiles per worker (gate|up, lm_head) -- each wave sees one
+//     or two tile segments, so its load pipeline never drains mid-kernel;
+//   * workgroup-level (512-thread workgroups, 1 per CU, the 8 waves split each segment's
+//     k-blocks and reduce through LDS in a fixed order): for matrices with fewer tiles
+//     than CUs (qkv, o, down), where wave-level workers would cut every tile into dozens
+//     of fp32 partials.
 //
-// Completion.  A segment that covers a whole tile runs the epilogue directly.  A tile
-// split across workgroups is finished by whichever of them arrives last: each writes its
-// fp32 partial to a workspace slot, fences (device scope), and bumps the tile's counter;
-// the last one sums the slots in segment order (deterministic) and runs the epilogue,
-// then re-arms the counter.  No workgroup ever waits for another.
+// Completion.  A worker whose segment covers a whole tile runs the epilogue directly.  A
+// tile split across workers is finished by whichever arrives last: each stores its fp32
+// partial with agent-scope atomic stores, waits for them to complete (s_waitcnt), then
+// bumps the tile's agent-scope counter; the last one reads the slots back with
+// agent-scope atomic loads in slot order (deterministic sum), runs the epilogue and
+// re-arms the counter.  Only agent-scope atomics touch the shared slots, so no L2
+// write-back / invalidate is needed, and no worker ever waits for another.
 //
 // Epilogues: STORE (fp16 y with the per-row scale), RESID (x += fp16(y), per-row sums of
-// squares; the last tile of the launch turns them into r = rsqrt(mean(x^2) + eps) for
-// the next GEMM's norm-on-load), SWIGLU (gate/up row-blocks interleaved), ARGMAX (fp32
-// logits + packed (value, index) atomicMax per row).
+// squares; the last tile of the launch turns them into r = 1/rms for the next GEMM's
+// norm-on-load), SWIGLU (gate/up row-blocks interleaved), ARGMAX (fp32 logits + packed
+// (value, index) atomicMax per row).
 #include "dfl_common.h"
 #include "dfl_kernels.h"
 
@@ -27,8 +36,7 @@ namespace dfl {
 
 namespace {
 
-constexpr int SK_WAVES = 8;
-constexpr int SK_THREADS = 64 * SK_WAVES;
+constexpr int WG_WAVES = 8;   // workgroup-level kernel
 
 template <int WT>
 struct KTraits;
@@ -43,8 +51,8 @@ struct KTraits<WT_F16> {
   static constexpr int NX = 1;
 };
 
-// First workgroup whose unit range contains unit u: max b with floor(b*U/G) <= u.
-DFL_DEV int wg_of(long long u, long long U, int G) { return (int)(((u + 1) * G - 1) / U); }
+// Largest worker index w with floor(w*U/NW) <= u (the worker holding unit u).
+DFL_DEV int worker_of(long long u, long long U, int NW) { return (int)(((u + 1) * NW - 1) / U); }
 
 // fp16(fp16(x * r) * g) for 8 packed halves (RMSNorm output expression).
 DFL_DEV u32x4 norm8(u32x4 xv, float r, u32x4 gv) {
@@ -55,112 +63,339 @@ DFL_DEV u32x4 norm8(u32x4 xv, float r, u32x4 gv) {
   return __builtin_bit_cast(u32x4, y);
 }
 
-}  // namespace
+DFL_DEV void store_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+DFL_DEV float load_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
-template <int WT, int EPI, bool NORM, int P>
-__global__ __launch_bounds__(SK_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void streamk_gemm_kernel(StreamArgs a) {
+// ---------------------------------------------------------------------------------------
+// One wave streams k-blocks [v0, v0 + nkb) of wave-tile t into acc0/acc1 (two 32-row
+// blocks x 32 activation columns).  Two register stages of P k-blocks alternate; loads
+// are unconditional (indices clamped to the last block, whose slots then contribute a
+// zero activation), and sched_barrier keeps each stage's loads issued ahead of use.
+// ---------------------------------------------------------------------------------------
+template <int WT, bool NORM, int P>
+DFL_DEV void stream_tile(const StreamArgs& a, const half_t* gsh, float rn, int goff, int lane,
+                         int t, int v0, int nkb, floatx16& acc0, floatx16& acc1) {
   constexpr int KBK = KTraits<WT>::KBK;
   constexpr int NX = KTraits<WT>::NX;
-  __shared__ float red[(SK_WAVES - 1) * 2 * 16 * 64];
+  acc0 = (floatx16){};
+  acc1 = (floatx16){};
+  if (nkb <= 0) return;
+  struct Stage {
+    u32x4 w0[P], w1[P], x[P][NX];
+  };
+  const uint4* w0p = a.W + ((size_t)(2 * t) * a.KB + v0) * 64 + lane;
+  const uint4* w1p = w0p + (size_t)a.KB * 64;
+  // activation records: int8 k-block kb = 32 k -> records (kb, 0), (kb, 1), this lane's
+  // entry; fp16 k-block kb = 16 k -> record (kb/2, g) at entry m + 32*(kb & 1)
+  const u32x4* xf = reinterpret_cast<const u32x4*>(a.X);
+  const int m = lane & 31, g = lane >> 5;
+  const int last = nkb - 1;
+  auto issue = [&](Stage& st, int base) {
+    static_for<0, P>([&](auto s) {
+      const int i = min(base + (int)s, last);
+      st.w0[s] = load_stream(w0p + (size_t)i * 64);
+      st.w1[s] = load_stream(w1p + (size_t)i * 64);
+      const int kb = v0 + i;
+      if constexpr (WT == WT_INT8) {
+        st.x[s][0] = xf[(size_t)(2 * kb) * 64 + lane];
+        st.x[s][NX - 1] = xf[(size_t)(2 * kb + 1) * 64 + lane];
+      } else {
+        st.x[s][0] = xf[(size_t)((kb >> 1) * 2 + g) * 64 + m + 32 * (kb & 1)];
+      }
+    });
+  };
+  auto consume = [&](const Stage& st, int base) {
+    static_for<0, P>([&](auto s) {
+      const int i = base + (int)s;
+      const bool valid = i < nkb;
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      u32x4 xa = st.x[s][0], xb = st.x[s][NX - 1];
+      if constexpr (NORM) {
+        const int kk = (v0 + min(i, last)) * KBK + goff;
+        xa = norm8(xa, rn, *reinterpret_cast<const u32x4*>(gsh + kk));
+        if constexpr (NX > 1) xb = norm8(xb, rn, *reinterpret_cast<const u32x4*>(gsh + kk + 8));
+        else xb = xa;
+      }
+      xa = valid ? xa : z;
+      xb = valid ? xb : z;
+      if constexpr (WT == WT_INT8) {
+        half8_t lo0, hi0, lo1, hi1;
+        dequant_i8x16(st.w0[s], lo0, hi0);
+        dequant_i8x16(st.w1[s], lo1, hi1);
+        const half8_t xl = as_half8(xa), xh = as_half8(xb);
+        acc0 = mfma32x32x16(lo0, xl, acc0);
+        acc1 = mfma32x32x16(lo1, xl, acc1);
+        acc0 = mfma32x32x16(hi0, xh, acc0);
+        acc1 = mfma32x32x16(hi1, xh, acc1);
+      } else {
+        const half8_t xv = as_half8(xa);
+        acc0 = mfma32x32x16(as_half8(st.w0[s]), xv, acc0);
+        acc1 = mfma32x32x16(as_half8(st.w1[s]), xv, acc1);
+      }
+    });
+  };
+  Stage A, B;
+  issue(A, 0);
+  for (int base = 0; base < nkb; base += 2 * P) {
+    issue(B, base + P);
+    __builtin_amdgcn_sched_barrier(0);
+    consume(A, base);
+    if (base + P >= nkb) break;
+    issue(A, base + 2 * P);
+    __builtin_amdgcn_sched_barrier(0);
+    consume(B, base + P);
+  }
+}
+
+// Cross-worker completion of tile t.  `slot` is this worker's index among the `count`
+// workers covering the tile.  Returns true (with the full sums in acc0/acc1) for the last
+// worker to arrive; the others return false after publishing their partial.
+DFL_DEV bool finish_split_tile(const StreamArgs& a, int lane, int t, int slot, int count,
+                               floatx16& acc0, floatx16& acc1) {
+  float* mine = a.ws + ((size_t)t * a.seg_cap + slot) * 2048;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    store_agent(mine + r * 64 + lane, acc0[r]);
+    store_agent(mine + 1024 + r * 64 + lane, acc1[r]);
+  }
+  // the partial stores complete (agent-coherent) before the counter moves
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  int prev = 0;
+  if (lane == 0)
+    prev = __hip_atomic_fetch_add(a.tile_cnt + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  prev = __shfl(prev, 0, 64);
+  if (prev != count - 1) return false;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  acc0 = (floatx16){};
+  acc1 = (floatx16){};
+  for (int j = 0; j < count; ++j) {
+    const float* src = a.ws + ((size_t)t * a.seg_cap + j) * 2048;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      acc0[r] += load_agent(src + r * 64 + lane);
+      acc1[r] += load_agent(src + 1024 + r * 64 + lane);
+    }
+  }
+  if (lane == 0) a.tile_cnt[t] = 0;   // next use is a later launch
+  return true;
+}
+
+// Epilogue of a completed tile t for the 32 activation rows held by this wave.
+// Row n of the packed matrix in accumulator r of block tt: n = (2t+tt)*32 + 8*(r/4)
+// + 4*g + (r%4), activation row m = lane % 32.
+template <int EPI>
+DFL_DEV void tile_epilogue(const StreamArgs& a, int lane, int t, const floatx16& acc0,
+                           const floatx16& acc1) {
+  const int m = lane & 31, g = lane >> 5;
+  const bool row_ok = m < a.M;
+  const int nb = (2 * t) * 32 + 4 * g;
+  if constexpr (EPI == EPI_STORE) {
+    if (!row_ok) return;
+    half_t* dst = a.out + (size_t)m * a.ldo + nb;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      half4_t o0, o1;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        o0[c] = f2h(acc0[4 * q + c] * h2f(a.scale[nb + 8 * q + c]));
+        o1[c] = f2h(acc1[4 * q + c] * h2f(a.scale[nb + 32 + 8 * q + c]));
+      }
+      *reinterpret_cast<half4_t*>(dst + 8 * q) = o0;
+      *reinterpret_cast<half4_t*>(dst + 32 + 8 * q) = o1;
+    }
+  } else if constexpr (EPI == EPI_RESID) {
+    // x is an AFL tile [32][N]; columns nb + 32*tt + 8*q + (0..3) of row m are 4
+    // consecutive halves of record (2t + tt, q & 1), entry m + 32*(q >> 1), offset 4g.
+    float ss = 0.f;
+    if (row_ok) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+          half_t* xp = a.x + afl_offset(m, nb + 32 * tt + 8 * q);
+          half4_t xv = *reinterpret_cast<const half4_t*>(xp);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const float acc = tt ? acc1[4 * q + c] : acc0[4 * q + c];
+            const float y = h2f(f2h(acc * h2f(a.scale[nb + 32 * tt + 8 * q + c])));
+            const half_t xn = f2h(h2f(xv[c]) + y);
+            xv[c] = xn;
+            ss += h2f(xn) * h2f(xn);
+          }
+          *reinterpret_cast<half4_t*>(xp) = xv;
+        }
+      }
+    }
+    ss += __shfl_xor(ss, 32, 64);
+    if (g == 0 && row_ok) store_agent(a.ss_part + (size_t)t * 32 + m, ss);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    int prev = 0;
+    if (lane == 0)
+      prev = __hip_atomic_fetch_add(a.done_cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    prev = __shfl(prev, 0, 64);
+    const int n_wt = a.N >> 6;
+    if (prev == n_wt - 1) {   // last tile of the launch: 1/rms per row for the next norm
+      // Lane (m, g) sums tiles g, g+2, ...; eight loads are issued before any is used
+      // (a dependent load per tile would serialise n_wt memory round trips).
+      float tot = 0.f;
+      if (row_ok) {
+        const float* sp = a.ss_part + m;
+        int tt = g;
+        for (; tt + 14 < n_wt; tt += 16) {
+          float v[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[j] = load_agent(sp + (size_t)(tt + 2 * j) * 32);
+          tot += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+        }
+        for (; tt < n_wt; tt += 2) tot += load_agent(sp + (size_t)tt * 32);
+      }
+      tot += __shfl_xor(tot, 32, 64);
+      if (g == 0 && row_ok) a.rnorm_out[m] = 1.0f / sqrtf(tot / (float)a.N + a.eps);
+      if (lane == 0) *a.done_cnt = 0;
+    }
+  } else if constexpr (EPI == EPI_SWIGLU) {
+    if (!row_ok) return;
+    // out is an AFL tile [32][N/2]: columns 32t + 8q + 4g + (0..3) of row m
+    const half_t* sg = a.scale + nb;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      half_t* dst = a.out + afl_offset(m, t * 32 + 8 * q + 4 * g);
+      half4_t o;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int r = 4 * q + c;
+        const float gv = h2f(f2h(acc0[r] * h2f(sg[8 * q + c])));
+        const float uv = h2f(f2h(acc1[r] * h2f(sg[32 + 8 * q + c])));
+        const float sig = h2f(f2h(1.0f / (1.0f + expf(-gv))));
+        const float sil = h2f(f2h(gv * sig));
+        o[c] = f2h(sil * uv);
+      }
+      *reinterpret_cast<half4_t*>(dst) = o;
+    }
+  } else {  // EPI_ARGMAX: fp16 weights, no scale
+    if (row_ok && a.logits) {
+      float* dst = a.logits + (size_t)m * a.ldl + nb;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        *reinterpret_cast<floatx4*>(dst + 8 * q) =
+            (floatx4){acc0[4 * q], acc0[4 * q + 1], acc0[4 * q + 2], acc0[4 * q + 3]};
+        *reinterpret_cast<floatx4*>(dst + 32 + 8 * q) =
+            (floatx4){acc1[4 * q], acc1[4 * q + 1], acc1[4 * q + 2], acc1[4 * q + 3]};
+      }
+    }
+    if (a.keys) {
+      // scan in increasing n so that strict '>' keeps the lowest index on ties
+      float best = -INFINITY;
+      int bn = 0x7fffffff;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int n = nb + 8 * (r >> 2) + (r & 3);
+        if (acc0[r] > best) { best = acc0[r]; bn = n; }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int n = nb + 32 + 8 * (r >> 2) + (r & 3);
+        if (acc1[r] > best) { best = acc1[r]; bn = n; }
+      }
+      const float ob = __shfl_xor(best, 32, 64);
+      const int on = __shfl_xor(bn, 32, 64);
+      if (ob > best || (ob == best && on < bn)) { best = ob; bn = on; }
+      if (g == 0 && row_ok && bn != 0x7fffffff) {
+        const unsigned long long key =
+            ((unsigned long long)float_order_key(best) << 32) | (0xFFFFFFFFu - (uint32_t)bn);
+        atomicMax(a.keys + m, key);
+      }
+    }
+  }
+}
+
+// Copy the RMSNorm gain into LDS (one barrier, at kernel start).
+template <bool NORM>
+DFL_DEV void load_gain(const StreamArgs& a, half_t* gsh, int K) {
+  if constexpr (NORM) {
+    for (int k = threadIdx.x; k < K; k += blockDim.x) gsh[k] = a.gnorm[k];
+    __syncthreads();
+  }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------------------
+// Wave-level workers: 4 independent waves per workgroup.
+// ---------------------------------------------------------------------------------------
+template <int WT, int EPI, bool NORM, int P>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void wsk_gemm_kernel(StreamArgs a) {
+  constexpr int KBK = KTraits<WT>::KBK;
   __shared__ half_t gsh[NORM ? 8192 : 8];
-  __shared__ int s_last;
+  load_gain<NORM>(a, gsh, a.KB * KBK);
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int m = lane & 31, g = lane >> 5;
-  const bool row_ok = m < a.M;
-  const int xr = row_ok ? m : 0;   // rows >= M read row 0: they only feed unstored columns
-  const int n_wt = a.N >> 6;
-  const long long U = (long long)n_wt * a.KB;
-  const int G = gridDim.x;
-  const int b = blockIdx.x;
-  const long long u0 = (long long)b * U / G, u1 = (long long)(b + 1) * U / G;
-
-  float rn = 1.0f;
-  if constexpr (NORM) {
-    rn = a.rnorm[xr];
-    const int K = a.KB * KBK;
-    for (int k = threadIdx.x; k < K; k += SK_THREADS) gsh[k] = a.gnorm[k];
-    __syncthreads();
-  }
-
-  const half_t* xrow = a.X + (size_t)xr * a.ldx + (WT == WT_INT8 ? 16 * g : 8 * g);
+  // rows >= M of the 32-row tile feed only their own (never stored) output columns
+  const int NW = gridDim.x * 4;
+  const int gw = blockIdx.x * 4 + w;
+  const long long U = (long long)(a.N >> 6) * a.KB;
+  const long long u0 = (long long)gw * U / NW, u1 = (long long)(gw + 1) * U / NW;
+  const float rn = NORM ? a.rnorm[m] : 1.0f;
   const int goff = (WT == WT_INT8 ? 16 * g : 8 * g);
 
-  struct Stage {
-    u32x4 w0[P], w1[P], x[P][NX];
-  };
+  for (long long u = u0; u < u1;) {
+    const int t = (int)(u / a.KB);
+    const int kbs = (int)(u - (long long)t * a.KB);
+    const int kbe = (int)min((long long)a.KB, (long long)kbs + (u1 - u));
+    floatx16 acc0, acc1;
+    stream_tile<WT, NORM, P>(a, gsh, rn, goff, lane, t, kbs, kbe - kbs, acc0, acc1);
+    bool complete = (kbs == 0 && kbe == a.KB);
+    if (!complete) {
+      const long long tu0 = (long long)t * a.KB;
+      const int first = worker_of(tu0, U, NW);
+      const int count = worker_of(tu0 + a.KB - 1, U, NW) - first + 1;
+      complete = finish_split_tile(a, lane, t, gw - first, count, acc0, acc1);
+    }
+    if (complete) tile_epilogue<EPI>(a, lane, t, acc0, acc1);
+    u += kbe - kbs;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Workgroup-level workers: 8 waves split each segment's k-blocks, LDS reduction.
+// ---------------------------------------------------------------------------------------
+template <int WT, int EPI, bool NORM, int P>
+__global__ __launch_bounds__(64 * WG_WAVES) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void gsk_gemm_kernel(StreamArgs a) {
+  constexpr int KBK = KTraits<WT>::KBK;
+  __shared__ float red[(WG_WAVES - 1) * 2048];
+  __shared__ half_t gsh[NORM ? 8192 : 8];
+  load_gain<NORM>(a, gsh, a.KB * KBK);
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int m = lane & 31, g = lane >> 5;
+  const int G = gridDim.x;
+  const int b = blockIdx.x;
+  const long long U = (long long)(a.N >> 6) * a.KB;
+  const long long u0 = (long long)b * U / G, u1 = (long long)(b + 1) * U / G;
+  const float rn = NORM ? a.rnorm[m] : 1.0f;
+  const int goff = (WT == WT_INT8 ? 16 * g : 8 * g);
 
   for (long long u = u0; u < u1;) {
     const int t = (int)(u / a.KB);
     const int kbs = (int)(u - (long long)t * a.KB);
     const int kbe = (int)min((long long)a.KB, (long long)kbs + (u1 - u));
     const int L = kbe - kbs;
-    // this wave's share of the segment
-    const int v0 = kbs + (w * L) / SK_WAVES, v1 = kbs + ((w + 1) * L) / SK_WAVES;
-    const int nkb = v1 - v0;
-
-    const uint4* w0p = a.W + ((size_t)(2 * t) * a.KB + v0) * 64 + lane;
-    const uint4* w1p = w0p + (size_t)a.KB * 64;
-    const half_t* xp0 = xrow + (size_t)v0 * KBK;
-
-    floatx16 acc0 = {}, acc1 = {};
-    auto issue = [&](Stage& st, int base, int last) {
-      static_for<0, P>([&](auto s) {
-        const int i = min(base + (int)s, last);
-        st.w0[s] = load_stream(w0p + (size_t)i * 64);
-        st.w1[s] = load_stream(w1p + (size_t)i * 64);
-        const half_t* xp = xp0 + (size_t)i * KBK;
-        static_for<0, NX>([&](auto x) { st.x[s][x] = load_vec(xp + 8 * x); });
-      });
-    };
-    auto consume = [&](const Stage& st, int base) {
-      static_for<0, P>([&](auto s) {
-        const int i = base + (int)s;
-        const bool valid = i < nkb;
-        const u32x4 z = {0u, 0u, 0u, 0u};
-        u32x4 xa = st.x[s][0], xb = st.x[s][NX - 1];
-        if constexpr (NORM) {
-          const int kk = (v0 + min(i, nkb - 1)) * KBK + goff;
-          xa = norm8(xa, rn, *reinterpret_cast<const u32x4*>(gsh + kk));
-          if constexpr (NX > 1) xb = norm8(xb, rn, *reinterpret_cast<const u32x4*>(gsh + kk + 8));
-          else xb = xa;
-        }
-        xa = valid ? xa : z;
-        xb = valid ? xb : z;
-        if constexpr (WT == WT_INT8) {
-          half8_t lo0, hi0, lo1, hi1;
-          dequant_i8x16(st.w0[s], lo0, hi0);
-          dequant_i8x16(st.w1[s], lo1, hi1);
-          const half8_t xl = as_half8(xa), xh = as_half8(xb);
-          acc0 = mfma32x32x16(lo0, xl, acc0);
-          acc1 = mfma32x32x16(lo1, xl, acc1);
-          acc0 = mfma32x32x16(hi0, xh, acc0);
-          acc1 = mfma32x32x16(hi1, xh, acc1);
-        } else {
-          const half8_t xv = as_half8(xa);
-          acc0 = mfma32x32x16(as_half8(st.w0[s]), xv, acc0);
-          acc1 = mfma32x32x16(as_half8(st.w1[s]), xv, acc1);
-        }
-      });
-    };
-    if (nkb > 0) {
-      const int last = nkb - 1;
-      Stage A, B;
-      issue(A, 0, last);
-      for (int base = 0; base < nkb; base += 2 * P) {
-        issue(B, base + P, last);
-        __builtin_amdgcn_sched_barrier(0);
-        consume(A, base);
-        if (base + P >= nkb) break;
-        issue(A, base + 2 * P, last);
-        __builtin_amdgcn_sched_barrier(0);
-        consume(B, base + P);
-      }
-    }
-
-    // ---- reduce the 8 waves' partials into wave 0 (fixed order) ----
+    const int v0 = kbs + (w * L) / WG_WAVES, v1 = kbs + ((w + 1) * L) / WG_WAVES;
+    floatx16 acc0, acc1;
+    stream_tile<WT, NORM, P>(a, gsh, rn, goff, lane, t, v0, v1 - v0, acc0, acc1);
     if (w != 0) {
       float* dst = red + (size_t)(w - 1) * 2048;
 #pragma unroll
@@ -172,7 +407,7 @@ void streamk_gemm_kernel(StreamArgs a) {
     __syncthreads();
     if (w == 0) {
 #pragma unroll
-      for (int j = 0; j < SK_WAVES - 1; ++j) {
+      for (int j = 0; j < WG_WAVES - 1; ++j) {
         const float* src = red + (size_t)j * 2048;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -182,176 +417,58 @@ void streamk_gemm_kernel(StreamArgs a) {
       }
       bool complete = (kbs == 0 && kbe == a.KB);
       if (!complete) {
-        // cross-workgroup split of tile t: slot j among the workgroups covering it
         const long long tu0 = (long long)t * a.KB;
-        const int first = wg_of(tu0, U, G);
-        const int count = wg_of(tu0 + a.KB - 1, U, G) - first + 1;
-        const int j = b - first;
-        float* slot = a.ws + ((size_t)t * a.seg_cap + j) * 2048;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          slot[r * 64 + lane] = acc0[r];
-          slot[1024 + r * 64 + lane] = acc1[r];
-        }
-        __threadfence();
-        int prev = 0;
-        if (lane == 0) prev = atomicAdd(a.tile_cnt + t, 1);
-        prev = __shfl(prev, 0, 64);
-        if (prev == count - 1) {
-          __threadfence();
-          acc0 = (floatx16){};
-          acc1 = (floatx16){};
-          for (int jj = 0; jj < count; ++jj) {
-            const float* src = a.ws + ((size_t)t * a.seg_cap + jj) * 2048;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              acc0[r] += __builtin_nontemporal_load(src + r * 64 + lane);
-              acc1[r] += __builtin_nontemporal_load(src + 1024 + r * 64 + lane);
-            }
-          }
-          if (lane == 0) a.tile_cnt[t] = 0;
-          complete = true;
-        }
+        const int first = worker_of(tu0, U, G);
+        const int count = worker_of(tu0 + a.KB - 1, U, G) - first + 1;
+        complete = finish_split_tile(a, lane, t, b - first, count, acc0, acc1);
       }
-      if (complete) {
-        // ---- epilogue for tile t: n = (2t + tt)*32 + 8*q + 4*g + (0..3) ----
-        const int nb = (2 * t) * 32 + 4 * g;
-        if constexpr (EPI == EPI_STORE) {
-          if (row_ok) {
-            half_t* dst = a.out + (size_t)m * a.ldo + nb;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              half4_t o0, o1;
-#pragma unroll
-              for (int c = 0; c < 4; ++c) {
-                o0[c] = f2h(acc0[4 * q + c] * h2f(a.scale[nb + 8 * q + c]));
-                o1[c] = f2h(acc1[4 * q + c] * h2f(a.scale[nb + 32 + 8 * q + c]));
-              }
-              *reinterpret_cast<half4_t*>(dst + 8 * q) = o0;
-              *reinterpret_cast<half4_t*>(dst + 32 + 8 * q) = o1;
-            }
-          }
-        } else if constexpr (EPI == EPI_RESID) {
-          float ss = 0.f;
-          if (row_ok) {
-            half_t* xr_ = a.x + (size_t)m * a.ldo + nb;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-#pragma unroll
-              for (int tt = 0; tt < 2; ++tt) {
-                half4_t xv = *reinterpret_cast<const half4_t*>(xr_ + 32 * tt + 8 * q);
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                  const float acc = tt ? acc1[4 * q + c] : acc0[4 * q + c];
-                  const float y = h2f(f2h(acc * h2f(a.scale[nb + 32 * tt + 8 * q + c])));
-                  const half_t xn = f2h(h2f(xv[c]) + y);
-                  xv[c] = xn;
-                  ss += h2f(xn) * h2f(xn);
-                }
-                *reinterpret_cast<half4_t*>(xr_ + 32 * tt + 8 * q) = xv;
-              }
-            }
-          }
-          ss += __shfl_xor(ss, 32, 64);
-          if (g == 0 && row_ok) a.ss_part[(size_t)t * 32 + m] = ss;
-          __threadfence();
-          int prev = 0;
-          if (lane == 0) prev = atomicAdd(a.done_cnt, 1);
-          prev = __shfl(prev, 0, 64);
-          if (prev == n_wt - 1) {   // last tile of the launch: per-row rsqrt for the next norm
-            __threadfence();
-            if (g == 0 && row_ok) {
-              float tot = 0.f;
-              for (int tt = 0; tt < n_wt; ++tt)
-                tot += __builtin_nontemporal_load(a.ss_part + (size_t)tt * 32 + m);
-              a.rnorm_out[m] = 1.0f / sqrtf(tot / (float)a.N + a.eps);
-            }
-            if (lane == 0) *a.done_cnt = 0;
-          }
-        } else if constexpr (EPI == EPI_SWIGLU) {
-          if (row_ok) {
-            const half_t* sg = a.scale + nb;
-            half_t* dst = a.out + (size_t)m * a.ldo + (size_t)t * 32 + 4 * g;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              half4_t o;
-#pragma unroll
-              for (int c = 0; c < 4; ++c) {
-                const int r = 4 * q + c;
-                const float gv = h2f(f2h(acc0[r] * h2f(sg[8 * q + c])));
-                const float uv = h2f(f2h(acc1[r] * h2f(sg[32 + 8 * q + c])));
-                const float sig = h2f(f2h(1.0f / (1.0f + expf(-gv))));
-                const float sil = h2f(f2h(gv * sig));
-                o[c] = f2h(sil * uv);
-              }
-              *reinterpret_cast<half4_t*>(dst + 8 * q) = o;
-            }
-          }
-        } else {  // EPI_ARGMAX: fp16 weights, no scale
-          if (row_ok && a.logits) {
-            float* dst = a.logits + (size_t)m * a.ldl + nb;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              *reinterpret_cast<floatx4*>(dst + 8 * q) =
-                  (floatx4){acc0[4 * q], acc0[4 * q + 1], acc0[4 * q + 2], acc0[4 * q + 3]};
-              *reinterpret_cast<floatx4*>(dst + 32 + 8 * q) =
-                  (floatx4){acc1[4 * q], acc1[4 * q + 1], acc1[4 * q + 2], acc1[4 * q + 3]};
-            }
-          }
-          if (a.keys) {
-            float best = -INFINITY;
-            int bn = 0x7fffffff;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int n = nb + 8 * (r >> 2) + (r & 3);
-              if (acc0[r] > best) { best = acc0[r]; bn = n; }
-            }
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int n = nb + 32 + 8 * (r >> 2) + (r & 3);
-              if (acc1[r] > best) { best = acc1[r]; bn = n; }
-            }
-            const float ob = __shfl_xor(best, 32, 64);
-            const int on = __shfl_xor(bn, 32, 64);
-            if (ob > best || (ob == best && on < bn)) { best = ob; bn = on; }
-            if (g == 0 && row_ok && bn != 0x7fffffff) {
-              const unsigned long long key =
-                  ((unsigned long long)float_order_key(best) << 32) | (0xFFFFFFFFu - (uint32_t)bn);
-              atomicMax(a.keys + m, key);
-            }
-          }
-        }
-      }
+      if (complete) tile_epilogue<EPI>(a, lane, t, acc0, acc1);
     }
     u += L;
     __syncthreads();   // red[] is reused by the next segment
   }
 }
 
-// Workgroups: one per CU, never more than the number of units.
-int streamk_grid(int N, int KB, int n_cu) {
-  const long long U = (long long)(N / 64) * KB;
-  return (int)std::max(1LL, std::min<long long>(n_cu, U));
-}
+// ---------------------------------------------------------------------------------------
+// Host-side planning and launch
+// ---------------------------------------------------------------------------------------
 
-// Workspace slots per tile for a given grid: ceil(KB / floor(U/G)) + 1.
-int streamk_seg_cap(int N, int KB, int G) {
-  const long long U = (long long)(N / 64) * KB;
-  const long long per = std::max(1LL, U / G);
-  return (int)((KB + per - 1) / per + 1);
+// Wave-level when a worker would see at least half a tile at 8 waves per CU; otherwise
+// the workgroup-level kernel (one 8-wave workgroup per CU).
+SKPlan streamk_plan(int N, int KB, int n_cu) {
+  // Workgroup-level workers, one per CU.  When there are fewer wave-tiles than CUs the
+  // worker count is the largest multiple of the tile count that fits, so every tile is
+  // split into the same number of equal k-ranges (no worker straddles two tiles).
+  // Measured on 256 CUs this beats independent-wave workers for every projection shape.
+  SKPlan p;
+  const long long nt = N / 64;
+  const long long U = nt * KB;
+  long long W = n_cu;
+  if (nt < n_cu) W = std::max(1LL, (long long)n_cu / nt) * nt;
+  p.wave_level = false;
+  p.workers = (int)std::max(1LL, std::min(W, U));
+  const long long per = std::max(1LL, U / p.workers);
+  p.seg_cap = (int)((KB + per - 1) / per + 1);
+  return p;
 }
 
 template <int WT, int EPI, bool NORM>
-static void launch_t(const StreamArgs& a, int G, hipStream_t st) {
-  hipLaunchKernelGGL((streamk_gemm_kernel<WT, EPI, NORM, 4>), dim3(G), dim3(SK_THREADS), 0, st, a);
+static void launch_t(const StreamArgs& a, const SKPlan& p, hipStream_t st) {
+  if (p.wave_level)
+    hipLaunchKernelGGL((wsk_gemm_kernel<WT, EPI, NORM, 4>), dim3(p.workers / 4), dim3(256), 0, st,
+                       a);
+  else
+    hipLaunchKernelGGL((gsk_gemm_kernel<WT, EPI, NORM, 4>), dim3(p.workers), dim3(64 * WG_WAVES), 0,
+                       st, a);
 }
 
-void launch_streamk_gemm(int wt, int epi, bool norm, const StreamArgs& a, int G, hipStream_t st) {
-#define DFL_SK_CASE(W_, E_)                                        \
-  if (wt == W_ && epi == E_) {                                     \
-    if (norm) launch_t<W_, E_, true>(a, G, st);                    \
-    else launch_t<W_, E_, false>(a, G, st);                        \
-    return;                                                        \
+void launch_streamk_gemm(int wt, int epi, bool norm, const StreamArgs& a, const SKPlan& p,
+                         hipStream_t st) {
+#define DFL_SK_CASE(W_, E_)                     \
+  if (wt == W_ && epi == E_) {                  \
+    if (norm) launch_t<W_, E_, true>(a, p, st); \
+    else launch_t<W_, E_, false>(a, p, st);     \
+    return;                                     \
   }
   DFL_SK_CASE(WT_INT8, EPI_STORE)
   DFL_SK_CASE(WT_INT8, EPI_RESID)
