@@ -48,6 +48,18 @@ def algorithmic_bytes(cfg, block, ctx):
             "total": nl * (per_layer_w + per_layer_s + kv) + lm}
 
 
+def traffic_per_launch(workload_name):
+    """HBM bytes per projection-GEMM launch from the committed counter measurement
+    (rocprofv3 FETCH_SIZE and WRITE_SIZE passes, scaled by a known-size copy kernel), or
+    None when no measurement for this workload is committed."""
+    path = os.path.join(ROOT, "profiles", f"hbm_traffic_{workload_name}.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["gemm_w8a16"]["bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def build_model(wl, seed, keep_host: bool):
     """Synthetic weights generated on the GPU, quantised by the library's W8A16
     quantiser and loaded.  Optionally keeps host copies for the CPU baseline."""
@@ -158,6 +170,9 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="run a plain device copy of this many MiB 3 times first (a known-size "
+                         "kernel for scaling FETCH_SIZE / WRITE_SIZE counter readings)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -178,6 +193,14 @@ def main():
         sys.exit(1)
     torch.manual_seed(args.seed)
     want_cpu = not args.no_cpu_baseline
+    if args.copy_probe_mib > 0:
+        n = (args.copy_probe_mib << 20) // 4
+        src = torch.ones(n, dtype=torch.int32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):   # elementwise kernel: reads n*4 bytes, writes n*4 bytes
+            torch.bitwise_not(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
     t_setup = time.perf_counter()
     model, host = build_model(wl, args.seed, keep_host=want_cpu)
     inp = synth.make_inputs_torch(cfg, wl.block, wl.ctx, seed=args.seed, device="cuda")
@@ -208,23 +231,64 @@ def main():
 
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
-    ev0.record(stream)
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    wall_s = time.perf_counter() - t0
-    ms_per_step = ev0.elapsed_time(ev1) / args.steps
+    def timed(k, gemm_events):
+        """k back-to-back blocks between two stream events.  With gemm_events the
+        stream-K GEMM launches also carry dispatch-timestamp events (no extra packets)."""
+        if gemm_events:
+            model.profile(True, gemm_only=True)
+            model.profile_read()
+        torch.cuda.synchronize()
+        ev0.record(stream)
+        t0 = time.perf_counter()
+        for _ in range(k):
+            step()
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        prof = None
+        if gemm_events:
+            prof = model.profile_read()
+            model.profile(False)
+        return ev0.elapsed_time(ev1) / k, wall, prof
+
+    ms_per_step, wall_s, _ = timed(args.steps, False)
     first_ids = out_ids.cpu().tolist()
+    # The same K steps again with dispatch-timestamp events on the GEMM launches: the
+    # kernel durations they give match a kernel trace, but attaching them lengthens the
+    # gaps between dispatches, so the headline latency comes from the plain run above.
+    ms_events, gprof = None, None
+    if not args.no_profile:
+        ms_events, _, gprof = timed(args.steps, True)
 
     nbytes = algorithmic_bytes(cfg, wl.block, wl.ctx)
     lat_us = ms_per_step * 1e3
     gbs = nbytes["total"] / (ms_per_step * 1e-3) / 1e9
 
+    def rate(r):
+        avg_s = r["ms"] * 1e-3 / r["launches"]
+        per_launch = r["bytes"] / r["launches"]
+        return per_launch, avg_s, per_launch / avg_s / 1e9
+
     roofline, kernels = None, None
+    if gprof and gprof.get("gemm_w8a16", {}).get("launches"):
+        per_launch, avg_s, ach = rate(gprof["gemm_w8a16"])
+        roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                    "traffic": traffic_per_launch(wl.name),
+                    "kernel": "gsk_gemm_kernel<int8,*> (stream-K W8A16 projections "
+                              "qkv/o/gate_up/down, one launch each per layer)",
+                    "bytes_per_launch": per_launch, "avg_launch_us": round(avg_s * 1e6, 3),
+                    "launches": gprof["gemm_w8a16"]["launches"]}
+        lm = gprof.get("lm_head_argmax", {})
+        if lm.get("launches"):
+            per_launch, avg_s, ach = rate(lm)
+            roofline["lm_head"] = {"kernel": "gsk_gemm_kernel<fp16,ARGMAX>", "achieved": round(ach, 1),
+                                   "frac": round(ach / HBM_PEAK_GBS, 4),
+                                   "bytes_per_launch": per_launch,
+                                   "avg_launch_us": round(avg_s * 1e6, 3)}
     if not args.no_profile and args.profile_steps > 0:
+        # per-group breakdown; groups other than the GEMMs are bracketed by marker events,
+        # which add a few microseconds of dispatch latency each
         model.profile(True)
         model.profile_read()
         for _ in range(args.profile_steps):
@@ -242,15 +306,6 @@ def main():
                 ent["gbs"] = r["bytes"] / (r["ms"] * 1e-3) / 1e9
                 ent["bytes_per_launch"] = r["bytes"] / r["launches"]
             kernels[name] = ent
-        g = prof.get("gemm_w8a16")
-        if g and g["launches"]:
-            avg_s = g["ms"] * 1e-3 / g["launches"]
-            per_launch = g["bytes"] / g["launches"]
-            ach = per_launch / avg_s / 1e9
-            roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
-                        "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-                        "kernel": "gsk_gemm_kernel<int8,*> (stream-K W8A16 projections qkv/o/gate_up/down)",
-                        "bytes_per_launch": per_launch, "avg_launch_us": avg_s * 1e6}
 
     cpu = None
     if want_cpu:
@@ -273,6 +328,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "phases": {"context_ingest_ms": round(ingest_ms, 3), "setup_s": round(setup_s, 1),
+                   "ms_per_step_with_gemm_events": (round(ms_events, 5) if ms_events else None),
                    "wall_ms_per_step": round(wall_s * 1e3 / args.steps, 4)},
         "kernels": kernels,
         "draft_ids_head": first_ids[:4],

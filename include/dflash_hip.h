@@ -128,8 +128,11 @@ int dfl_cache_kv(const dfl_ctx* ctx, int32_t layer, uint16_t** k, uint16_t** vt,
 
 /* Kernel timing with HIP events (the reference times phases and kernels with
  * time.perf_counter wrappers: bench_ane_profile.py:41-245, ANEKernel.run_timed
- * wrapper.rs:284-301).  While enabled, each kernel group launched by dfl_draft_block /
- * dfl_ingest_* is bracketed by events on its stream.  dfl_profile_read synchronises,
+ * wrapper.rs:284-301).  on = 1: each kernel group launched by dfl_draft_block /
+ * dfl_ingest_* is timed -- stream-K GEMM launches (projections, lm_head) by their own
+ * dispatch timestamps, other groups by events recorded around them on the stream.
+ * on = 2: only the stream-K GEMM launches, by dispatch timestamps, which adds no packets
+ * to the stream (usable inside a timed run).  on = 0: off.  dfl_profile_read synchronises,
  * returns per-category totals (name <= 31 chars each, in names[i*32]), launch counts
  * and algorithmic bytes (weights + scales for GEMMs, K/V read for attention), then
  * clears the records. */

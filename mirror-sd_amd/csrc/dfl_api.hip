@@ -104,7 +104,7 @@ struct dfl_ctx {
   half_t* fc_out = nullptr;   // [ING_ROWS][H] rounded fc output (ingest)
   GemmPlan p_qkv, p_o, p_gu, p_down, p_lm;
   std::vector<void*> allocs;
-  bool prof = false;
+  int prof = 0;   // 0 off, 1 every kernel group, 2 stream-K GEMM launches only
   std::vector<ProfRec> recs;
 
   ~dfl_ctx() {
@@ -131,21 +131,34 @@ struct dfl_ctx {
   }
 };
 
-// Brackets the kernels launched in its scope with events when profiling is on.
+// Times the kernels launched in its scope when profiling is on.  A marker scope records
+// events on the stream before and after the group (this adds marker packets, so it is
+// used only in mode 1).  An attached scope (one stream-K GEMM launch) hands its events
+// to the launch, which stores the kernel's own start and end timestamps in them: no
+// extra packets, so mode 2 leaves the stream's timing unchanged.
 struct ProfScope {
   dfl_ctx* c;
   int cat;
   long long bytes;
   hipStream_t st;
+  bool attached;
   hipEvent_t a = nullptr, b = nullptr;
-  ProfScope(dfl_ctx* c_, int cat_, long long bytes_, hipStream_t st_)
-      : c(c_), cat(cat_), bytes(bytes_), st(st_) {
-    if (c->prof && hipEventCreate(&a) == hipSuccess && hipEventCreate(&b) == hipSuccess)
-      (void)hipEventRecord(a, st);
+  ProfScope(dfl_ctx* c_, int cat_, long long bytes_, hipStream_t st_, bool attached_ = false)
+      : c(c_), cat(cat_), bytes(bytes_), st(st_), attached(attached_) {
+    const bool on = c->prof == 1 || (c->prof == 2 && attached);
+    if (!on) return;
+    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) {
+      if (a) (void)hipEventDestroy(a);
+      a = b = nullptr;
+      return;
+    }
+    if (!attached) (void)hipEventRecord(a, st);
   }
+  hipEvent_t start() const { return attached ? a : nullptr; }
+  hipEvent_t stop() const { return attached ? b : nullptr; }
   ~ProfScope() {
-    if (c->prof && a && b) {
-      (void)hipEventRecord(b, st);
+    if (a && b) {
+      if (!attached) (void)hipEventRecord(b, st);
       c->recs.push_back({cat, a, b, bytes});
     }
   }
@@ -396,7 +409,7 @@ static void skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const SKPlan& p,
   const long long wbytes = (wt == WT_INT8) ? (long long)N * KB * 32 + 2LL * N
                                            : (long long)N * KB * 16 * 2;
   for (int m0 = 0; m0 < M; m0 += 32) {
-    ProfScope ps(ctx, cat, wbytes, st);
+    ProfScope ps(ctx, cat, wbytes, st, /*attached=*/true);
     StreamArgs a{};
     a.W = W;
     a.scale = scale;
@@ -420,7 +433,7 @@ static void skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const SKPlan& p,
     a.logits = logits ? logits + (size_t)m0 * N : nullptr;
     a.ldl = N;
     a.keys = keys ? keys + m0 : nullptr;
-    launch_streamk_gemm(wt, epi, gnorm != nullptr, a, p, st);
+    launch_streamk_gemm(wt, epi, gnorm != nullptr, a, p, st, ps.start(), ps.stop());
   }
 }
 
@@ -704,7 +717,8 @@ int dfl_cache_kv(const dfl_ctx* ctx, int32_t layer, uint16_t** k, uint16_t** vt,
 
 int dfl_profile_enable(dfl_ctx* ctx, int32_t on) {
   if (!ctx) return fail(DFL_EINVAL, "dfl_profile_enable: null context");
-  ctx->prof = on != 0;
+  if (on < 0 || on > 2) return fail(DFL_EINVAL, "dfl_profile_enable: mode must be 0, 1 or 2");
+  ctx->prof = on;
   return DFL_OK;
 }
 

@@ -60,8 +60,10 @@ struct SKPlan {
   int seg_cap = 1;          // workspace slots per tile
 };
 SKPlan streamk_plan(int N, int KB, int n_cu);
+// ev_start / ev_stop (optional) receive the kernel's own start and end timestamps.
 void launch_streamk_gemm(int wt, int epi, bool norm, const StreamArgs& a, const SKPlan& p,
-                         hipStream_t st);
+                         hipStream_t st, hipEvent_t ev_start = nullptr,
+                         hipEvent_t ev_stop = nullptr);
 
 // ---- pack / quantise (dfl_pack.hip) ----
 // Symmetric per-row int8 quantisation of w [oc][ic] fp32.

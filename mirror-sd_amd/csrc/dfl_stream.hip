@@ -32,6 +32,8 @@
 #include "dfl_common.h"
 #include "dfl_kernels.h"
 
+#include <hip/hip_ext.h>
+
 namespace dfl {
 
 namespace {
@@ -452,23 +454,35 @@ SKPlan streamk_plan(int N, int KB, int n_cu) {
   return p;
 }
 
+// With events, the dispatch itself records its start / end time into them (the same
+// timestamps a kernel trace reports); no marker packets are added to the stream.
 template <int WT, int EPI, bool NORM>
-static void launch_t(const StreamArgs& a, const SKPlan& p, hipStream_t st) {
-  if (p.wave_level)
-    hipLaunchKernelGGL((wsk_gemm_kernel<WT, EPI, NORM, 4>), dim3(p.workers / 4), dim3(256), 0, st,
-                       a);
-  else
-    hipLaunchKernelGGL((gsk_gemm_kernel<WT, EPI, NORM, 4>), dim3(p.workers), dim3(64 * WG_WAVES), 0,
-                       st, a);
+static void launch_t(const StreamArgs& a, const SKPlan& p, hipStream_t st, hipEvent_t e0,
+                     hipEvent_t e1) {
+  if (p.wave_level) {
+    if (e0 || e1)
+      hipExtLaunchKernelGGL((wsk_gemm_kernel<WT, EPI, NORM, 4>), dim3(p.workers / 4), dim3(256),
+                            0, st, e0, e1, 0, a);
+    else
+      hipLaunchKernelGGL((wsk_gemm_kernel<WT, EPI, NORM, 4>), dim3(p.workers / 4), dim3(256), 0,
+                         st, a);
+  } else {
+    if (e0 || e1)
+      hipExtLaunchKernelGGL((gsk_gemm_kernel<WT, EPI, NORM, 4>), dim3(p.workers),
+                            dim3(64 * WG_WAVES), 0, st, e0, e1, 0, a);
+    else
+      hipLaunchKernelGGL((gsk_gemm_kernel<WT, EPI, NORM, 4>), dim3(p.workers),
+                         dim3(64 * WG_WAVES), 0, st, a);
+  }
 }
 
 void launch_streamk_gemm(int wt, int epi, bool norm, const StreamArgs& a, const SKPlan& p,
-                         hipStream_t st) {
-#define DFL_SK_CASE(W_, E_)                     \
-  if (wt == W_ && epi == E_) {                  \
-    if (norm) launch_t<W_, E_, true>(a, p, st); \
-    else launch_t<W_, E_, false>(a, p, st);     \
-    return;                                     \
+                         hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop) {
+#define DFL_SK_CASE(W_, E_)                                        \
+  if (wt == W_ && epi == E_) {                                     \
+    if (norm) launch_t<W_, E_, true>(a, p, st, ev_start, ev_stop); \
+    else launch_t<W_, E_, false>(a, p, st, ev_start, ev_stop);     \
+    return;                                                        \
   }
   DFL_SK_CASE(WT_INT8, EPI_STORE)
   DFL_SK_CASE(WT_INT8, EPI_RESID)

@@ -438,9 +438,12 @@ class DFlashDraftModel:
         return res[0] if len(res) == 1 else tuple(res)
 
     # ------------------------------------------------------------------ profiling
-    def profile(self, enable: bool = True):
-        """Bracket every kernel group with HIP events (see dfl_profile_enable)."""
-        _lib.check(self._L.dfl_profile_enable(self._ctx, 1 if enable else 0), "dfl_profile_enable")
+    def profile(self, enable: bool = True, gemm_only: bool = False):
+        """Time kernel groups with HIP events (see dfl_profile_enable).  ``gemm_only``
+        times just the stream-K GEMM launches by their dispatch timestamps, which leaves
+        the stream's timing unchanged."""
+        mode = 0 if not enable else (2 if gemm_only else 1)
+        _lib.check(self._L.dfl_profile_enable(self._ctx, mode), "dfl_profile_enable")
 
     def profile_read(self) -> Dict[str, dict]:
         """Per-category {ms, launches, bytes} since the last read (synchronises)."""

@@ -1,0 +1,131 @@
+"""Condense rocprofv3 output of a bench run into the short text kept under profiles/.
+
+Inputs (csv output of rocprofv3):
+  --stats   <dir>/<name>_kernel_stats.csv from ``--kernel-trace --stats``
+  --fetch   <dir>/<name>_counter_collection.csv from ``--pmc FETCH_SIZE``
+  --write   <dir>/<name>_counter_collection.csv from ``--pmc WRITE_SIZE``
+Both counter runs include a plain elementwise copy of known size (bench.py
+``--copy-probe-mib``); its readings give the factor that turns each counter into bytes
+(FETCH_SIZE / WRITE_SIZE are reported in KiB, but what one KiB of reading means depends
+on the request sizes the memory system sees, so it is calibrated rather than assumed).
+
+Writes a markdown summary and a json file with the per-launch HBM traffic of the
+W8A16 projection GEMMs and the lm_head GEMM (read by bench.py for ``roofline.traffic``).
+"""
+
+from __future__ import annotations
+
+import argparse
+import collections
+import csv
+import json
+import re
+import sys
+
+# kernel groups: (label, regex on the kernel name)
+GROUPS = [
+    ("proj_gemm_w8a16", r"gsk_gemm_kernel<0, [0-9], (true|false), 4>"),
+    ("qkv (STORE, norm-on-load)", r"gsk_gemm_kernel<0, 3, true, 4>"),
+    ("o / down (RESID)", r"gsk_gemm_kernel<0, 4, false, 4>"),
+    ("gate|up (SWIGLU, norm-on-load)", r"gsk_gemm_kernel<0, 1, true, 4>"),
+    ("lm_head (fp16, ARGMAX, norm-on-load)", r"gsk_gemm_kernel<1, 2, true, 4>"),
+    ("block attention", r"block_attn_kernel"),
+    ("attention merge", r"attn_merge_kernel"),
+    ("qk norm + rope", r"qk_rope_kernel"),
+    ("embed + norm", r"embed_norm_kernel"),
+    ("argmax finalize", r"argmax_finalize_kernel"),
+]
+COPY_RE = r"bitwise_not"
+
+
+def read_stats(path):
+    rows = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            rows[r["Name"]] = (int(r["Calls"]), float(r["TotalDurationNs"]))
+    return rows
+
+
+def read_counter(path):
+    per = collections.defaultdict(list)
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            per[r["Kernel_Name"]].append(float(r["Counter_Value"]))
+    return per
+
+
+def match(names, rx):
+    return [n for n in names if re.search(rx, n)]
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--stats", required=True)
+    ap.add_argument("--fetch")
+    ap.add_argument("--write")
+    ap.add_argument("--copy-mib", type=int, default=1024)
+    ap.add_argument("--workload", required=True)
+    ap.add_argument("--commands", default="", help="text of the commands that made the inputs")
+    ap.add_argument("--md", required=True)
+    ap.add_argument("--json")
+    a = ap.parse_args(argv)
+
+    stats = read_stats(a.stats)
+    out = [f"# rocprofv3 summary: {a.workload} draft block", ""]
+    if a.commands:
+        out += ["Commands:", "", "```", a.commands.strip(), "```", ""]
+    out += ["## Kernel durations (--kernel-trace --stats)", "",
+            "| group | calls | avg us | total ms |", "|---|---:|---:|---:|"]
+    for label, rx in GROUPS:
+        ns = match(stats, rx)
+        if not ns:
+            continue
+        calls = sum(stats[n][0] for n in ns)
+        tot = sum(stats[n][1] for n in ns)
+        out.append(f"| {label} | {calls} | {tot / calls / 1e3:.2f} | {tot / 1e6:.3f} |")
+    out.append("")
+
+    traffic = {}
+    if a.fetch and a.write:
+        fetch, write = read_counter(a.fetch), read_counter(a.write)
+        copy_bytes = a.copy_mib << 20
+        fc = [v for n in match(fetch, COPY_RE) for v in fetch[n]]
+        wc = [v for n in match(write, COPY_RE) for v in write[n]]
+        if not fc or not wc:
+            print("copy probe kernel not found in the counter runs", file=sys.stderr)
+            return 1
+        f_scale = copy_bytes / (sum(fc) / len(fc))   # bytes per unit of FETCH_SIZE
+        w_scale = copy_bytes / (sum(wc) / len(wc))
+        out += ["## HBM traffic per dispatch (--pmc FETCH_SIZE, --pmc WRITE_SIZE)", "",
+                f"Calibration: an elementwise copy of {a.copy_mib} MiB reads FETCH_SIZE "
+                f"{sum(fc) / len(fc):.1f} and WRITE_SIZE {sum(wc) / len(wc):.1f}; scale factors "
+                f"{f_scale / 1024:.3f} KiB per FETCH_SIZE unit, {w_scale / 1024:.3f} KiB per "
+                f"WRITE_SIZE unit.", "",
+                "| group | dispatches | read MB | written MB | total MB |", "|---|---:|---:|---:|---:|"]
+        for label, rx in GROUPS:
+            fv = [v for n in match(fetch, rx) for v in fetch[n]]
+            wv = [v for n in match(write, rx) for v in write[n]]
+            if not fv or not wv:
+                continue
+            rd = sum(fv) / len(fv) * f_scale
+            wr = sum(wv) / len(wv) * w_scale
+            out.append(f"| {label} | {len(fv)} | {rd / 1e6:.2f} | {wr / 1e6:.2f} | "
+                       f"{(rd + wr) / 1e6:.2f} |")
+            traffic[label] = {"read_bytes": rd, "write_bytes": wr, "bytes_per_launch": rd + wr}
+        out.append("")
+    with open(a.md, "w") as f:
+        f.write("\n".join(out) + "\n")
+    if a.json and traffic:
+        doc = {"workload": a.workload,
+               "gemm_w8a16": traffic.get("proj_gemm_w8a16"),
+               "lm_head": traffic.get("lm_head (fp16, ARGMAX, norm-on-load)"),
+               "attention": traffic.get("block attention")}
+        with open(a.json, "w") as f:
+            json.dump(doc, f, indent=1)
+            f.write("\n")
+    print("\n".join(out))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
