@@ -4,8 +4,10 @@ Every tensor gets its own generator, seeded from ``(seed, crc32(name))``, so a
 tensor's values do not depend on which other tensors were generated or in what
 order.  Two back-ends produce tensors of identical shapes and distributions:
 
-* ``numpy``  - ``numpy.random.default_rng([seed, crc32(name)])`` (PCG64).  Portable
-  and bit-reproducible; used for every shape that the CPU oracle also runs.
+* ``numpy``  - ``numpy.random.default_rng([seed, crc32(name)])`` (PCG64), or
+  ``[seed, crc32(name), b]`` for row block b of a tensor above 4 Mi elements.  Portable
+  and bit-reproducible (independent of the thread count used to fill it); used for
+  every shape that the CPU oracle also runs.
 * ``torch``  - ``torch.Generator`` on the target device, seeded with
   ``seed * 2**32 + crc32(name)``.  Used for the full-size benchmark shapes, where
   generating ~2.5 G samples on the host would dominate the run.  Its values differ
@@ -22,6 +24,7 @@ Tensor names follow the module attributes of the reference draft model
 
 from __future__ import annotations
 
+import os
 import zlib
 from typing import Dict, Iterator, Tuple
 
@@ -75,27 +78,66 @@ def weight_specs(cfg: DFlashConfig, n_feat: int = None, with_vocab: bool = True
         yield "lm_head.weight", (cfg.vocab_size, H), "f16"
 
 
-def np_normal(seed: int, name: str, shape, std: float = 1.0, dtype=np.float32) -> np.ndarray:
-    rng = np.random.default_rng([seed, _crc(name)])
-    x = rng.standard_normal(shape, dtype=np.float32)
+# Tensors above CHUNK_ELEMS elements are generated in row blocks of about that many
+# elements, block b from default_rng([seed, crc32(name), b]), so that large tensors can be
+# filled by several threads with a result that does not depend on the thread count.
+CHUNK_ELEMS = 1 << 22
+
+
+def _row_blocks(shape):
+    n = int(np.prod(shape))
+    if n <= CHUNK_ELEMS or len(shape) < 2:
+        return None
+    row = int(np.prod(shape[1:]))
+    rows = max(1, CHUNK_ELEMS // row)
+    return [(r0, min(shape[0], r0 + rows)) for r0 in range(0, shape[0], rows)]
+
+
+def _fill_normal(out, seed_seq, std):
+    rng = np.random.default_rng(seed_seq)
+    x = rng.standard_normal(out.shape, dtype=np.float32)
     if std != 1.0:
         x *= np.float32(std)
-    return x.astype(dtype, copy=False)
+    out[...] = x
+
+
+def _normal_jobs(seed: int, name: str, out: np.ndarray, std: float):
+    blocks = _row_blocks(out.shape)
+    if blocks is None:
+        return [(out, [seed, _crc(name)], std)]
+    return [(out[r0:r1], [seed, _crc(name), b], std) for b, (r0, r1) in enumerate(blocks)]
+
+
+def _run_jobs(jobs, threads=None):
+    from concurrent.futures import ThreadPoolExecutor
+    threads = threads or min(16, os.cpu_count() or 1)
+    if threads <= 1 or len(jobs) <= 1:
+        for j in jobs:
+            _fill_normal(*j)
+        return
+    with ThreadPoolExecutor(threads) as ex:
+        list(ex.map(lambda j: _fill_normal(*j), jobs))
+
+
+def np_normal(seed: int, name: str, shape, std: float = 1.0, dtype=np.float32) -> np.ndarray:
+    out = np.empty(shape, dtype=dtype)
+    _run_jobs(_normal_jobs(seed, name, out, std))
+    return out
 
 
 def make_weights_numpy(cfg: DFlashConfig, seed: int = 0, n_feat: int = None,
                        with_vocab: bool = True, with_fc: bool = True) -> Dict[str, np.ndarray]:
     """All draft tensors as numpy arrays (proj fp32, the rest fp16)."""
-    out = {}
+    out, jobs = {}, []
     for name, shape, kind in weight_specs(cfg, n_feat, with_vocab):
         if name == "fc.weight" and not with_fc:
             continue
         if kind == "ones":
             out[name] = np.ones(shape, dtype=np.float16)
-        elif kind == "f16":
-            out[name] = np_normal(seed, name, shape, 0.02, np.float16)
-        else:
-            out[name] = np_normal(seed, name, shape, 0.02, np.float32)
+            continue
+        out[name] = np.empty(shape, dtype=np.float16 if kind == "f16" else np.float32)
+        jobs += _normal_jobs(seed, name, out[name], 0.02)
+    _run_jobs(jobs)
     return out
 
 

@@ -1,0 +1,109 @@
+"""Write the golden fixtures of the draft forward (run on the CPU, from the repo root):
+
+    python tests/golden/make_golden.py [case ...]
+
+Each fixture holds the oracle's outputs for one named workload on the seeded synthetic
+inputs of ``mirror_sd_amd.synth`` (numpy back-end), plus crc32 digests of those inputs
+so a test can tell a change of the input recipe from a change of the results:
+
+  qwen3_4b_layer  1 layer, H2560, 32/8 heads, FFN 9728, block 16, context 64, inputs
+                  already fused (noise [16, 2560], context [64, 2560]); output the
+                  final-normed hidden [16, 2560] and the residual stream before it.
+  qwen3_8b_draft  5 layers, H4096, 32/8, FFN 12288, block 16, context 2048, fc fusion of
+                  5 x 4096 features, V151936; outputs hidden [16, 4096], argmax ids [16],
+                  the top-2 logits per row.
+  dflash_27b      5 layers, H5120, 40/8, FFN 17408, block 32, context 4096, V151936;
+                  same outputs for 32 rows.
+
+The oracle runs in its fp16-boundary mode (the MLX rounding points) with fp32
+accumulation for the two full models, fp64 for the single layer.
+"""
+
+from __future__ import annotations
+
+import os
+import sys
+import time
+import zlib
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "mirror-sd_amd"))
+
+from mirror_sd_amd import synth  # noqa: E402
+from mirror_sd_amd.config import workload  # noqa: E402
+from oracle import dflash_oracle as O  # noqa: E402
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+DIGEST_BYTES = 1 << 20
+
+
+def digest(a: np.ndarray) -> int:
+    """crc32 of the first MiB of the array's bytes, mixed with its shape and dtype."""
+    b = np.ascontiguousarray(a).view(np.uint8).ravel()[:DIGEST_BYTES].tobytes()
+    return zlib.crc32(f"{a.shape}{a.dtype}".encode() + b) & 0xFFFFFFFF
+
+
+def input_digests(tensors, inp):
+    names = sorted(tensors)
+    d = {f"w:{n}": digest(tensors[n]) for n in names}
+    d.update({f"in:{k}": digest(v) for k, v in inp.items()})
+    return d
+
+
+def top2(logits):
+    idx = np.argsort(-logits, axis=-1, kind="stable")[:, :2].astype(np.int32)
+    val = np.take_along_axis(logits, idx, axis=-1).astype(np.float32)
+    return idx, val
+
+
+def case_layer(name="qwen3_4b_layer", seed=0):
+    wl = workload(name)
+    cfg = wl.cfg
+    t = synth.make_weights_numpy(cfg, seed=seed, with_vocab=False, with_fc=False)
+    inp = synth.make_inputs_numpy(cfg, wl.block, wl.ctx, seed=seed, fused_context=True)
+    W = O.OracleWeights(cfg, t)
+    out, pre = O.draft_forward(W, inp["noise"], inp["context"], fp16=True, fused_context=True,
+                               return_prenorm=True)
+    return dict(hidden=out.astype(np.float16), prenorm=pre.astype(np.float16)), \
+        input_digests(t, inp)
+
+
+def case_full(name, seed=0):
+    wl = workload(name)
+    cfg = wl.cfg
+    t = synth.make_weights_numpy(cfg, seed=seed)
+    inp = synth.make_inputs_numpy(cfg, wl.block, wl.ctx, seed=seed)
+    dig = input_digests(t, inp)
+    W = O.OracleWeights(cfg, t)
+    del t
+    h, logits, ids = O.draft_block(W, inp["ids"], inp["target_hidden"], fp16=True,
+                                   dtype=np.float32)
+    ti, tv = top2(logits)
+    return dict(hidden=h.astype(np.float16), ids=ids.astype(np.int32), top2_idx=ti,
+                top2_val=tv), dig
+
+
+CASES = {
+    "qwen3_4b_layer": lambda: case_layer("qwen3_4b_layer"),
+    "qwen3_8b_draft": lambda: case_full("qwen3_8b_draft"),
+    "dflash_27b": lambda: case_full("dflash_27b"),
+}
+
+
+def main(argv):
+    names = argv or list(CASES)
+    for n in names:
+        t0 = time.time()
+        out, dig = CASES[n]()
+        keys = sorted(dig)
+        np.savez_compressed(os.path.join(HERE, f"{n}.npz"), **out,
+                            digest_names=np.array(keys), digest_values=np.array(
+                                [dig[k] for k in keys], dtype=np.uint32))
+        print(f"{n}: {time.time() - t0:.1f} s, outputs {sorted(out)}", flush=True)
+
+
+if __name__ == "__main__":
+    main(sys.argv[1:])
