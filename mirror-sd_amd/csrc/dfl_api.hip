@@ -96,8 +96,7 @@ struct dfl_ctx {
   float* rnorm = nullptr;        // [Bmax] 1/rms of the residual rows
   float* sk_ws = nullptr;        // split-tile partials
   int* sk_tile_cnt = nullptr;    // [max tiles]
-  float* sk_ss = nullptr;        // [max tiles][32]
-  int* sk_done = nullptr;        // [1]
+  float* sk_ss = nullptr;        // [m-tiles][H/64][32] row sums of squares of x (RESID output)
   SKPlan sk_qkv, sk_o, sk_gu, sk_down, sk_lm;
   float* ss_part = nullptr;   // [rows][ceil(H/1024)] per-chunk sums of squares
   int* row_cnt = nullptr;     // [rows] arrival counters of the reduce kernel
@@ -262,7 +261,7 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
     const size_t bm32 = ((Bm + 31) / 32) * 32;
     if ((r = x->alloc(&x->qkvbuf, Bm * x->NQKV)) || (r = x->alloc(&x->rnorm, bm32)) ||
         (r = x->alloc(&x->sk_ws, wsn)) || (r = x->alloc(&x->sk_tile_cnt, tiles, true)) ||
-        (r = x->alloc(&x->sk_ss, tiles * 32)) || (r = x->alloc(&x->sk_done, 1, true))) {
+        (r = x->alloc(&x->sk_ss, (bm32 / 32) * (size_t)(x->H / 64) * 32))) {
       delete x;
       return r;
     }
@@ -401,13 +400,16 @@ static void gemm(dfl_ctx* ctx, int cat, int wt, int epi, const uint4* W, const h
   launch_skinny_gemm(wt, epi, a, p.SK, (M + 31) / 32, st);
 }
 
-// Stream-K GEMM over the M rows of a block, in 32-row m-tiles.
+// Stream-K GEMM over the M rows of a block, in 32-row m-tiles.  A normed input (gnorm
+// set) takes its 1/rms rows from the embedding kernel (rn_from_ss false) or from the row
+// sums of squares that the previous RESID GEMM left in sk_ss (rn_from_ss true).
 static void skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const SKPlan& p,
                    const uint4* W, const half_t* scale, int N, int KB, const half_t* X, int ldx,
-                   int M, const half_t* gnorm, half_t* out, int ldo, half_t* xres,
-                   float* logits, unsigned long long* keys, hipStream_t st) {
+                   int M, const half_t* gnorm, bool rn_from_ss, half_t* out, int ldo,
+                   half_t* xres, float* logits, unsigned long long* keys, hipStream_t st) {
   const long long wbytes = (wt == WT_INT8) ? (long long)N * KB * 32 + 2LL * N
                                            : (long long)N * KB * 16 * 2;
+  const size_t ss_stride = (size_t)(ctx->H / 64) * 32;
   for (int m0 = 0; m0 < M; m0 += 32) {
     ProfScope ps(ctx, cat, wbytes, st, /*attached=*/true);
     StreamArgs a{};
@@ -419,6 +421,9 @@ static void skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const SKPlan& p,
     a.ldx = ldx;
     a.M = std::min(32, M - m0);
     a.rnorm = ctx->rnorm + m0;
+    a.ss_in = rn_from_ss ? ctx->sk_ss + (m0 / 32) * ss_stride : nullptr;
+    a.ss_tiles = ctx->H / 64;
+    a.ss_n = ctx->H;
     a.gnorm = gnorm;
     a.ws = ctx->sk_ws;
     a.seg_cap = p.seg_cap;
@@ -426,9 +431,7 @@ static void skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const SKPlan& p,
     a.out = out ? out + (size_t)m0 * ldo : nullptr;
     a.ldo = ldo;
     a.x = xres ? xres + (size_t)m0 * ldo : nullptr;
-    a.ss_part = ctx->sk_ss;
-    a.done_cnt = ctx->sk_done;
-    a.rnorm_out = ctx->rnorm + m0;
+    a.ss_part = ctx->sk_ss + (m0 / 32) * ss_stride;
     a.eps = ctx->cfg.rms_eps;
     a.logits = logits ? logits + (size_t)m0 * N : nullptr;
     a.ldl = N;
@@ -561,19 +564,20 @@ int dfl_draft_block(dfl_ctx* ctx, const uint16_t* noise_emb, const int32_t* ids,
 
   const int L = ctx->len + B;
   const int ratio = NH / NKV;
-  const int n_qt = (ratio * B + 31) / 32;
-  int n_chunks = std::max(1, 1024 / (NKV * n_qt));
-  n_chunks = std::min(n_chunks, std::min(MAX_CHUNKS, (L + 63) / 64));
-  n_chunks = std::max(n_chunks, 1);
-  int chunk = (L + n_chunks - 1) / n_chunks;
-  chunk = ((chunk + 31) / 32) * 32;
-  n_chunks = (L + chunk - 1) / chunk;
+  // Attention key split: about one workgroup per CU ((chunks x KV heads) ~ CUs) with
+  // chunks of at most 160 keys (one LDS stage) while there are at most MAX_CHUNKS.
+  const int kblocks = (L + 31) / 32;
+  const int n_split = std::max(1, std::min(std::min(MAX_CHUNKS, kblocks),
+                                            std::max((kblocks + 4) / 5, (ctx->n_cu + NKV - 1) / NKV)));
+  const int chunk = ((kblocks + n_split - 1) / n_split) * 32;
+  const int n_chunks = (L + chunk - 1) / chunk;
 
   for (int l = 0; l < ctx->active; ++l) {
     Layer& Ly = ctx->layers[l];
     // q|k|v = input_layernorm(x) @ [Wq; Wk; Wv]^T  (fp16 out)
     skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_STORE, ctx->sk_qkv, Ly.w_qkv, Ly.s_qkv, ctx->NQKV, H / 32,
-           ctx->x, H, B, Ly.in_norm, ctx->qkvbuf, ctx->NQKV, nullptr, nullptr, nullptr, st);
+           ctx->x, H, B, Ly.in_norm, /*rn_from_ss=*/l > 0, ctx->qkvbuf, ctx->NQKV, nullptr,
+           nullptr, nullptr, st);
     QKRopeArgs q{};
     q.qkv16 = ctx->qkvbuf;
     q.ws = nullptr;
@@ -621,19 +625,19 @@ int dfl_draft_block(dfl_ctx* ctx, const uint16_t* noise_emb, const int32_t* ids,
       ProfScope ps(ctx, P_ATTN, 2LL * NKV * L * 128 * 2, st);
       launch_block_attention(at, st);
     }
-    // x += attn @ Wo^T ; rnorm = 1/rms(x)
+    // x += attn @ Wo^T ; per-tile row sums of squares of x -> sk_ss
     skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_RESID, ctx->sk_o, Ly.w_o, Ly.s_o, H, NQ / 32, ctx->attn,
-           NQ, B, nullptr, nullptr, H, ctx->x, nullptr, nullptr, st);
+           NQ, B, nullptr, false, nullptr, H, ctx->x, nullptr, nullptr, st);
     // act = silu(gate(post_norm(x))) * up(post_norm(x))
     skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_SWIGLU, ctx->sk_gu, Ly.w_gu, Ly.s_gu, 2 * F, H / 32,
-           ctx->x, H, B, Ly.post_norm, ctx->act, F, nullptr, nullptr, nullptr, st);
-    // x += act @ Wdown^T ; rnorm = 1/rms(x)
+           ctx->x, H, B, Ly.post_norm, true, ctx->act, F, nullptr, nullptr, nullptr, st);
+    // x += act @ Wdown^T ; per-tile row sums of squares of x -> sk_ss
     skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_RESID, ctx->sk_down, Ly.w_down, Ly.s_down, H, F / 32,
-           ctx->act, F, B, nullptr, nullptr, H, ctx->x, nullptr, nullptr, st);
+           ctx->act, F, B, nullptr, false, nullptr, H, ctx->x, nullptr, nullptr, st);
   }
   if (out_logits || out_ids) {
     skgemm(ctx, P_LM_HEAD, WT_F16, EPI_ARGMAX, ctx->sk_lm, ctx->w_lm, nullptr, ctx->V, H / 16,
-           ctx->x, H, B, ctx->final_norm, nullptr, 0, nullptr, out_logits,
+           ctx->x, H, B, ctx->final_norm, true, nullptr, 0, nullptr, out_logits,
            out_ids ? ctx->keys : nullptr, st);
     if (out_ids) {
       ProfScope ps(ctx, P_ROWS, 0, st);
@@ -642,7 +646,7 @@ int dfl_draft_block(dfl_ctx* ctx, const uint16_t* noise_emb, const int32_t* ids,
   }
   if (out_hidden) {
     ProfScope ps(ctx, P_ROWS, 0, st);
-    launch_apply_norm(ctx->x, ctx->rnorm, ctx->final_norm, B, H,
+    launch_apply_norm(ctx->x, ctx->sk_ss, H / 64, ctx->cfg.rms_eps, ctx->final_norm, B, H,
                       reinterpret_cast<half_t*>(out_hidden), st);
   }
   if (out_prenorm) {

@@ -5,36 +5,72 @@
 // Data layout: Q [NH][B][128] (the ratio*B query rows of one KV head are contiguous),
 // K cache [NKV][cap][128], V cache transposed Vt [NKV][128][cap].
 //
-// One wave handles (key chunk, KV head, 32-row query tile):
+// Work split.  The keys are cut into chunks of <= 160 per split so that (splits x KV
+// heads) workgroups cover the CUs in one round.  One workgroup handles (chunk, KV head,
+// group of query tiles): its K and V are read from HBM once, through LDS, and shared by
+// every query head of the KV head.  Each 32-row query tile gets KW waves that take the
+// chunk's 32-key blocks round-robin; their (max, sum, O) states are merged in LDS at the
+// end, so one fp32 partial per (chunk, row) goes to the merge kernel.
+//
+// LDS stage (up to 5 key blocks): per block, K rows [32 keys][256 B] and Vt rows
+// [128 d][64 B], filled with direct global->LDS loads (global_load_lds_dwordx4, one wave
+// instruction = 1 KiB).  The 16-byte chunks of each row are XOR-swizzled so the MFMA
+// fragment reads below hit distinct banks (for 32- and 64-bank LDS alike).
+//
+// Per wave and 32-key block:
 //   S^T = K * Q^T   with v_mfma_f32_32x32x16_f16, keys on the MFMA M-axis;
-//   online softmax per query column (16 keys per lane + 16 in lane^32), fp32, log2 domain;
+//   softmax per query column (16 keys per lane + 16 in lane^32), fp32, log2 domain, with
+//   a lazily updated reference max (rescale only when a block's max exceeds it by > 8,
+//   so p <= 2^8, exact in the merge algebra);
 //   O^T += Vt * P   with P fed straight from the S^T accumulators converted to fp16.
-// K rows are loaded in a permuted order so that accumulator r of lane (q, g) holds key
+// K rows are read in a permuted order so that accumulator r of lane (q, g) holds key
 // 8g + r (r < 8) or 16 + 8g + (r - 8); those are exactly the 8-key groups the PV MFMA
-// needs as its B fragment, so P never goes through LDS.  A merge kernel combines the
-// chunk partials with their (max, sum) statistics.
+// needs as its B fragment, so P never goes through LDS.
 #include "dfl_common.h"
 #include "dfl_kernels.h"
 
+#include <algorithm>
+
 namespace dfl {
 
-__global__ __launch_bounds__(64) void block_attn_kernel(AttnArgs a) {
-  const int c = blockIdx.x, g = blockIdx.y, qt = blockIdx.z;
-  const int lane = threadIdx.x;
+namespace {
+
+constexpr int AT_STAGE_BLOCKS = 5;              // 32-key blocks per LDS stage
+constexpr int AT_KBLK = 32 * 256;               // K rows of one key block (bytes)
+constexpr int AT_VBLK = 128 * 64;               // Vt rows of one key block (bytes)
+constexpr int AT_STAGE_BYTES = AT_STAGE_BLOCKS * (AT_KBLK + AT_VBLK);
+constexpr int AT_PART_BYTES = (64 * 64 + 2 * 64) * 4;   // one wave's O accumulators + (m, l)
+constexpr float AT_RESCALE = 8.f;               // log2 slack of the lazy reference max
+
+// chunk slot of 16-byte chunk c in K row r (16 chunks per 256-byte row)
+DFL_DEV int kswz(int r) { return (r & 3) | (((r >> 3) & 1) << 2) | (((r >> 2) & 1) << 3); }
+// chunk slot of chunk c (8 keys) in Vt row d of a key block (4 chunks per 64-byte row)
+DFL_DEV int vswz(int d) { return ((d >> 1) & 3) ^ ((d >> 3) & 1); }
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+}  // namespace
+
+__global__ __launch_bounds__(768) void block_attn_kernel(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
+  const int c = blockIdx.x, g = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int KW = a.kw;
+  const int qtl = wv / KW, kwi = wv - qtl * KW;        // query tile in group, key lane
+  const int qt = blockIdx.z * a.q_per_group + qtl;
   const int q = lane & 31, gg = lane >> 5;
   const int ratio = a.NH / a.NKV;
   const int R = ratio * a.B;
   const int rq = qt * 32 + q;
   const bool row_ok = rq < R;
 
-  // Q fragments: step st covers d = 64*gg + 8*st + 0..7.
+  // Q fragments (step st covers d = 64*gg + 8*st + 0..7), loaded after the first
+  // stage's K/V loads are issued so the two latencies overlap.
   half8_t qf[8];
-  {
-    const uint4* qp = reinterpret_cast<const uint4*>(a.Q + ((size_t)g * R + (row_ok ? rq : 0)) * 128 +
-                                                     64 * gg);
-#pragma unroll
-    for (int st = 0; st < 8; ++st) qf[st] = as_half8(qp[st]);   // rows >= R: never stored
-  }
+  bool have_q = false;
+  const uint4* qp = reinterpret_cast<const uint4*>(a.Q + ((size_t)g * R + (row_ok ? rq : 0)) * 128 +
+                                                   64 * gg);   // rows >= R: never stored
 
   const int k_begin = c * a.chunk;
   const int k_end = min(a.L, k_begin + a.chunk);
@@ -42,72 +78,129 @@ __global__ __launch_bounds__(64) void block_attn_kernel(AttnArgs a) {
   // Permuted key row supplied by this lane as MFMA A row i = lane % 32.
   const int i = lane & 31;
   const int koff = 16 * (i >> 4) + 8 * ((i >> 2) & 1) + 4 * ((i >> 3) & 1) + (i & 3);
+  const int kxor = kswz(koff);
+  const int vrow = lane & 31;
 
   float mrun = -INFINITY, lrun = 0.f;
   floatx16 o[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) o[dt] = (floatx16){};
 
-  const half_t* kbase = a.Kc + (size_t)g * a.cap * 128 + 64 * gg;
-  const half_t* vbase = a.Vt + (size_t)g * 128 * a.cap + 8 * gg + (size_t)(lane & 31) * a.cap;
+  const half_t* kg = a.Kc + (size_t)g * a.cap * 128;
+  const half_t* vg = a.Vt + (size_t)g * 128 * a.cap;
+  const int vlast = (a.L - 1) & ~7;   // last 8-key group holding a valid key
 
-  // K fragment of a 32-key block: this lane's key row (clamped into the chunk so the
-  // address is valid; out-of-chunk keys are masked to -inf after the MFMA).
-  auto load_k = [&](u32x4 (&kf)[8], int kb) {
-    const int key = min(kb + koff, k_end - 1);
-    const half_t* kp = kbase + (size_t)key * 128;
-    static_for<0, 8>([&](auto st) { kf[st] = load_vec(kp + 8 * st); });
-  };
-  // V fragments (transposed cache): rows d = dt*32 + lane%32, keys kb + 8*gg + 0..7 and
-  // kb + 16 + 8*gg + 0..7.  Keys past L hold finite data (zero-initialised cache) and
-  // meet p = 0.
-  auto load_v = [&](u32x4 (&vf)[8], int kb) {
-    static_for<0, 4>([&](auto dt) {
-      const half_t* vp = vbase + (size_t)dt * 32 * a.cap + kb;
-      vf[2 * dt] = load_vec(vp);
-      vf[2 * dt + 1] = load_vec(vp + 16);
-    });
-  };
+  for (int k0 = k_begin; k0 < k_end; k0 += 32 * AT_STAGE_BLOCKS) {
+    const int nblk = min(AT_STAGE_BLOCKS, (k_end - k0 + 31) >> 5);
+    // 16 segments per key block: 8 for K (4 key rows each), 8 for Vt (16 d rows each).
+    // Keys past L are clamped to valid addresses; they are masked (K) or meet p = 0 (V).
+    for (int sgi = wv; sgi < 16 * nblk; sgi += nw) {
+      const int j = sgi >> 4, s = sgi & 15;
+      const half_t* src;
+      unsigned char* dst;
+      if (s < 8) {
+        const int r = 4 * s + (lane >> 4);                        // key row in the block
+        const int cc = (lane & 15) ^ kswz(r);
+        const int key = min(k0 + 32 * j + r, a.L - 1);
+        src = kg + (size_t)key * 128 + cc * 8;
+        dst = lds + j * AT_KBLK + s * 1024;
+      } else {
+        const int d = 16 * (s - 8) + (lane >> 2);
+        const int cc = (lane & 3) ^ vswz(d);
+        src = vg + (size_t)d * a.cap + min(k0 + 32 * j + 8 * cc, vlast);
+        dst = lds + AT_STAGE_BLOCKS * AT_KBLK + j * AT_VBLK + (s - 8) * 1024;
+      }
+      __builtin_amdgcn_global_load_lds((const void*)src, (lds_ptr_t)dst, 16, 0, 0);
+    }
+    if (!have_q) {
+#pragma unroll
+      for (int st = 0; st < 8; ++st) qf[st] = as_half8(qp[st]);
+      have_q = true;
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
 
-  u32x4 kcur[8], knext[8], vcur[8];
-  load_k(kcur, k_begin);
-  for (int kb = k_begin; kb < k_end; kb += 32) {
-    load_v(vcur, kb);
-    const bool more = kb + 32 < k_end;
-    load_k(knext, more ? kb + 32 : kb);
-    __builtin_amdgcn_sched_barrier(0);
-    floatx16 s = {};
-    static_for<0, 8>([&](auto st) { s = mfma32x32x16(as_half8(kcur[st]), qf[st], s); });
-    // Accumulator r holds key kb + (r < 8 ? 8*gg + r : 16 + 8*gg + r - 8).
-    float v[16];
-    float bmax = -INFINITY;
+    for (int j = kwi; j < nblk; j += KW) {
+      const unsigned char* kb_lds = lds + j * AT_KBLK + koff * 256;
+      const unsigned char* vb_lds = lds + AT_STAGE_BLOCKS * AT_KBLK + j * AT_VBLK;
+      floatx16 s = {};
+      static_for<0, 8>([&](auto st) {
+        const u32x4 kf =
+            *reinterpret_cast<const u32x4*>(kb_lds + (((8 * gg + st) ^ kxor) << 4));
+        s = mfma32x32x16(as_half8(kf), qf[st], s);
+      });
+      // Accumulator r holds key kbase + (r < 8 ? 8*gg + r : 16 + 8*gg + r - 8).
+      const int kbase = k0 + 32 * j;
+      float v[16];
+      if (kbase + 32 <= k_end) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int kr = kb + (r < 8 ? 8 * gg + r : 16 + 8 * gg + (r - 8));
-      v[r] = kr < k_end ? s[r] * a.scale_log2 : -INFINITY;
-      bmax = fmaxf(bmax, v[r]);
-    }
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-    const float mnew = fmaxf(mrun, bmax);
-    const float alpha = exp2f(mrun - mnew);
-    float psum = 0.f;
-    half8_t p1, p2;
+        for (int r = 0; r < 16; ++r) v[r] = s[r] * a.scale_log2;
+      } else {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float p = exp2f(v[r] - mnew);
-      const half_t ph = f2h(p);
-      psum += h2f(ph);
-      if (r < 8) p1[r] = ph; else p2[r - 8] = ph;
+        for (int r = 0; r < 16; ++r) {
+          const int kr = kbase + (r < 8 ? 8 * gg + r : 16 + 8 * gg + (r - 8));
+          v[r] = kr < k_end ? s[r] * a.scale_log2 : -INFINITY;
+        }
+      }
+      float bmax = v[0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) bmax = fmaxf(bmax, v[r]);
+      bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+      if (!__all(bmax <= mrun + AT_RESCALE)) {
+        const float mnew = bmax > mrun + AT_RESCALE ? bmax : mrun;
+        const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);
+        lrun *= alpha;
+        static_for<0, 4>([&](auto dt) { o[dt] *= alpha; });
+        mrun = mnew;
+      }
+      float psum = 0.f;
+      half8_t p1, p2;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const half_t ph = f2h(__builtin_amdgcn_exp2f(v[r] - mrun));
+        psum += h2f(ph);
+        if (r < 8) p1[r] = ph; else p2[r - 8] = ph;
+      }
+      lrun += psum + __shfl_xor(psum, 32, 64);
+      static_for<0, 4>([&](auto dt) {
+        const unsigned char* vr = vb_lds + (dt * 32 + vrow) * 64;
+        const int vx = vswz(dt * 32 + vrow);
+        const u32x4 v1 = *reinterpret_cast<const u32x4*>(vr + ((gg ^ vx) << 4));
+        const u32x4 v2 = *reinterpret_cast<const u32x4*>(vr + (((gg + 2) ^ vx) << 4));
+        o[dt] = mfma32x32x16(as_half8(v1), p1, o[dt]);
+        o[dt] = mfma32x32x16(as_half8(v2), p2, o[dt]);
+      });
     }
-    psum += __shfl_xor(psum, 32, 64);
-    lrun = lrun * alpha + psum;
-    mrun = mnew;
-    static_for<0, 4>([&](auto dt) {
-      o[dt] *= alpha;
-      o[dt] = mfma32x32x16(as_half8(vcur[2 * dt]), p1, o[dt]);
-      o[dt] = mfma32x32x16(as_half8(vcur[2 * dt + 1]), p2, o[dt]);
-    });
-    static_for<0, 8>([&](auto st) { kcur[st] = knext[st]; });
+    __syncthreads();   // the stage buffer is reused by the next stage (or the merge)
+  }
+
+  // Merge the KW key lanes of each query tile (fixed order), then store the partial.
+  if (KW > 1) {
+    float* part = reinterpret_cast<float*>(lds) + (size_t)(qtl * (KW - 1)) * (AT_PART_BYTES / 4);
+    if (kwi > 0) {
+      float* my = part + (size_t)(kwi - 1) * (AT_PART_BYTES / 4);
+      static_for<0, 4>([&](auto dt) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) my[(dt * 16 + r) * 64 + lane] = o[dt][r];
+      });
+      my[64 * 64 + lane] = mrun;
+      my[64 * 64 + 64 + lane] = lrun;
+    }
+    __syncthreads();
+    if (kwi > 0) return;
+    for (int w = 0; w < KW - 1; ++w) {
+      const float* ot = part + (size_t)w * (AT_PART_BYTES / 4);
+      const float m2 = ot[64 * 64 + lane], l2 = ot[64 * 64 + 64 + lane];
+      const float mn = fmaxf(mrun, m2);
+      if (mn == -INFINITY) continue;
+      const float a1 = __builtin_amdgcn_exp2f(mrun - mn), a2 = __builtin_amdgcn_exp2f(m2 - mn);
+      static_for<0, 4>([&](auto dt) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][r] = o[dt][r] * a1 + ot[(dt * 16 + r) * 64 + lane] * a2;
+      });
+      lrun = lrun * a1 + l2 * a2;
+      mrun = mn;
+    }
   }
 
   if (!row_ok) return;
@@ -161,10 +254,20 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(AttnArgs a) {
   a.O[afl_index(b, h * 128 + d, a.NH * 128)] = f2h(num / den_s);
 }
 
-void launch_block_attention(const AttnArgs& a, hipStream_t st) {
+void launch_block_attention(const AttnArgs& a_in, hipStream_t st) {
+  AttnArgs a = a_in;
   const int R = (a.NH / a.NKV) * a.B;
-  dim3 grid(a.n_chunks, a.NKV, (R + 31) / 32);
-  hipLaunchKernelGGL(block_attn_kernel, grid, dim3(64), 0, st, a);
+  const int n_qt = (R + 31) / 32;
+  a.q_per_group = std::min(n_qt, 8);
+  // Extra waves per query tile only where the tiles alone leave the CU short of waves;
+  // each takes at least one key block of the chunk.
+  const int cblocks = a.chunk / 32;
+  a.kw = a.q_per_group >= 3 ? 1 : std::max(1, std::min(std::min(4, cblocks), 12 / a.q_per_group));
+  const int groups = (n_qt + a.q_per_group - 1) / a.q_per_group;
+  const int merge_bytes = a.q_per_group * (a.kw - 1) * AT_PART_BYTES;
+  const int lds_bytes = std::max(AT_STAGE_BYTES, merge_bytes);
+  hipLaunchKernelGGL(block_attn_kernel, dim3(a.n_chunks, a.NKV, groups),
+                     dim3(64 * a.q_per_group * a.kw), lds_bytes, st, a);
   hipLaunchKernelGGL(attn_merge_kernel, dim3(a.NH * a.B), dim3(128), 0, st, a);
 }
 

@@ -38,7 +38,9 @@ struct StreamArgs {
   int N, KB;                // KB = K/32 (int8) or K/16 (fp16)
   const half_t* X;          // activations: one 32-row tile in the fragment layout (afl_offset)
   int ldx, M;
-  const float* rnorm;       // NORM: per-row 1/rms of X
+  const float* rnorm;       // NORM: per-row 1/rms of X (used when ss_in is null)
+  const float* ss_in;       // NORM: [ss_tiles][32] row sums of squares of X (RESID output)
+  int ss_tiles, ss_n;       //       tiles of ss_in, and the row length they sum over
   const half_t* gnorm;      // NORM: [K] gain (K <= 8192)
   float* ws;                // [N/64][seg_cap][2048] partials of tiles split across workgroups
   int seg_cap;
@@ -46,17 +48,14 @@ struct StreamArgs {
   half_t* out;              // STORE: row-major [M][ldo] fp16; SWIGLU: fragment-layout tile [32][N/2]
   int ldo;
   half_t* x;                // RESID: residual stream, fragment-layout tile [32][N], updated in place
-  float* ss_part;           // RESID: [N/64][32] per-tile row sums of squares
-  int* done_cnt;            // RESID: launch-wide tile counter (zero-initialised)
-  float* rnorm_out;         // RESID: [M] 1/rms of the updated rows
+  float* ss_part;           // RESID: [N/64][32] per-tile row sums of squares of the updated x
   float eps;
   float* logits;            // ARGMAX: optional [M][ldl] fp32
   int ldl;
   unsigned long long* keys; // ARGMAX: optional [M] packed (order(value) << 32 | ~index)
 };
 struct SKPlan {
-  bool wave_level = false;  // independent waves (4 per 256-thread workgroup) or 8-wave workgroups
-  int workers = 1;          // waves (wave-level) or workgroups (workgroup-level)
+  int workers = 1;          // workgroups (one per CU)
   int seg_cap = 1;          // workspace slots per tile
 };
 SKPlan streamk_plan(int N, int KB, int n_cu);
@@ -84,9 +83,10 @@ void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* no
                        int H, int V, const half_t* g, float eps, half_t* x, half_t* h,
                        float* rnorm, int* err, hipStream_t st);
 // x in the activation fragment layout (afl_index) [M][N] -> row-major h [M][N]:
-// h = fp16(fp16(x * r[m]) * g[n])  (apply_norm), or a plain copy (afl_to_rows).
-void launch_apply_norm(const half_t* x, const float* r, const half_t* g, int M, int N, half_t* h,
-                       hipStream_t st);
+// h = fp16(fp16(x * r[m]) * g[n])  (apply_norm), or a plain copy (afl_to_rows).  r[m] =
+// 1/rms of row m from ss [M/32 m-tiles][ss_tiles][32] (row sums of squares per column tile).
+void launch_apply_norm(const half_t* x, const float* ss, int ss_tiles, float eps, const half_t* g,
+                       int M, int N, half_t* h, hipStream_t st);
 void launch_afl_to_rows(const half_t* x, int M, int N, half_t* h, hipStream_t st);
 // v = sum_s ws[s][m][n] (fixed order) * scale[n] -> fp16; with residual:
 // x[m][n] = fp16(x[m][n] + v), else the rounded v goes to x (or to xs when x is null);
@@ -124,6 +124,7 @@ struct AttnArgs {
   int B, NH, NKV, cap, L; // L = number of valid keys
   int chunk;              // keys per split (multiple of 32)
   int n_chunks;
+  int q_per_group, kw;    // set by the launcher: query tiles per workgroup, waves per tile
   float scale_log2;       // head_dim^-0.5 * log2(e)
   float* Op;              // [n_chunks][NH*B][128] unnormalised partial outputs
   float* Ml;              // [n_chunks][NH*B][2] running (max, sum) in log2 domain

@@ -61,34 +61,46 @@ void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* no
                      V, g, eps, x, h, rnorm, err);
 }
 
-// x (activation fragment layout, [M][N]) -> row-major h; with r/g set, h = RMSNorm(x) * g.
+// x (activation fragment layout, [M][N]) -> row-major h; with ss/g set, h = RMSNorm(x) * g
+// where 1/rms of row m comes from ss [M/32][ss_tiles][32] (per-column-tile sums of squares).
 __global__ __launch_bounds__(256) void afl_rows_kernel(const half_t* __restrict__ x,
-                                                       const float* __restrict__ r,
-                                                       const half_t* __restrict__ g, int N,
-                                                       half_t* __restrict__ h) {
+                                                       const float* __restrict__ ss, int ss_tiles,
+                                                       float eps, const half_t* __restrict__ g,
+                                                       int N, half_t* __restrict__ h) {
+  __shared__ float rr_s;
   const int m = blockIdx.y;
+  if (ss) {
+    if (threadIdx.x < 64) {
+      const float* sp = ss + (size_t)(m >> 5) * ss_tiles * 32 + (m & 31);
+      float tot = 0.f;
+      for (int t = threadIdx.x; t < ss_tiles; t += 64) tot += sp[(size_t)t * 32];
+      tot = wave_sum(tot);
+      if (threadIdx.x == 0) rr_s = 1.0f / sqrtf(tot / (float)N + eps);
+    }
+    __syncthreads();
+  }
   const int n = (blockIdx.x * 256 + threadIdx.x) * 4;
   if (n >= N) return;
   // 4 consecutive columns (n % 4 == 0) are 4 consecutive halves of one record
   const half4_t xv = *reinterpret_cast<const half4_t*>(x + afl_index(m, n, N));
   half4_t o = xv;
-  if (r) {
-    const float rr = r[m];
+  if (ss) {
+    const float rr = rr_s;
 #pragma unroll
     for (int j = 0; j < 4; ++j) o[j] = rms_out(h2f(xv[j]), rr, g[n + j]);
   }
   *reinterpret_cast<half4_t*>(h + (size_t)m * N + n) = o;
 }
 
-void launch_apply_norm(const half_t* x, const float* r, const half_t* g, int M, int N, half_t* h,
-                       hipStream_t st) {
-  hipLaunchKernelGGL(afl_rows_kernel, dim3((N / 4 + 255) / 256, M), dim3(256), 0, st, x, r, g, N,
-                     h);
+void launch_apply_norm(const half_t* x, const float* ss, int ss_tiles, float eps, const half_t* g,
+                       int M, int N, half_t* h, hipStream_t st) {
+  hipLaunchKernelGGL(afl_rows_kernel, dim3((N / 4 + 255) / 256, M), dim3(256), 0, st, x, ss,
+                     ss_tiles, eps, g, N, h);
 }
 
 void launch_afl_to_rows(const half_t* x, int M, int N, half_t* h, hipStream_t st) {
   hipLaunchKernelGGL(afl_rows_kernel, dim3((N / 4 + 255) / 256, M), dim3(256), 0, st, x, nullptr,
-                     nullptr, N, h);
+                     0, 0.f, nullptr, N, h);
 }
 
 // Split-K reduction + residual + RMSNorm, parallel over (column chunk, row).

@@ -6,29 +6,28 @@
 // residual and SwiGLU epilogues write their outputs in the same layout.
 //
 // Partition.  The packed weight matrix (block layout: see dfl_gemm.hip) is a sequence of
-// U = (N/64) * KB work units (one 64-row wave-tile x one k-block), tile-major.  Workers
-// take equal contiguous unit ranges, so every CU streams the same number of bytes and
-// there is no second-round tail.  Two granularities:
-//   * wave-level (256-thread workgroups, 2 per CU, every wave an independent worker):
-//     for matrices with many tiles per worker (gate|up, lm_head) -- each wave sees one
-//     or two tile segments, so its load pipeline never drains mid-kernel;
-//   * workgroup-level (512-thread workgroups, 1 per CU, the 8 waves split each segment's
-//     k-blocks and reduce through LDS in a fixed order): for matrices with fewer tiles
-//     than CUs (qkv, o, down), where wave-level workers would cut every tile into dozens
-//     of fp32 partials.
+// U = (N/64) * KB work units (one 64-row wave-tile x one k-block), tile-major.  One
+// workgroup per CU takes an equal contiguous unit range, so every CU streams the same
+// number of bytes; the range crosses tile boundaries, which cut it into segments.
 //
-// Completion.  A worker whose segment covers a whole tile runs the epilogue directly.  A
-// tile split across workers is finished by whichever arrives last: each stores its fp32
-// partial with agent-scope atomic stores, waits for them to complete (s_waitcnt), then
-// bumps the tile's agent-scope counter; the last one reads the slots back with
-// agent-scope atomic loads in slot order (deterministic sum), runs the epilogue and
-// re-arms the counter.  Only agent-scope atomics touch the shared slots, so no L2
-// write-back / invalidate is needed, and no worker ever waits for another.
+// Workgroup = 4 streaming waves + 1 reducer wave.  The streaming waves split each
+// segment's k-blocks, write their fp32 partial to an LDS slot (two slot sets, used by
+// alternate segments) and go straight on to the next segment.  The reducer wave loads
+// the RMSNorm gain and 1/rms rows at the start, then for each segment in turn sums the 4
+// partials in a fixed order and completes the tile, so the cross-workgroup fix-up and the
+// epilogue overlap the next segment's weight stream instead of stalling it.
 //
-// Epilogues: STORE (fp16 y with the per-row scale), RESID (x += fp16(y), per-row sums of
-// squares; the last tile of the launch turns them into r = 1/rms for the next GEMM's
-// norm-on-load), SWIGLU (gate/up row-blocks interleaved), ARGMAX (fp32 logits + packed
-// (value, index) atomicMax per row).
+// Completion.  A segment covering a whole tile runs the epilogue directly.  A tile split
+// across workgroups is finished by whichever arrives last: each stores its fp32 partial
+// with agent-scope atomic stores, waits for them to complete (s_waitcnt), then bumps the
+// tile's agent-scope counter; the last one reads the slots back with agent-scope atomic
+// loads in slot order (deterministic sum), runs the epilogue and re-arms the counter.
+// Only agent-scope atomics touch the shared slots, so no L2 write-back / invalidate is
+// needed, and no workgroup ever waits for another.
+//
+// Epilogues: STORE (fp16 y with the per-row scale), RESID (x += fp16(y), per-tile row sums
+// of squares for the next GEMM's 1/rms), SWIGLU (gate/up row-blocks interleaved), ARGMAX
+// (fp32 logits + packed (value, index) atomicMax per row).
 #include "dfl_common.h"
 #include "dfl_kernels.h"
 
@@ -38,7 +37,10 @@ namespace dfl {
 
 namespace {
 
-constexpr int WG_WAVES = 8;   // workgroup-level kernel
+// Streaming waves per workgroup: one per SIMD.  (A second streaming wave on a SIMD loses
+// the issue arbitration to the older one and finishes its equal share ~40 % later.)
+// The reducer wave shares SIMD 0.
+constexpr int WG_WAVES = 4;
 
 template <int WT>
 struct KTraits;
@@ -56,13 +58,33 @@ struct KTraits<WT_F16> {
 // Largest worker index w with floor(w*U/NW) <= u (the worker holding unit u).
 DFL_DEV int worker_of(long long u, long long U, int NW) { return (int)(((u + 1) * NW - 1) / U); }
 
-// fp16(fp16(x * r) * g) for 8 packed halves (RMSNorm output expression).
+// fp32(x * r) for the low / high fp16 half of a dword, in one v_fma_mix_f32 (fma with a
+// -0.0 addend is the exactly rounded product, signed zeros included) instead of a
+// convert and a multiply.
+DFL_DEV float mul_f16lo_f32(uint32_t xv, float r) {
+  float d;
+  asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(d) : "v"(xv), "v"(r), "v"(-0.0f));
+  return d;
+}
+DFL_DEV float mul_f16hi_f32(uint32_t xv, float r) {
+  float d;
+  asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+      : "=v"(d) : "v"(xv), "v"(r), "v"(-0.0f));
+  return d;
+}
+
+// fp16(fp16(x * r) * g) for 8 packed halves (RMSNorm output expression).  The second
+// product is a packed fp16 multiply: the product of two fp16 values is exact in fp32, so
+// rounding it to fp16 once is the same as the fp32 multiply followed by the conversion.
 DFL_DEV u32x4 norm8(u32x4 xv, float r, u32x4 gv) {
-  const half8_t x = as_half8(xv), gg = as_half8(gv);
-  half8_t y;
+  u32x4 o;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) y[j] = f2h(h2f(f2h(h2f(x[j]) * r)) * h2f(gg[j]));
-  return __builtin_bit_cast(u32x4, y);
+  for (int j = 0; j < 4; ++j) {
+    half2_t p = (half2_t){f2h(mul_f16lo_f32(xv[j], r)), f2h(mul_f16hi_f32(xv[j], r))};
+    p = p * __builtin_bit_cast(half2_t, gv[j]);
+    o[j] = __builtin_bit_cast(uint32_t, p);
+  }
+  return o;
 }
 
 DFL_DEV void store_agent(float* p, float v) {
@@ -73,84 +95,135 @@ DFL_DEV float load_agent(const float* p) {
 }
 
 // ---------------------------------------------------------------------------------------
-// One wave streams k-blocks [v0, v0 + nkb) of wave-tile t into acc0/acc1 (two 32-row
-// blocks x 32 activation columns).  Two register stages of P k-blocks alternate; loads
-// are unconditional (indices clamped to the last block, whose slots then contribute a
-// zero activation), and sched_barrier keeps each stage's loads issued ahead of use.
+// Streaming wave w takes units u0 + w, u0 + w + WG_WAVES, ... of the workgroup's range
+// [u0, u1) (unit = 64-row wave-tile t x k-block kb, u = t * KB + kb), crossing tile
+// boundaries in one continuous load pipeline.  Two register stages of P units alternate
+// (sched_barrier keeps each stage's loads issued ahead of use); loads past the wave's last
+// unit repeat its address and are not consumed.  Every tile the range touches is one
+// segment: when the wave leaves a tile it hands its fp32 partial (two 32x32 accumulators,
+// zero if it had no unit there) to the reducer wave through LDS slot set (segment & 1),
+// while the next tile's loads are already in flight.
 // ---------------------------------------------------------------------------------------
 template <int WT, bool NORM, int P>
-DFL_DEV void stream_tile(const StreamArgs& a, const half_t* gsh, float rn, int goff, int lane,
-                         int t, int v0, int nkb, floatx16& acc0, floatx16& acc1) {
+DFL_DEV void stream_range(const StreamArgs& a, const half_t* gsh, const float* rn_lds,
+                          int* ready, float (*red)[WG_WAVES][2048], int* arrived, int* reduced,
+                          long long u0, long long u1, int w, int lane) {
   constexpr int KBK = KTraits<WT>::KBK;
   constexpr int NX = KTraits<WT>::NX;
-  acc0 = (floatx16){};
-  acc1 = (floatx16){};
-  if (nkb <= 0) return;
-  struct Stage {
-    u32x4 w0[P], w1[P], x[P][NX];
-  };
-  const uint4* w0p = a.W + ((size_t)(2 * t) * a.KB + v0) * 64 + lane;
-  const uint4* w1p = w0p + (size_t)a.KB * 64;
+  const int m = lane & 31, g = lane >> 5;
+  const int goff = (WT == WT_INT8 ? 16 * g : 8 * g);
+  const int KB = a.KB;
   // activation records: int8 k-block kb = 32 k -> records (kb, 0), (kb, 1), this lane's
   // entry; fp16 k-block kb = 16 k -> record (kb/2, g) at entry m + 32*(kb & 1)
   const u32x4* xf = reinterpret_cast<const u32x4*>(a.X);
-  const int m = lane & 31, g = lane >> 5;
-  const int last = nkb - 1;
-  auto issue = [&](Stage& st, int base) {
-    static_for<0, P>([&](auto s) {
-      const int i = min(base + (int)s, last);
-      st.w0[s] = load_stream(w0p + (size_t)i * 64);
-      st.w1[s] = load_stream(w1p + (size_t)i * 64);
-      const int kb = v0 + i;
-      if constexpr (WT == WT_INT8) {
-        st.x[s][0] = xf[(size_t)(2 * kb) * 64 + lane];
-        st.x[s][NX - 1] = xf[(size_t)(2 * kb + 1) * 64 + lane];
-      } else {
-        st.x[s][0] = xf[(size_t)((kb >> 1) * 2 + g) * 64 + m + 32 * (kb & 1)];
-      }
-    });
+
+  floatx16 acc0 = (floatx16){}, acc1 = (floatx16){};
+  int si = 0;   // segments flushed so far
+  auto flush = [&]() {
+    // slot set si & 1 was last used by segment si - 2: wait until it has been reduced
+    while (__hip_atomic_load(reduced, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < si - 1)
+      __builtin_amdgcn_s_sleep(1);
+    float* dst = red[si & 1][w];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      dst[r * 64 + lane] = acc0[r];
+      dst[1024 + r * 64 + lane] = acc1[r];
+    }
+    if (lane == 0)
+      __hip_atomic_fetch_add(&arrived[si & 1], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    acc0 = (floatx16){};
+    acc1 = (floatx16){};
+    ++si;
   };
-  auto consume = [&](const Stage& st, int base) {
-    static_for<0, P>([&](auto s) {
-      const int i = base + (int)s;
-      const bool valid = i < nkb;
-      const u32x4 z = {0u, 0u, 0u, 0u};
-      u32x4 xa = st.x[s][0], xb = st.x[s][NX - 1];
-      if constexpr (NORM) {
-        const int kk = (v0 + min(i, last)) * KBK + goff;
-        xa = norm8(xa, rn, *reinterpret_cast<const u32x4*>(gsh + kk));
-        if constexpr (NX > 1) xb = norm8(xb, rn, *reinterpret_cast<const u32x4*>(gsh + kk + 8));
-        else xb = xa;
-      }
-      xa = valid ? xa : z;
-      xb = valid ? xb : z;
-      if constexpr (WT == WT_INT8) {
-        half8_t lo0, hi0, lo1, hi1;
-        dequant_i8x16(st.w0[s], lo0, hi0);
-        dequant_i8x16(st.w1[s], lo1, hi1);
-        const half8_t xl = as_half8(xa), xh = as_half8(xb);
-        acc0 = mfma32x32x16(lo0, xl, acc0);
-        acc1 = mfma32x32x16(lo1, xl, acc1);
-        acc0 = mfma32x32x16(hi0, xh, acc0);
-        acc1 = mfma32x32x16(hi1, xh, acc1);
-      } else {
-        const half8_t xv = as_half8(xa);
-        acc0 = mfma32x32x16(as_half8(st.w0[s]), xv, acc0);
-        acc1 = mfma32x32x16(as_half8(st.w1[s]), xv, acc1);
-      }
-    });
-  };
-  Stage A, B;
-  issue(A, 0);
-  for (int base = 0; base < nkb; base += 2 * P) {
-    issue(B, base + P);
-    __builtin_amdgcn_sched_barrier(0);
-    consume(A, base);
-    if (base + P >= nkb) break;
-    issue(A, base + 2 * P);
-    __builtin_amdgcn_sched_barrier(0);
-    consume(B, base + P);
+
+  const int t_first = (int)(u0 / KB);
+  const int t_last = (int)((u1 - 1) / KB);
+  const long long g0 = u0 + w;
+  const int J = g0 < u1 ? (int)((u1 - g0 + WG_WAVES - 1) / WG_WAVES) : 0;
+  int ct = (int)(min(g0, u1 - 1) / KB);          // consume cursor: tile of the next unit
+  for (int t = t_first; t < ct; ++t) flush();   // leading tiles without a unit of this wave
+  if (J > 0) {
+    // issue cursor (t, kb) of the next unit to load; advanced by WG_WAVES (< KB) units
+    int it = ct, ikb = (int)(g0 - (long long)ct * KB), issued = 0;
+    struct Stage {
+      u32x4 w0[P], w1[P], x[P][NX];
+      int kb[P], t[P];
+    };
+    auto issue = [&](Stage& st) {
+      static_for<0, P>([&](auto s) {
+        const uint4* wp = a.W + ((size_t)(2 * it) * KB + ikb) * 64 + lane;
+        st.w0[s] = load_stream(wp);
+        st.w1[s] = load_stream(wp + (size_t)KB * 64);
+        st.kb[s] = ikb;
+        st.t[s] = it;
+        if constexpr (WT == WT_INT8) {
+          st.x[s][0] = xf[(size_t)(2 * ikb) * 64 + lane];
+          st.x[s][NX - 1] = xf[(size_t)(2 * ikb + 1) * 64 + lane];
+        } else {
+          st.x[s][0] = xf[(size_t)((ikb >> 1) * 2 + g) * 64 + m + 32 * (ikb & 1)];
+        }
+        if (++issued < J) {
+          ikb += WG_WAVES;
+          while (ikb >= KB) {   // KB may be smaller than WG_WAVES
+            ikb -= KB;
+            ++it;
+          }
+        }
+      });
+    };
+    float rn = 1.0f;
+    auto consume = [&](const Stage& st, int base) {
+      static_for<0, P>([&](auto s) {
+        if (base + (int)s < J) {
+          while (ct < st.t[s]) {   // left a tile (or tiles): hand over its partial
+            flush();
+            ++ct;
+          }
+          u32x4 xa = st.x[s][0], xb = st.x[s][NX - 1];
+          if constexpr (NORM) {
+            const int kk = st.kb[s] * KBK + goff;
+            xa = norm8(xa, rn, *reinterpret_cast<const u32x4*>(gsh + kk));
+            if constexpr (NX > 1) xb = norm8(xb, rn, *reinterpret_cast<const u32x4*>(gsh + kk + 8));
+            else xb = xa;
+          }
+          if constexpr (WT == WT_INT8) {
+            half8_t lo0, hi0, lo1, hi1;
+            dequant_i8x16(st.w0[s], lo0, hi0);
+            dequant_i8x16(st.w1[s], lo1, hi1);
+            const half8_t xl = as_half8(xa), xh = as_half8(xb);
+            acc0 = mfma32x32x16(lo0, xl, acc0);
+            acc1 = mfma32x32x16(lo1, xl, acc1);
+            acc0 = mfma32x32x16(hi0, xh, acc0);
+            acc1 = mfma32x32x16(hi1, xh, acc1);
+          } else {
+            const half8_t xv = as_half8(xa);
+            acc0 = mfma32x32x16(as_half8(st.w0[s]), xv, acc0);
+            acc1 = mfma32x32x16(as_half8(st.w1[s]), xv, acc1);
+          }
+        }
+      });
+    };
+
+    Stage A, B;
+    issue(A);
+    if constexpr (NORM) {
+      // gain and 1/rms come from the reducer wave's prologue
+      while (__hip_atomic_load(ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
+        __builtin_amdgcn_s_sleep(1);
+      rn = rn_lds[m];
+    }
+    for (int base = 0; base < J; base += 2 * P) {
+      issue(B);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(A, base);
+      if (base + P >= J) break;
+      issue(A);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(B, base + P);
+    }
   }
+  // the tile of the last unit, then trailing tiles without a unit of this wave
+  for (int t = ct; t <= t_last; ++t) flush();
 }
 
 // Cross-worker completion of tile t.  `slot` is this worker's index among the `count`
@@ -236,33 +309,6 @@ DFL_DEV void tile_epilogue(const StreamArgs& a, int lane, int t, const floatx16&
     }
     ss += __shfl_xor(ss, 32, 64);
     if (g == 0 && row_ok) store_agent(a.ss_part + (size_t)t * 32 + m, ss);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    int prev = 0;
-    if (lane == 0)
-      prev = __hip_atomic_fetch_add(a.done_cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    prev = __shfl(prev, 0, 64);
-    const int n_wt = a.N >> 6;
-    if (prev == n_wt - 1) {   // last tile of the launch: 1/rms per row for the next norm
-      // Lane (m, g) sums tiles g, g+2, ...; eight loads are issued before any is used
-      // (a dependent load per tile would serialise n_wt memory round trips).
-      float tot = 0.f;
-      if (row_ok) {
-        const float* sp = a.ss_part + m;
-        int tt = g;
-        for (; tt + 14 < n_wt; tt += 16) {
-          float v[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) v[j] = load_agent(sp + (size_t)(tt + 2 * j) * 32);
-          tot += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-        }
-        for (; tt < n_wt; tt += 2) tot += load_agent(sp + (size_t)tt * 32);
-      }
-      tot += __shfl_xor(tot, 32, 64);
-      if (g == 0 && row_ok) a.rnorm_out[m] = 1.0f / sqrtf(tot / (float)a.N + a.eps);
-      if (lane == 0) *a.done_cnt = 0;
-    }
   } else if constexpr (EPI == EPI_SWIGLU) {
     if (!row_ok) return;
     // out is an AFL tile [32][N/2]: columns 32t + 8q + 4g + (0..3) of row m
@@ -319,50 +365,95 @@ DFL_DEV void tile_epilogue(const StreamArgs& a, int lane, int t, const floatx16&
   }
 }
 
-// Copy the RMSNorm gain into LDS (one barrier, at kernel start).
-template <bool NORM>
-DFL_DEV void load_gain(const StreamArgs& a, half_t* gsh, int K) {
-  if constexpr (NORM) {
-    for (int k = threadIdx.x; k < K; k += blockDim.x) gsh[k] = a.gnorm[k];
-    __syncthreads();
+// 1/rms of activation row m (lane & 31) from the per-tile sums of squares of the RESID
+// epilogue that produced X: lane (m, g) adds tiles g, g+2, ... with eight loads in flight.
+DFL_DEV float rn_from_ss(const float* ss, int tiles, int n, float eps, int lane) {
+  const int m = lane & 31, g = lane >> 5;
+  const float* sp = ss + m;
+  float tot = 0.f;
+  int tt = g;
+  for (; tt + 14 < tiles; tt += 16) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = sp[(size_t)(tt + 2 * j) * 32];
+    tot += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
   }
+  for (; tt < tiles; tt += 2) tot += sp[(size_t)tt * 32];
+  tot += __shfl_xor(tot, 32, 64);
+  return 1.0f / sqrtf(tot / (float)n + eps);
 }
 
 }  // namespace
 
 // ---------------------------------------------------------------------------------------
-// Wave-level workers: 4 independent waves per workgroup.
+// The stream-K kernel: one workgroup per CU, 4 streaming waves + 1 reducer wave.
 // ---------------------------------------------------------------------------------------
 template <int WT, int EPI, bool NORM, int P>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void wsk_gemm_kernel(StreamArgs a) {
+__global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_gemm_kernel(StreamArgs a) {
   constexpr int KBK = KTraits<WT>::KBK;
+  __shared__ float red[2][WG_WAVES][2048];     // partial slots, two sets
   __shared__ half_t gsh[NORM ? 8192 : 8];
-  load_gain<NORM>(a, gsh, a.KB * KBK);
+  __shared__ float rn_s[32];
+  // arrived[p]: partials written for segments of parity p (monotonic: a set is rewritten
+  // only after its previous segment was reduced); reduced: segments summed so far
+  __shared__ int arrived[2], reduced, ready;
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int m = lane & 31, g = lane >> 5;
-  // rows >= M of the 32-row tile feed only their own (never stored) output columns
-  const int NW = gridDim.x * 4;
-  const int gw = blockIdx.x * 4 + w;
+  const int G = gridDim.x;
+  const int b = blockIdx.x;
   const long long U = (long long)(a.N >> 6) * a.KB;
-  const long long u0 = (long long)gw * U / NW, u1 = (long long)(gw + 1) * U / NW;
-  const float rn = NORM ? a.rnorm[m] : 1.0f;
-  const int goff = (WT == WT_INT8 ? 16 * g : 8 * g);
+  const long long u0 = (long long)b * U / G, u1 = (long long)(b + 1) * U / G;
+  if (u0 >= u1) return;   // (the plan never makes more workgroups than units)
+  if (threadIdx.x == 0) {
+    arrived[0] = arrived[1] = 0;
+    reduced = 0;
+    ready = 0;
+  }
+  __syncthreads();
 
-  for (long long u = u0; u < u1;) {
+  if (w < WG_WAVES) {
+    stream_range<WT, NORM, P>(a, gsh, rn_s, &ready, red, arrived, &reduced, u0, u1, w, lane);
+    return;
+  }
+
+  // ---- reducer wave ----
+  if constexpr (NORM) {
+    const int K = a.KB * KBK;
+    for (int k = lane * 8; k < K; k += 64 * 8)
+      *reinterpret_cast<u32x4*>(gsh + k) = *reinterpret_cast<const u32x4*>(a.gnorm + k);
+    const float rn = a.ss_in ? rn_from_ss(a.ss_in, a.ss_tiles, a.ss_n, a.eps, lane)
+                             : a.rnorm[lane & 31];
+    if (lane < 32) rn_s[lane] = rn;
+    __builtin_amdgcn_s_waitcnt(0);
+    if (lane == 0) __hip_atomic_store(&ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  int si = 0;
+  for (long long u = u0; u < u1; ++si) {
     const int t = (int)(u / a.KB);
     const int kbs = (int)(u - (long long)t * a.KB);
     const int kbe = (int)min((long long)a.KB, (long long)kbs + (u1 - u));
-    floatx16 acc0, acc1;
-    stream_tile<WT, NORM, P>(a, gsh, rn, goff, lane, t, kbs, kbe - kbs, acc0, acc1);
+    while (__hip_atomic_load(&arrived[si & 1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
+           WG_WAVES * ((si >> 1) + 1))
+      __builtin_amdgcn_s_sleep(1);
+    floatx16 acc0 = (floatx16){}, acc1 = (floatx16){};
+#pragma unroll 1
+    for (int j = 0; j < WG_WAVES; ++j) {
+      const float* src = red[si & 1][j];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        acc0[r] += src[r * 64 + lane];
+        acc1[r] += src[1024 + r * 64 + lane];
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);   // slot reads done before the set is handed back
+    if (lane == 0) __hip_atomic_store(&reduced, si + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     bool complete = (kbs == 0 && kbe == a.KB);
     if (!complete) {
       const long long tu0 = (long long)t * a.KB;
-      const int first = worker_of(tu0, U, NW);
-      const int count = worker_of(tu0 + a.KB - 1, U, NW) - first + 1;
-      complete = finish_split_tile(a, lane, t, gw - first, count, acc0, acc1);
+      const int first = worker_of(tu0, U, G);
+      const int count = worker_of(tu0 + a.KB - 1, U, G) - first + 1;
+      complete = finish_split_tile(a, lane, t, b - first, count, acc0, acc1);
     }
     if (complete) tile_epilogue<EPI>(a, lane, t, acc0, acc1);
     u += kbe - kbs;
@@ -370,84 +461,18 @@ void wsk_gemm_kernel(StreamArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Workgroup-level workers: 8 waves split each segment's k-blocks, LDS reduction.
-// ---------------------------------------------------------------------------------------
-template <int WT, int EPI, bool NORM, int P>
-__global__ __launch_bounds__(64 * WG_WAVES) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void gsk_gemm_kernel(StreamArgs a) {
-  constexpr int KBK = KTraits<WT>::KBK;
-  __shared__ float red[(WG_WAVES - 1) * 2048];
-  __shared__ half_t gsh[NORM ? 8192 : 8];
-  load_gain<NORM>(a, gsh, a.KB * KBK);
-
-  const int lane = threadIdx.x & 63;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int m = lane & 31, g = lane >> 5;
-  const int G = gridDim.x;
-  const int b = blockIdx.x;
-  const long long U = (long long)(a.N >> 6) * a.KB;
-  const long long u0 = (long long)b * U / G, u1 = (long long)(b + 1) * U / G;
-  const float rn = NORM ? a.rnorm[m] : 1.0f;
-  const int goff = (WT == WT_INT8 ? 16 * g : 8 * g);
-
-  for (long long u = u0; u < u1;) {
-    const int t = (int)(u / a.KB);
-    const int kbs = (int)(u - (long long)t * a.KB);
-    const int kbe = (int)min((long long)a.KB, (long long)kbs + (u1 - u));
-    const int L = kbe - kbs;
-    const int v0 = kbs + (w * L) / WG_WAVES, v1 = kbs + ((w + 1) * L) / WG_WAVES;
-    floatx16 acc0, acc1;
-    stream_tile<WT, NORM, P>(a, gsh, rn, goff, lane, t, v0, v1 - v0, acc0, acc1);
-    if (w != 0) {
-      float* dst = red + (size_t)(w - 1) * 2048;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        dst[r * 64 + lane] = acc0[r];
-        dst[1024 + r * 64 + lane] = acc1[r];
-      }
-    }
-    __syncthreads();
-    if (w == 0) {
-#pragma unroll
-      for (int j = 0; j < WG_WAVES - 1; ++j) {
-        const float* src = red + (size_t)j * 2048;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          acc0[r] += src[r * 64 + lane];
-          acc1[r] += src[1024 + r * 64 + lane];
-        }
-      }
-      bool complete = (kbs == 0 && kbe == a.KB);
-      if (!complete) {
-        const long long tu0 = (long long)t * a.KB;
-        const int first = worker_of(tu0, U, G);
-        const int count = worker_of(tu0 + a.KB - 1, U, G) - first + 1;
-        complete = finish_split_tile(a, lane, t, b - first, count, acc0, acc1);
-      }
-      if (complete) tile_epilogue<EPI>(a, lane, t, acc0, acc1);
-    }
-    u += L;
-    __syncthreads();   // red[] is reused by the next segment
-  }
-}
-
-// ---------------------------------------------------------------------------------------
 // Host-side planning and launch
 // ---------------------------------------------------------------------------------------
 
-// Wave-level when a worker would see at least half a tile at 8 waves per CU; otherwise
-// the workgroup-level kernel (one 8-wave workgroup per CU).
 SKPlan streamk_plan(int N, int KB, int n_cu) {
-  // Workgroup-level workers, one per CU.  When there are fewer wave-tiles than CUs the
-  // worker count is the largest multiple of the tile count that fits, so every tile is
-  // split into the same number of equal k-ranges (no worker straddles two tiles).
-  // Measured on 256 CUs this beats independent-wave workers for every projection shape.
+  // One workgroup per CU.  When there are fewer wave-tiles than CUs the worker count is
+  // the largest multiple of the tile count that fits, so every tile is split into the
+  // same number of equal k-ranges (no worker straddles two tiles).
   SKPlan p;
   const long long nt = N / 64;
   const long long U = nt * KB;
   long long W = n_cu;
   if (nt < n_cu) W = std::max(1LL, (long long)n_cu / nt) * nt;
-  p.wave_level = false;
   p.workers = (int)std::max(1LL, std::min(W, U));
   const long long per = std::max(1LL, U / p.workers);
   p.seg_cap = (int)((KB + per - 1) / per + 1);
@@ -459,21 +484,11 @@ SKPlan streamk_plan(int N, int KB, int n_cu) {
 template <int WT, int EPI, bool NORM>
 static void launch_t(const StreamArgs& a, const SKPlan& p, hipStream_t st, hipEvent_t e0,
                      hipEvent_t e1) {
-  if (p.wave_level) {
-    if (e0 || e1)
-      hipExtLaunchKernelGGL((wsk_gemm_kernel<WT, EPI, NORM, 4>), dim3(p.workers / 4), dim3(256),
-                            0, st, e0, e1, 0, a);
-    else
-      hipLaunchKernelGGL((wsk_gemm_kernel<WT, EPI, NORM, 4>), dim3(p.workers / 4), dim3(256), 0,
-                         st, a);
-  } else {
-    if (e0 || e1)
-      hipExtLaunchKernelGGL((gsk_gemm_kernel<WT, EPI, NORM, 4>), dim3(p.workers),
-                            dim3(64 * WG_WAVES), 0, st, e0, e1, 0, a);
-    else
-      hipLaunchKernelGGL((gsk_gemm_kernel<WT, EPI, NORM, 4>), dim3(p.workers),
-                         dim3(64 * WG_WAVES), 0, st, a);
-  }
+  const dim3 grid(p.workers), block(64 * (WG_WAVES + 1));
+  if (e0 || e1)
+    hipExtLaunchKernelGGL((gsk_gemm_kernel<WT, EPI, NORM, 4>), grid, block, 0, st, e0, e1, 0, a);
+  else
+    hipLaunchKernelGGL((gsk_gemm_kernel<WT, EPI, NORM, 4>), grid, block, 0, st, a);
 }
 
 void launch_streamk_gemm(int wt, int epi, bool norm, const StreamArgs& a, const SKPlan& p,
