@@ -51,6 +51,8 @@ typedef struct dfl_config {
   int32_t max_ctx;         /* KV-cache capacity in context rows            */
   float rms_eps;           /* rms_norm_eps                                 */
   double rope_theta;       /* rope_theta (neox / split-half RoPE)          */
+  int32_t max_seqs;        /* independent sequences (each its own KV cache) for
+                              dfl_draft_batch; 0 or 1 = single sequence      */
 } dfl_config;
 
 /* Create / destroy a draft context (replaces ANEDraftModel.__init__ kernel compile
@@ -105,6 +107,19 @@ int dfl_ingest_fused(dfl_ctx* ctx, const uint16_t* ctx_hidden, int32_t C, void* 
 int dfl_draft_block(dfl_ctx* ctx, const uint16_t* noise_emb, const int32_t* ids, int32_t B,
                     uint16_t* out_hidden, uint16_t* out_prenorm, float* out_logits,
                     int32_t* out_ids, void* stream);
+
+/* Batched drafting (no counterpart in the single-sequence reference; it stacks what the
+ * serial caller does per sequence, generate.py:591-609, for sequences 0 .. n_seq-1):
+ * one block of B rows for each sequence, rows stacked sequence-major (row = s*B + b) in
+ * every input and output buffer, same meaning as dfl_draft_block per row.  Each sequence
+ * attends to its own cached context (ragged lengths allowed) plus its own block, at its
+ * own positions.  The projections run once over all n_seq*B rows. */
+int dfl_draft_batch(dfl_ctx* ctx, int32_t n_seq, const uint16_t* noise_emb, const int32_t* ids,
+                    int32_t B, uint16_t* out_hidden, uint16_t* out_prenorm, float* out_logits,
+                    int32_t* out_ids, void* stream);
+/* Select the sequence (0 <= seq < max_seqs) that dfl_ingest_*, dfl_draft_block and the
+ * dfl_cache_* calls address.  A context starts with sequence 0 selected. */
+int dfl_select_seq(dfl_ctx* ctx, int32_t seq);
 
 /* Run only the first n draft layers (DFlashDraftModel.num_draft_layers, dflash.py:382,
  * 394, lowered by generate.py:423-426); 1 <= n <= n_layers.  Ingest then fills only

@@ -59,11 +59,18 @@ struct ProfRec {
   long long bytes;
 };
 
+// Cache bookkeeping of one sequence (DFlashKVCache.offset and its row count).
+struct SeqState {
+  int len = 0;             // cached context rows
+  long long offset = 0;    // absolute position of the next row
+  int last_block = 0;      // rows of the last drafted block (committable)
+};
+
 struct Layer {
   uint4 *w_qkv = nullptr, *w_o = nullptr, *w_gu = nullptr, *w_down = nullptr;
   half_t *s_qkv = nullptr, *s_o = nullptr, *s_gu = nullptr, *s_down = nullptr;
   half_t *in_norm = nullptr, *post_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
-  half_t *Kc = nullptr, *Vt = nullptr;
+  half_t *Kc = nullptr, *Vt = nullptr;   // [max_seqs][NKV][cap][128], [max_seqs][NKV][128][cap]
   bool loaded = false;
 };
 
@@ -72,6 +79,14 @@ struct Layer {
 struct dfl_ctx {
   dfl_config cfg;
   int H, NH, NKV, F, NL, NQKV, Bmax, cap, V, NF;
+  int S = 1;                 // sequences (independent KV caches)
+  int RM = 0;                // activation rows: S * Bmax
+  int cur = 0;               // sequence addressed by the single-sequence calls
+  size_t kv_seq = 0;         // elements of one sequence's K (or Vt) cache per layer
+  std::vector<SeqState> seqs;
+  SeqState& sq() { return seqs[cur]; }
+  half_t* kc(const Layer& L, int seq) const { return L.Kc + (size_t)seq * kv_seq; }
+  half_t* vt(const Layer& L, int seq) const { return L.Vt + (size_t)seq * kv_seq; }
   std::vector<Layer> layers;
   uint4* w_fc = nullptr;
   half_t* hidden_norm = nullptr;
@@ -81,9 +96,6 @@ struct dfl_ctx {
   const half_t* embed = nullptr;
   bool head_loaded = false;
   int active = 0;   // layers run per call (num_draft_layers)
-  int len = 0;
-  long long offset = 0;
-  int last_block = 0;
   half_t *x = nullptr, *h = nullptr, *Q = nullptr, *attn = nullptr, *act = nullptr,
          *ctxbuf = nullptr;
   float* ws = nullptr;
@@ -92,8 +104,8 @@ struct dfl_ctx {
   int* err = nullptr;
   // stream-K GEMM state (block step)
   int n_cu = 256;
-  half_t* qkvbuf = nullptr;      // [Bmax][NQKV] fp16 projections
-  float* rnorm = nullptr;        // [Bmax] 1/rms of the residual rows
+  half_t* qkvbuf = nullptr;      // [RM][NQKV] fp16 projections
+  float* rnorm = nullptr;        // [RM] 1/rms of the residual rows
   float* sk_ws = nullptr;        // split-tile partials
   int* sk_tile_cnt = nullptr;    // [max tiles]
   float* sk_ss = nullptr;        // [m-tiles][H/64][32] row sums of squares of x (RESID output)
@@ -198,6 +210,8 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
   if (c.n_target_feat < 0) return fail(DFL_EINVAL, "dfl_create: n_target_feat must be >= 0");
   if (!(c.rms_eps > 0.f) || !(c.rope_theta > 0.0))
     return fail(DFL_EINVAL, "dfl_create: rms_eps and rope_theta must be positive");
+  if (c.max_seqs < 0 || c.max_seqs > 64)
+    return fail(DFL_EINVAL, "dfl_create: max_seqs must be in [0, 64] (0 means 1)");
 
   dfl_ctx* x = new dfl_ctx();
   x->cfg = c;
@@ -211,6 +225,10 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
   x->V = c.vocab;
   x->NF = c.n_target_feat;
   x->cap = ((c.max_ctx + c.max_block + 63) / 64) * 64;
+  x->S = std::max(1, c.max_seqs);
+  x->RM = x->S * x->Bmax;
+  x->kv_seq = (size_t)x->NKV * x->cap * 128;
+  x->seqs.resize(x->S);
   x->layers.resize(c.n_layers);
   x->active = c.n_layers;
   x->p_qkv = plan_for(x->NQKV, x->H / 32, EPI_PARTIAL);
@@ -219,7 +237,7 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
   x->p_down = plan_for(x->H, x->F / 32, EPI_PARTIAL);
   x->p_lm = plan_for(std::max(x->V, 64), x->H / 16, EPI_ARGMAX);
 
-  const size_t Bm = x->Bmax;
+  const size_t Bm = x->RM;   // activation rows of a (batched) block step
   size_t ws = std::max({(size_t)x->p_qkv.S_x * Bm * x->NQKV, (size_t)x->p_o.S_x * Bm * x->H,
                         (size_t)x->p_down.S_x * Bm * x->H});
   ws = std::max(ws, (size_t)ING_ROWS * std::max(x->H, 2 * x->NKV * 128));
@@ -267,7 +285,7 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
     }
   }
   for (auto& L : x->layers) {
-    const size_t kv = (size_t)x->NKV * x->cap * 128;
+    const size_t kv = x->kv_seq * x->S;
     if ((r = x->alloc(&L.Kc, kv, true)) || (r = x->alloc(&L.Vt, kv, true))) {
       delete x;
       return r;
@@ -476,14 +494,14 @@ static void ingest_kv_rows(dfl_ctx* ctx, const half_t* ctxrows, int rows, int r0
     q.q_norm = L.q_norm;
     q.k_norm = L.k_norm;
     q.eps = ctx->cfg.rms_eps;
-    q.pos0 = ctx->offset + r0;
+    q.pos0 = ctx->sq().offset + r0;
     q.log2_theta = std::log2(ctx->cfg.rope_theta);
     q.Q = nullptr;
     q.q_rows = 0;
-    q.Kc = L.Kc;
-    q.Vt = L.Vt;
+    q.Kc = ctx->kc(L, ctx->cur);
+    q.Vt = ctx->vt(L, ctx->cur);
     q.cap = ctx->cap;
-    q.cache_row0 = ctx->len + r0;
+    q.cache_row0 = ctx->sq().len + r0;
     ProfScope ps(ctx, P_INGEST_KV, 0, st);
     launch_qk_rope(q, st);
   }
@@ -492,15 +510,15 @@ static void ingest_kv_rows(dfl_ctx* ctx, const half_t* ctxrows, int rows, int r0
 static int ingest(dfl_ctx* ctx, const uint16_t* src, int C, bool fused, void* stream) {
   if (!ctx || (!src && C > 0)) return fail(DFL_EINVAL, "dfl_ingest: null argument");
   if (C < 0) return fail(DFL_EINVAL, "dfl_ingest: negative row count");
-  if ((long long)ctx->len + C > ctx->cfg.max_ctx)
-    return fail(DFL_ERANGE, "dfl_ingest: context rows " + std::to_string(ctx->len + C) +
+  if ((long long)ctx->sq().len + C > ctx->cfg.max_ctx)
+    return fail(DFL_ERANGE, "dfl_ingest: context rows " + std::to_string(ctx->sq().len + C) +
                                 " exceed max_ctx " + std::to_string(ctx->cfg.max_ctx));
   DFL_TRY(layers_ready(ctx, "dfl_ingest"));
   if (!fused && !ctx->fc_loaded) return fail(DFL_ESTATE, "dfl_ingest_context: fc not loaded");
   hipStream_t st = (hipStream_t)stream;
   const int H = ctx->H;
   const int K = ctx->NF * H;
-  ctx->last_block = 0;
+  ctx->sq().last_block = 0;
   for (int r0 = 0; r0 < C; r0 += ING_ROWS) {
     const int rows = std::min(ING_ROWS, C - r0);
     const half_t* ctxrows;
@@ -522,8 +540,8 @@ static int ingest(dfl_ctx* ctx, const uint16_t* src, int C, bool fused, void* st
     ingest_kv_rows(ctx, ctxrows, rows, r0, st);
   }
   DFL_TRY(check_launch("ingest"));
-  ctx->len += C;
-  ctx->offset += C;
+  ctx->sq().len += C;
+  ctx->sq().offset += C;
   return DFL_OK;
 }
 
@@ -535,126 +553,163 @@ int dfl_ingest_fused(dfl_ctx* ctx, const uint16_t* ctx_hidden, int32_t C, void* 
   return ingest(ctx, ctx_hidden, C, true, stream);
 }
 
-int dfl_draft_block(dfl_ctx* ctx, const uint16_t* noise_emb, const int32_t* ids, int32_t B,
-                    uint16_t* out_hidden, uint16_t* out_prenorm, float* out_logits,
-                    int32_t* out_ids, void* stream) {
-  if (!ctx) return fail(DFL_EINVAL, "dfl_draft_block: null context");
+// One draft block for sequences seq0 .. seq0 + n_seq - 1 together: B rows each, stacked
+// sequence-major (row = i * B + b).  The projections run once over all n_seq * B rows;
+// Q/K norm + RoPE and attention run per sequence against its own cache.
+static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
+                      const uint16_t* noise_emb, const int32_t* ids, int32_t B,
+                      uint16_t* out_hidden, uint16_t* out_prenorm, float* out_logits,
+                      int32_t* out_ids, void* stream) {
+  const std::string w(who);
   if (B <= 0 || B > ctx->Bmax)
-    return fail(DFL_ERANGE, "dfl_draft_block: block size " + std::to_string(B) +
-                                " outside [1, max_block=" + std::to_string(ctx->Bmax) + "]");
+    return fail(DFL_ERANGE, w + ": block size " + std::to_string(B) + " outside [1, max_block=" +
+                                std::to_string(ctx->Bmax) + "]");
   if ((noise_emb == nullptr) == (ids == nullptr))
-    return fail(DFL_EINVAL, "dfl_draft_block: pass exactly one of noise_emb / ids");
-  if (ids && !ctx->embed) return fail(DFL_ESTATE, "dfl_draft_block: embedding not loaded");
-  if (!ctx->head_loaded) return fail(DFL_ESTATE, "dfl_draft_block: final norm not loaded");
-  if ((out_logits || out_ids) && !ctx->w_lm)
-    return fail(DFL_ESTATE, "dfl_draft_block: lm_head not loaded");
-  if (ctx->len + B > ctx->cap) return fail(DFL_ERANGE, "dfl_draft_block: cache capacity exceeded");
-  DFL_TRY(layers_ready(ctx, "dfl_draft_block"));
+    return fail(DFL_EINVAL, w + ": pass exactly one of noise_emb / ids");
+  if (ids && !ctx->embed) return fail(DFL_ESTATE, w + ": embedding not loaded");
+  if (!ctx->head_loaded) return fail(DFL_ESTATE, w + ": final norm not loaded");
+  if ((out_logits || out_ids) && !ctx->w_lm) return fail(DFL_ESTATE, w + ": lm_head not loaded");
+  for (int i = 0; i < n_seq; ++i)
+    if (ctx->seqs[seq0 + i].len + B > ctx->cap)
+      return fail(DFL_ERANGE, w + ": cache capacity exceeded (sequence " +
+                                  std::to_string(seq0 + i) + ")");
+  DFL_TRY(layers_ready(ctx, who));
 
   hipStream_t st = (hipStream_t)stream;
   const int H = ctx->H, NH = ctx->NH, NKV = ctx->NKV, F = ctx->F, NQ = NH * 128;
+  const int M = n_seq * B;
   const float eps = ctx->cfg.rms_eps;
   // x = embedding rows (residual stream); rnorm = 1/rms(x).  Every projection whose input
   // is an RMSNorm output applies the norm on its activation load.
   {
     ProfScope ps(ctx, P_ROWS, 0, st);
-    launch_embed_norm(ids, ctx->embed, reinterpret_cast<const half_t*>(noise_emb), B, H, ctx->V,
+    launch_embed_norm(ids, ctx->embed, reinterpret_cast<const half_t*>(noise_emb), M, H, ctx->V,
                       ctx->layers[0].in_norm, eps, ctx->x, nullptr, ctx->rnorm, ctx->err, st);
   }
 
-  const int L = ctx->len + B;
-  const int ratio = NH / NKV;
-  // Attention key split: about one workgroup per CU ((chunks x KV heads) ~ CUs) with
-  // chunks of at most 160 keys (one LDS stage) while there are at most MAX_CHUNKS.
-  const int kblocks = (L + 31) / 32;
-  const int n_split = std::max(1, std::min(std::min(MAX_CHUNKS, kblocks),
-                                            std::max((kblocks + 4) / 5, (ctx->n_cu + NKV - 1) / NKV)));
-  const int chunk = ((kblocks + n_split - 1) / n_split) * 32;
-  const int n_chunks = (L + chunk - 1) / chunk;
+  // Attention key split per sequence: about one workgroup per CU ((chunks x KV heads) ~
+  // CUs) with chunks of at most 160 keys (one LDS stage) while there are at most MAX_CHUNKS.
+  auto attn_split = [&](int L, int& chunk, int& n_chunks) {
+    const int kblocks = (L + 31) / 32;
+    const int n_split = std::max(1, std::min(std::min(MAX_CHUNKS, kblocks),
+                                              std::max((kblocks + 4) / 5, (ctx->n_cu + NKV - 1) / NKV)));
+    chunk = ((kblocks + n_split - 1) / n_split) * 32;
+    n_chunks = (L + chunk - 1) / chunk;
+  };
 
   for (int l = 0; l < ctx->active; ++l) {
     Layer& Ly = ctx->layers[l];
     // q|k|v = input_layernorm(x) @ [Wq; Wk; Wv]^T  (fp16 out)
     skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_STORE, ctx->sk_qkv, Ly.w_qkv, Ly.s_qkv, ctx->NQKV, H / 32,
-           ctx->x, H, B, Ly.in_norm, /*rn_from_ss=*/l > 0, ctx->qkvbuf, ctx->NQKV, nullptr,
+           ctx->x, H, M, Ly.in_norm, /*rn_from_ss=*/l > 0, ctx->qkvbuf, ctx->NQKV, nullptr,
            nullptr, nullptr, st);
-    QKRopeArgs q{};
-    q.qkv16 = ctx->qkvbuf;
-    q.ws = nullptr;
-    q.S_x = 0;
-    q.M = B;
-    q.N = ctx->NQKV;
-    q.col_slot0 = 0;
-    q.scale = Ly.s_qkv;
-    q.slot0 = 0;
-    q.n_slots = NH + 2 * NKV;
-    q.NH = NH;
-    q.NKV = NKV;
-    q.q_norm = Ly.q_norm;
-    q.k_norm = Ly.k_norm;
-    q.eps = eps;
-    q.pos0 = ctx->offset;
-    q.log2_theta = std::log2(ctx->cfg.rope_theta);
-    q.Q = ctx->Q;
-    q.q_rows = B;
-    q.Kc = Ly.Kc;
-    q.Vt = Ly.Vt;
-    q.cap = ctx->cap;
-    q.cache_row0 = ctx->len;
-    {
-      ProfScope ps(ctx, P_QK_ROPE, 0, st);
-      launch_qk_rope(q, st);
-    }
-
-    AttnArgs at{};
-    at.Q = ctx->Q;
-    at.Kc = Ly.Kc;
-    at.Vt = Ly.Vt;
-    at.B = B;
-    at.NH = NH;
-    at.NKV = NKV;
-    at.cap = ctx->cap;
-    at.L = L;
-    at.chunk = chunk;
-    at.n_chunks = n_chunks;
-    at.scale_log2 = (float)(1.4426950408889634 / std::sqrt(128.0));
-    at.Op = ctx->Op;
-    at.Ml = ctx->Ml;
-    at.O = ctx->attn;
-    {
-      ProfScope ps(ctx, P_ATTN, 2LL * NKV * L * 128 * 2, st);
-      launch_block_attention(at, st);
+    for (int i = 0; i < n_seq; ++i) {
+      const SeqState& sqs = ctx->seqs[seq0 + i];
+      QKRopeArgs q{};
+      q.qkv16 = ctx->qkvbuf + (size_t)i * B * ctx->NQKV;
+      q.ws = nullptr;
+      q.S_x = 0;
+      q.M = B;
+      q.N = ctx->NQKV;
+      q.col_slot0 = 0;
+      q.scale = Ly.s_qkv;
+      q.slot0 = 0;
+      q.n_slots = NH + 2 * NKV;
+      q.NH = NH;
+      q.NKV = NKV;
+      q.q_norm = Ly.q_norm;
+      q.k_norm = Ly.k_norm;
+      q.eps = eps;
+      q.pos0 = sqs.offset;
+      q.log2_theta = std::log2(ctx->cfg.rope_theta);
+      q.Q = ctx->Q + (size_t)i * NH * B * 128;
+      q.q_rows = B;
+      q.Kc = ctx->kc(Ly, seq0 + i);
+      q.Vt = ctx->vt(Ly, seq0 + i);
+      q.cap = ctx->cap;
+      q.cache_row0 = sqs.len;
+      {
+        ProfScope ps(ctx, P_QK_ROPE, 0, st);
+        launch_qk_rope(q, st);
+      }
+      AttnArgs at{};
+      at.Q = q.Q;
+      at.Kc = q.Kc;
+      at.Vt = q.Vt;
+      at.B = B;
+      at.NH = NH;
+      at.NKV = NKV;
+      at.cap = ctx->cap;
+      at.L = sqs.len + B;
+      attn_split(at.L, at.chunk, at.n_chunks);
+      at.scale_log2 = (float)(1.4426950408889634 / std::sqrt(128.0));
+      at.Op = ctx->Op;
+      at.Ml = ctx->Ml;
+      at.O = ctx->attn;
+      at.o_row0 = i * B;
+      {
+        ProfScope ps(ctx, P_ATTN, 2LL * NKV * at.L * 128 * 2, st);
+        launch_block_attention(at, st);
+      }
     }
     // x += attn @ Wo^T ; per-tile row sums of squares of x -> sk_ss
     skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_RESID, ctx->sk_o, Ly.w_o, Ly.s_o, H, NQ / 32, ctx->attn,
-           NQ, B, nullptr, false, nullptr, H, ctx->x, nullptr, nullptr, st);
+           NQ, M, nullptr, false, nullptr, H, ctx->x, nullptr, nullptr, st);
     // act = silu(gate(post_norm(x))) * up(post_norm(x))
     skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_SWIGLU, ctx->sk_gu, Ly.w_gu, Ly.s_gu, 2 * F, H / 32,
-           ctx->x, H, B, Ly.post_norm, true, ctx->act, F, nullptr, nullptr, nullptr, st);
+           ctx->x, H, M, Ly.post_norm, true, ctx->act, F, nullptr, nullptr, nullptr, st);
     // x += act @ Wdown^T ; per-tile row sums of squares of x -> sk_ss
     skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_RESID, ctx->sk_down, Ly.w_down, Ly.s_down, H, F / 32,
-           ctx->act, F, B, nullptr, false, nullptr, H, ctx->x, nullptr, nullptr, st);
+           ctx->act, F, M, nullptr, false, nullptr, H, ctx->x, nullptr, nullptr, st);
   }
   if (out_logits || out_ids) {
     skgemm(ctx, P_LM_HEAD, WT_F16, EPI_ARGMAX, ctx->sk_lm, ctx->w_lm, nullptr, ctx->V, H / 16,
-           ctx->x, H, B, ctx->final_norm, true, nullptr, 0, nullptr, out_logits,
+           ctx->x, H, M, ctx->final_norm, true, nullptr, 0, nullptr, out_logits,
            out_ids ? ctx->keys : nullptr, st);
     if (out_ids) {
       ProfScope ps(ctx, P_ROWS, 0, st);
-      launch_argmax_finalize(ctx->keys, B, out_ids, st);
+      launch_argmax_finalize(ctx->keys, M, out_ids, st);
     }
   }
   if (out_hidden) {
     ProfScope ps(ctx, P_ROWS, 0, st);
-    launch_apply_norm(ctx->x, ctx->sk_ss, H / 64, ctx->cfg.rms_eps, ctx->final_norm, B, H,
+    launch_apply_norm(ctx->x, ctx->sk_ss, H / 64, ctx->cfg.rms_eps, ctx->final_norm, M, H,
                       reinterpret_cast<half_t*>(out_hidden), st);
   }
   if (out_prenorm) {
     ProfScope ps(ctx, P_ROWS, 0, st);
-    launch_afl_to_rows(ctx->x, B, H, reinterpret_cast<half_t*>(out_prenorm), st);
+    launch_afl_to_rows(ctx->x, M, H, reinterpret_cast<half_t*>(out_prenorm), st);
   }
-  DFL_TRY(check_launch("dfl_draft_block"));
-  ctx->last_block = B;
+  DFL_TRY(check_launch(who));
+  for (int i = 0; i < n_seq; ++i) ctx->seqs[seq0 + i].last_block = B;
+  return DFL_OK;
+}
+
+int dfl_draft_block(dfl_ctx* ctx, const uint16_t* noise_emb, const int32_t* ids, int32_t B,
+                    uint16_t* out_hidden, uint16_t* out_prenorm, float* out_logits,
+                    int32_t* out_ids, void* stream) {
+  if (!ctx) return fail(DFL_EINVAL, "dfl_draft_block: null context");
+  return draft_rows(ctx, "dfl_draft_block", ctx->cur, 1, noise_emb, ids, B, out_hidden,
+                    out_prenorm, out_logits, out_ids, stream);
+}
+
+int dfl_draft_batch(dfl_ctx* ctx, int32_t n_seq, const uint16_t* noise_emb, const int32_t* ids,
+                    int32_t B, uint16_t* out_hidden, uint16_t* out_prenorm, float* out_logits,
+                    int32_t* out_ids, void* stream) {
+  if (!ctx) return fail(DFL_EINVAL, "dfl_draft_batch: null context");
+  if (n_seq < 1 || n_seq > ctx->S)
+    return fail(DFL_ERANGE, "dfl_draft_batch: n_seq must be in [1, max_seqs=" +
+                                std::to_string(ctx->S) + "]");
+  return draft_rows(ctx, "dfl_draft_batch", 0, n_seq, noise_emb, ids, B, out_hidden, out_prenorm,
+                    out_logits, out_ids, stream);
+}
+
+int dfl_select_seq(dfl_ctx* ctx, int32_t seq) {
+  if (!ctx) return fail(DFL_EINVAL, "dfl_select_seq: null context");
+  if (seq < 0 || seq >= ctx->S)
+    return fail(DFL_ERANGE, "dfl_select_seq: sequence " + std::to_string(seq) + " outside [0, " +
+                                std::to_string(ctx->S) + ")");
+  ctx->cur = seq;
   return DFL_OK;
 }
 
@@ -669,52 +724,53 @@ int dfl_set_num_layers(dfl_ctx* ctx, int32_t n) {
 int dfl_cache_trim(dfl_ctx* ctx, int32_t n) {
   if (!ctx) return fail(DFL_EINVAL, "dfl_cache_trim: null context");
   if (n < 0) return fail(DFL_EINVAL, "dfl_cache_trim: negative count");
-  const int k = std::min(n, ctx->len);   // DFlashKVCache.trim clamps the length at 0
-  ctx->len -= k;
-  ctx->offset -= n;
-  ctx->last_block = 0;
+  SeqState& q = ctx->sq();
+  const int k = std::min(n, q.len);   // DFlashKVCache.trim clamps the length at 0
+  q.len -= k;
+  q.offset -= n;
+  q.last_block = 0;
   return DFL_OK;
 }
 
 int dfl_cache_commit(dfl_ctx* ctx, int32_t n) {
   if (!ctx) return fail(DFL_EINVAL, "dfl_cache_commit: null context");
-  if (n < 0 || n > ctx->last_block)
+  SeqState& q = ctx->sq();
+  if (n < 0 || n > q.last_block)
     return fail(DFL_EINVAL, "dfl_cache_commit: n must be in [0, rows of the last block]");
-  if (ctx->len + n > ctx->cfg.max_ctx) return fail(DFL_ERANGE, "dfl_cache_commit: max_ctx exceeded");
-  ctx->len += n;
-  ctx->offset += n;
-  ctx->last_block = 0;
+  if (q.len + n > ctx->cfg.max_ctx) return fail(DFL_ERANGE, "dfl_cache_commit: max_ctx exceeded");
+  q.len += n;
+  q.offset += n;
+  q.last_block = 0;
   return DFL_OK;
 }
 
 int dfl_cache_reset(dfl_ctx* ctx) {
   if (!ctx) return fail(DFL_EINVAL, "dfl_cache_reset: null context");
-  ctx->len = 0;
-  ctx->offset = 0;
-  ctx->last_block = 0;
+  ctx->sq() = SeqState{};
   return DFL_OK;
 }
 
 int dfl_cache_set_offset(dfl_ctx* ctx, int64_t offset) {
   if (!ctx) return fail(DFL_EINVAL, "dfl_cache_set_offset: null context");
   if (offset < 0) return fail(DFL_EINVAL, "dfl_cache_set_offset: negative offset");
-  ctx->offset = offset;
-  ctx->last_block = 0;
+  ctx->sq().offset = offset;
+  ctx->sq().last_block = 0;
   return DFL_OK;
 }
 
 int dfl_cache_state(const dfl_ctx* ctx, int32_t* len, int64_t* offset) {
   if (!ctx) return fail(DFL_EINVAL, "dfl_cache_state: null context");
-  if (len) *len = ctx->len;
-  if (offset) *offset = ctx->offset;
+  const SeqState& q = ctx->seqs[ctx->cur];
+  if (len) *len = q.len;
+  if (offset) *offset = q.offset;
   return DFL_OK;
 }
 
 int dfl_cache_kv(const dfl_ctx* ctx, int32_t layer, uint16_t** k, uint16_t** vt, int32_t* cap) {
   if (!ctx) return fail(DFL_EINVAL, "dfl_cache_kv: null context");
   if (layer < 0 || layer >= ctx->NL) return fail(DFL_ERANGE, "dfl_cache_kv: layer out of range");
-  if (k) *k = reinterpret_cast<uint16_t*>(ctx->layers[layer].Kc);
-  if (vt) *vt = reinterpret_cast<uint16_t*>(ctx->layers[layer].Vt);
+  if (k) *k = reinterpret_cast<uint16_t*>(ctx->kc(ctx->layers[layer], ctx->cur));
+  if (vt) *vt = reinterpret_cast<uint16_t*>(ctx->vt(ctx->layers[layer], ctx->cur));
   if (cap) *cap = ctx->cap;
   return DFL_OK;
 }

@@ -251,7 +251,7 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(AttnArgs a) {
 #pragma unroll 8
   for (int c = 0; c < nc; ++c) num += op[(size_t)c * NB * 128] * wts[c];
   const int h = rowg / a.B, b = rowg - h * a.B;
-  a.O[afl_index(b, h * 128 + d, a.NH * 128)] = f2h(num / den_s);
+  a.O[afl_index(a.o_row0 + b, h * 128 + d, a.NH * 128)] = f2h(num / den_s);
 }
 
 void launch_block_attention(const AttnArgs& a_in, hipStream_t st) {

@@ -128,7 +128,9 @@ struct AttnArgs {
   float scale_log2;       // head_dim^-0.5 * log2(e)
   float* Op;              // [n_chunks][NH*B][128] unnormalised partial outputs
   float* Ml;              // [n_chunks][NH*B][2] running (max, sum) in log2 domain
-  half_t* O;              // [B][NH*128] final output, activation fragment layout
+  half_t* O;              // final output rows o_row0 .. o_row0 + B - 1 of an activation
+                          // fragment layout tile set with NH*128 columns
+  int o_row0;
 };
 void launch_block_attention(const AttnArgs& a, hipStream_t st);
 

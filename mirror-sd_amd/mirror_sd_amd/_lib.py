@@ -30,6 +30,7 @@ class DflConfig(ctypes.Structure):
         ("head_dim", c_int32), ("intermediate", c_int32), ("n_layers", c_int32),
         ("n_target_feat", c_int32), ("vocab", c_int32), ("max_block", c_int32),
         ("max_ctx", c_int32), ("rms_eps", ctypes.c_float), ("rope_theta", ctypes.c_double),
+        ("max_seqs", c_int32),
     ]
 
 
@@ -49,6 +50,9 @@ SIGNATURES = {
     "dfl_ingest_fused": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p]),
     "dfl_draft_block": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, c_void_p, c_void_p,
                                   c_void_p, c_void_p, c_void_p]),
+    "dfl_draft_batch": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p, c_int32, c_void_p,
+                                  c_void_p, c_void_p, c_void_p, c_void_p]),
+    "dfl_select_seq": (c_int32, [c_void_p, c_int32]),
     "dfl_set_num_layers": (c_int32, [c_void_p, c_int32]),
     "dfl_cache_trim": (c_int32, [c_void_p, c_int32]),
     "dfl_cache_commit": (c_int32, [c_void_p, c_int32]),

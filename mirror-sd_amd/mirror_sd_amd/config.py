@@ -141,6 +141,7 @@ class Workload:
     description: str = ""
     with_lm_head: bool = True
     n_feat: int = 5
+    seq_ctx: tuple = ()   # batched workloads: context rows of each sequence
 
 
 def _draft_cfg(hidden, heads, kv_heads, ffn, layers, vocab=151936, theta=1e6,
@@ -164,6 +165,8 @@ def workload(name: str) -> Workload:
     qwen3_8b_draft  : 5 layers, H4096, 32/8, FFN 12288, block 16, ctx 2048, V151936.
     dflash_27b      : 5 layers, H5120, 40/8, FFN 17408, block 32, ctx 4096, V151936.
     dflash_27b_ctxN : dflash_27b at context N (64, 2048, 4096, 16384, 32768).
+    llama8b_batch   : 5 layers, H4096, 32/8, FFN 14336, V128256, theta 5e5; 8 sequences x
+                      block 32 with contexts U[512, 8192] from seed 1 (mask id V-1).
     """
     if name == "qwen3_4b_layer":
         cfg = _draft_cfg(2560, 32, 8, 9728, 1, block=16)
@@ -178,6 +181,14 @@ def workload(name: str) -> Workload:
         cfg = _draft_cfg(5120, 40, 8, 17408, 5, block=32)
         return Workload(name, cfg, block=32, ctx=ctx,
                         description=f"5 layers, H5120, 40/8 heads, FFN 17408, block 32, ctx {ctx}, V151936")
+    if name == "llama8b_batch":
+        # 8 independent sequences x block 32; ragged contexts drawn U[512, 8192] from seed 1
+        import numpy as np
+        ctxs = tuple(int(c) for c in np.random.default_rng(1).integers(512, 8193, 8))
+        cfg = _draft_cfg(4096, 32, 8, 14336, 5, vocab=128256, theta=5e5, block=32)
+        return Workload(name, cfg, block=32, ctx=max(ctxs), seq_ctx=ctxs,
+                        description="5 layers, H4096, 32/8 heads, FFN 14336, V128256, theta 5e5, "
+                                    f"8 sequences x block 32, contexts {list(ctxs)}")
     if name == "tiny":
         cfg = _draft_cfg(256, 4, 2, 512, 2, vocab=1024, block=8)
         return Workload(name, cfg, block=8, ctx=24, description="test shape")

@@ -95,7 +95,7 @@ class DFlashDraftModel:
     """MI355X draft model behind the reference ``DFlashDraftModel`` interface."""
 
     def __init__(self, config: DFlashConfig, max_ctx: int = 8192, max_block: Optional[int] = None,
-                 device=None, n_target_feat: Optional[int] = None):
+                 device=None, n_target_feat: Optional[int] = None, max_seqs: int = 1):
         import torch
         self.config = config
         self.block_size = config.block_size
@@ -112,7 +112,8 @@ class DFlashDraftModel:
             intermediate=config.intermediate_size, n_layers=config.num_hidden_layers,
             n_target_feat=self.n_feat, vocab=config.vocab_size, max_block=self.max_block,
             max_ctx=self.max_ctx_len, rms_eps=config.rms_norm_eps,
-            rope_theta=float(config.rope_theta))
+            rope_theta=float(config.rope_theta), max_seqs=int(max_seqs))
+        self.max_seqs = max(1, int(max_seqs))
         h = ctypes.c_void_p()
         with torch.cuda.device(self.device):
             _lib.check(self._L.dfl_create(ctypes.byref(cfg), ctypes.byref(h)), "dfl_create")
@@ -435,6 +436,70 @@ class DFlashDraftModel:
             res.append(out_l)
         if return_hidden:
             res.append(out_h)
+        return res[0] if len(res) == 1 else tuple(res)
+
+    # ------------------------------------------------------------------ batched drafting
+    def select_seq(self, seq: int):
+        """Address sequence ``seq`` with the single-sequence calls (ingest, draft, cache)."""
+        _lib.check(self._L.dfl_select_seq(self._ctx, int(seq)), "dfl_select_seq")
+
+    def cache_tensors(self, seq: int = 0):
+        """Device views (K [NKV, cap, 128], Vt [NKV, 128, cap]) per layer of one sequence."""
+        self.select_seq(seq)
+        try:
+            return self._make_cache_views()
+        finally:
+            self.select_seq(0)
+
+    def ingest_seq(self, seq: int, target_hidden, fused_context: bool = False, reset: bool = True):
+        """Append context rows to sequence ``seq``'s cache (fc fusion + per-layer K/V),
+        after clearing it when ``reset``."""
+        self._apply_num_layers()
+        self.select_seq(seq)
+        try:
+            if reset:
+                _lib.check(self._L.dfl_cache_reset(self._ctx), "dfl_cache_reset")
+            self._ingest(target_hidden, fused=fused_context)
+        finally:
+            self.select_seq(0)
+
+    def draft_batch(self, ids=None, noise=None, return_logits=False, return_hidden=False):
+        """One block for each of sequences 0 .. n_seq-1 at once: ``ids`` [n_seq, B] (or
+        ``noise`` [n_seq, B, H]) -> argmax ids [n_seq, B] (+ fp32 logits [n_seq, B, V],
+        final-normed hidden [n_seq, B, H]).  Each sequence attends to its own cached
+        context plus its block (the block rows stay uncommitted, as after draft())."""
+        import torch
+        self._apply_num_layers()
+        H, V = self.config.hidden_size, self.config.vocab_size
+        if noise is not None:
+            noise = noise.to(self.device, torch.float16).contiguous()
+            n_seq, B = noise.shape[0], noise.shape[1]
+            if noise.dim() != 3 or noise.shape[2] != H:
+                raise ValueError(f"noise must be [n_seq, B, {H}]")
+            src_n, src_i = noise, None
+        else:
+            ids = torch.as_tensor(ids, dtype=torch.int32)
+            if ids.dim() != 2:
+                raise ValueError("ids must be [n_seq, B]")
+            n_seq, B = ids.shape
+            if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= V):
+                raise ValueError(f"token id outside [0, {V})")
+            src_n, src_i = None, ids.to(self.device).contiguous()
+        if not all(self._layers_loaded[:self.num_draft_layers]) or not self._has_lm:
+            raise RuntimeError("weights (with lm_head) not loaded")
+        M = n_seq * B
+        out_h = torch.empty((M, H), dtype=torch.float16, device=self.device) if return_hidden else None
+        out_l = torch.empty((M, V), dtype=torch.float32, device=self.device) if return_logits else None
+        out_i = torch.empty((M,), dtype=torch.int32, device=self.device)
+        _lib.check(self._L.dfl_draft_batch(
+            self._ctx, n_seq, _lib.ptr(src_n), _lib.ptr(src_i), B, _lib.ptr(out_h), None,
+            _lib.ptr(out_l), _lib.ptr(out_i), self._stream()), "dfl_draft_batch")
+        self._keep["draft_src"] = (src_n, src_i)
+        res = [out_i.reshape(n_seq, B)]
+        if return_logits:
+            res.append(out_l.reshape(n_seq, B, V))
+        if return_hidden:
+            res.append(out_h.reshape(n_seq, B, H))
         return res[0] if len(res) == 1 else tuple(res)
 
     # ------------------------------------------------------------------ profiling

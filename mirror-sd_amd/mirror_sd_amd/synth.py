@@ -202,3 +202,21 @@ def make_inputs_torch(cfg: DFlashConfig, block: int, ctx: int, seed: int = 0, de
     ids = np.full((block,), cfg.mask_token_id, dtype=np.int32)
     ids[0] = rng.integers(0, cfg.vocab_size)
     return {"target_hidden": th, "ids": torch.from_numpy(ids).to(device)}
+
+
+def make_batch_inputs_numpy(cfg: DFlashConfig, block: int, seq_ctx, seed: int = 0,
+                            n_feat: int = None):
+    """Inputs of a batched draft: per sequence i, ``target_hidden`` [seq_ctx[i], n_feat*H]
+    fp16 N(0,1) and block ids ``[id0, mask * (block-1)]`` (tensor names suffixed .s<i>)."""
+    H = cfg.hidden_size
+    nf = cfg.num_target_features if n_feat is None else n_feat
+    out = []
+    for i, c in enumerate(seq_ctx):
+        rng = np.random.default_rng([seed, _crc(f"input.ids.s{i}")])
+        ids = np.full((block,), cfg.mask_token_id, dtype=np.int32)
+        ids[0] = rng.integers(0, cfg.vocab_size)
+        out.append({"target_hidden": np_normal(seed, f"input.target_hidden.s{i}", (int(c), nf * H),
+                                               1.0, np.float16),
+                    "ids": ids})
+    return out
+

@@ -14,6 +14,10 @@ so a test can tell a change of the input recipe from a change of the results:
                   the top-2 logits per row.
   dflash_27b      5 layers, H5120, 40/8, FFN 17408, block 32, context 4096, V151936;
                   same outputs for 32 rows.
+  llama8b_batch   5 layers, H4096, 32/8, FFN 14336, V128256, theta 5e5; 8 independent
+                  sequences x block 32 with contexts [4146, 4443, 6312, 7812, 779, 1619, 6833,
+                  7798]; each sequence run through the single-sequence oracle; outputs stacked
+                  sequence-major: hidden [256, 4096], ids [256], top-2 logits per row.
 
 The oracle runs in its fp16-boundary mode (the MLX rounding points) with fp32
 accumulation for the two full models, fp64 for the single layer.
@@ -86,10 +90,32 @@ def case_full(name, seed=0):
                 top2_val=tv), dig
 
 
+def case_batch(name="llama8b_batch", seed=0):
+    wl = workload(name)
+    cfg = wl.cfg
+    t = synth.make_weights_numpy(cfg, seed=seed)
+    inps = synth.make_batch_inputs_numpy(cfg, wl.block, wl.seq_ctx, seed=seed)
+    dig = input_digests(t, {f"{k}.s{i}": v for i, inp in enumerate(inps) for k, v in inp.items()})
+    W = O.OracleWeights(cfg, t)
+    del t
+    hs, idss, tis, tvs = [], [], [], []
+    for inp in inps:
+        h, logits, ids = O.draft_block(W, inp["ids"], inp["target_hidden"], fp16=True,
+                                       dtype=np.float32)
+        ti, tv = top2(logits)
+        hs.append(h.astype(np.float16))
+        idss.append(ids.astype(np.int32))
+        tis.append(ti)
+        tvs.append(tv)
+    return dict(hidden=np.concatenate(hs), ids=np.concatenate(idss), top2_idx=np.concatenate(tis),
+                top2_val=np.concatenate(tvs)), dig
+
+
 CASES = {
     "qwen3_4b_layer": lambda: case_layer("qwen3_4b_layer"),
     "qwen3_8b_draft": lambda: case_full("qwen3_8b_draft"),
     "dflash_27b": lambda: case_full("dflash_27b"),
+    "llama8b_batch": lambda: case_batch("llama8b_batch"),
 }
 
 

@@ -53,3 +53,15 @@ def test_full_fixture_consistent(name):
     assert np.all(g["top2_val"][:, 0] >= g["top2_val"][:, 1])
     rms = np.sqrt((g["hidden"].astype(np.float64) ** 2).mean(-1))
     np.testing.assert_allclose(rms, 1.0, atol=5e-3)   # norm gains are 1
+
+
+def test_batch_fixture_inputs_match_recipe():
+    name = "llama8b_batch"
+    wl = workload(name)
+    t = synth.make_weights_numpy(wl.cfg, seed=0)
+    inps = synth.make_batch_inputs_numpy(wl.cfg, wl.block, wl.seq_ctx, seed=0)
+    dig = input_digests(t, {f"{k}.s{i}": v for i, inp in enumerate(inps) for k, v in inp.items()})
+    g = load(name)
+    assert dig == stored_digests(g)
+    assert g["ids"].shape == (wl.block * len(wl.seq_ctx),)
+    np.testing.assert_array_equal(g["ids"], g["top2_idx"][:, 0])
