@@ -29,6 +29,7 @@ int fail(int code, const std::string& msg) {
 
 constexpr int ING_ROWS = 1024;     // context rows per ingest pass
 constexpr int MAX_CHUNKS = 64;     // attention key splits
+constexpr int MT_MAX = 8;          // 32-row m-tiles per M-split GEMM launch
 constexpr int TARGET_WAVES = 2048; // ~8 waves per CU on 256 CUs
 
 struct GemmPlan {
@@ -277,6 +278,8 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
       tiles = std::max(tiles, (size_t)(pr.second / 64));
     }
     const size_t bm32 = ((Bm + 31) / 32) * 32;
+    // split-tile partials hold one 32x64 slot per m-tile of a launch
+    wsn *= (size_t)std::min<size_t>(MT_MAX, bm32 / 32);
     if ((r = x->alloc(&x->qkvbuf, Bm * x->NQKV)) || (r = x->alloc(&x->rnorm, bm32)) ||
         (r = x->alloc(&x->sk_ws, wsn)) || (r = x->alloc(&x->sk_tile_cnt, tiles, true)) ||
         (r = x->alloc(&x->sk_ss, (bm32 / 32) * (size_t)(x->H / 64) * 32))) {
@@ -418,17 +421,22 @@ static void gemm(dfl_ctx* ctx, int cat, int wt, int epi, const uint4* W, const h
   launch_skinny_gemm(wt, epi, a, p.SK, (M + 31) / 32, st);
 }
 
-// Stream-K GEMM over the M rows of a block, in 32-row m-tiles.  A normed input (gnorm
-// set) takes its 1/rms rows from the embedding kernel (rn_from_ss false) or from the row
-// sums of squares that the previous RESID GEMM left in sk_ss (rn_from_ss true).
+// Stream-K GEMM over the M rows of a block: one 32-row m-tile per launch of the
+// single-tile kernel, or up to 8 m-tiles per launch of the M-split kernel (each weight
+// block read once for all of them).  A normed input (gnorm set) takes its 1/rms rows from
+// the embedding kernel (rn_from_ss false) or from the row sums of squares that the
+// previous RESID GEMM left in sk_ss (rn_from_ss true).
 static void skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const SKPlan& p,
                    const uint4* W, const half_t* scale, int N, int KB, const half_t* X, int ldx,
                    int M, const half_t* gnorm, bool rn_from_ss, half_t* out, int ldo,
                    half_t* xres, float* logits, unsigned long long* keys, hipStream_t st) {
   const long long wbytes = (wt == WT_INT8) ? (long long)N * KB * 32 + 2LL * N
                                            : (long long)N * KB * 16 * 2;
-  const size_t ss_stride = (size_t)(ctx->H / 64) * 32;
-  for (int m0 = 0; m0 < M; m0 += 32) {
+  const int ss_stride = (ctx->H / 64) * 32;
+  const int n_mt = (M + 31) / 32;
+  for (int g0 = 0; g0 < n_mt; g0 += MT_MAX) {
+    const int mt_n = std::min(MT_MAX, n_mt - g0);
+    const int m0 = g0 * 32;
     ProfScope ps(ctx, cat, wbytes, st, /*attached=*/true);
     StreamArgs a{};
     a.W = W;
@@ -437,11 +445,13 @@ static void skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const SKPlan& p,
     a.KB = KB;
     a.X = X + (size_t)m0 * ldx;
     a.ldx = ldx;
-    a.M = std::min(32, M - m0);
+    a.M = std::min(32 * mt_n, M - m0);
+    a.MT = mt_n;
     a.rnorm = ctx->rnorm + m0;
-    a.ss_in = rn_from_ss ? ctx->sk_ss + (m0 / 32) * ss_stride : nullptr;
+    a.ss_in = rn_from_ss ? ctx->sk_ss + (size_t)g0 * ss_stride : nullptr;
     a.ss_tiles = ctx->H / 64;
     a.ss_n = ctx->H;
+    a.ss_mstride = ss_stride;
     a.gnorm = gnorm;
     a.ws = ctx->sk_ws;
     a.seg_cap = p.seg_cap;
@@ -449,12 +459,15 @@ static void skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const SKPlan& p,
     a.out = out ? out + (size_t)m0 * ldo : nullptr;
     a.ldo = ldo;
     a.x = xres ? xres + (size_t)m0 * ldo : nullptr;
-    a.ss_part = ctx->sk_ss + (m0 / 32) * ss_stride;
+    a.ss_part = ctx->sk_ss + (size_t)g0 * ss_stride;
     a.eps = ctx->cfg.rms_eps;
     a.logits = logits ? logits + (size_t)m0 * N : nullptr;
     a.ldl = N;
     a.keys = keys ? keys + m0 : nullptr;
-    launch_streamk_gemm(wt, epi, gnorm != nullptr, a, p, st, ps.start(), ps.stop());
+    if (mt_n == 1)
+      launch_streamk_gemm(wt, epi, gnorm != nullptr, a, p, st, ps.start(), ps.stop());
+    else
+      launch_streamk_gemm_m(wt, epi, gnorm != nullptr, a, p, st, ps.start(), ps.stop());
   }
 }
 

@@ -38,9 +38,11 @@ struct StreamArgs {
   int N, KB;                // KB = K/32 (int8) or K/16 (fp16)
   const half_t* X;          // activations: one 32-row tile in the fragment layout (afl_offset)
   int ldx, M;
+  int MT;                   // M-split kernel: 32-row m-tiles of X (M <= 32 * MT)
   const float* rnorm;       // NORM: per-row 1/rms of X (used when ss_in is null)
   const float* ss_in;       // NORM: [ss_tiles][32] row sums of squares of X (RESID output)
   int ss_tiles, ss_n;       //       tiles of ss_in, and the row length they sum over
+  int ss_mstride;           // floats from one m-tile's ss_in / ss_part block to the next
   const half_t* gnorm;      // NORM: [K] gain (K <= 8192)
   float* ws;                // [N/64][seg_cap][2048] partials of tiles split across workgroups
   int seg_cap;
@@ -59,6 +61,13 @@ struct SKPlan {
   int seg_cap = 1;          // workspace slots per tile
 };
 SKPlan streamk_plan(int N, int KB, int n_cu);
+// M-split variant for 2 <= MT <= 8 m-tiles (M <= 256 rows): every weight block is read
+// once for all m-tiles.  X, out, x, ss_*, rnorm, logits, keys point at m-tile 0; m-tile mt
+// is 32*mt rows further (ss blocks ss_mstride floats further).  ws holds
+// [N/64][seg_cap][MT][2048] floats.
+void launch_streamk_gemm_m(int wt, int epi, bool norm, const StreamArgs& a, const SKPlan& p,
+                           hipStream_t st, hipEvent_t ev_start = nullptr,
+                           hipEvent_t ev_stop = nullptr);
 // ev_start / ev_stop (optional) receive the kernel's own start and end timestamps.
 void launch_streamk_gemm(int wt, int epi, bool norm, const StreamArgs& a, const SKPlan& p,
                          hipStream_t st, hipEvent_t ev_start = nullptr,

@@ -277,9 +277,11 @@ DFL_DEV void tile_epilogue(const StreamArgs& a, int lane, int t, const floatx16&
     for (int q = 0; q < 4; ++q) {
       half4_t o0, o1;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        o0[c] = f2h(acc0[4 * q + c] * h2f(a.scale[nb + 8 * q + c]));
-        o1[c] = f2h(acc1[4 * q + c] * h2f(a.scale[nb + 32 + 8 * q + c]));
+      for (int c = 0; c < 4; ++c) {   // fp16 weights carry no scale
+        const float s0 = a.scale ? h2f(a.scale[nb + 8 * q + c]) : 1.0f;
+        const float s1 = a.scale ? h2f(a.scale[nb + 32 + 8 * q + c]) : 1.0f;
+        o0[c] = f2h(acc0[4 * q + c] * s0);
+        o1[c] = f2h(acc1[4 * q + c] * s1);
       }
       *reinterpret_cast<half4_t*>(dst + 8 * q) = o0;
       *reinterpret_cast<half4_t*>(dst + 32 + 8 * q) = o1;
@@ -383,6 +385,165 @@ DFL_DEV float rn_from_ss(const float* ss, int tiles, int n, float eps, int lane)
   return 1.0f / sqrtf(tot / (float)n + eps);
 }
 
+// ---------------------------------------------------------------------------------------
+// M-split mode (2 <= MT <= 8 activation m-tiles): streaming wave w owns m-tiles
+// w*MTW .. w*MTW + MTW - 1 and walks every unit of the workgroup range in order, so each
+// weight block is read from HBM once (the other waves hit the cache) and dequantised in
+// registers once per wave for MTW m-tiles.  At each tile end the wave hands its MTW
+// partials to the reducer through LDS slot set (segment & 1).
+// ---------------------------------------------------------------------------------------
+template <int WT, bool NORM, int P, int MTW>
+DFL_DEV void stream_range_m(const StreamArgs& a, const half_t* gsh, const float* rn_lds,
+                            int* ready, float (*red)[WG_WAVES][MTW][2048], int* arrived,
+                            int* reduced, long long u0, long long u1, int w, int lane) {
+  constexpr int KBK = KTraits<WT>::KBK;
+  constexpr int NX = KTraits<WT>::NX;
+  const int m = lane & 31, g = lane >> 5;
+  const int goff = (WT == WT_INT8 ? 16 * g : 8 * g);
+  const int KB = a.KB;
+  const int mt0 = w * MTW;
+  const int nmt = max(0, min(MTW, a.MT - mt0));   // m-tiles of this wave
+  const size_t xstride = (size_t)32 * a.ldx;      // halves from one AFL m-tile to the next
+
+  floatx16 acc[MTW][2];
+#pragma unroll
+  for (int j = 0; j < MTW; ++j) acc[j][0] = acc[j][1] = (floatx16){};
+  int si = 0;
+  auto flush = [&]() {
+    while (__hip_atomic_load(reduced, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < si - 1)
+      __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int j = 0; j < MTW; ++j) {
+      float* dst = red[si & 1][w][j];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        dst[r * 64 + lane] = acc[j][0][r];
+        dst[1024 + r * 64 + lane] = acc[j][1][r];
+      }
+      acc[j][0] = acc[j][1] = (floatx16){};
+    }
+    if (lane == 0)
+      __hip_atomic_fetch_add(&arrived[si & 1], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    ++si;
+  };
+  const int t_first = (int)(u0 / KB);
+  const int t_last = (int)((u1 - 1) / KB);
+  if (nmt == 0) {   // no m-tile here: hand over zero partials, in step with the others
+    for (int t = t_first; t <= t_last; ++t) flush();
+    return;
+  }
+  const u32x4* xf[MTW];
+#pragma unroll
+  for (int j = 0; j < MTW; ++j)
+    xf[j] = reinterpret_cast<const u32x4*>(a.X + (size_t)(mt0 + min(j, nmt - 1)) * xstride);
+
+  const int J = (int)(u1 - u0);
+  int ct = t_first;
+  int it = t_first, ikb = (int)(u0 - (long long)t_first * KB), issued = 0;
+  struct Stage {
+    u32x4 w0[P], w1[P], x[P][MTW][NX];
+    int kb[P], t[P];
+  };
+  auto issue = [&](Stage& st) {
+    static_for<0, P>([&](auto s) {
+      const uint4* wp = a.W + ((size_t)(2 * it) * KB + ikb) * 64 + lane;
+      st.w0[s] = load_stream(wp);
+      st.w1[s] = load_stream(wp + (size_t)KB * 64);
+      st.kb[s] = ikb;
+      st.t[s] = it;
+#pragma unroll
+      for (int j = 0; j < MTW; ++j) {
+        if constexpr (WT == WT_INT8) {
+          st.x[s][j][0] = xf[j][(size_t)(2 * ikb) * 64 + lane];
+          st.x[s][j][NX - 1] = xf[j][(size_t)(2 * ikb + 1) * 64 + lane];
+        } else {
+          st.x[s][j][0] = xf[j][(size_t)((ikb >> 1) * 2 + g) * 64 + m + 32 * (ikb & 1)];
+        }
+      }
+      if (++issued < J) {
+        if (++ikb == KB) {
+          ikb = 0;
+          ++it;
+        }
+      }
+    });
+  };
+  float rn[MTW];
+#pragma unroll
+  for (int j = 0; j < MTW; ++j) rn[j] = 1.0f;
+  auto consume = [&](const Stage& st, int base) {
+    static_for<0, P>([&](auto s) {
+      if (base + (int)s < J) {
+        while (ct < st.t[s]) {
+          flush();
+          ++ct;
+        }
+        half8_t lo0, hi0, lo1, hi1;
+        if constexpr (WT == WT_INT8) {
+          dequant_i8x16(st.w0[s], lo0, hi0);
+          dequant_i8x16(st.w1[s], lo1, hi1);
+        }
+#pragma unroll
+        for (int j = 0; j < MTW; ++j) {
+          if (j < nmt) {
+            u32x4 xa = st.x[s][j][0], xb = st.x[s][j][NX - 1];
+            if constexpr (NORM) {
+              const int kk = st.kb[s] * KBK + goff;
+              xa = norm8(xa, rn[j], *reinterpret_cast<const u32x4*>(gsh + kk));
+              if constexpr (NX > 1)
+                xb = norm8(xb, rn[j], *reinterpret_cast<const u32x4*>(gsh + kk + 8));
+              else xb = xa;
+            }
+            if constexpr (WT == WT_INT8) {
+              const half8_t xl = as_half8(xa), xh = as_half8(xb);
+              acc[j][0] = mfma32x32x16(lo0, xl, acc[j][0]);
+              acc[j][1] = mfma32x32x16(lo1, xl, acc[j][1]);
+              acc[j][0] = mfma32x32x16(hi0, xh, acc[j][0]);
+              acc[j][1] = mfma32x32x16(hi1, xh, acc[j][1]);
+            } else {
+              const half8_t xv = as_half8(xa);
+              acc[j][0] = mfma32x32x16(as_half8(st.w0[s]), xv, acc[j][0]);
+              acc[j][1] = mfma32x32x16(as_half8(st.w1[s]), xv, acc[j][1]);
+            }
+          }
+        }
+      }
+    });
+  };
+
+  Stage A, B;
+  issue(A);
+  if constexpr (NORM) {
+    while (__hip_atomic_load(ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
+      __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int j = 0; j < MTW; ++j) rn[j] = rn_lds[(mt0 + min(j, nmt - 1)) * 32 + m];
+  }
+  for (int base = 0; base < J; base += 2 * P) {
+    issue(B);
+    __builtin_amdgcn_sched_barrier(0);
+    consume(A, base);
+    if (base + P >= J) break;
+    issue(A);
+    __builtin_amdgcn_sched_barrier(0);
+    consume(B, base + P);
+  }
+  for (int t = ct; t <= t_last; ++t) flush();
+}
+
+// The arguments of m-tile mt as seen by tile_epilogue (a 32-row view).
+DFL_DEV StreamArgs mtile_view(const StreamArgs& a, int mt) {
+  StreamArgs v = a;
+  v.M = min(32, a.M - 32 * mt);
+  const size_t rows = (size_t)32 * mt;
+  if (a.out) v.out = a.out + rows * a.ldo;   // STORE rows / SWIGLU AFL tiles (ldo = N/2)
+  if (a.x) v.x = a.x + rows * a.N;           // RESID AFL tiles
+  if (a.ss_part) v.ss_part = a.ss_part + (size_t)mt * a.ss_mstride;
+  if (a.logits) v.logits = a.logits + rows * a.ldl;
+  if (a.keys) v.keys = a.keys + rows;
+  return v;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------------------
@@ -461,6 +622,118 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_gemm_kernel(StreamArg
 }
 
 // ---------------------------------------------------------------------------------------
+// The M-split stream-K kernel (2 <= MT <= 8): same partition, reducer and completion as
+// gsk_gemm_kernel, with the m-tiles (not the k-blocks) divided among the streaming waves.
+// ---------------------------------------------------------------------------------------
+template <int WT, int EPI, bool NORM, int P, int MTW>
+__global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_gemm_m_kernel(StreamArgs a) {
+  constexpr int KBK = KTraits<WT>::KBK;
+  __shared__ float red[2][WG_WAVES][MTW][2048];
+  __shared__ half_t gsh[NORM ? 8192 : 8];
+  __shared__ float rn_s[32 * WG_WAVES * MTW];
+  __shared__ int arrived[2], reduced, ready;
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int G = gridDim.x;
+  const int b = blockIdx.x;
+  const long long U = (long long)(a.N >> 6) * a.KB;
+  const long long u0 = (long long)b * U / G, u1 = (long long)(b + 1) * U / G;
+  if (u0 >= u1) return;
+  if (threadIdx.x == 0) {
+    arrived[0] = arrived[1] = 0;
+    reduced = 0;
+    ready = 0;
+  }
+  __syncthreads();
+
+  if (w < WG_WAVES) {
+    stream_range_m<WT, NORM, P, MTW>(a, gsh, rn_s, &ready, red, arrived, &reduced, u0, u1, w,
+                                     lane);
+    return;
+  }
+
+  // ---- reducer wave ----
+  if constexpr (NORM) {
+    const int K = a.KB * KBK;
+    for (int k = lane * 8; k < K; k += 64 * 8)
+      *reinterpret_cast<u32x4*>(gsh + k) = *reinterpret_cast<const u32x4*>(a.gnorm + k);
+    for (int mt = 0; mt < a.MT; ++mt) {
+      const float rn = a.ss_in ? rn_from_ss(a.ss_in + (size_t)mt * a.ss_mstride, a.ss_tiles,
+                                            a.ss_n, a.eps, lane)
+                               : a.rnorm[mt * 32 + (lane & 31)];
+      if (lane < 32) rn_s[mt * 32 + lane] = rn;
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    if (lane == 0) __hip_atomic_store(&ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  int si = 0;
+  for (long long u = u0; u < u1; ++si) {
+    const int t = (int)(u / a.KB);
+    const int kbs = (int)(u - (long long)t * a.KB);
+    const int kbe = (int)min((long long)a.KB, (long long)kbs + (u1 - u));
+    while (__hip_atomic_load(&arrived[si & 1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
+           WG_WAVES * ((si >> 1) + 1))
+      __builtin_amdgcn_s_sleep(1);
+    const bool whole = (kbs == 0 && kbe == a.KB);
+    int slot = 0, count = 1;
+    if (!whole) {
+      const long long tu0 = (long long)t * a.KB;
+      const int first = worker_of(tu0, U, G);
+      count = worker_of(tu0 + a.KB - 1, U, G) - first + 1;
+      slot = b - first;
+    }
+    // whole tile: epilogue straight from LDS; split tile: publish all m-tile partials,
+    // then the last workgroup to arrive sums them slot by slot
+    for (int mt = 0; mt < a.MT; ++mt) {
+      const float* src = red[si & 1][mt / MTW][mt % MTW];
+      floatx16 acc0, acc1;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        acc0[r] = src[r * 64 + lane];
+        acc1[r] = src[1024 + r * 64 + lane];
+      }
+      if (whole) {
+        tile_epilogue<EPI>(mtile_view(a, mt), lane, t, acc0, acc1);
+      } else {
+        float* mine = a.ws + (((size_t)t * a.seg_cap + slot) * a.MT + mt) * 2048;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          store_agent(mine + r * 64 + lane, acc0[r]);
+          store_agent(mine + 1024 + r * 64 + lane, acc1[r]);
+        }
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);   // slot reads (and partial stores) done
+    if (lane == 0) __hip_atomic_store(&reduced, si + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (!whole) {
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      int prev = 0;
+      if (lane == 0)
+        prev = __hip_atomic_fetch_add(a.tile_cnt + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      prev = __shfl(prev, 0, 64);
+      if (prev == count - 1) {
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        for (int mt = 0; mt < a.MT; ++mt) {
+          floatx16 acc0 = (floatx16){}, acc1 = (floatx16){};
+          for (int j = 0; j < count; ++j) {
+            const float* src = a.ws + (((size_t)t * a.seg_cap + j) * a.MT + mt) * 2048;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              acc0[r] += load_agent(src + r * 64 + lane);
+              acc1[r] += load_agent(src + 1024 + r * 64 + lane);
+            }
+          }
+          tile_epilogue<EPI>(mtile_view(a, mt), lane, t, acc0, acc1);
+        }
+        if (lane == 0) a.tile_cnt[t] = 0;   // next use is a later launch
+      }
+    }
+    u += kbe - kbs;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // Host-side planning and launch
 // ---------------------------------------------------------------------------------------
 
@@ -489,6 +762,42 @@ static void launch_t(const StreamArgs& a, const SKPlan& p, hipStream_t st, hipEv
     hipExtLaunchKernelGGL((gsk_gemm_kernel<WT, EPI, NORM, 4>), grid, block, 0, st, e0, e1, 0, a);
   else
     hipLaunchKernelGGL((gsk_gemm_kernel<WT, EPI, NORM, 4>), grid, block, 0, st, a);
+}
+
+template <int WT, int EPI, bool NORM, int MTW>
+static void launch_m_w(const StreamArgs& a, const SKPlan& p, hipStream_t st, hipEvent_t e0,
+                       hipEvent_t e1) {
+  constexpr int P = (WT == WT_INT8) ? 3 : 4;
+  const dim3 grid(p.workers), block(64 * (WG_WAVES + 1));
+  if (e0 || e1)
+    hipExtLaunchKernelGGL((gsk_gemm_m_kernel<WT, EPI, NORM, P, MTW>), grid, block, 0, st, e0, e1,
+                          0, a);
+  else
+    hipLaunchKernelGGL((gsk_gemm_m_kernel<WT, EPI, NORM, P, MTW>), grid, block, 0, st, a);
+}
+
+// One m-tile per streaming wave up to 4 m-tiles, two up to 8.
+template <int WT, int EPI, bool NORM>
+static void launch_m_t(const StreamArgs& a, const SKPlan& p, hipStream_t st, hipEvent_t e0,
+                       hipEvent_t e1) {
+  if (a.MT <= WG_WAVES) launch_m_w<WT, EPI, NORM, 1>(a, p, st, e0, e1);
+  else launch_m_w<WT, EPI, NORM, 2>(a, p, st, e0, e1);
+}
+
+void launch_streamk_gemm_m(int wt, int epi, bool norm, const StreamArgs& a, const SKPlan& p,
+                           hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop) {
+#define DFL_SKM_CASE(W_, E_)                                         \
+  if (wt == W_ && epi == E_) {                                       \
+    if (norm) launch_m_t<W_, E_, true>(a, p, st, ev_start, ev_stop); \
+    else launch_m_t<W_, E_, false>(a, p, st, ev_start, ev_stop);     \
+    return;                                                          \
+  }
+  DFL_SKM_CASE(WT_INT8, EPI_STORE)
+  DFL_SKM_CASE(WT_INT8, EPI_RESID)
+  DFL_SKM_CASE(WT_INT8, EPI_SWIGLU)
+  DFL_SKM_CASE(WT_F16, EPI_ARGMAX)
+  DFL_SKM_CASE(WT_F16, EPI_STORE)
+#undef DFL_SKM_CASE
 }
 
 void launch_streamk_gemm(int wt, int epi, bool norm, const StreamArgs& a, const SKPlan& p,

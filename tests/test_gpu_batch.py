@@ -36,16 +36,19 @@ def _check_ids(ids, lg, ref_ids, top2_idx, top2_val, what):
     assert not bad.any(), f"{what}: argmax differs at rows {np.nonzero(bad)[0].tolist()}"
 
 
-def test_batch_small_matches_oracle_and_single_sequence():
+@pytest.mark.parametrize("seq_ctx,B", [((24, 5, 17), 8),                       # 24 rows
+                                       ((7, 30, 11, 2, 19, 25, 4, 13), 16),   # 128 rows
+                                       ((9, 3, 28, 14, 6, 21), 32)])          # 192 rows
+def test_batch_small_matches_oracle_and_single_sequence(seq_ctx, B):
+    """Stacked rows below one m-tile, 4 m-tiles and 6 m-tiles (the single-tile and the
+    two M-split GEMM variants)."""
     from mirror_sd_amd.dflash import DFlashDraftModel
     wl = workload("tiny")
     cfg = wl.cfg
-    seq_ctx = (24, 5, 17)
-    B = wl.block
     t = synth.make_weights_numpy(cfg, seed=3)
     inps = synth.make_batch_inputs_numpy(cfg, B, seq_ctx, seed=3)
     W = O.OracleWeights(cfg, t)
-    m = DFlashDraftModel(cfg, max_ctx=max(seq_ctx), max_seqs=len(seq_ctx))
+    m = DFlashDraftModel(cfg, max_ctx=max(seq_ctx), max_block=B, max_seqs=len(seq_ctx))
     m.load_weights(torch_tensors(t, "cuda"))
     for i, inp in enumerate(inps):
         m.ingest_seq(i, torch.from_numpy(inp["target_hidden"]))
