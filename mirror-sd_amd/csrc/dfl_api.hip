@@ -27,27 +27,9 @@ int fail(int code, const std::string& msg) {
     if (e_ != hipSuccess) return fail(DFL_EHIP, std::string(#x) + ": " + hipGetErrorString(e_)); \
   } while (0)
 
-constexpr int ING_ROWS = 1024;     // context rows per ingest pass
+constexpr int ING_ROWS = 256;      // context rows per ingest pass (8 m-tiles)
 constexpr int MAX_CHUNKS = 64;     // attention key splits
 constexpr int MT_MAX = 8;          // 32-row m-tiles per M-split GEMM launch
-constexpr int TARGET_WAVES = 2048; // ~8 waves per CU on 256 CUs
-
-struct GemmPlan {
-  int SK = 4;
-  int S_x = 1;
-};
-
-GemmPlan plan_for(int N, int KB, int epi) {
-  GemmPlan p;
-  const int n_wt = N / 64;
-  p.SK = (n_wt >= TARGET_WAVES) ? 1 : (2 * n_wt >= TARGET_WAVES ? 2 : 4);
-  if (epi != EPI_PARTIAL) return p;
-  const int waves = n_wt * p.SK;
-  int sx = (TARGET_WAVES + waves - 1) / waves;
-  const int maxsx = std::max(1, KB / (p.SK * 2));
-  p.S_x = std::max(1, std::min(std::min(sx, maxsx), 16));
-  return p;
-}
 
 enum ProfCat { P_GEMM_W8 = 0, P_LM_HEAD, P_ATTN, P_QK_ROPE, P_ROWS, P_INGEST_FC, P_INGEST_KV, P_N };
 const char* const kProfNames[P_N] = {"gemm_w8a16",   "lm_head_argmax", "attention",
@@ -98,8 +80,7 @@ struct dfl_ctx {
   bool head_loaded = false;
   int active = 0;   // layers run per call (num_draft_layers)
   half_t *x = nullptr, *h = nullptr, *Q = nullptr, *attn = nullptr, *act = nullptr,
-         *ctxbuf = nullptr;
-  float* ws = nullptr;
+         *ctxbuf = nullptr;   // ctxbuf: fragment-layout tiles of the pass's fused context rows
   float *Op = nullptr, *Ml = nullptr;
   unsigned long long* keys = nullptr;
   int* err = nullptr;
@@ -111,10 +92,11 @@ struct dfl_ctx {
   int* sk_tile_cnt = nullptr;    // [max tiles]
   float* sk_ss = nullptr;        // [m-tiles][H/64][32] row sums of squares of x (RESID output)
   SKPlan sk_qkv, sk_o, sk_gu, sk_down, sk_lm;
-  float* ss_part = nullptr;   // [rows][ceil(H/1024)] per-chunk sums of squares
-  int* row_cnt = nullptr;     // [rows] arrival counters of the reduce kernel
-  half_t* fc_out = nullptr;   // [ING_ROWS][H] rounded fc output (ingest)
-  GemmPlan p_qkv, p_o, p_gu, p_down, p_lm;
+  // context ingest (ING_ROWS rows per pass)
+  half_t* ing_x = nullptr;    // fragment-layout tiles of the pass's target_hidden rows
+  half_t* fc_out = nullptr;   // [ING_ROWS][H] fc output (fp16, row-major)
+  half_t* kvbuf = nullptr;    // [ING_ROWS][2*NKV*128] K|V projections (fp16, row-major)
+  SKPlan sk_ifc, sk_ikv;
   std::vector<void*> allocs;
   int prof = 0;   // 0 off, 1 every kernel group, 2 stream-K GEMM launches only
   std::vector<ProfRec> recs;
@@ -232,28 +214,20 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
   x->seqs.resize(x->S);
   x->layers.resize(c.n_layers);
   x->active = c.n_layers;
-  x->p_qkv = plan_for(x->NQKV, x->H / 32, EPI_PARTIAL);
-  x->p_o = plan_for(x->H, x->NH * 128 / 32, EPI_PARTIAL);
-  x->p_gu = plan_for(2 * x->F, x->H / 32, EPI_SWIGLU);
-  x->p_down = plan_for(x->H, x->F / 32, EPI_PARTIAL);
-  x->p_lm = plan_for(std::max(x->V, 64), x->H / 16, EPI_ARGMAX);
 
   const size_t Bm = x->RM;   // activation rows of a (batched) block step
-  size_t ws = std::max({(size_t)x->p_qkv.S_x * Bm * x->NQKV, (size_t)x->p_o.S_x * Bm * x->H,
-                        (size_t)x->p_down.S_x * Bm * x->H});
-  ws = std::max(ws, (size_t)ING_ROWS * std::max(x->H, 2 * x->NKV * 128));
   int r = DFL_OK;
   // x / attn / act are 32-row tiles in the activation fragment layout (zero padded rows)
   const size_t Bt = ((Bm + 31) / 32) * 32;
   if ((r = x->alloc(&x->x, Bt * x->H, true)) || (r = x->alloc(&x->h, Bm * x->H)) ||
       (r = x->alloc(&x->Q, (size_t)x->NH * Bm * 128)) ||
       (r = x->alloc(&x->attn, Bt * x->NH * 128, true)) || (r = x->alloc(&x->act, Bt * x->F, true)) ||
-      (r = x->alloc(&x->ctxbuf, (size_t)ING_ROWS * x->H)) || (r = x->alloc(&x->ws, ws)) ||
+      (r = x->alloc(&x->ctxbuf, (size_t)ING_ROWS * x->H)) ||
+      (r = x->alloc(&x->ing_x, (size_t)ING_ROWS * std::max(1, x->NF) * x->H)) ||
+      (r = x->alloc(&x->kvbuf, (size_t)ING_ROWS * 2 * x->NKV * 128)) ||
       (r = x->alloc(&x->Op, (size_t)MAX_CHUNKS * x->NH * Bm * 128)) ||
       (r = x->alloc(&x->Ml, (size_t)MAX_CHUNKS * x->NH * Bm * 2)) ||
       (r = x->alloc(&x->keys, Bm, true)) || (r = x->alloc(&x->err, 1, true)) ||
-      (r = x->alloc(&x->ss_part, std::max<size_t>(Bm, ING_ROWS) * 8)) ||
-      (r = x->alloc(&x->row_cnt, std::max<size_t>(Bm, ING_ROWS), true)) ||
       (r = x->alloc(&x->fc_out, (size_t)ING_ROWS * x->H))) {
     delete x;
     return r;
@@ -280,6 +254,11 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
     const size_t bm32 = ((Bm + 31) / 32) * 32;
     // split-tile partials hold one 32x64 slot per m-tile of a launch
     wsn *= (size_t)std::min<size_t>(MT_MAX, bm32 / 32);
+    // ingest GEMMs: fc (fp16, K = n_target_feat * H) and the K|V rows of w_qkv, 8 m-tiles
+    x->sk_ifc = plan(x->H, std::max(1, x->NF) * x->H / 16);
+    x->sk_ikv = plan(2 * x->NKV * 128, x->H / 32);
+    wsn = std::max(wsn, (size_t)(x->H / 64) * x->sk_ifc.seg_cap * 2048 * MT_MAX);
+    wsn = std::max(wsn, (size_t)(2 * x->NKV * 128 / 64) * x->sk_ikv.seg_cap * 2048 * MT_MAX);
     if ((r = x->alloc(&x->qkvbuf, Bm * x->NQKV)) || (r = x->alloc(&x->rnorm, bm32)) ||
         (r = x->alloc(&x->sk_ws, wsn)) || (r = x->alloc(&x->sk_tile_cnt, tiles, true)) ||
         (r = x->alloc(&x->sk_ss, (bm32 / 32) * (size_t)(x->H / 64) * 32))) {
@@ -396,37 +375,12 @@ int dfl_load_head(dfl_ctx* ctx, const uint16_t* final_norm, const uint16_t* embe
   return DFL_OK;
 }
 
-static void gemm(dfl_ctx* ctx, int cat, int wt, int epi, const uint4* W, const half_t* scale,
-                 const half_t* X, int ldx, int M, int N, int KB, GemmPlan p, half_t* out,
-                 int ldo, float* logits, unsigned long long* keys, hipStream_t st) {
-  // algorithmic bytes: the weight matrix (+ int8 scales), streamed once per m-tile
-  const long long wbytes = (wt == WT_INT8) ? (long long)N * KB * 32 + 2LL * N
-                                           : (long long)N * KB * 16 * 2;
-  ProfScope ps(ctx, cat, wbytes * ((M + 31) / 32), st);
-  SkinnyArgs a{};
-  a.W = W;
-  a.scale = scale;
-  a.X = X;
-  a.ldx = ldx;
-  a.M = M;
-  a.N = N;
-  a.KB = KB;
-  a.S_x = p.S_x;
-  a.ws = ctx->ws;
-  a.out = out;
-  a.ldo = ldo;
-  a.logits = logits;
-  a.ldl = N;
-  a.keys = keys;
-  launch_skinny_gemm(wt, epi, a, p.SK, (M + 31) / 32, st);
-}
-
 // Stream-K GEMM over the M rows of a block: one 32-row m-tile per launch of the
 // single-tile kernel, or up to 8 m-tiles per launch of the M-split kernel (each weight
 // block read once for all of them).  A normed input (gnorm set) takes its 1/rms rows from
 // the embedding kernel (rn_from_ss false) or from the row sums of squares that the
 // previous RESID GEMM left in sk_ss (rn_from_ss true).
-static void skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const SKPlan& p,
+static int skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const SKPlan& p,
                    const uint4* W, const half_t* scale, int N, int KB, const half_t* X, int ldx,
                    int M, const half_t* gnorm, bool rn_from_ss, half_t* out, int ldo,
                    half_t* xres, float* logits, unsigned long long* keys, hipStream_t st) {
@@ -464,11 +418,12 @@ static void skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const SKPlan& p,
     a.logits = logits ? logits + (size_t)m0 * N : nullptr;
     a.ldl = N;
     a.keys = keys ? keys + m0 : nullptr;
-    if (mt_n == 1)
-      launch_streamk_gemm(wt, epi, gnorm != nullptr, a, p, st, ps.start(), ps.stop());
-    else
-      launch_streamk_gemm_m(wt, epi, gnorm != nullptr, a, p, st, ps.start(), ps.stop());
+    const bool ok =
+        mt_n == 1 ? launch_streamk_gemm(wt, epi, gnorm != nullptr, a, p, st, ps.start(), ps.stop())
+                  : launch_streamk_gemm_m(wt, epi, gnorm != nullptr, a, p, st, ps.start(), ps.stop());
+    if (!ok) return fail(DFL_EINVAL, "no GEMM kernel for this weight type / epilogue");
   }
+  return DFL_OK;
 }
 
 static int layers_ready(dfl_ctx* ctx, const char* who) {
@@ -478,28 +433,59 @@ static int layers_ready(dfl_ctx* ctx, const char* who) {
   return DFL_OK;
 }
 
-// Per-layer K/V of `rows` fused context rows in ctx->ctxbuf, appended at cache row
-// len + r0 with absolute position offset + r0.
-static void ingest_kv_rows(dfl_ctx* ctx, const half_t* ctxrows, int rows, int r0, hipStream_t st) {
+// fp16 GEMM output rows (STORE epilogue) of `rows` fragment-layout activation rows, over
+// one M-split launch per 8 m-tiles (single-tile kernel for one m-tile).
+static int ingest_gemm(dfl_ctx* ctx, int cat, int wt, const SKPlan& p, const uint4* W,
+                        const half_t* scale, int N, int KB, const half_t* X, int K, int rows,
+                        half_t* out, hipStream_t st) {
+  const long long wbytes = (wt == WT_INT8) ? (long long)N * KB * 32 + 2LL * N
+                                           : (long long)N * KB * 16 * 2;
+  const int n_mt = (rows + 31) / 32;
+  for (int g0 = 0; g0 < n_mt; g0 += MT_MAX) {
+    const int mt_n = std::min(MT_MAX, n_mt - g0);
+    const int m0 = g0 * 32;
+    ProfScope ps(ctx, cat, wbytes, st, /*attached=*/true);
+    StreamArgs a{};
+    a.W = W;
+    a.scale = scale;
+    a.N = N;
+    a.KB = KB;
+    a.X = X + (size_t)m0 * K;
+    a.ldx = K;
+    a.M = std::min(32 * mt_n, rows - m0);
+    a.MT = mt_n;
+    a.ws = ctx->sk_ws;
+    a.seg_cap = p.seg_cap;
+    a.tile_cnt = ctx->sk_tile_cnt;
+    a.out = out + (size_t)m0 * N;
+    a.ldo = N;
+    a.eps = ctx->cfg.rms_eps;
+    const bool ok = mt_n == 1
+                        ? launch_streamk_gemm(wt, EPI_STORE, false, a, p, st, ps.start(), ps.stop())
+                        : launch_streamk_gemm_m(wt, EPI_STORE, false, a, p, st, ps.start(),
+                                                ps.stop());
+    if (!ok) return fail(DFL_EINVAL, "no GEMM kernel for this weight type / epilogue");
+  }
+  return DFL_OK;
+}
+
+// Per-layer K/V of `rows` fused context rows (fragment-layout tiles in ctx->ctxbuf):
+// k_norm + RoPE on K, appended at cache row len + r0 with absolute position offset + r0.
+static int ingest_kv_rows(dfl_ctx* ctx, int rows, int r0, hipStream_t st) {
   const int H = ctx->H, NH = ctx->NH, NKV = ctx->NKV;
   const int KB = H / 32;
   const int Nkv = 2 * NKV * 128;
-  GemmPlan p;
-  p.SK = 4;
-  p.S_x = 1;
   for (int l = 0; l < ctx->active; ++l) {
     Layer& L = ctx->layers[l];
-    const uint4* Wkv = L.w_qkv + (size_t)(NH * 4) * KB * 64;
-    gemm(ctx, P_INGEST_KV, WT_INT8, EPI_PARTIAL, Wkv, nullptr, ctxrows, H, rows, Nkv, KB, p, nullptr, 0,
-         nullptr, nullptr, st);
-    QKRopeArgs q{};   // value-initialised: qkv16 must stay null on this path
-    q.qkv16 = nullptr;
-    q.ws = ctx->ws;
-    q.S_x = 1;
+    const uint4* Wkv = L.w_qkv + (size_t)(NH * 4) * KB * 64;   // rows NH*128 .. of [q;k;v]
+    DFL_TRY(ingest_gemm(ctx, P_INGEST_KV, WT_INT8, ctx->sk_ikv, Wkv, L.s_qkv + NH * 128, Nkv,
+                        KB, ctx->ctxbuf, H, rows, ctx->kvbuf, st));
+    QKRopeArgs q{};
+    q.qkv16 = ctx->kvbuf;
     q.M = rows;
     q.N = Nkv;
     q.col_slot0 = NH;
-    q.scale = L.s_qkv;
+    q.scale = nullptr;
     q.slot0 = NH;
     q.n_slots = 2 * NKV;
     q.NH = NH;
@@ -518,6 +504,7 @@ static void ingest_kv_rows(dfl_ctx* ctx, const half_t* ctxrows, int rows, int r0
     ProfScope ps(ctx, P_INGEST_KV, 0, st);
     launch_qk_rope(q, st);
   }
+  return DFL_OK;
 }
 
 static int ingest(dfl_ctx* ctx, const uint16_t* src, int C, bool fused, void* stream) {
@@ -531,26 +518,26 @@ static int ingest(dfl_ctx* ctx, const uint16_t* src, int C, bool fused, void* st
   hipStream_t st = (hipStream_t)stream;
   const int H = ctx->H;
   const int K = ctx->NF * H;
+  const half_t* in = reinterpret_cast<const half_t*>(src);
   ctx->sq().last_block = 0;
   for (int r0 = 0; r0 < C; r0 += ING_ROWS) {
     const int rows = std::min(ING_ROWS, C - r0);
-    const half_t* ctxrows;
     if (fused) {
-      ctxrows = reinterpret_cast<const half_t*>(src) + (size_t)r0 * H;
-    } else {
-      GemmPlan p;
-      p.SK = 4;
-      p.S_x = 1;
-      gemm(ctx, P_INGEST_FC, WT_F16, EPI_PARTIAL, ctx->w_fc, nullptr,
-           reinterpret_cast<const half_t*>(src) + (size_t)r0 * K, K, rows, H, K / 16, p, nullptr,
-           0, nullptr, nullptr, st);
       ProfScope ps(ctx, P_INGEST_FC, 0, st);
-      launch_reduce_resid_norm(ctx->ws, 1, rows, H, nullptr, nullptr, false, ctx->hidden_norm,
-                               ctx->cfg.rms_eps, ctx->ctxbuf, H, ctx->fc_out, ctx->ss_part,
-                               ctx->row_cnt, st);
-      ctxrows = ctx->ctxbuf;
+      launch_rows_to_afl(in + (size_t)r0 * H, rows, H, H, ctx->ctxbuf, st);
+    } else {
+      // hidden_norm(fc(target_hidden)): fc output rounded to fp16 (Linear), then RMSNorm
+      {
+        ProfScope ps(ctx, P_INGEST_FC, 0, st);
+        launch_rows_to_afl(in + (size_t)r0 * K, rows, K, K, ctx->ing_x, st);
+      }
+      DFL_TRY(ingest_gemm(ctx, P_INGEST_FC, WT_F16, ctx->sk_ifc, ctx->w_fc, nullptr, H, K / 16,
+                          ctx->ing_x, K, rows, ctx->fc_out, st));
+      ProfScope ps(ctx, P_INGEST_FC, 0, st);
+      launch_rms_norm_afl(ctx->fc_out, rows, H, ctx->hidden_norm, ctx->cfg.rms_eps, ctx->ctxbuf,
+                          st);
     }
-    ingest_kv_rows(ctx, ctxrows, rows, r0, st);
+    DFL_TRY(ingest_kv_rows(ctx, rows, r0, st));
   }
   DFL_TRY(check_launch("ingest"));
   ctx->sq().len += C;
@@ -613,19 +600,17 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
   for (int l = 0; l < ctx->active; ++l) {
     Layer& Ly = ctx->layers[l];
     // q|k|v = input_layernorm(x) @ [Wq; Wk; Wv]^T  (fp16 out)
-    skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_STORE, ctx->sk_qkv, Ly.w_qkv, Ly.s_qkv, ctx->NQKV, H / 32,
+    DFL_TRY(skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_STORE, ctx->sk_qkv, Ly.w_qkv, Ly.s_qkv, ctx->NQKV, H / 32,
            ctx->x, H, M, Ly.in_norm, /*rn_from_ss=*/l > 0, ctx->qkvbuf, ctx->NQKV, nullptr,
-           nullptr, nullptr, st);
+           nullptr, nullptr, st));
     for (int i = 0; i < n_seq; ++i) {
       const SeqState& sqs = ctx->seqs[seq0 + i];
       QKRopeArgs q{};
       q.qkv16 = ctx->qkvbuf + (size_t)i * B * ctx->NQKV;
-      q.ws = nullptr;
-      q.S_x = 0;
       q.M = B;
       q.N = ctx->NQKV;
       q.col_slot0 = 0;
-      q.scale = Ly.s_qkv;
+      q.scale = nullptr;
       q.slot0 = 0;
       q.n_slots = NH + 2 * NKV;
       q.NH = NH;
@@ -666,19 +651,19 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
       }
     }
     // x += attn @ Wo^T ; per-tile row sums of squares of x -> sk_ss
-    skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_RESID, ctx->sk_o, Ly.w_o, Ly.s_o, H, NQ / 32, ctx->attn,
-           NQ, M, nullptr, false, nullptr, H, ctx->x, nullptr, nullptr, st);
+    DFL_TRY(skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_RESID, ctx->sk_o, Ly.w_o, Ly.s_o, H, NQ / 32, ctx->attn,
+           NQ, M, nullptr, false, nullptr, H, ctx->x, nullptr, nullptr, st));
     // act = silu(gate(post_norm(x))) * up(post_norm(x))
-    skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_SWIGLU, ctx->sk_gu, Ly.w_gu, Ly.s_gu, 2 * F, H / 32,
-           ctx->x, H, M, Ly.post_norm, true, ctx->act, F, nullptr, nullptr, nullptr, st);
+    DFL_TRY(skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_SWIGLU, ctx->sk_gu, Ly.w_gu, Ly.s_gu, 2 * F, H / 32,
+           ctx->x, H, M, Ly.post_norm, true, ctx->act, F, nullptr, nullptr, nullptr, st));
     // x += act @ Wdown^T ; per-tile row sums of squares of x -> sk_ss
-    skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_RESID, ctx->sk_down, Ly.w_down, Ly.s_down, H, F / 32,
-           ctx->act, F, M, nullptr, false, nullptr, H, ctx->x, nullptr, nullptr, st);
+    DFL_TRY(skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_RESID, ctx->sk_down, Ly.w_down, Ly.s_down, H, F / 32,
+           ctx->act, F, M, nullptr, false, nullptr, H, ctx->x, nullptr, nullptr, st));
   }
   if (out_logits || out_ids) {
-    skgemm(ctx, P_LM_HEAD, WT_F16, EPI_ARGMAX, ctx->sk_lm, ctx->w_lm, nullptr, ctx->V, H / 16,
+    DFL_TRY(skgemm(ctx, P_LM_HEAD, WT_F16, EPI_ARGMAX, ctx->sk_lm, ctx->w_lm, nullptr, ctx->V, H / 16,
            ctx->x, H, M, ctx->final_norm, true, nullptr, 0, nullptr, out_logits,
-           out_ids ? ctx->keys : nullptr, st);
+           out_ids ? ctx->keys : nullptr, st));
     if (out_ids) {
       ProfScope ps(ctx, P_ROWS, 0, st);
       launch_argmax_finalize(ctx->keys, M, out_ids, st);

@@ -9,27 +9,7 @@
 namespace dfl {
 
 enum { WT_INT8 = 0, WT_F16 = 1 };
-enum { EPI_PARTIAL = 0, EPI_SWIGLU = 1, EPI_ARGMAX = 2, EPI_STORE = 3, EPI_RESID = 4 };
-
-struct SkinnyArgs {
-  const uint4* W;        // packed weight blocks
-  const half_t* scale;   // [N] per packed row (int8 weights) or nullptr
-  const half_t* X;       // activations, row-major, leading dimension ldx
-  int ldx;
-  int M;                 // activation rows
-  int N;                 // packed weight rows (multiple of 64)
-  int KB;                // k-blocks: K/32 (int8) or K/16 (fp16)
-  int S_x;               // k-splits across workgroups
-  float* ws;             // EPI_PARTIAL: [S_x][M][N] fp32
-  half_t* out;           // EPI_SWIGLU: [M][ldo] fp16, N/2 columns
-  int ldo;
-  float* logits;         // EPI_ARGMAX: optional [M][ldl] fp32
-  int ldl;
-  unsigned long long* keys;  // EPI_ARGMAX: optional [M] packed (order(value) << 32 | ~index)
-};
-
-void launch_skinny_gemm(int wt, int epi, const SkinnyArgs& a, int SK, int n_mtiles,
-                        hipStream_t st);
+enum { EPI_SWIGLU = 1, EPI_ARGMAX = 2, EPI_STORE = 3, EPI_RESID = 4 };
 
 // ---- stream-K weight-streaming GEMM for M <= 32 rows (dfl_stream.hip) ----
 struct StreamArgs {
@@ -65,11 +45,13 @@ SKPlan streamk_plan(int N, int KB, int n_cu);
 // once for all m-tiles.  X, out, x, ss_*, rnorm, logits, keys point at m-tile 0; m-tile mt
 // is 32*mt rows further (ss blocks ss_mstride floats further).  ws holds
 // [N/64][seg_cap][MT][2048] floats.
-void launch_streamk_gemm_m(int wt, int epi, bool norm, const StreamArgs& a, const SKPlan& p,
+// Both launchers return false (and launch nothing) for a weight type / epilogue pair
+// they have no kernel for.
+bool launch_streamk_gemm_m(int wt, int epi, bool norm, const StreamArgs& a, const SKPlan& p,
                            hipStream_t st, hipEvent_t ev_start = nullptr,
                            hipEvent_t ev_stop = nullptr);
 // ev_start / ev_stop (optional) receive the kernel's own start and end timestamps.
-void launch_streamk_gemm(int wt, int epi, bool norm, const StreamArgs& a, const SKPlan& p,
+bool launch_streamk_gemm(int wt, int epi, bool norm, const StreamArgs& a, const SKPlan& p,
                          hipStream_t st, hipEvent_t ev_start = nullptr,
                          hipEvent_t ev_stop = nullptr);
 
@@ -97,23 +79,23 @@ void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* no
 void launch_apply_norm(const half_t* x, const float* ss, int ss_tiles, float eps, const half_t* g,
                        int M, int N, half_t* h, hipStream_t st);
 void launch_afl_to_rows(const half_t* x, int M, int N, half_t* h, hipStream_t st);
-// v = sum_s ws[s][m][n] (fixed order) * scale[n] -> fp16; with residual:
-// x[m][n] = fp16(x[m][n] + v), else the rounded v goes to x (or to xs when x is null);
-// then, if h != nullptr, h[m][n] = RMSNorm(row m) * g.  Grid: (ceil(N/1024), M);
-// ss_part [M][ceil(N/1024)] and cnt [M] (zero-initialised, self-resetting) are scratch.
-void launch_reduce_resid_norm(const float* ws, int S_x, int M, int N, const half_t* scale,
-                              half_t* x, bool residual, const half_t* g, float eps, half_t* h,
-                              int ldh, half_t* xs, float* ss_part, int* cnt, hipStream_t st);
-// QKV reduce + per-head RMSNorm + neox RoPE + scatter.  Rows m use position pos0 + m.
-// Head slots [0, NH) -> Q[h][m][d] (q_rows rows per head); slots [NH, NH+NKV) -> K
-// cache rows (cache_row0 + m); [NH+NKV, NH+2NKV) -> Vt cache columns.  The partial sums
-// hold head slots col_slot0 .. col_slot0 + N/128 - 1 (so the ingest path can project
-// only K and V); scale is indexed by the absolute slot.
+// Row-major rows [rows][ld] (first K columns, K % 8 == 0) -> fragment-layout tiles
+// [ceil(rows/32)][32][K], zero-padded to whole tiles.
+void launch_rows_to_afl(const half_t* src, int rows, int K, int ld, half_t* dst, hipStream_t st);
+// h = RMSNorm(x) * g of row-major fp16 rows [rows][H], written as fragment-layout tiles
+// (zero-padded to whole tiles).
+void launch_rms_norm_afl(const half_t* src, int rows, int H, const half_t* g, float eps,
+                         half_t* dst, hipStream_t st);
+// Per-head RMSNorm + neox RoPE + scatter of fp16 projections qkv16 [M][N] (scaled and
+// rounded by the GEMM epilogue).  Rows m use position pos0 + m.  Head slots [0, NH) -> Q[h][m][d]
+// (q_rows rows per head); slots [NH, NH+NKV) -> K cache rows (cache_row0 + m);
+// [NH+NKV, NH+2NKV) -> Vt cache columns.  Column 0 of qkv16 is head slot col_slot0 (so the
+// ingest path can project only K and V).
 struct QKRopeArgs {
-  const half_t* qkv16;                       // if set: fp16 projections [M][N] (scaled)
-  const float* ws; int S_x; int M; int N;   // else partial sums [S_x][M][N]
-  int col_slot0;                             // head slot of ws column 0
-  const half_t* scale;                       // [(NH+2NKV)*128]
+  const half_t* qkv16;
+  int M; int N;
+  int col_slot0;                             // head slot of qkv16 column 0
+  const half_t* scale;                       // unused (kept zero)
   int slot0, n_slots;                        // head slots handled (q,k,v numbering)
   int NH, NKV;
   const half_t* q_norm; const half_t* k_norm; float eps;

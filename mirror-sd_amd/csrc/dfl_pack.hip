@@ -1,4 +1,14 @@
 // Weight preparation kernels: the W8A16 quantiser and the HBM block packers.
+//
+// Weight layout in HBM (written once at load by the pack kernels): blocks of 32 rows x
+// KBK k-values (KBK = 32 for int8, 16 for fp16), 1 KiB each, ordered [row-block][k-block];
+// inside a block lane l's 16 bytes are
+//   int8: W[rb*32 + l%32][kb*32 + 16*(l/32) + 0..15]
+//   fp16: W[rb*32 + l%32][kb*16 +  8*(l/32) + 0..7]
+// so one wave-wide 128-bit load reads 1 KiB contiguous and hands every lane its
+// v_mfma_f32_32x32x16_f16 A-fragment directly (int8: two MFMAs per load, after the exact
+// int8 -> fp16 conversion).  Per-row fp16 scales are kept apart and applied in the GEMM
+// epilogue: y = s * sum x*q is exact reassociation (each fp16*int8 product is exact in fp32).
 #include "dfl_common.h"
 #include "dfl_kernels.h"
 

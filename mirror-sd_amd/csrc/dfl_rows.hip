@@ -98,76 +98,70 @@ void launch_apply_norm(const half_t* x, const float* ss, int ss_tiles, float eps
                      ss_tiles, eps, g, N, h);
 }
 
+// Row-major fp16 rows [rows][ld] (first K columns) -> activation fragment layout tiles
+// [ceil(rows/32)][32][K]; rows past `rows` in the last tile are zero.  One thread per
+// 8 consecutive columns (one 16-byte run in both layouts).
+__global__ __launch_bounds__(256) void rows_to_afl_kernel(const half_t* __restrict__ src,
+                                                          int rows, int K, int ld,
+                                                          half_t* __restrict__ dst) {
+  const int r = blockIdx.y;
+  const int k = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (k >= K) return;
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (r < rows) v = *reinterpret_cast<const u32x4*>(src + (size_t)r * ld + k);
+  *reinterpret_cast<u32x4*>(dst + afl_index(r, k, K)) = v;
+}
+
+void launch_rows_to_afl(const half_t* src, int rows, int K, int ld, half_t* dst, hipStream_t st) {
+  const int tiles_rows = ((rows + 31) / 32) * 32;
+  hipLaunchKernelGGL(rows_to_afl_kernel, dim3((K / 8 + 255) / 256, tiles_rows), dim3(256), 0, st,
+                     src, rows, K, ld, dst);
+}
+
+// RMSNorm of row-major fp16 rows [rows][H] (h = fp16(fp16(x * r) * g), r = 1/rms in fp32)
+// written in the activation fragment layout; padded rows of the last tile are zero.
+__global__ __launch_bounds__(ROW_THREADS) void rms_norm_afl_kernel(const half_t* __restrict__ src,
+                                                                   int rows, int H,
+                                                                   const half_t* __restrict__ g,
+                                                                   float eps,
+                                                                   half_t* __restrict__ dst) {
+  __shared__ float red[16];
+  const int r = blockIdx.x;
+  if (r >= rows) {   // zero padding rows
+    for (int k = threadIdx.x * 8; k < H; k += ROW_THREADS * 8)
+      *reinterpret_cast<u32x4*>(dst + afl_index(r, k, H)) = (u32x4){0u, 0u, 0u, 0u};
+    return;
+  }
+  const half_t* xr = src + (size_t)r * H;
+  float ss = 0.f;
+  for (int k = threadIdx.x * 8; k < H; k += ROW_THREADS * 8) {
+    const half8_t v = as_half8(*reinterpret_cast<const u32x4*>(xr + k));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += h2f(v[j]) * h2f(v[j]);
+  }
+  ss = block_sum(ss, red);
+  const float rr = 1.0f / sqrtf(ss / (float)H + eps);
+  for (int k = threadIdx.x * 8; k < H; k += ROW_THREADS * 8) {
+    const half8_t v = as_half8(*reinterpret_cast<const u32x4*>(xr + k));
+    half8_t o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = rms_out(h2f(v[j]), rr, g[k + j]);
+    *reinterpret_cast<u32x4*>(dst + afl_index(r, k, H)) = __builtin_bit_cast(u32x4, o);
+  }
+}
+
+void launch_rms_norm_afl(const half_t* src, int rows, int H, const half_t* g, float eps,
+                         half_t* dst, hipStream_t st) {
+  const int tiles_rows = ((rows + 31) / 32) * 32;
+  hipLaunchKernelGGL(rms_norm_afl_kernel, dim3(tiles_rows), dim3(ROW_THREADS), 0, st, src, rows, H,
+                     g, eps, dst);
+}
+
 void launch_afl_to_rows(const half_t* x, int M, int N, half_t* h, hipStream_t st) {
   hipLaunchKernelGGL(afl_rows_kernel, dim3((N / 4 + 255) / 256, M), dim3(256), 0, st, x, nullptr,
                      0, 0.f, nullptr, N, h);
 }
 
-// Split-K reduction + residual + RMSNorm, parallel over (column chunk, row).
-// Each workgroup handles RED_COLS columns of one row: sums the S_x partials in a fixed
-// order, applies the per-row weight scale, rounds to fp16 (Linear output), adds the
-// residual (fp16 add), stores x and its chunk's sum of squares.  The last chunk of a
-// row to finish (device-scope counter; every chunk fences its stores before counting)
-// sums the chunk partials in a fixed order and writes h = RMSNorm(x) * g for the whole
-// row, then re-arms the counter for the next launch.
-constexpr int RED_THREADS = 256;
-constexpr int RED_COLS = 4 * RED_THREADS;
-
-__global__ __launch_bounds__(RED_THREADS) void reduce_resid_norm_kernel(
-    const float* __restrict__ ws, int S_x, int M, int N, const half_t* __restrict__ scale,
-    half_t* x, int residual, const half_t* __restrict__ g, float eps, half_t* __restrict__ h,
-    int ldh, half_t* __restrict__ xs_out, float* __restrict__ ss_part, int* __restrict__ cnt) {
-  __shared__ float sm[16];
-  __shared__ int last_flag;
-  const int chunk = blockIdx.x, m = blockIdx.y, NC = gridDim.x;
-  const int n0 = chunk * RED_COLS + threadIdx.x * 4;
-  // x may be null (no residual stream): then the rounded projection goes to xs_out.
-  half_t* xrow = (x ? x : xs_out) + (size_t)m * N;
-  float ss = 0.f;
-  if (n0 < N) {   // N is a multiple of 64, so a 4-column group is all in or all out
-    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < S_x; ++s)
-      acc += *reinterpret_cast<const floatx4*>(ws + ((size_t)s * M + m) * N + n0);
-    half4_t out;
-    const half4_t xo = residual ? *reinterpret_cast<const half4_t*>(xrow + n0) : (half4_t){};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float y = h2f(f2h(scale ? acc[j] * h2f(scale[n0 + j]) : acc[j]));
-      if (residual) y = h2f(f2h(h2f(xo[j]) + y));
-      out[j] = f2h(y);
-      ss += y * y;
-    }
-    *reinterpret_cast<half4_t*>(xrow + n0) = out;
-  }
-  if (!h) return;
-  ss = block_sum(ss, sm);
-  if (threadIdx.x == 0) ss_part[(size_t)m * NC + chunk] = ss;
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) last_flag = (atomicAdd(cnt + m, 1) == NC - 1);
-  __syncthreads();
-  if (!last_flag) return;
-  __threadfence();
-  float tot = 0.f;
-  for (int c = 0; c < NC; ++c) tot += __builtin_nontemporal_load(ss_part + (size_t)m * NC + c);
-  const float r = 1.0f / sqrtf(tot / (float)N + eps);
-  for (int n = threadIdx.x * 4; n < N; n += RED_COLS) {
-    const half4_t xv = __builtin_nontemporal_load(reinterpret_cast<const half4_t*>(xrow + n));
-    half4_t o;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) o[j] = rms_out(h2f(xv[j]), r, g[n + j]);
-    *reinterpret_cast<half4_t*>(h + (size_t)m * ldh + n) = o;
-  }
-  if (threadIdx.x == 0) cnt[m] = 0;
-}
-
-void launch_reduce_resid_norm(const float* ws, int S_x, int M, int N, const half_t* scale,
-                              half_t* x, bool residual, const half_t* g, float eps, half_t* h,
-                              int ldh, half_t* xs, float* ss_part, int* cnt, hipStream_t st) {
-  dim3 grid((N + RED_COLS - 1) / RED_COLS, M);
-  hipLaunchKernelGGL(reduce_resid_norm_kernel, grid, dim3(RED_THREADS), 0, st, ws, S_x, M, N,
-                     scale, x, residual ? 1 : 0, g, eps, h, ldh, xs, ss_part, cnt);
-}
 
 // One wave per (row m, head slot); lane j holds head elements j and j + 64, which are
 // exactly the neox RoPE pair (dflash.py:263-275, split-half rotation), so the
@@ -178,21 +172,10 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(QKRopeArgs a) {
   if (p >= (long long)a.M * a.n_slots) return;
   const int m = (int)(p / a.n_slots);
   const int slot = a.slot0 + (int)(p - (long long)m * a.n_slots);
-  const int n0 = slot * 128 + lane, n1 = n0 + 64;
   const int c0 = (slot - a.col_slot0) * 128 + lane;
-  float v0 = 0.f, v1 = 0.f;
-  if (a.qkv16) {   // already scaled and rounded by the GEMM epilogue
-    v0 = h2f(a.qkv16[(size_t)m * a.N + c0]);
-    v1 = h2f(a.qkv16[(size_t)m * a.N + c0 + 64]);
-  } else {
-    for (int s = 0; s < a.S_x; ++s) {
-      const float* wsr = a.ws + ((size_t)s * a.M + m) * a.N;
-      v0 += wsr[c0];
-      v1 += wsr[c0 + 64];
-    }
-    v0 = h2f(f2h(v0 * h2f(a.scale[n0])));   // Linear output is fp16
-    v1 = h2f(f2h(v1 * h2f(a.scale[n1])));
-  }
+  // projections already scaled and rounded to fp16 (Linear output) by the GEMM epilogue
+  const float v0 = h2f(a.qkv16[(size_t)m * a.N + c0]);
+  const float v1 = h2f(a.qkv16[(size_t)m * a.N + c0 + 64]);
   const int kv_slot0 = a.NH + a.NKV;
   if (slot >= kv_slot0) {   // V head: no norm, no rotation
     const int gk = slot - kv_slot0;

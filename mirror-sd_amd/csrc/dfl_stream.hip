@@ -5,7 +5,7 @@
 // activation fragments, like weight fragments, arrive as contiguous 1 KiB wave loads; the
 // residual and SwiGLU epilogues write their outputs in the same layout.
 //
-// Partition.  The packed weight matrix (block layout: see dfl_gemm.hip) is a sequence of
+// Partition.  The packed weight matrix (block layout: see dfl_pack.hip) is a sequence of
 // U = (N/64) * KB work units (one 64-row wave-tile x one k-block), tile-major.  One
 // workgroup per CU takes an equal contiguous unit range, so every CU streams the same
 // number of bytes; the range crosses tile boundaries, which cut it into segments.
@@ -784,13 +784,13 @@ static void launch_m_t(const StreamArgs& a, const SKPlan& p, hipStream_t st, hip
   else launch_m_w<WT, EPI, NORM, 2>(a, p, st, e0, e1);
 }
 
-void launch_streamk_gemm_m(int wt, int epi, bool norm, const StreamArgs& a, const SKPlan& p,
+bool launch_streamk_gemm_m(int wt, int epi, bool norm, const StreamArgs& a, const SKPlan& p,
                            hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop) {
 #define DFL_SKM_CASE(W_, E_)                                         \
   if (wt == W_ && epi == E_) {                                       \
     if (norm) launch_m_t<W_, E_, true>(a, p, st, ev_start, ev_stop); \
     else launch_m_t<W_, E_, false>(a, p, st, ev_start, ev_stop);     \
-    return;                                                          \
+    return true;                                                     \
   }
   DFL_SKM_CASE(WT_INT8, EPI_STORE)
   DFL_SKM_CASE(WT_INT8, EPI_RESID)
@@ -798,21 +798,24 @@ void launch_streamk_gemm_m(int wt, int epi, bool norm, const StreamArgs& a, cons
   DFL_SKM_CASE(WT_F16, EPI_ARGMAX)
   DFL_SKM_CASE(WT_F16, EPI_STORE)
 #undef DFL_SKM_CASE
+  return false;
 }
 
-void launch_streamk_gemm(int wt, int epi, bool norm, const StreamArgs& a, const SKPlan& p,
+bool launch_streamk_gemm(int wt, int epi, bool norm, const StreamArgs& a, const SKPlan& p,
                          hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop) {
 #define DFL_SK_CASE(W_, E_)                                        \
   if (wt == W_ && epi == E_) {                                     \
     if (norm) launch_t<W_, E_, true>(a, p, st, ev_start, ev_stop); \
     else launch_t<W_, E_, false>(a, p, st, ev_start, ev_stop);     \
-    return;                                                        \
+    return true;                                                   \
   }
   DFL_SK_CASE(WT_INT8, EPI_STORE)
   DFL_SK_CASE(WT_INT8, EPI_RESID)
   DFL_SK_CASE(WT_INT8, EPI_SWIGLU)
   DFL_SK_CASE(WT_F16, EPI_ARGMAX)
+  DFL_SK_CASE(WT_F16, EPI_STORE)
 #undef DFL_SK_CASE
+  return false;
 }
 
 }  // namespace dfl
