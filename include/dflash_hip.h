@@ -133,6 +133,12 @@ int dfl_cache_trim(dfl_ctx* ctx, int32_t n);
  * (what update_and_fetch did before the caller's trim). */
 int dfl_cache_commit(dfl_ctx* ctx, int32_t n);
 int dfl_cache_reset(dfl_ctx* ctx);
+/* Sink + sliding-window eviction (DFlashKVCache(sink_size, window_size) and
+ * _apply_window, dflash.py:160-193): clears the cache, then keeps the first `sink` rows and
+ * the newest `window` rows once more than sink + window are cached.  Both 0 (or either 0,
+ * as in the reference) = no eviction.  sink + window within the cache capacity; a drafted
+ * block must fit in the window.  dfl_cache_reset keeps the setting. */
+int dfl_cache_set_window(dfl_ctx* ctx, int32_t sink, int32_t window);
 /* Set the absolute position of the next context row without touching cached rows
  * (the ANE caller assigns cache.offset directly, generate.py:1409-1417). */
 int dfl_cache_set_offset(dfl_ctx* ctx, int64_t offset);
@@ -140,6 +146,10 @@ int dfl_cache_set_offset(dfl_ctx* ctx, int64_t offset);
 int dfl_cache_state(const dfl_ctx* ctx, int32_t* len, int64_t* offset);
 /* Device pointers of layer `layer`'s cache: K [NKV][cap][128], Vt [NKV][128][cap]. */
 int dfl_cache_kv(const dfl_ctx* ctx, int32_t layer, uint16_t** k, uint16_t** vt, int32_t* cap);
+/* The cache row holding each cached row in the reference's order (sink rows, then the
+ * window oldest first) -- the order of DFlashKVCache.keys (dflash.py:170-193).  Writes
+ * *n = cached rows and, if rows != NULL, rows[0 .. *n). */
+int dfl_cache_rows(const dfl_ctx* ctx, int32_t* rows, int32_t max_rows, int32_t* n);
 
 /* Kernel timing with HIP events (the reference times phases and kernels with
  * time.perf_counter wrappers: bench_ane_profile.py:41-245, ANEKernel.run_timed

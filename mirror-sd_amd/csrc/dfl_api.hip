@@ -43,10 +43,43 @@ struct ProfRec {
 };
 
 // Cache bookkeeping of one sequence (DFlashKVCache.offset and its row count).
+//
+// With a window (DFlashKVCache(sink_size, window_size), dflash.py:160-193) the cache keeps
+// the first `sink` rows and the newest `window` rows.  Rows past the sink live in a ring of
+// `window` cache rows: an append overwrites the oldest ring row once the ring is full, and
+// a trim steps the ring back over its newest rows.  Attention is indifferent to key order,
+// so the set of rows it sees is exactly the reference's concatenated sink + window.
 struct SeqState {
-  int len = 0;             // cached context rows
+  int len = 0;             // cached rows (the reference cache's key count)
   long long offset = 0;    // absolute position of the next row
   int last_block = 0;      // rows of the last drafted block (committable)
+  int sink = 0, window = 0;
+  long long ring_j = 0;    // rows appended to the ring (less trimmed ones)
+
+  // cache rows of the next n appended rows: sink rows from row0, then the ring
+  void slots(int n, int& row0, int& sink_fill, int& j0) const {
+    row0 = len;
+    sink_fill = window ? std::max(0, std::min(sink - len, n)) : 0;
+    j0 = window ? (int)(ring_j % window) : 0;
+  }
+  void append(int n) {
+    if (!window) {
+      len += n;
+      return;
+    }
+    const int sf = std::max(0, std::min(sink - len, n));
+    ring_j += n - sf;
+    len = std::min(len + n, sink + window);
+  }
+  void trim(int n) {
+    if (window) ring_j -= std::min(n, std::max(0, len - sink));
+    len = std::max(0, len - n);
+  }
+  // key index range attention scans (ring rows never written stay masked)
+  int key_range() const {
+    if (!window || len <= sink) return len;
+    return sink + (int)std::min<long long>(window, ring_j);
+  }
 };
 
 struct Layer {
@@ -500,7 +533,9 @@ static int ingest_kv_rows(dfl_ctx* ctx, int rows, int r0, hipStream_t st) {
     q.Kc = ctx->kc(L, ctx->cur);
     q.Vt = ctx->vt(L, ctx->cur);
     q.cap = ctx->cap;
-    q.cache_row0 = ctx->sq().len + r0;
+    ctx->sq().slots(rows, q.cache_row0, q.sink_fill, q.ring_j0);
+    q.ring_S = ctx->sq().sink;
+    q.ring_W = ctx->sq().window;
     ProfScope ps(ctx, P_INGEST_KV, 0, st);
     launch_qk_rope(q, st);
   }
@@ -510,7 +545,7 @@ static int ingest_kv_rows(dfl_ctx* ctx, int rows, int r0, hipStream_t st) {
 static int ingest(dfl_ctx* ctx, const uint16_t* src, int C, bool fused, void* stream) {
   if (!ctx || (!src && C > 0)) return fail(DFL_EINVAL, "dfl_ingest: null argument");
   if (C < 0) return fail(DFL_EINVAL, "dfl_ingest: negative row count");
-  if ((long long)ctx->sq().len + C > ctx->cfg.max_ctx)
+  if (!ctx->sq().window && (long long)ctx->sq().len + C > ctx->cfg.max_ctx)
     return fail(DFL_ERANGE, "dfl_ingest: context rows " + std::to_string(ctx->sq().len + C) +
                                 " exceed max_ctx " + std::to_string(ctx->cfg.max_ctx));
   DFL_TRY(layers_ready(ctx, "dfl_ingest"));
@@ -538,9 +573,9 @@ static int ingest(dfl_ctx* ctx, const uint16_t* src, int C, bool fused, void* st
                           st);
     }
     DFL_TRY(ingest_kv_rows(ctx, rows, r0, st));
+    ctx->sq().append(rows);
   }
   DFL_TRY(check_launch("ingest"));
-  ctx->sq().len += C;
   ctx->sq().offset += C;
   return DFL_OK;
 }
@@ -570,9 +605,10 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
   if (!ctx->head_loaded) return fail(DFL_ESTATE, w + ": final norm not loaded");
   if ((out_logits || out_ids) && !ctx->w_lm) return fail(DFL_ESTATE, w + ": lm_head not loaded");
   for (int i = 0; i < n_seq; ++i)
-    if (ctx->seqs[seq0 + i].len + B > ctx->cap)
-      return fail(DFL_ERANGE, w + ": cache capacity exceeded (sequence " +
-                                  std::to_string(seq0 + i) + ")");
+    if (ctx->seqs[seq0 + i].window ? B > ctx->seqs[seq0 + i].window
+                                   : ctx->seqs[seq0 + i].len + B > ctx->cap)
+      return fail(DFL_ERANGE, w + ": cache capacity exceeded, or block larger than the cache "
+                                  "window (sequence " + std::to_string(seq0 + i) + ")");
   DFL_TRY(layers_ready(ctx, who));
 
   hipStream_t st = (hipStream_t)stream;
@@ -625,7 +661,9 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
       q.Kc = ctx->kc(Ly, seq0 + i);
       q.Vt = ctx->vt(Ly, seq0 + i);
       q.cap = ctx->cap;
-      q.cache_row0 = sqs.len;
+      sqs.slots(B, q.cache_row0, q.sink_fill, q.ring_j0);
+      q.ring_S = sqs.sink;
+      q.ring_W = sqs.window;
       {
         ProfScope ps(ctx, P_QK_ROPE, 0, st);
         launch_qk_rope(q, st);
@@ -638,7 +676,14 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
       at.NH = NH;
       at.NKV = NKV;
       at.cap = ctx->cap;
-      at.L = sqs.len + B;
+      SeqState after = sqs;   // the block's rows appended (evicting as the window requires)
+      after.append(B);
+      at.L = after.key_range();
+      at.ring_S = after.sink;
+      at.ring_W = after.window;
+      at.ring_j = after.window ? (int)(after.ring_j % after.window) : 0;
+      at.ring_len = std::max(0, after.len - after.sink);
+      at.sink_len = std::min(after.len, after.sink);
       attn_split(at.L, at.chunk, at.n_chunks);
       at.scale_log2 = (float)(1.4426950408889634 / std::sqrt(128.0));
       at.Op = ctx->Op;
@@ -679,7 +724,14 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
     launch_afl_to_rows(ctx->x, M, H, reinterpret_cast<half_t*>(out_prenorm), st);
   }
   DFL_TRY(check_launch(who));
-  for (int i = 0; i < n_seq; ++i) ctx->seqs[seq0 + i].last_block = B;
+  // the block's rows stay written but uncommitted: append + trim (a window keeps the
+  // rows the block evicted evicted, as the reference's trim after update_and_fetch does)
+  for (int i = 0; i < n_seq; ++i) {
+    SeqState& q = ctx->seqs[seq0 + i];
+    q.append(B);
+    q.trim(B);
+    q.last_block = B;
+  }
   return DFL_OK;
 }
 
@@ -723,8 +775,7 @@ int dfl_cache_trim(dfl_ctx* ctx, int32_t n) {
   if (!ctx) return fail(DFL_EINVAL, "dfl_cache_trim: null context");
   if (n < 0) return fail(DFL_EINVAL, "dfl_cache_trim: negative count");
   SeqState& q = ctx->sq();
-  const int k = std::min(n, q.len);   // DFlashKVCache.trim clamps the length at 0
-  q.len -= k;
+  q.trim(n);   // DFlashKVCache.trim clamps the length at 0
   q.offset -= n;
   q.last_block = 0;
   return DFL_OK;
@@ -735,8 +786,9 @@ int dfl_cache_commit(dfl_ctx* ctx, int32_t n) {
   SeqState& q = ctx->sq();
   if (n < 0 || n > q.last_block)
     return fail(DFL_EINVAL, "dfl_cache_commit: n must be in [0, rows of the last block]");
-  if (q.len + n > ctx->cfg.max_ctx) return fail(DFL_ERANGE, "dfl_cache_commit: max_ctx exceeded");
-  q.len += n;
+  if (!q.window && q.len + n > ctx->cfg.max_ctx)
+    return fail(DFL_ERANGE, "dfl_cache_commit: max_ctx exceeded");
+  q.append(n);   // the block's rows are still in their cache rows
   q.offset += n;
   q.last_block = 0;
   return DFL_OK;
@@ -744,7 +796,23 @@ int dfl_cache_commit(dfl_ctx* ctx, int32_t n) {
 
 int dfl_cache_reset(dfl_ctx* ctx) {
   if (!ctx) return fail(DFL_EINVAL, "dfl_cache_reset: null context");
+  const int sink = ctx->sq().sink, window = ctx->sq().window;
   ctx->sq() = SeqState{};
+  ctx->sq().sink = sink;
+  ctx->sq().window = window;
+  return DFL_OK;
+}
+
+int dfl_cache_set_window(dfl_ctx* ctx, int32_t sink, int32_t window) {
+  if (!ctx) return fail(DFL_EINVAL, "dfl_cache_set_window: null context");
+  if (sink < 0 || window < 0) return fail(DFL_EINVAL, "dfl_cache_set_window: negative size");
+  if ((long long)sink + window > ctx->cap)
+    return fail(DFL_ERANGE, "dfl_cache_set_window: sink + window exceed the cache capacity");
+  ctx->sq() = SeqState{};
+  if (sink > 0 && window > 0) {   // the reference evicts only when both are set
+    ctx->sq().sink = sink;
+    ctx->sq().window = window;
+  }
   return DFL_OK;
 }
 
@@ -761,6 +829,22 @@ int dfl_cache_state(const dfl_ctx* ctx, int32_t* len, int64_t* offset) {
   const SeqState& q = ctx->seqs[ctx->cur];
   if (len) *len = q.len;
   if (offset) *offset = q.offset;
+  return DFL_OK;
+}
+
+int dfl_cache_rows(const dfl_ctx* ctx, int32_t* rows, int32_t max_rows, int32_t* n) {
+  if (!ctx || !n) return fail(DFL_EINVAL, "dfl_cache_rows: null argument");
+  const SeqState& q = ctx->seqs[ctx->cur];
+  *n = q.len;
+  if (!rows) return DFL_OK;
+  if (max_rows < q.len) return fail(DFL_ERANGE, "dfl_cache_rows: buffer too small");
+  const int ns = q.window ? std::min(q.len, q.sink) : q.len;
+  for (int i = 0; i < ns; ++i) rows[i] = i;
+  const int rl = q.len - ns;   // ring rows, oldest first
+  for (int i = 0; i < rl; ++i) {
+    const long long j = q.ring_j - rl + i;
+    rows[ns + i] = q.sink + (int)(((j % q.window) + q.window) % q.window);
+  }
   return DFL_OK;
 }
 

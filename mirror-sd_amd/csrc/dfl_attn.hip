@@ -132,7 +132,20 @@ __global__ __launch_bounds__(768) void block_attn_kernel(AttnArgs a) {
       // Accumulator r holds key kbase + (r < 8 ? 8*gg + r : 16 + 8*gg + r - 8).
       const int kbase = k0 + 32 * j;
       float v[16];
-      if (kbase + 32 <= k_end) {
+      if (a.ring_W > 0) {   // sink + window cache: only the valid ring rows count
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kr = kbase + (r < 8 ? 8 * gg + r : 16 + 8 * gg + (r - 8));
+          bool ok = kr < k_end;
+          if (kr < a.ring_S) {
+            ok = ok && kr < a.sink_len;
+          } else {
+            const int back = (a.ring_j - 1 - (kr - a.ring_S)) % a.ring_W;
+            ok = ok && (back < 0 ? back + a.ring_W : back) < a.ring_len;
+          }
+          v[r] = ok ? s[r] * a.scale_log2 : -INFINITY;
+        }
+      } else if (kbase + 32 <= k_end) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) v[r] = s[r] * a.scale_log2;
       } else {
@@ -157,7 +170,8 @@ __global__ __launch_bounds__(768) void block_attn_kernel(AttnArgs a) {
       half8_t p1, p2;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const half_t ph = f2h(__builtin_amdgcn_exp2f(v[r] - mrun));
+        // masked keys contribute 0 (also when every key so far was masked, mrun = -inf)
+        const half_t ph = v[r] == -INFINITY ? (half_t)0.0f : f2h(__builtin_amdgcn_exp2f(v[r] - mrun));
         psum += h2f(ph);
         if (r < 8) p1[r] = ph; else p2[r - 8] = ph;
       }

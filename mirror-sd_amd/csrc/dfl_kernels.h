@@ -102,7 +102,18 @@ struct QKRopeArgs {
   long long pos0; double log2_theta;
   half_t* Q; int q_rows;                     // [NH][q_rows][128]
   half_t* Kc; half_t* Vt; int cap; int cache_row0;  // K [NKV][cap][128], Vt [NKV][128][cap]
+  // sink + window cache (ring_W > 0): of the appended rows, the first sink_fill go to
+  // cache rows cache_row0 + m (filling the sink), later ones to ring row
+  // ring_S + ((ring_j0 + m - sink_fill) mod ring_W)
+  int ring_S, ring_W, ring_j0, sink_fill;
 };
+// -1: a ring row that a later row of the same launch overwrites (more than ring_W ring
+// rows appended at once keep only the newest ring_W), so it is not written at all
+DFL_DEV int cache_slot(const QKRopeArgs& a, int m) {
+  if (a.ring_W == 0 || m < a.sink_fill) return a.cache_row0 + m;
+  if (m - a.sink_fill < a.M - a.sink_fill - a.ring_W) return -1;
+  return a.ring_S + (a.ring_j0 + (m - a.sink_fill)) % a.ring_W;
+}
 void launch_qk_rope(const QKRopeArgs& a, hipStream_t st);
 // ids[m] = ~low32(keys[m]); keys[m] = 0.
 void launch_argmax_finalize(unsigned long long* keys, int M, int32_t* ids, hipStream_t st);
@@ -122,6 +133,9 @@ struct AttnArgs {
   half_t* O;              // final output rows o_row0 .. o_row0 + B - 1 of an activation
                           // fragment layout tile set with NH*128 columns
   int o_row0;
+  // sink + window cache (ring_W > 0): keys [0, ring_S) valid below sink_len; key ring_S + p
+  // valid when (ring_j - 1 - p) mod ring_W < ring_len (the ring_len newest ring rows)
+  int ring_S, ring_W, ring_j, ring_len, sink_len;
 };
 void launch_block_attention(const AttnArgs& a, hipStream_t st);
 

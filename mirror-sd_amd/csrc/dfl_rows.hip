@@ -173,13 +173,15 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(QKRopeArgs a) {
   const int m = (int)(p / a.n_slots);
   const int slot = a.slot0 + (int)(p - (long long)m * a.n_slots);
   const int c0 = (slot - a.col_slot0) * 128 + lane;
+  const int crow = slot >= a.NH ? cache_slot(a, m) : 0;
+  if (crow < 0) return;   // whole wave: one (row, head slot) per wave
   // projections already scaled and rounded to fp16 (Linear output) by the GEMM epilogue
   const float v0 = h2f(a.qkv16[(size_t)m * a.N + c0]);
   const float v1 = h2f(a.qkv16[(size_t)m * a.N + c0 + 64]);
   const int kv_slot0 = a.NH + a.NKV;
   if (slot >= kv_slot0) {   // V head: no norm, no rotation
     const int gk = slot - kv_slot0;
-    half_t* vt = a.Vt + (size_t)gk * 128 * a.cap + a.cache_row0 + m;
+    half_t* vt = a.Vt + (size_t)gk * 128 * a.cap + crow;
     vt[(size_t)lane * a.cap] = f2h(v0);
     vt[(size_t)(lane + 64) * a.cap] = f2h(v1);
     return;
@@ -202,7 +204,7 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(QKRopeArgs a) {
     dst = a.Q + ((size_t)slot * a.q_rows + m) * 128;
   } else {
     const int gk = slot - a.NH;
-    dst = a.Kc + ((size_t)gk * a.cap + a.cache_row0 + m) * 128;
+    dst = a.Kc + ((size_t)gk * a.cap + crow) * 128;
   }
   dst[lane] = o0;
   dst[lane + 64] = o1;

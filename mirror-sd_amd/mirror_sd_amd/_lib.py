@@ -57,6 +57,9 @@ SIGNATURES = {
     "dfl_cache_trim": (c_int32, [c_void_p, c_int32]),
     "dfl_cache_commit": (c_int32, [c_void_p, c_int32]),
     "dfl_cache_reset": (c_int32, [c_void_p]),
+    "dfl_cache_set_window": (c_int32, [c_void_p, c_int32, c_int32]),
+    "dfl_cache_rows": (c_int32, [c_void_p, ctypes.POINTER(c_int32), c_int32,
+                                 ctypes.POINTER(c_int32)]),
     "dfl_cache_set_offset": (c_int32, [c_void_p, c_int64]),
     "dfl_cache_state": (c_int32, [c_void_p, ctypes.POINTER(c_int32), ctypes.POINTER(c_int64)]),
     "dfl_cache_kv": (c_int32, [c_void_p, c_int32, ctypes.POINTER(c_void_p),

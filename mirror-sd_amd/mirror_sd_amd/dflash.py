@@ -46,8 +46,10 @@ class DFlashKVCache:
 
     ``offset`` counts absolute positions, ``trim(n)`` drops the last n rows exactly as
     the reference does; the device cache is reconciled with these handles at the next
-    forward call.  ``keys`` / ``values`` are device views ``[1, NKV, L, 128]`` (keys
-    after k_norm and RoPE, as the reference stores them).
+    forward call.  ``keys`` / ``values`` are ``[1, NKV, L, 128]`` (keys after k_norm and
+    RoPE, as the reference stores them), in the reference's row order: with a sink +
+    window the device keeps the window as a ring, and the rows are gathered in order
+    (sink rows, then the window oldest first).
     """
 
     def __init__(self, model: "DFlashDraftModel", layer: int, generation: int,
@@ -66,19 +68,31 @@ class DFlashKVCache:
             self._len = max(self._len - n, 0)
             self.offset -= n
 
+    def _appended(self, n: int):
+        """Book n appended rows: a sink + window cache holds at most sink + window
+        (_apply_window, dflash.py:179-193)."""
+        self._len += n
+        self.offset += n
+        if self.sink_size > 0 and self.window_size > 0:
+            self._len = min(self._len, self.sink_size + self.window_size)
+        self._has_keys = True
+
+    def _rows(self):
+        return self._model._cache_rows()
+
     @property
     def keys(self):
         if not self._has_keys:
             return None
         k, vt = self._model._cache_tensors[self.layer]
-        return k[:, :self._len].unsqueeze(0)
+        return k[:, self._rows()].unsqueeze(0)
 
     @property
     def values(self):
         if not self._has_keys:
             return None
         k, vt = self._model._cache_tensors[self.layer]
-        return vt[:, :, :self._len].transpose(1, 2).unsqueeze(0)
+        return vt[:, :, self._rows()].transpose(1, 2).unsqueeze(0)
 
     def update_and_fetch(self, keys, values):
         raise NotImplementedError(
@@ -277,12 +291,24 @@ class DFlashDraftModel:
     # ------------------------------------------------------------------ cache
     def make_cache(self, sink_size: int = 64, window_size: int = 1024) -> List[DFlashKVCache]:
         """dflash.py:405-406.  One live cache per model: a new cache resets the device
-        cache and invalidates older handles.  Sink/window eviction (dflash.py:179-193)
-        is not performed on the device; a cache that would evict raises."""
+        cache and invalidates older handles.  With sink_size and window_size both set,
+        the device cache keeps the first sink_size rows and the newest window_size rows
+        (dflash.py:179-193)."""
         self._gen += 1
-        _lib.check(self._L.dfl_cache_reset(self._ctx), "dfl_cache_reset")
+        _lib.check(self._L.dfl_cache_set_window(self._ctx, int(sink_size), int(window_size)),
+                   "dfl_cache_set_window")
         return [DFlashKVCache(self, i, self._gen, sink_size, window_size)
                 for i in range(self.num_draft_layers)]
+
+    def _cache_rows(self):
+        """Cache rows of the cached rows in the reference's order (a device index tensor)."""
+        import torch
+        n = ctypes.c_int32()
+        _lib.check(self._L.dfl_cache_rows(self._ctx, None, 0, ctypes.byref(n)), "dfl_cache_rows")
+        buf = (ctypes.c_int32 * max(1, n.value))()
+        _lib.check(self._L.dfl_cache_rows(self._ctx, buf, n.value, ctypes.byref(n)),
+                   "dfl_cache_rows")
+        return torch.tensor(list(buf)[:n.value], dtype=torch.long, device=self.device)
 
     def _device_state(self):
         n = ctypes.c_int32()
@@ -308,14 +334,6 @@ class DFlashDraftModel:
         elif want_len < dev_len:
             _lib.check(self._L.dfl_cache_trim(self._ctx, dev_len - want_len), "dfl_cache_trim")
         _lib.check(self._L.dfl_cache_set_offset(self._ctx, want_off), "dfl_cache_set_offset")
-
-    def _check_window(self, cache, new_rows):
-        for c in cache:
-            if c.sink_size > 0 and c.window_size > 0 and \
-                    c._len + new_rows > c.sink_size + c.window_size:
-                raise NotImplementedError(
-                    "sink/window eviction of the draft cache is not implemented on the GPU; "
-                    "use make_cache(0, 0) or a context below sink+window rows")
 
     # ------------------------------------------------------------------ forward
     def _apply_num_layers(self):
@@ -395,14 +413,11 @@ class DFlashDraftModel:
             _lib.check(self._L.dfl_cache_reset(self._ctx), "dfl_cache_reset")
             return out_h.unsqueeze(0)
         cache = list(cache)[:self.num_draft_layers]
-        self._check_window(cache, C + q)
         self._sync_cache(cache)
         self._ingest(target_hidden)
         out_h, _, _, _ = self._draft(noise=noise_embedding)
-        for c in cache:
-            c._len += C + q
-            c.offset += C + q
-            c._has_keys = True
+        for c in cache:       # context + block rows, as update_and_fetch leaves them
+            c._appended(C + q)
         return out_h.unsqueeze(0)
 
     def draft(self, ids, target_hidden=None, cache=None, return_logits=False,
@@ -426,9 +441,7 @@ class DFlashDraftModel:
             if cache is not None:
                 C = target_hidden.shape[-2]
                 for c in cache:
-                    c._len += C
-                    c.offset += C
-                    c._has_keys = True
+                    c._appended(C)
         out_h, _, out_l, out_i = self._draft(ids=ids, want_hidden=return_hidden,
                                              want_logits=return_logits, want_ids=True)
         res = [out_i]

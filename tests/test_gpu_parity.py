@@ -191,3 +191,44 @@ def test_bad_token_id_rejected():
     with pytest.raises(ValueError):   # context beyond capacity
         m.draft(torch.from_numpy(inp["ids"]),
                 torch.zeros((wl.ctx + 1, 2 * cfg.hidden_size * 5 // 2), dtype=torch.float16))
+
+
+@pytest.mark.parametrize("sink,window", [(4, 16), (0, 0)])
+def test_window_cache_protocol_matches_oracle(sink, window):
+    """Reference serial protocol over several steps with DFlashKVCache(sink, window):
+    forward(ctx rows, block) -> trim(block) -> ..., eviction of middle rows included
+    (dflash.py:160-212).  Outputs and the cached keys/values (in the reference's row
+    order) match the oracle's cache restatement."""
+    wl, cfg, t, inp, W = _full_case("tiny", seed=2)
+    B = wl.block
+    steps = (10, 7, 12, 3, 20, 1)
+    th_all = synth.np_normal(2, "window.th", (sum(steps), 5 * cfg.hidden_size), 1.0, np.float16)
+    noise = O.embed(W, inp["ids"]).astype(np.float16)
+    m = _model(cfg, max_ctx=sum(steps) + B)
+    m.load_weights(torch_tensors(t, "cuda"))
+    cache = m.make_cache(sink, window)
+    ocache = [O.OracleKVCache(sink, window) for _ in range(cfg.num_hidden_layers)]
+    ne = torch.from_numpy(noise)[None]
+    r0 = 0
+    for i, C in enumerate(steps):
+        th = th_all[r0:r0 + C]
+        r0 += C
+        ref = O.draft_forward(W, noise, th, cache=ocache, fp16=True)
+        out = m(ne, torch.from_numpy(th)[None], cache=cache)
+        torch.cuda.synchronize()
+        assert_close_fp16(out[0].float().cpu().numpy(), ref, what=f"step {i}")
+        for c in cache:
+            c.trim(B)
+        for c in ocache:
+            c.trim(B)
+        assert cache[0].offset == ocache[0].offset
+        assert cache[0].keys.shape[2] == ocache[0].keys.shape[1], f"step {i} cache length"
+    # one more forward so the device reconciles its cache with the handles, then compare
+    m._sync_cache(list(cache))
+    for layer in range(cfg.num_hidden_layers):
+        assert_close_fp16(cache[layer].keys[0].float().cpu().numpy(), ocache[layer].keys,
+                          what=f"layer {layer} keys")
+        assert_close_fp16(cache[layer].values[0].float().cpu().numpy(), ocache[layer].values,
+                          what=f"layer {layer} values")
+    if window:
+        assert ocache[0].keys.shape[1] == sink + window - B   # eviction happened
