@@ -165,7 +165,19 @@ int dfl_profile_enable(dfl_ctx* ctx, int32_t on);
 int dfl_profile_read(dfl_ctx* ctx, int32_t max_cat, char* names, double* total_ms,
                      int64_t* launches, int64_t* bytes, int32_t* n_cat);
 
-/* Sticky device-side error flags (bit 0: a token id outside [0, vocab)); reading clears. */
+/* Block noise embedding (generate.py:594-597 builds embed([anchor, mask x (B-1)])), with the
+ * soft anchor of the parallel caller (generate.py:1419-1437): out_noise [B][H] fp16 rows
+ * embed[ids[b]] of the loaded embedding; when correction_logits ([V] verify logits at the
+ * correction position, logits_dtype 0 fp32 / 1 fp16 / 2 bf16) is not NULL, row 0 is instead
+ * sum_r softmax(l)_r * embed[i_r] over the top_k (1..8, the reference uses 8) largest
+ * logits l at ids i_r -- fp32 softmax and sum, cast to fp16; lower index first on equal
+ * logits, NaN after every number.  V <= vocab. */
+int dfl_embed_block(dfl_ctx* ctx, const int32_t* ids, int32_t B, const void* correction_logits,
+                    int32_t logits_dtype, int32_t V, int32_t top_k, uint16_t* out_noise,
+                    void* stream);
+
+/* Sticky device-side error flags (bit 0: a token id outside [0, vocab); bit 1: soft-anchor
+ * logits without a single number); reading clears. */
 int dfl_device_errors(dfl_ctx* ctx, int32_t* flags, void* stream);
 
 #ifdef __cplusplus

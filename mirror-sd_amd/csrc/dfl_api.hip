@@ -116,6 +116,7 @@ struct dfl_ctx {
          *ctxbuf = nullptr;   // ctxbuf: fragment-layout tiles of the pass's fused context rows
   float *Op = nullptr, *Ml = nullptr;
   unsigned long long* keys = nullptr;
+  unsigned long long* sa_cand = nullptr;   // soft-anchor top-k candidates per scan workgroup
   int* err = nullptr;
   // stream-K GEMM state (block step)
   int n_cu = 256;
@@ -261,6 +262,7 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
       (r = x->alloc(&x->Op, (size_t)MAX_CHUNKS * x->NH * Bm * 128)) ||
       (r = x->alloc(&x->Ml, (size_t)MAX_CHUNKS * x->NH * Bm * 2)) ||
       (r = x->alloc(&x->keys, Bm, true)) || (r = x->alloc(&x->err, 1, true)) ||
+      (r = x->alloc(&x->sa_cand, (size_t)SA_BLOCKS * SA_TOPK_MAX)) ||
       (r = x->alloc(&x->fc_out, (size_t)ING_ROWS * x->H))) {
     delete x;
     return r;
@@ -893,6 +895,27 @@ int dfl_profile_read(dfl_ctx* ctx, int32_t max_cat, char* names, double* total_m
   }
   *n_cat = nc;
   return rc;
+}
+
+int dfl_embed_block(dfl_ctx* ctx, const int32_t* ids, int32_t B, const void* correction_logits,
+                    int32_t logits_dtype, int32_t V, int32_t top_k, uint16_t* out_noise,
+                    void* stream) {
+  const std::string w = "dfl_embed_block";
+  if (!ctx || !ids || !out_noise) return fail(DFL_EINVAL, w + ": null argument");
+  if (!ctx->embed) return fail(DFL_ESTATE, w + ": embedding not loaded");
+  if (B < 1 || B > 65535) return fail(DFL_EINVAL, w + ": block rows must be in [1, 65535]");
+  if (correction_logits) {
+    if (logits_dtype < 0 || logits_dtype > 2)
+      return fail(DFL_EINVAL, w + ": logits_dtype must be 0 (fp32), 1 (fp16) or 2 (bf16)");
+    if (top_k < 1 || top_k > SA_TOPK_MAX)
+      return fail(DFL_EINVAL, w + ": top_k must be in [1, " + std::to_string(SA_TOPK_MAX) + "]");
+    if (V < top_k || V > ctx->V)
+      return fail(DFL_EINVAL, w + ": logits length must be in [top_k, vocab]");
+  }
+  launch_embed_block(ids, B, ctx->embed, ctx->V, ctx->H, correction_logits, logits_dtype, V,
+                     top_k, ctx->sa_cand, reinterpret_cast<half_t*>(out_noise), ctx->err,
+                     (hipStream_t)stream);
+  return check_launch(w.c_str());
 }
 
 int dfl_device_errors(dfl_ctx* ctx, int32_t* flags, void* stream) {

@@ -70,6 +70,13 @@ void launch_pack_f16(const half_t* w, int rows, int K, uint4* dst, hipStream_t s
 // x[b] = ids ? embed[ids[b]] : noise[b] (x in the activation fragment layout, K = H);
 // rnorm[b] = 1/rms(x[b]); optionally
 // h[b] = RMSNorm(x[b]) * g.  An id outside [0, V) yields a zero row and sets *err |= 1.
+// Block embedding rows (generate.py:594-597) with an optional soft anchor in row 0
+// (generate.py:1419-1437); logits_dtype 0 fp32, 1 fp16, 2 bf16; cand holds
+// SA_BLOCKS * SA_TOPK_MAX keys.  err bit 0: token id out of range; bit 1: logits all NaN.
+constexpr int SA_TOPK_MAX = 8, SA_BLOCKS = 64;
+void launch_embed_block(const int32_t* ids, int B, const half_t* embed, int Vemb, int H,
+                        const void* logits, int logits_dtype, int V, int top_k,
+                        unsigned long long* cand, half_t* out, int* err, hipStream_t st);
 void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* noise, int B,
                        int H, int V, const half_t* g, float eps, half_t* x, half_t* h,
                        float* rnorm, int* err, hipStream_t st);

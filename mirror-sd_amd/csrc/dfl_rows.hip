@@ -229,4 +229,151 @@ void launch_argmax_finalize(unsigned long long* keys, int M, int32_t* ids, hipSt
                      M, ids);
 }
 
+// ---- block embedding with the soft anchor (generate.py:1419-1437) ----
+// noise rows = embed[ids[b]]; with correction logits, row 0 is instead
+//   sum_r softmax(top logits)_r * embed[top id_r]   (top_k largest logits, fp32 softmax and
+// fp32 sum, cast to fp16).  The top-k runs in two launches: SA_BLOCKS workgroups each keep
+// the top_k of a contiguous slice of the vocabulary, then workgroup 0 of the embedding
+// launch merges the SA_BLOCKS * SA_TOPK_MAX candidates.  Ranking: larger logit first,
+// lower index on ties, NaN after every number.
+
+template <int DT>
+DFL_DEV float logit_value(const void* p, size_t i) {
+  if constexpr (DT == 0) return reinterpret_cast<const float*>(p)[i];
+  else if constexpr (DT == 1) return h2f(reinterpret_cast<const half_t*>(p)[i]);
+  else return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(p)[i] << 16);   // bf16
+}
+
+DFL_DEV unsigned long long rank_key(float v, uint32_t i) {
+  if (v != v) return 0ull;   // NaN: never selected ahead of a number; 0 also marks "empty"
+  return ((unsigned long long)float_order_key(v) << 32) | (0xFFFFFFFFu - i);
+}
+DFL_DEV uint32_t rank_index(unsigned long long key) {
+  return 0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull);
+}
+
+// t: descending list; insert x if it beats the last entry (one bubble pass keeps the order)
+DFL_DEV void topk_push(unsigned long long (&t)[SA_TOPK_MAX], unsigned long long x) {
+  if (x <= t[SA_TOPK_MAX - 1]) return;
+  t[SA_TOPK_MAX - 1] = x;
+#pragma unroll
+  for (int i = SA_TOPK_MAX - 1; i > 0; --i) {
+    const unsigned long long a = t[i - 1], b = t[i];
+    t[i - 1] = a > b ? a : b;
+    t[i] = a > b ? b : a;
+  }
+}
+
+DFL_DEV unsigned long long wave_max_u64(unsigned long long v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const unsigned long long w = __shfl_xor(v, o, 64);
+    v = w > v ? w : v;
+  }
+  return v;
+}
+
+// The k largest keys held in the block's per-thread lists -> out[0 .. k) (shared memory),
+// 0 where fewer exist.  Keys are unique (they carry the index), so one thread pops.
+DFL_DEV void block_topk(unsigned long long (&t)[SA_TOPK_MAX], int k, unsigned long long* sm,
+                        unsigned long long* out) {
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, nw = blockDim.x >> 6;
+  for (int r = 0; r < k; ++r) {
+    const unsigned long long c = wave_max_u64(t[0]);
+    if (l == 0) sm[w] = c;
+    __syncthreads();
+    unsigned long long best = sm[0];
+    for (int i = 1; i < nw; ++i) best = sm[i] > best ? sm[i] : best;
+    if (best != 0ull && t[0] == best) {
+#pragma unroll
+      for (int i = 0; i < SA_TOPK_MAX - 1; ++i) t[i] = t[i + 1];
+      t[SA_TOPK_MAX - 1] = 0ull;
+    }
+    if (threadIdx.x == 0) out[r] = best;
+    __syncthreads();   // sm is rewritten by the next round
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void topk_scan_kernel(const void* __restrict__ logits, int V,
+                                                        int k, unsigned long long* __restrict__ cand) {
+  __shared__ unsigned long long sm[16], top[SA_TOPK_MAX];
+  unsigned long long t[SA_TOPK_MAX];
+#pragma unroll
+  for (int i = 0; i < SA_TOPK_MAX; ++i) t[i] = 0ull;
+  const int chunk = (V + gridDim.x - 1) / gridDim.x;
+  const int lo = blockIdx.x * chunk, hi = min(V, lo + chunk);
+  for (int i = lo + (int)threadIdx.x; i < hi; i += blockDim.x)
+    topk_push(t, rank_key(logit_value<DT>(logits, i), (uint32_t)i));
+  block_topk(t, k, sm, top);
+  if (threadIdx.x < SA_TOPK_MAX)
+    cand[blockIdx.x * SA_TOPK_MAX + threadIdx.x] = (int)threadIdx.x < k ? top[threadIdx.x] : 0ull;
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void embed_block_kernel(
+    const int32_t* __restrict__ ids, const half_t* __restrict__ embed, int Vemb, int H,
+    const void* __restrict__ logits, int k, const unsigned long long* __restrict__ cand,
+    half_t* __restrict__ out, int* __restrict__ err) {
+  const int b = blockIdx.x;
+  half_t* dst = out + (size_t)b * H;
+  if (b == 0 && logits) {
+    __shared__ unsigned long long sm[16], top[SA_TOPK_MAX];
+    __shared__ float wgt[SA_TOPK_MAX];
+    __shared__ int row[SA_TOPK_MAX];
+    unsigned long long t[SA_TOPK_MAX];
+#pragma unroll
+    for (int i = 0; i < SA_TOPK_MAX; ++i) t[i] = 0ull;
+    for (int i = threadIdx.x; i < SA_BLOCKS * SA_TOPK_MAX; i += blockDim.x) topk_push(t, cand[i]);
+    block_topk(t, k, sm, top);
+    if (threadIdx.x == 0) {
+      // softmax over the selected logits in fp32; top[0] holds the largest
+      float v[SA_TOPK_MAX], s = 0.f;
+      const float mx = top[0] ? logit_value<DT>(logits, rank_index(top[0])) : 0.f;
+      for (int r = 0; r < k; ++r) {
+        row[r] = top[r] ? (int)rank_index(top[r]) : -1;
+        v[r] = row[r] >= 0 ? expf(logit_value<DT>(logits, row[r]) - mx) : 0.f;
+        s += v[r];
+      }
+      if (!top[0]) atomicOr(err, 2);   // no number among the logits: zero anchor row
+      for (int r = 0; r < k; ++r) wgt[r] = top[0] ? v[r] / s : 0.f;
+    }
+    __syncthreads();
+    for (int c = threadIdx.x; c < H; c += blockDim.x) {
+      float acc = 0.f;
+      for (int r = 0; r < k; ++r)
+        if (row[r] >= 0) acc += wgt[r] * h2f(embed[(size_t)row[r] * H + c]);
+      dst[c] = f2h(acc);
+    }
+    return;
+  }
+  const int id = ids[b];
+  const bool bad = id < 0 || id >= Vemb;   // out-of-range token id: flag it, zero row
+  if (bad && threadIdx.x == 0) atomicOr(err, 1);
+  const half_t* src = embed + (size_t)(bad ? 0 : id) * H;
+  for (int c = threadIdx.x; c < H; c += blockDim.x) dst[c] = bad ? (half_t)0.0f : src[c];
+}
+
+template <int DT>
+static void launch_embed_block_t(const int32_t* ids, int B, const half_t* embed, int Vemb, int H,
+                                 const void* logits, int V, int top_k, unsigned long long* cand,
+                                 half_t* out, int* err, hipStream_t st) {
+  if (logits)
+    hipLaunchKernelGGL(topk_scan_kernel<DT>, dim3(SA_BLOCKS), dim3(256), 0, st, logits, V, top_k,
+                       cand);
+  hipLaunchKernelGGL(embed_block_kernel<DT>, dim3(B), dim3(256), 0, st, ids, embed, Vemb, H,
+                     logits, top_k, cand, out, err);
+}
+
+void launch_embed_block(const int32_t* ids, int B, const half_t* embed, int Vemb, int H,
+                        const void* logits, int logits_dtype, int V, int top_k,
+                        unsigned long long* cand, half_t* out, int* err, hipStream_t st) {
+  if (logits_dtype == 0)
+    launch_embed_block_t<0>(ids, B, embed, Vemb, H, logits, V, top_k, cand, out, err, st);
+  else if (logits_dtype == 1)
+    launch_embed_block_t<1>(ids, B, embed, Vemb, H, logits, V, top_k, cand, out, err, st);
+  else
+    launch_embed_block_t<2>(ids, B, embed, Vemb, H, logits, V, top_k, cand, out, err, st);
+}
+
 }  // namespace dfl

@@ -68,6 +68,8 @@ SIGNATURES = {
     "dfl_profile_read": (c_int32, [c_void_p, c_int32, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
                                    ctypes.POINTER(c_int64), ctypes.POINTER(c_int64),
                                    ctypes.POINTER(c_int32)]),
+    "dfl_embed_block": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p, c_int32, c_int32,
+                                  c_int32, c_void_p, c_void_p]),
     "dfl_device_errors": (c_int32, [c_void_p, ctypes.POINTER(c_int32), c_void_p]),
 }
 

@@ -144,6 +144,9 @@ class DFlashDraftModel:
         self._prepared = None
         self._out_hidden = None
         self._out_ids = None
+        self._split_bufs = None
+        self._draft_stream = None
+        self._done = None
 
     # ------------------------------------------------------------------ lifecycle
     def close(self):
@@ -560,43 +563,132 @@ class DFlashDraftModel:
         """Return the raw target_hidden; fc + hidden_norm run inside the ingest kernel."""
         return target_hidden
 
+    # Dispatch probes of the parallel caller (generate.py:1320-1333): no GPU fallback model
+    # is needed (the context limit is max_ctx_len rows of device cache), and b_logits is
+    # non-None once an lm_head is loaded, which selects the fused read_draft_tokens path.
+    gpu_fallback = None
+
+    @property
+    def b_logits(self):
+        return True if self._has_lm else None
+
+    def embed_block(self, block_ids, correction_logits=None, top_k: int = 8):
+        """Noise embedding [1, B, H] fp16 of the block ids (generate.py:594-597), rows of
+        the loaded target embedding.  With ``correction_logits`` ([V] verify logits at the
+        correction position, fp32/fp16/bf16) row 0 is the soft anchor of
+        generate.py:1419-1437: sum_i softmax(top-k logits)_i * embed(i)."""
+        import torch
+        if not self._has_embed:
+            raise RuntimeError("embedding not loaded")
+        ids = torch.as_tensor(block_ids, dtype=torch.int32).reshape(-1)
+        V_emb = self.config.vocab_size
+        if ids.numel() == 0:
+            raise ValueError("block_ids is empty")
+        if int(ids.min()) < 0 or int(ids.max()) >= V_emb:
+            raise ValueError(f"token id outside [0, {V_emb})")
+        ids = ids.to(self.device).contiguous()
+        B, H = ids.numel(), self.config.hidden_size
+        out = torch.empty((B, H), dtype=torch.float16, device=self.device)
+        lg, code, V = None, 0, 0
+        if correction_logits is not None:
+            codes = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+            lg = correction_logits.reshape(-1).to(self.device)
+            if lg.dtype not in codes:
+                lg = lg.float()
+            lg = lg.contiguous()
+            code, V = codes[lg.dtype], lg.numel()
+        _lib.check(self._L.dfl_embed_block(self._ctx, ids.data_ptr(), B, _lib.ptr(lg), code, V,
+                                           int(top_k), out.data_ptr(), self._stream()),
+                   "dfl_embed_block")
+        self._keep["embed_src"] = (ids, lg)
+        return out.unsqueeze(0)
+
     def prepare_forward(self, noise_embedding, precomputed_context, cache, target_hidden):
-        """ane_model.py:538-562: stage inputs on the calling thread."""
+        """ane_model.py:538-562: stage the inputs and output buffers on the calling thread
+        (the caller's current stream); run_kernels does the GPU work on the draft's own
+        stream, which first waits for everything queued so far on the caller's stream."""
         import torch
         self._apply_num_layers()
+        if not all(self._layers_loaded[:self.num_draft_layers]) or not self._has_head:
+            raise RuntimeError("weights not loaded")
         rope_offset = 0
         if cache is not None and len(cache) > 0 and cache[0].offset > 0:
-            rope_offset = cache[0].offset
-        ctx_len = target_hidden.shape[-2]
-        if ctx_len > self.max_ctx_len:
-            raise ValueError(f"ctx_len={ctx_len} exceeds max_ctx_len={self.max_ctx_len}")
-        ne = noise_embedding.to(self.device, torch.float16).contiguous()
-        th = target_hidden.to(self.device, torch.float16).contiguous()
+            rope_offset = int(cache[0].offset)
+        th = precomputed_context if precomputed_context is not None else target_hidden
+        ne = noise_embedding
+        if th.dim() == 3:
+            if th.shape[0] != 1:
+                raise ValueError("batch size must be 1")
+            th = th[0]
+        if ne.dim() == 3:
+            if ne.shape[0] != 1:
+                raise ValueError("batch size must be 1")
+            ne = ne[0]
+        H = self.config.hidden_size
+        if th.shape[-2] > self.max_ctx_len:
+            raise ValueError(f"ctx_len={th.shape[-2]} exceeds max_ctx_len={self.max_ctx_len}")
+        if th.shape[-1] != self.n_feat * H:
+            raise ValueError(f"target_hidden must be [C, {self.n_feat * H}], got {tuple(th.shape)}")
+        if ne.shape[-1] != H or not 1 <= ne.shape[0] <= self.max_block:
+            raise ValueError(f"noise_embedding must be [B <= {self.max_block}, {H}]")
+        ne = ne.to(self.device, torch.float16).contiguous()
+        th = th.to(self.device, torch.float16).contiguous()
+        B = ne.shape[0]
+        if self._split_bufs is None or self._split_bufs[0].shape[0] != B:
+            self._split_bufs = (torch.empty((B, H), dtype=torch.float16, device=self.device),
+                                torch.empty((B,), dtype=torch.int32, device=self.device))
+        if self._draft_stream is None:
+            self._draft_stream = torch.cuda.Stream(device=self.device)   # default priority
+            self._done = torch.cuda.Event()
+        ds = self._draft_stream
+        ds.wait_stream(torch.cuda.current_stream(self.device))
+        for t in (ne, th) + self._split_bufs:
+            t.record_stream(ds)
         self._prepared = (ne, th, rope_offset)
+        self._out_hidden = self._out_ids = None
 
-    def run_kernels(self):
-        """ane_model.py:564-589: the ANE path keeps no K/V and re-ingests the current
-        target_hidden with RoPE positions starting at cache.offset."""
+    def run_kernels(self, wait: bool = True):
+        """ane_model.py:564-589 on the draft's own HIP stream.  Only library calls (ctypes
+        releases the GIL around each), so a worker thread can run it while the caller's
+        stream does the target verify (generate.py:1339-1345, 1469-1477).  The ANE path
+        keeps no K/V: the step's target_hidden is re-ingested at RoPE positions from
+        cache.offset.  ``wait`` (default, as the ANE call blocks) returns once the draft
+        is done; read_output / read_draft_tokens order the caller's stream after it."""
         if self._prepared is None:
             raise RuntimeError("prepare_forward() must be called first")
         ne, th, rope_offset = self._prepared
-        _lib.check(self._L.dfl_cache_reset(self._ctx), "dfl_cache_reset")
-        _lib.check(self._L.dfl_cache_set_offset(self._ctx, int(rope_offset)),
-                   "dfl_cache_set_offset")
+        out_h, out_i = self._split_bufs
+        L, ctx, st = self._L, self._ctx, self._draft_stream.cuda_stream
+        _lib.check(L.dfl_cache_reset(ctx), "dfl_cache_reset")
+        _lib.check(L.dfl_cache_set_offset(ctx, int(rope_offset)), "dfl_cache_set_offset")
         self._gen += 1
-        self._ingest(th)
-        h, _, _, ids = self._draft(noise=ne, want_hidden=True, want_ids=self._has_lm)
-        self._out_hidden, self._out_ids = h, ids
+        if th.shape[0]:
+            _lib.check(L.dfl_ingest_context(ctx, th.data_ptr(), th.shape[0], st),
+                       "dfl_ingest_context")
+        _lib.check(L.dfl_draft_block(ctx, ne.data_ptr(), None, ne.shape[0], out_h.data_ptr(),
+                                     None, None, out_i.data_ptr() if self._has_lm else None, st),
+                   "dfl_draft_block")
+        self._done.record(self._draft_stream)
+        if wait:
+            self._done.synchronize()
+        self._out_hidden, self._out_ids = out_h, (out_i if self._has_lm else None)
+
+    def _after_draft(self, t):
+        import torch
+        torch.cuda.current_stream(self.device).wait_event(self._done)
+        return t.clone()   # the buffers are rewritten by the next run_kernels
 
     def read_output(self):
+        """ane_model.py:591-594: final-normed hidden [1, q, H] fp16."""
         if self._out_hidden is None:
             raise RuntimeError("run_kernels() has not produced an output")
-        return self._out_hidden.unsqueeze(0)
+        return self._after_draft(self._out_hidden).unsqueeze(0)
 
     def read_draft_tokens(self):
+        """ane_model.py:596-604 / read_argmax (wrapper.rs:108-140): argmax ids [1, q]."""
         if self._out_ids is None:
             raise RuntimeError("lm_head not loaded -- no draft tokens")
-        return self._out_ids.reshape(1, -1)
+        return self._after_draft(self._out_ids).reshape(1, -1)
 
     def run_prepared(self):
         self.run_kernels()

@@ -22,6 +22,9 @@ It restates, in numpy, the reference's MLX draft forward and its W8A16 quantiser
 * ``OracleKVCache``       DFlashKVCache, dflash.py:139-212
 * ``lm_head_argmax``      generate.py:604-606 + target.py:192-197 + dflash.py:133-136
                           (greedy: first index of the maximum, as wrapper.rs:124-134)
+* ``soft_anchor``         generate.py:1419-1437 (top-k of the verify logits, fp32 softmax,
+                          weighted sum of their embedding rows); ``embed_block`` the block
+                          noise embedding of generate.py:1419-1420 with it in row 0
 
 Two arithmetic modes:
 
@@ -334,6 +337,38 @@ def draft_forward(W: OracleWeights, noise: np.ndarray, target_hidden: np.ndarray
 def embed(W: OracleWeights, ids: np.ndarray) -> np.ndarray:
     """embed_tokens(ids) (generate.py:594-597; target.py:188-189)."""
     return W.embed[np.asarray(ids, dtype=np.int64)]
+
+
+def soft_anchor(embed_table: np.ndarray, logits: np.ndarray, top_k: int = 8) -> np.ndarray:
+    """generate.py:1424-1435: ``top_ids = argsort(-logits)[:k]``; ``w = softmax(fp32 top
+    logits)``; anchor = sum_i w_i * embed(top_ids_i) in fp32, cast to the embedding dtype.
+
+    Order: larger logit first, lower index on equal logits (stable sort), NaN after every
+    number (mx.argsort's order on ties and NaN is not documented).  The sum runs over the
+    selected rows in rank order."""
+    lg = np.asarray(logits).astype(np.float32).ravel()
+    key = np.where(np.isnan(lg), np.float32(np.inf), -lg)
+    order = np.argsort(key, kind="stable")[:top_k]
+    order = order[~np.isnan(lg[order])]
+    if order.size == 0:
+        return np.zeros(embed_table.shape[1], dtype=embed_table.dtype)
+    v = lg[order]
+    e = np.exp(v - v[0]).astype(np.float32)
+    w = (e / e.sum(dtype=np.float32)).astype(np.float32)
+    acc = np.zeros(embed_table.shape[1], dtype=np.float32)
+    for r, i in enumerate(order):
+        acc = acc + w[r] * embed_table[i].astype(np.float32)
+    return acc.astype(embed_table.dtype)
+
+
+def embed_block(embed_table: np.ndarray, ids: np.ndarray, correction_logits=None,
+                top_k: int = 8) -> np.ndarray:
+    """Block noise embedding: rows embed(ids) (generate.py:1419-1420), row 0 replaced by the
+    soft anchor when correction logits are given (generate.py:1422-1437)."""
+    out = embed_table[np.asarray(ids, dtype=np.int64)].copy()
+    if correction_logits is not None:
+        out[0] = soft_anchor(embed_table, correction_logits, top_k)
+    return out
 
 
 def lm_head_logits(h: np.ndarray, w_lm: np.ndarray, dtype=F64, chunk: int = 16384) -> np.ndarray:

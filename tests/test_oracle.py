@@ -443,3 +443,79 @@ def test_cache_window_eviction():
     assert c.keys[0, :, 0].tolist() == [0, 1, 5, 6, 7] and c.offset == 8
     c.trim(2)
     assert c.keys[0, :, 0].tolist() == [0, 1, 5] and c.offset == 6
+
+
+# ---------------------------------------------------------------------------
+# Soft anchor (generate.py:1419-1437)
+# ---------------------------------------------------------------------------
+
+def _emb(V=300, H=32, seed=0):
+    return np.random.default_rng(seed).normal(0, 0.02, (V, H)).astype(np.float16)
+
+
+def test_soft_anchor_top1_is_argmax_row():
+    E = _emb()
+    lg = np.random.default_rng(1).normal(0, 3, E.shape[0]).astype(np.float32)
+    np.testing.assert_array_equal(O.soft_anchor(E, lg, top_k=1), E[int(np.argmax(lg))])
+
+
+def test_soft_anchor_dominant_logit_gives_its_row():
+    E = _emb()
+    lg = np.random.default_rng(2).normal(0, 1, E.shape[0]).astype(np.float32)
+    lg[123] = 200.0   # exp(x - 200) underflows to 0 for every other selected logit
+    np.testing.assert_array_equal(O.soft_anchor(E, lg), E[123])
+
+
+def test_soft_anchor_equal_logits_give_mean_row():
+    E = _emb()
+    lg = np.full(E.shape[0], -5.0, dtype=np.float32)
+    top = [7, 40, 41, 99, 150, 151, 200, 299]
+    lg[top] = 2.5
+    want = E[top].astype(np.float64).mean(0)
+    got = O.soft_anchor(E, lg).astype(np.float64)
+    np.testing.assert_allclose(got, want, atol=1e-5, rtol=2e-3)
+
+
+def test_soft_anchor_two_rows_closed_form():
+    """Logits differing by ln 3 (the rest at -inf) weigh the rows 3/4 and 1/4."""
+    E = _emb()
+    lg = np.full(E.shape[0], -np.inf, dtype=np.float32)
+    lg[10], lg[20] = 1.0 + math.log(3.0), 1.0
+    want = 0.75 * E[10].astype(np.float64) + 0.25 * E[20].astype(np.float64)
+    np.testing.assert_allclose(O.soft_anchor(E, lg).astype(np.float64), want, atol=2e-5)
+
+
+def test_soft_anchor_selection_and_weights_against_library():
+    """The selected ids are the top-k by np.argpartition; the weights are scipy's softmax."""
+    from scipy.special import softmax
+    E = _emb(V=1000, H=16)
+    lg = np.random.default_rng(3).normal(0, 2, 1000).astype(np.float32)
+    top = np.argpartition(-lg, 8)[:8]
+    w = softmax(lg[top].astype(np.float64))
+    want = (w[:, None] * E[top].astype(np.float64)).sum(0)
+    np.testing.assert_allclose(O.soft_anchor(E, lg).astype(np.float64), want, atol=1e-5,
+                               rtol=2e-3)
+
+
+def test_soft_anchor_ties_pick_lowest_ids_and_skip_nan():
+    E = _emb()
+    lg = np.zeros(E.shape[0], dtype=np.float32)
+    lg[[5, 9, 250]] = np.nan
+    # every number ties: the 3 lowest non-NaN ids are 0, 1, 2
+    want = E[[0, 1, 2]].astype(np.float64).mean(0)
+    np.testing.assert_allclose(O.soft_anchor(E, lg, top_k=3).astype(np.float64), want,
+                               atol=1e-5, rtol=2e-3)
+    lg2 = np.full(E.shape[0], np.nan, dtype=np.float32)
+    lg2[17] = -3.0
+    np.testing.assert_array_equal(O.soft_anchor(E, lg2), E[17])
+
+
+def test_embed_block_rows():
+    E = _emb()
+    ids = np.array([3, 299, 299, 0])
+    np.testing.assert_array_equal(O.embed_block(E, ids), E[ids])
+    lg = np.zeros(E.shape[0], dtype=np.float32)
+    lg[42] = 300.0
+    out = O.embed_block(E, ids, lg)
+    np.testing.assert_array_equal(out[0], E[42])
+    np.testing.assert_array_equal(out[1:], E[ids[1:]])
