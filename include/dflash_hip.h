@@ -96,6 +96,19 @@ int dfl_ingest_context(dfl_ctx* ctx, const uint16_t* target_hidden, int32_t C, v
 /* Same for context rows that are already fused ([C][H] fp16): skips fc + hidden_norm. */
 int dfl_ingest_fused(dfl_ctx* ctx, const uint16_t* ctx_hidden, int32_t C, void* stream);
 
+/* Context capture fused with the ingest: the n_feats tapped target-layer outputs
+ * (forward_with_hidden_states, target.py:258-278, in target_layer_ids order) are read
+ * where they lie -- feats[j] -> [C][ld] fp16 device rows, first H columns used, 16-byte
+ * aligned, ld >= H and ld % 8 == 0 -- as if concatenated along the hidden axis
+ * (extract_context_feature, dflash.py:122-130) and passed to dfl_ingest_context.
+ * n_feats must equal n_target_feat. */
+int dfl_ingest_features(dfl_ctx* ctx, const uint16_t* const* feats, int32_t n_feats,
+                        int64_t ld, int32_t C, void* stream);
+/* extract_context_feature materialised: out [C][n_feats * H] fp16 (16-byte aligned) =
+ * the feature rows concatenated along the hidden axis; same feats / ld rules. */
+int dfl_concat_features(const uint16_t* const* feats, int32_t n_feats, int64_t ld, int32_t C,
+                        int32_t H, uint16_t* out, void* stream);
+
 /* Draft one block (DFlashDraftModel.__call__, dflash.py:384-403, with the block K/V
  * appended and trimmed again as generate.py:599-609 does; ANEDraftModel.run_kernels +
  * read_output + read_draft_tokens, ane_model.py:564-604; read_argmax, wrapper.rs:108-140).

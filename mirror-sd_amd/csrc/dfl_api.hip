@@ -544,8 +544,11 @@ static int ingest_kv_rows(dfl_ctx* ctx, int rows, int r0, hipStream_t st) {
   return DFL_OK;
 }
 
-static int ingest(dfl_ctx* ctx, const uint16_t* src, int C, bool fused, void* stream) {
-  if (!ctx || (!src && C > 0)) return fail(DFL_EINVAL, "dfl_ingest: null argument");
+// Context rows from one row-major buffer (src: [C][n_target_feat * H], or [C][H] already
+// fused), or with feats set from the tapped layers' own tensors (src unused).
+static int ingest(dfl_ctx* ctx, const uint16_t* src, int C, bool fused, void* stream,
+                  const FeatPtrs* feats = nullptr) {
+  if (!ctx || (!src && !feats && C > 0)) return fail(DFL_EINVAL, "dfl_ingest: null argument");
   if (C < 0) return fail(DFL_EINVAL, "dfl_ingest: negative row count");
   if (!ctx->sq().window && (long long)ctx->sq().len + C > ctx->cfg.max_ctx)
     return fail(DFL_ERANGE, "dfl_ingest: context rows " + std::to_string(ctx->sq().len + C) +
@@ -566,7 +569,13 @@ static int ingest(dfl_ctx* ctx, const uint16_t* src, int C, bool fused, void* st
       // hidden_norm(fc(target_hidden)): fc output rounded to fp16 (Linear), then RMSNorm
       {
         ProfScope ps(ctx, P_INGEST_FC, 0, st);
-        launch_rows_to_afl(in + (size_t)r0 * K, rows, K, K, ctx->ing_x, st);
+        if (feats) {
+          FeatPtrs f = *feats;
+          for (int j = 0; j < f.n; ++j) f.p[j] += (size_t)r0 * f.ld;
+          launch_feats_to_afl(f, rows, H, ctx->ing_x, st);
+        } else {
+          launch_rows_to_afl(in + (size_t)r0 * K, rows, K, K, ctx->ing_x, st);
+        }
       }
       DFL_TRY(ingest_gemm(ctx, P_INGEST_FC, WT_F16, ctx->sk_ifc, ctx->w_fc, nullptr, H, K / 16,
                           ctx->ing_x, K, rows, ctx->fc_out, st));
@@ -588,6 +597,49 @@ int dfl_ingest_context(dfl_ctx* ctx, const uint16_t* target_hidden, int32_t C, v
 
 int dfl_ingest_fused(dfl_ctx* ctx, const uint16_t* ctx_hidden, int32_t C, void* stream) {
   return ingest(ctx, ctx_hidden, C, true, stream);
+}
+
+static int feat_ptrs(const uint16_t* const* feats, int32_t n_feats, int64_t ld, int H,
+                     const char* who, FeatPtrs& f) {
+  const std::string w(who);
+  if (!feats) return fail(DFL_EINVAL, w + ": null feature array");
+  if (n_feats < 1 || n_feats > MAX_FEATS)
+    return fail(DFL_EINVAL, w + ": n_feats must be in [1, " + std::to_string(MAX_FEATS) + "]");
+  if (ld < H || ld % 8)
+    return fail(DFL_EINVAL, w + ": row stride must be >= hidden and a multiple of 8");
+  f.n = n_feats;
+  f.ld = ld;
+  for (int j = 0; j < n_feats; ++j) {
+    if (!feats[j]) return fail(DFL_EINVAL, w + ": null feature pointer " + std::to_string(j));
+    if (reinterpret_cast<uintptr_t>(feats[j]) & 15)
+      return fail(DFL_EINVAL, w + ": feature " + std::to_string(j) + " not 16-byte aligned");
+    f.p[j] = reinterpret_cast<const half_t*>(feats[j]);
+  }
+  return DFL_OK;
+}
+
+int dfl_ingest_features(dfl_ctx* ctx, const uint16_t* const* feats, int32_t n_feats,
+                        int64_t ld, int32_t C, void* stream) {
+  if (!ctx) return fail(DFL_EINVAL, "dfl_ingest_features: null argument");
+  FeatPtrs f{};
+  DFL_TRY(feat_ptrs(feats, n_feats, ld, ctx->H, "dfl_ingest_features", f));
+  if (n_feats != ctx->NF)
+    return fail(DFL_EINVAL, "dfl_ingest_features: " + std::to_string(n_feats) +
+                                " features, the fc expects " + std::to_string(ctx->NF));
+  return ingest(ctx, nullptr, C, false, stream, &f);
+}
+
+int dfl_concat_features(const uint16_t* const* feats, int32_t n_feats, int64_t ld, int32_t C,
+                        int32_t H, uint16_t* out, void* stream) {
+  if (!out || C < 0 || H <= 0 || H % 8)
+    return fail(DFL_EINVAL, "dfl_concat_features: bad output, rows or hidden (H % 8 == 0)");
+  FeatPtrs f{};
+  DFL_TRY(feat_ptrs(feats, n_feats, ld, H, "dfl_concat_features", f));
+  if (reinterpret_cast<uintptr_t>(out) & 15)
+    return fail(DFL_EINVAL, "dfl_concat_features: output not 16-byte aligned");
+  if (C == 0) return DFL_OK;
+  launch_concat_feats(f, C, H, reinterpret_cast<half_t*>(out), (hipStream_t)stream);
+  return check_launch("dfl_concat_features");
 }
 
 // One draft block for sequences seq0 .. seq0 + n_seq - 1 together: B rows each, stacked

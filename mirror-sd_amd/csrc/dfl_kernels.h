@@ -77,6 +77,16 @@ constexpr int SA_TOPK_MAX = 8, SA_BLOCKS = 64;
 void launch_embed_block(const int32_t* ids, int B, const half_t* embed, int Vemb, int H,
                         const void* logits, int logits_dtype, int V, int top_k,
                         unsigned long long* cand, half_t* out, int* err, hipStream_t st);
+// Feature tensors of the tapped target layers: p[j] -> [rows][ld] fp16 (first H columns
+// used), 16-byte aligned, ld % 8 == 0.
+constexpr int MAX_FEATS = 16;
+struct FeatPtrs {
+  const half_t* p[MAX_FEATS];
+  int n;
+  long long ld;
+};
+void launch_feats_to_afl(const FeatPtrs& f, int rows, int H, half_t* dst, hipStream_t st);
+void launch_concat_feats(const FeatPtrs& f, int rows, int H, half_t* out, hipStream_t st);
 void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* noise, int B,
                        int H, int V, const half_t* g, float eps, half_t* x, half_t* h,
                        float* rnorm, int* err, hipStream_t st);

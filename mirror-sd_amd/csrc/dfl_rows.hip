@@ -118,6 +118,45 @@ void launch_rows_to_afl(const half_t* src, int rows, int K, int ld, half_t* dst,
                      src, rows, K, ld, dst);
 }
 
+// Same for the concatenation of nf feature tensors along the hidden axis
+// (extract_context_feature, dflash.py:122-130): column k of the fused row comes from
+// feature k / H at column k % H; H % 8 == 0, so one 8-column chunk never straddles two.
+__global__ __launch_bounds__(256) void feats_to_afl_kernel(FeatPtrs f, int rows, int H,
+                                                           half_t* __restrict__ dst) {
+  const int r = blockIdx.y;
+  const int K = f.n * H;
+  const int k = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (k >= K) return;
+  const int j = k / H;
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (r < rows) v = *reinterpret_cast<const u32x4*>(f.p[j] + (size_t)r * f.ld + (k - j * H));
+  *reinterpret_cast<u32x4*>(dst + afl_index(r, k, K)) = v;
+}
+
+void launch_feats_to_afl(const FeatPtrs& f, int rows, int H, half_t* dst, hipStream_t st) {
+  const int tiles_rows = ((rows + 31) / 32) * 32;
+  hipLaunchKernelGGL(feats_to_afl_kernel, dim3((f.n * H / 8 + 255) / 256, tiles_rows), dim3(256),
+                     0, st, f, rows, H, dst);
+}
+
+// Row-major concatenation [rows][nf * H] of the feature tensors (the materialised
+// extract_context_feature).
+__global__ __launch_bounds__(256) void concat_feats_kernel(FeatPtrs f, int H,
+                                                           half_t* __restrict__ out) {
+  const int r = blockIdx.y;
+  const int K = f.n * H;
+  const int k = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (k >= K) return;
+  const int j = k / H;
+  *reinterpret_cast<u32x4*>(out + (size_t)r * K + k) =
+      *reinterpret_cast<const u32x4*>(f.p[j] + (size_t)r * f.ld + (k - j * H));
+}
+
+void launch_concat_feats(const FeatPtrs& f, int rows, int H, half_t* out, hipStream_t st) {
+  hipLaunchKernelGGL(concat_feats_kernel, dim3((f.n * H / 8 + 255) / 256, rows), dim3(256), 0, st,
+                     f, H, out);
+}
+
 // RMSNorm of row-major fp16 rows [rows][H] (h = fp16(fp16(x * r) * g), r = 1/rms in fp32)
 // written in the activation fragment layout; padded rows of the last tile are zero.
 __global__ __launch_bounds__(ROW_THREADS) void rms_norm_afl_kernel(const half_t* __restrict__ src,

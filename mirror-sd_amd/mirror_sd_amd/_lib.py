@@ -48,6 +48,10 @@ SIGNATURES = {
     "dfl_load_head": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "dfl_ingest_context": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p]),
     "dfl_ingest_fused": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p]),
+    "dfl_ingest_features": (c_int32, [c_void_p, ctypes.POINTER(c_void_p), c_int32,
+                                      ctypes.c_int64, c_int32, c_void_p]),
+    "dfl_concat_features": (c_int32, [ctypes.POINTER(c_void_p), c_int32, ctypes.c_int64,
+                                      c_int32, c_int32, c_void_p, c_void_p]),
     "dfl_draft_block": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, c_void_p, c_void_p,
                                   c_void_p, c_void_p, c_void_p]),
     "dfl_draft_batch": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p, c_int32, c_void_p,

@@ -108,18 +108,28 @@ def build_target_layer_ids(num_target_layers: int, num_draft_layers: int) -> Lis
             for i in range(num_draft_layers)]
 
 
+def select_context_features(hidden_states: Sequence, layer_ids: Sequence[int]) -> list:
+    """The tensors extract_context_feature concatenates (dflash.py:124-129): all of them
+    when there is one per layer id, else (every layer output, embedding at index 0)
+    layer ``lid`` read at ``lid + 1``."""
+    if len(hidden_states) == len(layer_ids):
+        return list(hidden_states)
+    return [hidden_states[lid + 1] for lid in layer_ids]
+
+
 def extract_context_feature(hidden_states: Sequence, layer_ids: Sequence[int]):
     """dflash.py:122-130: concatenate tapped layer outputs along the feature axis.
 
-    Works on torch tensors or numpy arrays.  When ``hidden_states`` holds every
-    layer output (embedding at index 0), layer ``lid`` is read at ``lid + 1``.
+    Works on torch tensors or numpy arrays; GPU tensors are concatenated by the library's
+    copy kernel.  ``DFlashDraftModel`` also takes the list itself as ``target_hidden`` and
+    then reads the tensors where they lie (no concatenated copy).
     """
-    if len(hidden_states) == len(layer_ids):
-        sel = list(hidden_states)
-    else:
-        sel = [hidden_states[lid + 1] for lid in layer_ids]
+    sel = select_context_features(hidden_states, layer_ids)
     first = sel[0]
     if hasattr(first, "detach"):  # torch
+        if first.is_cuda:
+            from .dflash import concat_features
+            return concat_features(sel)
         import torch
         return torch.cat(sel, dim=-1)
     import numpy as np

@@ -343,8 +343,26 @@ class DFlashDraftModel:
         n = int(self.num_draft_layers)
         _lib.check(self._L.dfl_set_num_layers(self._ctx, n), "dfl_set_num_layers")
 
+    def ingest_features(self, hidden_states, layer_ids=None):
+        """Ingest context rows straight from the target's tapped layer outputs
+        (target.py:258-278), in the selection of extract_context_feature
+        (dflash.py:122-130) for ``layer_ids`` (default: the config's)."""
+        from .config import select_context_features
+        ids = self.config.target_layer_ids if layer_ids is None else layer_ids
+        feats = select_context_features(hidden_states, ids)
+        if len(feats) != self.n_feat:
+            raise ValueError(f"{len(feats)} feature tensors, the fc expects {self.n_feat}")
+        arr, n, ld, C, keep = _feature_ptrs(feats, self.config.hidden_size, self.device)
+        if C:
+            _lib.check(self._L.dfl_ingest_features(self._ctx, arr, n, ld, C, self._stream()),
+                       "dfl_ingest_features")
+        self._keep["ingest_src"] = keep
+        return C
+
     def _ingest(self, target_hidden, fused: bool = False):
         import torch
+        if isinstance(target_hidden, (list, tuple)):
+            return self.ingest_features(target_hidden)
         th = target_hidden
         if th.dim() == 3:
             if th.shape[0] != 1:
@@ -353,7 +371,7 @@ class DFlashDraftModel:
         th = th.to(self.device, torch.float16).contiguous()
         C = th.shape[0]
         if C == 0:
-            return
+            return 0
         if fused:
             if th.shape[1] != self.config.hidden_size:
                 raise ValueError(f"fused context must be [C, {self.config.hidden_size}]")
@@ -366,6 +384,7 @@ class DFlashDraftModel:
             _lib.check(self._L.dfl_ingest_context(self._ctx, th.data_ptr(), C, self._stream()),
                        "dfl_ingest_context")
         self._keep["ingest_src"] = th   # keep alive until the stream passes it
+        return C
 
     def _draft(self, noise=None, ids=None, want_hidden=True, want_prenorm=False,
                want_logits=False, want_ids=False):
@@ -399,7 +418,8 @@ class DFlashDraftModel:
         return out_h, out_p, out_l, out_i
 
     def __call__(self, noise_embedding, target_hidden, mask=None, cache=None, **kwargs):
-        """dflash.py:384-403.  noise_embedding [1, q, H], target_hidden [1, C, nf*H];
+        """dflash.py:384-403.  noise_embedding [1, q, H], target_hidden [1, C, nf*H] (or
+        the list of the nf tapped layer outputs [1, C, H], read without concatenating);
         returns final-normed hidden [1, q, H] (fp16).  With ``cache`` the context rows
         are appended to the cache and the block rows are left in it (offset += C + q)
         until the caller's ``trim(q)``, exactly as update_and_fetch + trim behave."""
@@ -407,7 +427,6 @@ class DFlashDraftModel:
             raise ValueError("DFlash drafting is non-causal; mask must be None (dflash.py:215-233)")
         self._apply_num_layers()
         q = noise_embedding.shape[-2]
-        C = target_hidden.shape[-2]
         if cache is None:
             _lib.check(self._L.dfl_cache_reset(self._ctx), "dfl_cache_reset")
             self._gen += 1
@@ -417,7 +436,7 @@ class DFlashDraftModel:
             return out_h.unsqueeze(0)
         cache = list(cache)[:self.num_draft_layers]
         self._sync_cache(cache)
-        self._ingest(target_hidden)
+        C = self._ingest(target_hidden)
         out_h, _, _, _ = self._draft(noise=noise_embedding)
         for c in cache:       # context + block rows, as update_and_fetch leaves them
             c._appended(C + q)
@@ -440,9 +459,8 @@ class DFlashDraftModel:
             cache = list(cache)[:self.num_draft_layers]
             self._sync_cache(cache)
         if target_hidden is not None:
-            self._ingest(target_hidden, fused=fused_context)
+            C = self._ingest(target_hidden, fused=fused_context)
             if cache is not None:
-                C = target_hidden.shape[-2]
                 for c in cache:
                     c._appended(C)
         out_h, _, out_l, out_i = self._draft(ids=ids, want_hidden=return_hidden,
@@ -693,6 +711,49 @@ class DFlashDraftModel:
     def run_prepared(self):
         self.run_kernels()
         return self.read_output()
+
+
+def _feature_ptrs(feats, H: int, device):
+    """Device pointer array of fp16 [C, H] feature rows with one common row stride.
+    Accepts [1, C, H] or [C, H] tensors; copies only what is not already fp16 on the
+    device with unit column stride and a stride shared by all."""
+    import torch
+    rows = []
+    for f in feats:
+        t = f
+        if t.dim() == 3:
+            if t.shape[0] != 1:
+                raise ValueError("batch size must be 1")
+            t = t[0]
+        if t.dim() != 2 or t.shape[1] != H:
+            raise ValueError(f"feature tensors must be [C, {H}], got {tuple(f.shape)}")
+        if t.device != device or t.dtype != torch.float16:
+            t = t.to(device, torch.float16)
+        rows.append(t)
+    C = rows[0].shape[0]
+    if any(t.shape[0] != C for t in rows):
+        raise ValueError("feature tensors differ in row count")
+    ld = rows[0].stride(0)
+    ok = all(t.stride(1) == 1 and t.stride(0) == ld and t.data_ptr() % 16 == 0 for t in rows)
+    if not ok or ld % 8 or ld < H:
+        rows = [t.contiguous() for t in rows]
+        ld = H
+    arr = (ctypes.c_void_p * len(rows))(*[t.data_ptr() for t in rows])
+    return arr, len(rows), ld, C, rows
+
+
+def concat_features(feats):
+    """extract_context_feature of GPU tensors: [1, C, n*H] (or [C, n*H]) fp16 through
+    dfl_concat_features."""
+    import torch
+    first = feats[0]
+    H = first.shape[-1]
+    arr, n, ld, C, keep = _feature_ptrs(feats, H, first.device)
+    out = torch.empty((C, n * H), dtype=torch.float16, device=first.device)
+    L = _lib.load()
+    _lib.check(L.dfl_concat_features(arr, n, ld, C, H, out.data_ptr(),
+                                     _lib.stream_handle()), "dfl_concat_features")
+    return out.unsqueeze(0) if first.dim() == 3 else out
 
 
 def _wrap_device(ptr: int, shape, device):

@@ -1,0 +1,95 @@
+"""Context-feature capture fused with the ingest (dflash.py:122-130, target.py:258-278):
+the tapped target-layer outputs are read where they lie instead of being concatenated into
+target_hidden first.  Results must equal the concatenated path bit for bit (the same fc
+GEMM over the same fragment-layout rows), and the oracle within the draft tolerance."""
+
+import numpy as np
+import pytest
+
+from oracle import dflash_oracle as O
+from mirror_sd_amd import synth
+from mirror_sd_amd.config import extract_context_feature, workload
+from parity_util import assert_close_fp16, torch_tensors
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def case():
+    from mirror_sd_amd.dflash import DFlashDraftModel
+    wl = workload("tiny")
+    cfg = wl.cfg
+    t = synth.make_weights_numpy(cfg, seed=8)
+    inp = synth.make_inputs_numpy(cfg, wl.block, wl.ctx, seed=8)
+    m = DFlashDraftModel(cfg, max_ctx=wl.ctx + 64)
+    m.load_weights(torch_tensors(t, "cuda"))
+    th = torch.from_numpy(inp["target_hidden"]).cuda()
+    H = cfg.hidden_size
+    feats = [th[:, j * H:(j + 1) * H].contiguous()[None] for j in range(m.n_feat)]
+    return dict(cfg=cfg, t=t, inp=inp, m=m, th=th, feats=feats)
+
+
+def _bits(x):
+    return x.cpu().numpy().view(np.uint16) if x.dtype == torch.float16 else x.cpu().numpy()
+
+
+def test_feature_list_equals_concatenated_target_hidden(case):
+    m, th, feats, inp = case["m"], case["th"], case["feats"], case["inp"]
+    ids = torch.from_numpy(inp["ids"])
+    i0, h0 = m.draft(ids, th, return_hidden=True)
+    i1, h1 = m.draft(ids, feats, return_hidden=True)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(_bits(h1), _bits(h0))
+    np.testing.assert_array_equal(_bits(i1), _bits(i0))
+    W = O.OracleWeights(case["cfg"], case["t"])
+    h_ref, _, ids_ref = O.draft_block(W, inp["ids"], inp["target_hidden"], fp16=True)
+    assert_close_fp16(h1.float().cpu().numpy(), h_ref, what="features")
+    np.testing.assert_array_equal(i1.cpu().numpy(), ids_ref)
+
+
+def test_strided_features_and_all_layer_outputs(case):
+    """Features as column slices of wider buffers (read in place through the row stride),
+    and the every-layer-output list (embedding first) selected at lid + 1."""
+    m, th, feats, inp = case["m"], case["th"], case["feats"], case["inp"]
+    cfg = case["cfg"]
+    H, C = cfg.hidden_size, th.shape[0]
+    wide = [torch.zeros((1, C, 3 * H), dtype=torch.float16, device="cuda") for _ in feats]
+    for w, f in zip(wide, feats):
+        w[:, :, H:2 * H] = f
+    strided = [w[:, :, H:2 * H] for w in wide]
+    assert strided[0].stride(1) == 3 * H
+    ids = torch.from_numpy(inp["ids"])
+    i0, h0 = m.draft(ids, th, return_hidden=True)
+    i1, h1 = m.draft(ids, strided, return_hidden=True)
+    lids = cfg.target_layer_ids
+    everything = [torch.full((1, C, H), 7.0, dtype=torch.float16, device="cuda")
+                  for _ in range(max(lids) + 2)]
+    for j, lid in enumerate(lids):
+        everything[lid + 1] = feats[j]
+    i2, h2 = m.draft(ids, everything, return_hidden=True)   # selection at lid + 1
+    torch.cuda.synchronize()
+    for i, h in ((i1, h1), (i2, h2)):
+        np.testing.assert_array_equal(_bits(h), _bits(h0))
+        np.testing.assert_array_equal(_bits(i), _bits(i0))
+
+
+def test_concat_features_kernel(case):
+    feats, th = case["feats"], case["th"]
+    out = extract_context_feature(feats, case["cfg"].target_layer_ids)
+    torch.cuda.synchronize()
+    assert tuple(out.shape) == (1,) + tuple(th.shape)
+    np.testing.assert_array_equal(_bits(out[0]), _bits(th))
+    ragged = torch.randn(5, 3 * 64, device="cuda").half()
+    parts = [ragged[:, :64], ragged[:, 64:128], ragged[:, 128:]]
+    np.testing.assert_array_equal(_bits(extract_context_feature(parts, [0, 1, 2])), _bits(ragged))
+
+
+def test_feature_arguments_rejected(case):
+    m, feats = case["m"], case["feats"]
+    with pytest.raises(ValueError):
+        m.ingest_features(feats[:-1], layer_ids=list(range(len(feats) - 1)))
+    with pytest.raises(ValueError):
+        m.ingest_features([feats[0]] * (len(feats) - 1) + [feats[0][:, :-1]],
+                          layer_ids=list(range(len(feats))))
