@@ -60,14 +60,14 @@ def traffic_per_launch(workload_name):
         return None
 
 
-def build_model(wl, seed, keep_host: bool):
+def build_model(wl, seed, keep_host: bool, max_ctx: int = 0):
     """Synthetic weights generated on the GPU, quantised by the library's W8A16
     quantiser and loaded.  Optionally keeps host copies for the CPU baseline."""
     import torch
     from mirror_sd_amd.dflash import DFlashDraftModel
     from mirror_sd_amd import synth
     cfg = wl.cfg
-    m = DFlashDraftModel(cfg, max_ctx=wl.ctx, max_block=max(wl.block, 32))
+    m = DFlashDraftModel(cfg, max_ctx=max_ctx or wl.ctx, max_block=max(wl.block, 32))
     host = {}
     names = [n for n, _, _ in synth.weight_specs(cfg)]
     gen = dict(synth.make_weights_torch(cfg, seed=seed, device="cuda",
@@ -170,6 +170,9 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
+    ap.add_argument("--sweep", default="",
+                    help="comma-separated contexts: after the headline, time the block step "
+                         "at each of these context lengths too (context-sweep report)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run a plain device copy of this many MiB 3 times first (a known-size "
                          "kernel for scaling FETCH_SIZE / WRITE_SIZE counter readings)")
@@ -202,7 +205,9 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     t_setup = time.perf_counter()
-    model, host = build_model(wl, args.seed, keep_host=want_cpu)
+    sweep = [int(c) for c in args.sweep.split(",") if c.strip()]
+    model, host = build_model(wl, args.seed, keep_host=want_cpu,
+                              max_ctx=max([wl.ctx] + sweep))
     inp = synth.make_inputs_torch(cfg, wl.block, wl.ctx, seed=args.seed, device="cuda")
     th, ids = inp["target_hidden"], inp["ids"]
     setup_s = time.perf_counter() - t_setup
@@ -307,6 +312,31 @@ def main():
                 ent["bytes_per_launch"] = r["bytes"] / r["launches"]
             kernels[name] = ent
 
+    context_sweep = None
+    if sweep:
+        # the block step against other resident context lengths (same weights)
+        context_sweep = {}
+        for C in sweep:
+            sw = synth.make_inputs_torch(cfg, wl.block, C, seed=args.seed, device="cuda")
+            model.make_cache(0, 0)
+            torch.cuda.synchronize()
+            ev0.record(stream)
+            _lib.check(L.dfl_ingest_context(ctx, sw["target_hidden"].data_ptr(), C, sh),
+                       "dfl_ingest_context")
+            ev1.record(stream)
+            torch.cuda.synchronize()
+            ing = ev0.elapsed_time(ev1)
+            del sw
+            for _ in range(args.warmup):
+                step()
+            ms_c, _, _ = timed(args.steps, False)
+            nb = algorithmic_bytes(cfg, wl.block, C)["total"]
+            context_sweep[str(C)] = {"block_us": round(ms_c * 1e3, 2),
+                                     "hbm_gbps": round(nb / (ms_c * 1e-3) / 1e9, 1),
+                                     "ingest_ms": round(ing, 3)}
+            print(f"context {C}: block {ms_c * 1e3:.1f} us, ingest {ing:.2f} ms",
+                  file=sys.stderr, flush=True)
+
     cpu = None
     if want_cpu:
         try:
@@ -331,6 +361,7 @@ def main():
                    "ms_per_step_with_gemm_events": (round(ms_events, 5) if ms_events else None),
                    "wall_ms_per_step": round(wall_s * 1e3 / args.steps, 4)},
         "kernels": kernels,
+        "context_sweep": context_sweep,
         "draft_ids_head": first_ids[:4],
     }
     print(json.dumps(out), flush=True)

@@ -14,6 +14,8 @@ so a test can tell a change of the input recipe from a change of the results:
                   the top-2 logits per row.
   dflash_27b      5 layers, H5120, 40/8, FFN 17408, block 32, context 4096, V151936;
                   same outputs for 32 rows.
+  dflash_27b_ctxN the 27B-class draft at context N in {64, 2048, 16384, 32768} (the context
+                  sweep; N = 4096 is dflash_27b): same weights (seed 0), inputs of N rows.
   llama8b_batch   5 layers, H4096, 32/8, FFN 14336, V128256, theta 5e5; 8 independent
                   sequences x block 32 with contexts [4146, 4443, 6312, 7812, 779, 1619, 6833,
                   7798]; each sequence run through the single-sequence oracle; outputs stacked
@@ -115,6 +117,8 @@ CASES = {
     "qwen3_4b_layer": lambda: case_layer("qwen3_4b_layer"),
     "qwen3_8b_draft": lambda: case_full("qwen3_8b_draft"),
     "dflash_27b": lambda: case_full("dflash_27b"),
+    **{f"dflash_27b_ctx{c}": (lambda c=c: case_full(f"dflash_27b_ctx{c}"))
+       for c in (64, 2048, 16384, 32768)},
     "llama8b_batch": lambda: case_batch("llama8b_batch"),
 }
 

@@ -78,3 +78,70 @@ def test_full_draft_matches_golden(name):
     bad = (ids != g["ids"]) & ~near_tie
     assert not bad.any(), f"{name}: argmax differs at rows {np.nonzero(bad)[0].tolist()}"
     m.close()
+
+
+# ---------------------------------------------------------------------------
+# Context sweep: the 27B-class draft at contexts 64 .. 32768 (context 4096 is the case
+# above).  One model (seed-0 weights, cache for 32768 rows) drafts against each context.
+# ---------------------------------------------------------------------------
+
+SWEEP = (64, 2048, 16384, 32768)
+
+
+@pytest.fixture(scope="module")
+def sweep_model():
+    from mirror_sd_amd.dflash import DFlashDraftModel
+    wl = workload("dflash_27b_ctx32768")
+    print("context sweep: generating weights", flush=True)
+    t = synth.make_weights_numpy(wl.cfg, seed=0)
+    m = DFlashDraftModel(wl.cfg, max_ctx=max(SWEEP))
+    m.load_weights(torch_tensors(t, "cuda"))
+    digests = input_digests(t, {})
+    del t
+    torch.cuda.empty_cache()
+    yield m, digests
+    m.close()
+
+
+def _check_against(g, name, ids, logits, h):
+    assert_close_fp16(h.float().cpu().numpy(), g["hidden"], what=f"{name} final hidden")
+    lg = logits.cpu().numpy()
+    ids = ids.cpu().numpy()
+    np.testing.assert_array_equal(ids, np.argmax(lg, axis=-1))
+    got_top = np.take_along_axis(lg, g["top2_idx"].astype(np.int64), axis=-1)
+    assert np.abs(got_top - g["top2_val"]).max() < LOGIT_TOL
+    gap = g["top2_val"][:, 0] - g["top2_val"][:, 1]
+    near_tie = (gap < LOGIT_TOL) & (ids == g["top2_idx"][:, 1])
+    bad = (ids != g["ids"]) & ~near_tie
+    assert not bad.any(), f"{name}: argmax differs at rows {np.nonzero(bad)[0].tolist()}"
+
+
+@pytest.mark.parametrize("ctx", SWEEP)
+def test_context_sweep_matches_golden(sweep_model, ctx):
+    m, wdig = sweep_model
+    name = f"dflash_27b_ctx{ctx}"
+    g = load(name)
+    wl = workload(name)
+    print(f"case {name}: generating inputs", flush=True)
+    inp = synth.make_inputs_numpy(wl.cfg, wl.block, wl.ctx, seed=0)
+    want = dict(zip(g["digest_names"].tolist(), g["digest_values"].tolist()))
+    got = dict(wdig)
+    got.update(input_digests({}, inp))
+    assert got == want
+    print(f"case {name}: drafting", flush=True)
+    th = torch.from_numpy(inp["target_hidden"]).cuda()
+    ids, logits, h = m.draft(torch.from_numpy(inp["ids"]), th, return_logits=True,
+                             return_hidden=True)
+    torch.cuda.synchronize()
+    _check_against(g, name, ids, logits, h)
+    if ctx == max(SWEEP):
+        # the same context ingested in three uneven calls (a 31-row one among them)
+        from mirror_sd_amd import _lib
+        _lib.check(m._L.dfl_cache_reset(m._ctx), "dfl_cache_reset")
+        m._gen += 1
+        for a, b in ((0, 5000), (5000, 5031), (5031, ctx)):
+            m._ingest(th[a:b])
+        h2, _, lg2, ids2 = m._draft(ids=torch.from_numpy(inp["ids"]), want_logits=True,
+                                    want_ids=True)
+        torch.cuda.synchronize()
+        _check_against(g, name + " (chunked ingest)", ids2, lg2, h2)
