@@ -218,9 +218,15 @@ def main():
     sh = stream.cuda_stream
     out_ids = torch.empty((wl.block,), dtype=torch.int32, device="cuda")
 
-    # context ingest (fc fusion + per-layer K/V), timed as its own phase
-    model.make_cache(0, 0)
+    # context ingest (fc fusion + per-layer K/V), timed as its own phase after one untimed
+    # ingest (the first GEMM calls load the BLAS library's kernels)
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_first = time.perf_counter()
+    model.make_cache(0, 0)
+    _lib.check(L.dfl_ingest_context(ctx, th.data_ptr(), wl.ctx, sh), "dfl_ingest_context")
+    torch.cuda.synchronize()
+    first_ingest_s = time.perf_counter() - t_first
+    model.make_cache(0, 0)
     torch.cuda.synchronize()
     ev0.record(stream)
     _lib.check(L.dfl_ingest_context(ctx, th.data_ptr(), wl.ctx, sh), "dfl_ingest_context")
@@ -357,7 +363,8 @@ def main():
         "algorithmic_bytes_per_block": nbytes["total"],
         "roofline": roofline,
         "cpu_baseline": cpu,
-        "phases": {"context_ingest_ms": round(ingest_ms, 3), "setup_s": round(setup_s, 1),
+        "phases": {"context_ingest_ms": round(ingest_ms, 3),
+                   "first_ingest_s": round(first_ingest_s, 3), "setup_s": round(setup_s, 1),
                    "ms_per_step_with_gemm_events": (round(ms_events, 5) if ms_events else None),
                    "wall_ms_per_step": round(wall_s * 1e3 / args.steps, 4)},
         "kernels": kernels,

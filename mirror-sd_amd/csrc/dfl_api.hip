@@ -7,6 +7,8 @@
 #include <string>
 #include <vector>
 
+#include <rocblas/rocblas.h>
+
 #include "dflash_hip.h"
 #include "dfl_kernels.h"
 
@@ -27,7 +29,7 @@ int fail(int code, const std::string& msg) {
     if (e_ != hipSuccess) return fail(DFL_EHIP, std::string(#x) + ": " + hipGetErrorString(e_)); \
   } while (0)
 
-constexpr int ING_ROWS = 256;      // context rows per ingest pass (8 m-tiles)
+constexpr int ING_MAX = 4096;      // context rows per ingest pass (at most)
 constexpr int MAX_CHUNKS = 64;     // attention key splits
 constexpr int MT_MAX = 8;          // 32-row m-tiles per M-split GEMM launch
 
@@ -87,6 +89,7 @@ struct Layer {
   half_t *s_qkv = nullptr, *s_o = nullptr, *s_gu = nullptr, *s_down = nullptr;
   half_t *in_norm = nullptr, *post_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
   half_t *Kc = nullptr, *Vt = nullptr;   // [max_seqs][NKV][cap][128], [max_seqs][NKV][128][cap]
+  half_t* w_kv16 = nullptr;              // [2*NKV*128][H] fp16 copy of the k|v int8 rows
   bool loaded = false;
 };
 
@@ -104,7 +107,7 @@ struct dfl_ctx {
   half_t* kc(const Layer& L, int seq) const { return L.Kc + (size_t)seq * kv_seq; }
   half_t* vt(const Layer& L, int seq) const { return L.Vt + (size_t)seq * kv_seq; }
   std::vector<Layer> layers;
-  uint4* w_fc = nullptr;
+  half_t* w_fc = nullptr;    // [H][n_target_feat * H] fc weight, row-major fp16
   half_t* hidden_norm = nullptr;
   bool fc_loaded = false;
   half_t* final_norm = nullptr;
@@ -112,8 +115,7 @@ struct dfl_ctx {
   const half_t* embed = nullptr;
   bool head_loaded = false;
   int active = 0;   // layers run per call (num_draft_layers)
-  half_t *x = nullptr, *h = nullptr, *Q = nullptr, *attn = nullptr, *act = nullptr,
-         *ctxbuf = nullptr;   // ctxbuf: fragment-layout tiles of the pass's fused context rows
+  half_t *x = nullptr, *h = nullptr, *Q = nullptr, *attn = nullptr, *act = nullptr;
   float *Op = nullptr, *Ml = nullptr;
   unsigned long long* keys = nullptr;
   unsigned long long* sa_cand = nullptr;   // soft-anchor top-k candidates per scan workgroup
@@ -126,16 +128,18 @@ struct dfl_ctx {
   int* sk_tile_cnt = nullptr;    // [max tiles]
   float* sk_ss = nullptr;        // [m-tiles][H/64][32] row sums of squares of x (RESID output)
   SKPlan sk_qkv, sk_o, sk_gu, sk_down, sk_lm;
-  // context ingest (ING_ROWS rows per pass)
-  half_t* ing_x = nullptr;    // fragment-layout tiles of the pass's target_hidden rows
-  half_t* fc_out = nullptr;   // [ING_ROWS][H] fc output (fp16, row-major)
-  half_t* kvbuf = nullptr;    // [ING_ROWS][2*NKV*128] K|V projections (fp16, row-major)
-  SKPlan sk_ifc, sk_ikv;
+  // context ingest: `ing` rows per pass; the (compute-bound) GEMMs run on rocBLAS
+  int ing = 0;
+  rocblas_handle blas = nullptr;
+  float* fc32 = nullptr;      // [ing][H] fc GEMM rows (fp32)
+  half_t* xn = nullptr;       // [ing][H] hidden_norm(fc) rows (fp16, row-major)
+  float* kv32 = nullptr;      // [ing][2*NKV*128] K|V GEMM rows (fp32)
   std::vector<void*> allocs;
   int prof = 0;   // 0 off, 1 every kernel group, 2 stream-K GEMM launches only
   std::vector<ProfRec> recs;
 
   ~dfl_ctx() {
+    if (blas) (void)rocblas_destroy_handle(blas);
     for (auto& r : recs) {
       (void)hipEventDestroy(r.a);
       (void)hipEventDestroy(r.b);
@@ -204,6 +208,47 @@ static int check_launch(const char* what) {
   return DFL_OK;
 }
 
+// Y (row-major [n][m], fp32, row stride ldy) = beta * Y + B A^T for row-major fp16 A [m][k]
+// (row stride lda) and B [n][k] (row stride ldb): in rocBLAS's column-major terms
+// Y^T = A^T(op transpose) * B^T, fp32 accumulation.
+static int blas_gemm(dfl_ctx* ctx, int m, int n, int k, const half_t* A, int lda, const half_t* B,
+                     int ldb, float beta, float* Y, int ldy, hipStream_t st) {
+  rocblas_status s = rocblas_set_stream(ctx->blas, st);
+  if (s == rocblas_status_success) {
+    const float one = 1.0f;
+    s = rocblas_gemm_ex(ctx->blas, rocblas_operation_transpose, rocblas_operation_none, m, n, k,
+                        &one, A, rocblas_datatype_f16_r, lda, B, rocblas_datatype_f16_r, ldb,
+                        &beta, Y, rocblas_datatype_f32_r, ldy, Y, rocblas_datatype_f32_r, ldy,
+                        rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+  }
+  if (s == rocblas_status_success) return DFL_OK;
+  return fail(DFL_EHIP, std::string("rocblas_gemm_ex (") + std::to_string(m) + "x" +
+                            std::to_string(n) + "x" + std::to_string(k) +
+                            "): " + rocblas_status_to_string(s));
+}
+
+// Ingest buffers and the rocBLAS handle.  The handle works in a fixed workspace owned by
+// the context (a GEMM that wanted more fails with an error instead of allocating), so no
+// later call allocates device memory.
+constexpr size_t BLAS_WS_BYTES = 128ull << 20;
+
+static int setup_ingest(dfl_ctx* x) {
+  const int H = x->H, Nkv = 2 * x->NKV * 128;
+  x->ing = std::max(32, std::min(ING_MAX, ((x->cfg.max_ctx + 31) / 32) * 32));
+  int r = DFL_OK;
+  if ((r = x->alloc(&x->kv32, (size_t)x->ing * Nkv))) return r;
+  if (x->NF > 0 && ((r = x->alloc(&x->fc32, (size_t)x->ing * H)) ||
+                    (r = x->alloc(&x->xn, (size_t)x->ing * H))))
+    return r;
+  if (rocblas_create_handle(&x->blas) != rocblas_status_success)
+    return fail(DFL_EHIP, "dfl_create: rocblas_create_handle failed");
+  unsigned char* ws = nullptr;
+  if ((r = x->alloc(&ws, BLAS_WS_BYTES))) return r;
+  if (rocblas_set_workspace(x->blas, ws, BLAS_WS_BYTES) != rocblas_status_success)
+    return fail(DFL_EHIP, "dfl_create: rocblas_set_workspace failed");
+  return DFL_OK;
+}
+
 extern "C" {
 
 const char* dfl_last_error(void) { return g_err.c_str(); }
@@ -256,14 +301,10 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
   if ((r = x->alloc(&x->x, Bt * x->H, true)) || (r = x->alloc(&x->h, Bm * x->H)) ||
       (r = x->alloc(&x->Q, (size_t)x->NH * Bm * 128)) ||
       (r = x->alloc(&x->attn, Bt * x->NH * 128, true)) || (r = x->alloc(&x->act, Bt * x->F, true)) ||
-      (r = x->alloc(&x->ctxbuf, (size_t)ING_ROWS * x->H)) ||
-      (r = x->alloc(&x->ing_x, (size_t)ING_ROWS * std::max(1, x->NF) * x->H)) ||
-      (r = x->alloc(&x->kvbuf, (size_t)ING_ROWS * 2 * x->NKV * 128)) ||
       (r = x->alloc(&x->Op, (size_t)MAX_CHUNKS * x->NH * Bm * 128)) ||
       (r = x->alloc(&x->Ml, (size_t)MAX_CHUNKS * x->NH * Bm * 2)) ||
       (r = x->alloc(&x->keys, Bm, true)) || (r = x->alloc(&x->err, 1, true)) ||
-      (r = x->alloc(&x->sa_cand, (size_t)SA_BLOCKS * SA_TOPK_MAX)) ||
-      (r = x->alloc(&x->fc_out, (size_t)ING_ROWS * x->H))) {
+      (r = x->alloc(&x->sa_cand, (size_t)SA_BLOCKS * SA_TOPK_MAX))) {
     delete x;
     return r;
   }
@@ -289,11 +330,6 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
     const size_t bm32 = ((Bm + 31) / 32) * 32;
     // split-tile partials hold one 32x64 slot per m-tile of a launch
     wsn *= (size_t)std::min<size_t>(MT_MAX, bm32 / 32);
-    // ingest GEMMs: fc (fp16, K = n_target_feat * H) and the K|V rows of w_qkv, 8 m-tiles
-    x->sk_ifc = plan(x->H, std::max(1, x->NF) * x->H / 16);
-    x->sk_ikv = plan(2 * x->NKV * 128, x->H / 32);
-    wsn = std::max(wsn, (size_t)(x->H / 64) * x->sk_ifc.seg_cap * 2048 * MT_MAX);
-    wsn = std::max(wsn, (size_t)(2 * x->NKV * 128 / 64) * x->sk_ikv.seg_cap * 2048 * MT_MAX);
     if ((r = x->alloc(&x->qkvbuf, Bm * x->NQKV)) || (r = x->alloc(&x->rnorm, bm32)) ||
         (r = x->alloc(&x->sk_ws, wsn)) || (r = x->alloc(&x->sk_tile_cnt, tiles, true)) ||
         (r = x->alloc(&x->sk_ss, (bm32 / 32) * (size_t)(x->H / 64) * 32))) {
@@ -307,6 +343,10 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
       delete x;
       return r;
     }
+  }
+  if ((r = setup_ingest(x))) {
+    delete x;
+    return r;
   }
   *out = x;
   return DFL_OK;
@@ -355,6 +395,7 @@ int dfl_load_layer_w8(dfl_ctx* ctx, int layer, const int8_t* const q[7],
     DFL_TRY(ctx->alloc(&L.post_norm, (size_t)H));
     DFL_TRY(ctx->alloc(&L.q_norm, (size_t)128));
     DFL_TRY(ctx->alloc(&L.k_norm, (size_t)128));
+    DFL_TRY(ctx->alloc(&L.w_kv16, (size_t)2 * NKV * 128 * H));
   }
   auto S = [&](int i) { return reinterpret_cast<const half_t*>(scale[i]); };
   // fused QKV: row-blocks [0, NH*4) = q_proj, then k_proj, then v_proj
@@ -366,6 +407,9 @@ int dfl_load_layer_w8(dfl_ctx* ctx, int layer, const int8_t* const q[7],
   launch_pack_i8(q[4], S(4), F, H, L.w_gu, L.s_gu, 0, 2, st);
   launch_pack_i8(q[5], S(5), F, H, L.w_gu, L.s_gu, 1, 2, st);
   launch_pack_i8(q[6], S(6), H, F, L.w_down, L.s_down, 0, 1, st);
+  // exact fp16 copies of the k and v rows for the context-ingest GEMM
+  launch_i8_to_f16(q[1], (size_t)NKV * 128 * H, L.w_kv16, st);
+  launch_i8_to_f16(q[2], (size_t)NKV * 128 * H, L.w_kv16 + (size_t)NKV * 128 * H, st);
   DFL_HIP(hipMemcpyAsync(L.in_norm, in_norm, H * 2, hipMemcpyDeviceToDevice, st));
   DFL_HIP(hipMemcpyAsync(L.post_norm, post_norm, H * 2, hipMemcpyDeviceToDevice, st));
   DFL_HIP(hipMemcpyAsync(L.q_norm, q_norm, 256, hipMemcpyDeviceToDevice, st));
@@ -382,12 +426,11 @@ int dfl_load_fc(dfl_ctx* ctx, const uint16_t* fc_weight, const uint16_t* hidden_
   hipStream_t st = (hipStream_t)stream;
   const int K = ctx->NF * ctx->H;
   if (!ctx->w_fc) {
-    DFL_TRY(ctx->alloc(&ctx->w_fc, (size_t)ctx->H * K / 8));
+    DFL_TRY(ctx->alloc(&ctx->w_fc, (size_t)ctx->H * K));
     DFL_TRY(ctx->alloc(&ctx->hidden_norm, (size_t)ctx->H));
   }
-  launch_pack_f16(reinterpret_cast<const half_t*>(fc_weight), ctx->H, K, ctx->w_fc, st);
+  DFL_HIP(hipMemcpyAsync(ctx->w_fc, fc_weight, (size_t)ctx->H * K * 2, hipMemcpyDeviceToDevice, st));
   DFL_HIP(hipMemcpyAsync(ctx->hidden_norm, hidden_norm, ctx->H * 2, hipMemcpyDeviceToDevice, st));
-  DFL_TRY(check_launch("pack fc"));
   ctx->fc_loaded = true;
   return DFL_OK;
 }
@@ -468,59 +511,25 @@ static int layers_ready(dfl_ctx* ctx, const char* who) {
   return DFL_OK;
 }
 
-// fp16 GEMM output rows (STORE epilogue) of `rows` fragment-layout activation rows, over
-// one M-split launch per 8 m-tiles (single-tile kernel for one m-tile).
-static int ingest_gemm(dfl_ctx* ctx, int cat, int wt, const SKPlan& p, const uint4* W,
-                        const half_t* scale, int N, int KB, const half_t* X, int K, int rows,
-                        half_t* out, hipStream_t st) {
-  const long long wbytes = (wt == WT_INT8) ? (long long)N * KB * 32 + 2LL * N
-                                           : (long long)N * KB * 16 * 2;
-  const int n_mt = (rows + 31) / 32;
-  for (int g0 = 0; g0 < n_mt; g0 += MT_MAX) {
-    const int mt_n = std::min(MT_MAX, n_mt - g0);
-    const int m0 = g0 * 32;
-    ProfScope ps(ctx, cat, wbytes, st, /*attached=*/true);
-    StreamArgs a{};
-    a.W = W;
-    a.scale = scale;
-    a.N = N;
-    a.KB = KB;
-    a.X = X + (size_t)m0 * K;
-    a.ldx = K;
-    a.M = std::min(32 * mt_n, rows - m0);
-    a.MT = mt_n;
-    a.ws = ctx->sk_ws;
-    a.seg_cap = p.seg_cap;
-    a.tile_cnt = ctx->sk_tile_cnt;
-    a.out = out + (size_t)m0 * N;
-    a.ldo = N;
-    a.eps = ctx->cfg.rms_eps;
-    const bool ok = mt_n == 1
-                        ? launch_streamk_gemm(wt, EPI_STORE, false, a, p, st, ps.start(), ps.stop())
-                        : launch_streamk_gemm_m(wt, EPI_STORE, false, a, p, st, ps.start(),
-                                                ps.stop());
-    if (!ok) return fail(DFL_EINVAL, "no GEMM kernel for this weight type / epilogue");
-  }
-  return DFL_OK;
-}
-
-// Per-layer K/V of `rows` fused context rows (fragment-layout tiles in ctx->ctxbuf):
-// k_norm + RoPE on K, appended at cache row len + r0 with absolute position offset + r0.
-static int ingest_kv_rows(dfl_ctx* ctx, int rows, int r0, hipStream_t st) {
+// Per-layer K/V of `rows` fused context rows (row-major fp16, row stride ld): the K|V
+// projection on rocBLAS (fp32 rows), then per-row scale + fp16 rounding, k_norm + RoPE on K,
+// appended at cache row len + r0 with absolute position offset + r0.
+static int ingest_kv_rows(dfl_ctx* ctx, const half_t* rows_src, int ld, int rows, int r0,
+                          hipStream_t st) {
   const int H = ctx->H, NH = ctx->NH, NKV = ctx->NKV;
-  const int KB = H / 32;
   const int Nkv = 2 * NKV * 128;
   for (int l = 0; l < ctx->active; ++l) {
     Layer& L = ctx->layers[l];
-    const uint4* Wkv = L.w_qkv + (size_t)(NH * 4) * KB * 64;   // rows NH*128 .. of [q;k;v]
-    DFL_TRY(ingest_gemm(ctx, P_INGEST_KV, WT_INT8, ctx->sk_ikv, Wkv, L.s_qkv + NH * 128, Nkv,
-                        KB, ctx->ctxbuf, H, rows, ctx->kvbuf, st));
+    {
+      ProfScope ps(ctx, P_INGEST_KV, 0, st);
+      DFL_TRY(blas_gemm(ctx, Nkv, rows, H, L.w_kv16, H, rows_src, ld, 0.f, ctx->kv32, Nkv, st));
+    }
     QKRopeArgs q{};
-    q.qkv16 = ctx->kvbuf;
+    q.qkv32 = ctx->kv32;
+    q.oscale = L.s_qkv + NH * 128;   // scales of the k|v rows, in row order
     q.M = rows;
     q.N = Nkv;
     q.col_slot0 = NH;
-    q.scale = nullptr;
     q.slot0 = NH;
     q.n_slots = 2 * NKV;
     q.NH = NH;
@@ -560,30 +569,28 @@ static int ingest(dfl_ctx* ctx, const uint16_t* src, int C, bool fused, void* st
   const int K = ctx->NF * H;
   const half_t* in = reinterpret_cast<const half_t*>(src);
   ctx->sq().last_block = 0;
-  for (int r0 = 0; r0 < C; r0 += ING_ROWS) {
-    const int rows = std::min(ING_ROWS, C - r0);
+  for (int r0 = 0; r0 < C; r0 += ctx->ing) {
+    const int rows = std::min(ctx->ing, C - r0);
     if (fused) {
-      ProfScope ps(ctx, P_INGEST_FC, 0, st);
-      launch_rows_to_afl(in + (size_t)r0 * H, rows, H, H, ctx->ctxbuf, st);
+      DFL_TRY(ingest_kv_rows(ctx, in + (size_t)r0 * H, H, rows, r0, st));
     } else {
-      // hidden_norm(fc(target_hidden)): fc output rounded to fp16 (Linear), then RMSNorm
+      // hidden_norm(fc(target_hidden)): fc output rounded to fp16 (Linear), then RMSNorm.
+      // Tapped-layer features: fc(concat(f_j)) = sum_j f_j W_fc[:, jH:(j+1)H]^T.
       {
         ProfScope ps(ctx, P_INGEST_FC, 0, st);
         if (feats) {
-          FeatPtrs f = *feats;
-          for (int j = 0; j < f.n; ++j) f.p[j] += (size_t)r0 * f.ld;
-          launch_feats_to_afl(f, rows, H, ctx->ing_x, st);
+          for (int j = 0; j < feats->n; ++j)
+            DFL_TRY(blas_gemm(ctx, H, rows, H, ctx->w_fc + (size_t)j * H, K,
+                              feats->p[j] + (size_t)r0 * feats->ld, (int)feats->ld,
+                              j ? 1.f : 0.f, ctx->fc32, H, st));
         } else {
-          launch_rows_to_afl(in + (size_t)r0 * K, rows, K, K, ctx->ing_x, st);
+          DFL_TRY(blas_gemm(ctx, H, rows, K, ctx->w_fc, K, in + (size_t)r0 * K, K, 0.f,
+                            ctx->fc32, H, st));
         }
+        launch_fc_norm_rows(ctx->fc32, rows, H, ctx->hidden_norm, ctx->cfg.rms_eps, ctx->xn, st);
       }
-      DFL_TRY(ingest_gemm(ctx, P_INGEST_FC, WT_F16, ctx->sk_ifc, ctx->w_fc, nullptr, H, K / 16,
-                          ctx->ing_x, K, rows, ctx->fc_out, st));
-      ProfScope ps(ctx, P_INGEST_FC, 0, st);
-      launch_rms_norm_afl(ctx->fc_out, rows, H, ctx->hidden_norm, ctx->cfg.rms_eps, ctx->ctxbuf,
-                          st);
+      DFL_TRY(ingest_kv_rows(ctx, ctx->xn, H, rows, r0, st));
     }
-    DFL_TRY(ingest_kv_rows(ctx, rows, r0, st));
     ctx->sq().append(rows);
   }
   DFL_TRY(check_launch("ingest"));
@@ -700,7 +707,6 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
       q.M = B;
       q.N = ctx->NQKV;
       q.col_slot0 = 0;
-      q.scale = nullptr;
       q.slot0 = 0;
       q.n_slots = NH + 2 * NKV;
       q.NH = NH;

@@ -85,8 +85,10 @@ struct FeatPtrs {
   int n;
   long long ld;
 };
-void launch_feats_to_afl(const FeatPtrs& f, int rows, int H, half_t* dst, hipStream_t st);
 void launch_concat_feats(const FeatPtrs& f, int rows, int H, half_t* out, hipStream_t st);
+void launch_fc_norm_rows(const float* fc32, int rows, int H, const half_t* g, float eps,
+                         half_t* xn, hipStream_t st);
+void launch_i8_to_f16(const int8_t* q, size_t n, half_t* out, hipStream_t st);
 void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* noise, int B,
                        int H, int V, const half_t* g, float eps, half_t* x, half_t* h,
                        float* rnorm, int* err, hipStream_t st);
@@ -96,23 +98,16 @@ void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* no
 void launch_apply_norm(const half_t* x, const float* ss, int ss_tiles, float eps, const half_t* g,
                        int M, int N, half_t* h, hipStream_t st);
 void launch_afl_to_rows(const half_t* x, int M, int N, half_t* h, hipStream_t st);
-// Row-major rows [rows][ld] (first K columns, K % 8 == 0) -> fragment-layout tiles
-// [ceil(rows/32)][32][K], zero-padded to whole tiles.
-void launch_rows_to_afl(const half_t* src, int rows, int K, int ld, half_t* dst, hipStream_t st);
-// h = RMSNorm(x) * g of row-major fp16 rows [rows][H], written as fragment-layout tiles
-// (zero-padded to whole tiles).
-void launch_rms_norm_afl(const half_t* src, int rows, int H, const half_t* g, float eps,
-                         half_t* dst, hipStream_t st);
-// Per-head RMSNorm + neox RoPE + scatter of fp16 projections qkv16 [M][N] (scaled and
-// rounded by the GEMM epilogue).  Rows m use position pos0 + m.  Head slots [0, NH) -> Q[h][m][d]
+// Per-head RMSNorm + neox RoPE + scatter of projections [M][N]: fp16 qkv16 (scaled and
+// rounded by the GEMM epilogue) or fp32 qkv32 (scaled and rounded here).  Rows m use position pos0 + m.  Head slots [0, NH) -> Q[h][m][d]
 // (q_rows rows per head); slots [NH, NH+NKV) -> K cache rows (cache_row0 + m);
 // [NH+NKV, NH+2NKV) -> Vt cache columns.  Column 0 of qkv16 is head slot col_slot0 (so the
 // ingest path can project only K and V).
 struct QKRopeArgs {
-  const half_t* qkv16;
+  const half_t* qkv16;                       // projection rows [M][N], fp16 (scaled), or
+  const float* qkv32; const half_t* oscale;  // fp32 GEMM rows [M][N] + fp16 scale per column
   int M; int N;
-  int col_slot0;                             // head slot of qkv16 column 0
-  const half_t* scale;                       // unused (kept zero)
+  int col_slot0;                             // head slot of column 0
   int slot0, n_slots;                        // head slots handled (q,k,v numbering)
   int NH, NKV;
   const half_t* q_norm; const half_t* k_norm; float eps;

@@ -98,47 +98,6 @@ void launch_apply_norm(const half_t* x, const float* ss, int ss_tiles, float eps
                      ss_tiles, eps, g, N, h);
 }
 
-// Row-major fp16 rows [rows][ld] (first K columns) -> activation fragment layout tiles
-// [ceil(rows/32)][32][K]; rows past `rows` in the last tile are zero.  One thread per
-// 8 consecutive columns (one 16-byte run in both layouts).
-__global__ __launch_bounds__(256) void rows_to_afl_kernel(const half_t* __restrict__ src,
-                                                          int rows, int K, int ld,
-                                                          half_t* __restrict__ dst) {
-  const int r = blockIdx.y;
-  const int k = (blockIdx.x * 256 + threadIdx.x) * 8;
-  if (k >= K) return;
-  u32x4 v = {0u, 0u, 0u, 0u};
-  if (r < rows) v = *reinterpret_cast<const u32x4*>(src + (size_t)r * ld + k);
-  *reinterpret_cast<u32x4*>(dst + afl_index(r, k, K)) = v;
-}
-
-void launch_rows_to_afl(const half_t* src, int rows, int K, int ld, half_t* dst, hipStream_t st) {
-  const int tiles_rows = ((rows + 31) / 32) * 32;
-  hipLaunchKernelGGL(rows_to_afl_kernel, dim3((K / 8 + 255) / 256, tiles_rows), dim3(256), 0, st,
-                     src, rows, K, ld, dst);
-}
-
-// Same for the concatenation of nf feature tensors along the hidden axis
-// (extract_context_feature, dflash.py:122-130): column k of the fused row comes from
-// feature k / H at column k % H; H % 8 == 0, so one 8-column chunk never straddles two.
-__global__ __launch_bounds__(256) void feats_to_afl_kernel(FeatPtrs f, int rows, int H,
-                                                           half_t* __restrict__ dst) {
-  const int r = blockIdx.y;
-  const int K = f.n * H;
-  const int k = (blockIdx.x * 256 + threadIdx.x) * 8;
-  if (k >= K) return;
-  const int j = k / H;
-  u32x4 v = {0u, 0u, 0u, 0u};
-  if (r < rows) v = *reinterpret_cast<const u32x4*>(f.p[j] + (size_t)r * f.ld + (k - j * H));
-  *reinterpret_cast<u32x4*>(dst + afl_index(r, k, K)) = v;
-}
-
-void launch_feats_to_afl(const FeatPtrs& f, int rows, int H, half_t* dst, hipStream_t st) {
-  const int tiles_rows = ((rows + 31) / 32) * 32;
-  hipLaunchKernelGGL(feats_to_afl_kernel, dim3((f.n * H / 8 + 255) / 256, tiles_rows), dim3(256),
-                     0, st, f, rows, H, dst);
-}
-
 // Row-major concatenation [rows][nf * H] of the feature tensors (the materialised
 // extract_context_feature).
 __global__ __launch_bounds__(256) void concat_feats_kernel(FeatPtrs f, int H,
@@ -157,43 +116,40 @@ void launch_concat_feats(const FeatPtrs& f, int rows, int H, half_t* out, hipStr
                      f, H, out);
 }
 
-// RMSNorm of row-major fp16 rows [rows][H] (h = fp16(fp16(x * r) * g), r = 1/rms in fp32)
-// written in the activation fragment layout; padded rows of the last tile are zero.
-__global__ __launch_bounds__(ROW_THREADS) void rms_norm_afl_kernel(const half_t* __restrict__ src,
-                                                                   int rows, int H,
-                                                                   const half_t* __restrict__ g,
+// hidden_norm(fc(.)) for the ingest: fc32 [rows][H] fp32 GEMM rows, rounded to fp16 (the
+// Linear output), then RMSNorm (fp16(fp16(x * r) * g)) into row-major fp16 xn [rows][H].
+__global__ __launch_bounds__(ROW_THREADS) void fc_norm_rows_kernel(const float* __restrict__ fc32,
+                                                                   int H, const half_t* __restrict__ g,
                                                                    float eps,
-                                                                   half_t* __restrict__ dst) {
+                                                                   half_t* __restrict__ xn) {
   __shared__ float red[16];
   const int r = blockIdx.x;
-  if (r >= rows) {   // zero padding rows
-    for (int k = threadIdx.x * 8; k < H; k += ROW_THREADS * 8)
-      *reinterpret_cast<u32x4*>(dst + afl_index(r, k, H)) = (u32x4){0u, 0u, 0u, 0u};
-    return;
-  }
-  const half_t* xr = src + (size_t)r * H;
+  const float* src = fc32 + (size_t)r * H;
+  float v[ROW_MAXV];
   float ss = 0.f;
-  for (int k = threadIdx.x * 8; k < H; k += ROW_THREADS * 8) {
-    const half8_t v = as_half8(*reinterpret_cast<const u32x4*>(xr + k));
 #pragma unroll
-    for (int j = 0; j < 8; ++j) ss += h2f(v[j]) * h2f(v[j]);
+  for (int i = 0; i < ROW_MAXV; ++i) {
+    const int k = threadIdx.x + i * ROW_THREADS;
+    v[i] = 0.f;
+    if (k < H) {
+      v[i] = h2f(f2h(src[k]));
+      ss += v[i] * v[i];
+    }
   }
   ss = block_sum(ss, red);
   const float rr = 1.0f / sqrtf(ss / (float)H + eps);
-  for (int k = threadIdx.x * 8; k < H; k += ROW_THREADS * 8) {
-    const half8_t v = as_half8(*reinterpret_cast<const u32x4*>(xr + k));
-    half8_t o;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = rms_out(h2f(v[j]), rr, g[k + j]);
-    *reinterpret_cast<u32x4*>(dst + afl_index(r, k, H)) = __builtin_bit_cast(u32x4, o);
+  for (int i = 0; i < ROW_MAXV; ++i) {
+    const int k = threadIdx.x + i * ROW_THREADS;
+    if (k < H) xn[(size_t)r * H + k] = rms_out(v[i], rr, g[k]);
   }
 }
 
-void launch_rms_norm_afl(const half_t* src, int rows, int H, const half_t* g, float eps,
-                         half_t* dst, hipStream_t st) {
-  const int tiles_rows = ((rows + 31) / 32) * 32;
-  hipLaunchKernelGGL(rms_norm_afl_kernel, dim3(tiles_rows), dim3(ROW_THREADS), 0, st, src, rows, H,
-                     g, eps, dst);
+void launch_fc_norm_rows(const float* fc32, int rows, int H, const half_t* g, float eps,
+                         half_t* xn, hipStream_t st) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(fc_norm_rows_kernel, dim3(rows), dim3(ROW_THREADS), 0, st, fc32, H, g, eps,
+                     xn);
 }
 
 void launch_afl_to_rows(const half_t* x, int M, int N, half_t* h, hipStream_t st) {
@@ -214,9 +170,16 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(QKRopeArgs a) {
   const int c0 = (slot - a.col_slot0) * 128 + lane;
   const int crow = slot >= a.NH ? cache_slot(a, m) : 0;
   if (crow < 0) return;   // whole wave: one (row, head slot) per wave
-  // projections already scaled and rounded to fp16 (Linear output) by the GEMM epilogue
-  const float v0 = h2f(a.qkv16[(size_t)m * a.N + c0]);
-  const float v1 = h2f(a.qkv16[(size_t)m * a.N + c0 + 64]);
+  // projections scaled and rounded to fp16 (Linear output): by the GEMM epilogue (qkv16),
+  // or here from the fp32 GEMM rows and the per-row scales (qkv32, oscale)
+  float v0, v1;
+  if (a.qkv32) {
+    v0 = h2f(f2h(a.qkv32[(size_t)m * a.N + c0] * h2f(a.oscale[c0])));
+    v1 = h2f(f2h(a.qkv32[(size_t)m * a.N + c0 + 64] * h2f(a.oscale[c0 + 64])));
+  } else {
+    v0 = h2f(a.qkv16[(size_t)m * a.N + c0]);
+    v1 = h2f(a.qkv16[(size_t)m * a.N + c0 + 64]);
+  }
   const int kv_slot0 = a.NH + a.NKV;
   if (slot >= kv_slot0) {   // V head: no norm, no rotation
     const int gk = slot - kv_slot0;

@@ -1,7 +1,9 @@
 """Context-feature capture fused with the ingest (dflash.py:122-130, target.py:258-278):
 the tapped target-layer outputs are read where they lie instead of being concatenated into
-target_hidden first.  Results must equal the concatenated path bit for bit (the same fc
-GEMM over the same fragment-layout rows), and the oracle within the draft tolerance."""
+target_hidden first.  The fc then runs as one GEMM per feature block accumulated in fp32
+rather than one GEMM over the concatenation, so the two paths agree to fp32 summation
+order: hidden states within SAME_TOL (cosine >= 0.99999, max-abs <= 4e-3) and identical
+argmax ids; both match the oracle within the draft tolerance."""
 
 import numpy as np
 import pytest
@@ -31,6 +33,13 @@ def case():
     return dict(cfg=cfg, t=t, inp=inp, m=m, th=th, feats=feats)
 
 
+SAME_TOL = dict(cos_min=0.99999, max_abs=4e-3)
+
+
+def _same(h_a, h_b, what):
+    assert_close_fp16(h_a.float().cpu().numpy(), h_b.float().cpu().numpy(), what=what, **SAME_TOL)
+
+
 def _bits(x):
     return x.cpu().numpy().view(np.uint16) if x.dtype == torch.float16 else x.cpu().numpy()
 
@@ -41,7 +50,7 @@ def test_feature_list_equals_concatenated_target_hidden(case):
     i0, h0 = m.draft(ids, th, return_hidden=True)
     i1, h1 = m.draft(ids, feats, return_hidden=True)
     torch.cuda.synchronize()
-    np.testing.assert_array_equal(_bits(h1), _bits(h0))
+    _same(h1, h0, "features vs concatenated")
     np.testing.assert_array_equal(_bits(i1), _bits(i0))
     W = O.OracleWeights(case["cfg"], case["t"])
     h_ref, _, ids_ref = O.draft_block(W, inp["ids"], inp["target_hidden"], fp16=True)
@@ -70,8 +79,10 @@ def test_strided_features_and_all_layer_outputs(case):
         everything[lid + 1] = feats[j]
     i2, h2 = m.draft(ids, everything, return_hidden=True)   # selection at lid + 1
     torch.cuda.synchronize()
+    _same(h1, h2, "strided vs every-layer list")   # the same fc GEMMs: equal bit for bit
+    np.testing.assert_array_equal(_bits(h1), _bits(h2))
     for i, h in ((i1, h1), (i2, h2)):
-        np.testing.assert_array_equal(_bits(h), _bits(h0))
+        _same(h, h0, "features vs concatenated")
         np.testing.assert_array_equal(_bits(i), _bits(i0))
 
 
