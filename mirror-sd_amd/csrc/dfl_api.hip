@@ -511,6 +511,18 @@ static int layers_ready(dfl_ctx* ctx, const char* who) {
   return DFL_OK;
 }
 
+// Cache placement of the next n rows of sequence seq (its current state) at absolute
+// position pos0.
+static void rope_seq(dfl_ctx* ctx, int seq, const Layer& L, long long pos0, int n, RopeSeq& r) {
+  const SeqState& q = ctx->seqs[seq];
+  r.pos0 = pos0;
+  r.Kc = ctx->kc(L, seq);
+  r.Vt = ctx->vt(L, seq);
+  q.slots(n, r.cache_row0, r.sink_fill, r.ring_j0);
+  r.ring_S = q.sink;
+  r.ring_W = q.window;
+}
+
 // Per-layer K/V of `rows` fused context rows (row-major fp16, row stride ld): the K|V
 // projection on rocBLAS (fp32 rows), then per-row scale + fp16 rounding, k_norm + RoPE on K,
 // appended at cache row len + r0 with absolute position offset + r0.
@@ -529,6 +541,7 @@ static int ingest_kv_rows(dfl_ctx* ctx, const half_t* rows_src, int ld, int rows
     q.oscale = L.s_qkv + NH * 128;   // scales of the k|v rows, in row order
     q.M = rows;
     q.N = Nkv;
+    q.n_seq = 1;
     q.col_slot0 = NH;
     q.slot0 = NH;
     q.n_slots = 2 * NKV;
@@ -537,16 +550,10 @@ static int ingest_kv_rows(dfl_ctx* ctx, const half_t* rows_src, int ld, int rows
     q.q_norm = L.q_norm;
     q.k_norm = L.k_norm;
     q.eps = ctx->cfg.rms_eps;
-    q.pos0 = ctx->sq().offset + r0;
     q.log2_theta = std::log2(ctx->cfg.rope_theta);
     q.Q = nullptr;
-    q.q_rows = 0;
-    q.Kc = ctx->kc(L, ctx->cur);
-    q.Vt = ctx->vt(L, ctx->cur);
     q.cap = ctx->cap;
-    ctx->sq().slots(rows, q.cache_row0, q.sink_fill, q.ring_j0);
-    q.ring_S = ctx->sq().sink;
-    q.ring_W = ctx->sq().window;
+    rope_seq(ctx, ctx->cur, L, ctx->sq().offset + r0, rows, q.sq[0]);
     ProfScope ps(ctx, P_INGEST_KV, 0, st);
     launch_qk_rope(q, st);
   }
@@ -700,12 +707,14 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
     DFL_TRY(skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_STORE, ctx->sk_qkv, Ly.w_qkv, Ly.s_qkv, ctx->NQKV, H / 32,
            ctx->x, H, M, Ly.in_norm, /*rn_from_ss=*/l > 0, ctx->qkvbuf, ctx->NQKV, nullptr,
            nullptr, nullptr, st));
-    for (int i = 0; i < n_seq; ++i) {
-      const SeqState& sqs = ctx->seqs[seq0 + i];
+    // Q/K norm + RoPE and attention, up to SEQ_MAX sequences per launch
+    for (int g0 = 0; g0 < n_seq; g0 += SEQ_MAX) {
+      const int gn = std::min(SEQ_MAX, n_seq - g0);
       QKRopeArgs q{};
-      q.qkv16 = ctx->qkvbuf + (size_t)i * B * ctx->NQKV;
+      q.qkv16 = ctx->qkvbuf + (size_t)g0 * B * ctx->NQKV;
       q.M = B;
       q.N = ctx->NQKV;
+      q.n_seq = gn;
       q.col_slot0 = 0;
       q.slot0 = 0;
       q.n_slots = NH + 2 * NKV;
@@ -714,46 +723,46 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
       q.q_norm = Ly.q_norm;
       q.k_norm = Ly.k_norm;
       q.eps = eps;
-      q.pos0 = sqs.offset;
       q.log2_theta = std::log2(ctx->cfg.rope_theta);
-      q.Q = ctx->Q + (size_t)i * NH * B * 128;
-      q.q_rows = B;
-      q.Kc = ctx->kc(Ly, seq0 + i);
-      q.Vt = ctx->vt(Ly, seq0 + i);
+      q.Q = ctx->Q + (size_t)g0 * NH * B * 128;
       q.cap = ctx->cap;
-      sqs.slots(B, q.cache_row0, q.sink_fill, q.ring_j0);
-      q.ring_S = sqs.sink;
-      q.ring_W = sqs.window;
-      {
-        ProfScope ps(ctx, P_QK_ROPE, 0, st);
-        launch_qk_rope(q, st);
-      }
       AttnArgs at{};
       at.Q = q.Q;
-      at.Kc = q.Kc;
-      at.Vt = q.Vt;
       at.B = B;
       at.NH = NH;
       at.NKV = NKV;
       at.cap = ctx->cap;
-      SeqState after = sqs;   // the block's rows appended (evicting as the window requires)
-      after.append(B);
-      at.L = after.key_range();
-      at.ring_S = after.sink;
-      at.ring_W = after.window;
-      at.ring_j = after.window ? (int)(after.ring_j % after.window) : 0;
-      at.ring_len = std::max(0, after.len - after.sink);
-      at.sink_len = std::min(after.len, after.sink);
-      attn_split(at.L, at.chunk, at.n_chunks);
+      at.n_seq = gn;
       at.scale_log2 = (float)(1.4426950408889634 / std::sqrt(128.0));
       at.Op = ctx->Op;
       at.Ml = ctx->Ml;
       at.O = ctx->attn;
-      at.o_row0 = i * B;
-      {
-        ProfScope ps(ctx, P_ATTN, 2LL * NKV * at.L * 128 * 2, st);
-        launch_block_attention(at, st);
+      long long kv_bytes = 0;
+      for (int i = 0; i < gn; ++i) {
+        const int sidx = seq0 + g0 + i;
+        rope_seq(ctx, sidx, Ly, ctx->seqs[sidx].offset, B, q.sq[i]);
+        SeqState after = ctx->seqs[sidx];   // the block's rows appended (evicting as the
+        after.append(B);                     // window requires)
+        AttnSeq& as = at.sq[i];
+        as.Kc = q.sq[i].Kc;
+        as.Vt = q.sq[i].Vt;
+        as.L = after.key_range();
+        as.ring_S = after.sink;
+        as.ring_W = after.window;
+        as.ring_j = after.window ? (int)(after.ring_j % after.window) : 0;
+        as.ring_len = std::max(0, after.len - after.sink);
+        as.sink_len = std::min(after.len, after.sink);
+        as.o_row0 = (g0 + i) * B;
+        attn_split(as.L, as.chunk, as.n_chunks);
+        at.max_chunks = std::max(at.max_chunks, as.n_chunks);
+        kv_bytes += 2LL * NKV * as.L * 128 * 2;
       }
+      {
+        ProfScope ps(ctx, P_QK_ROPE, 0, st);
+        launch_qk_rope(q, st);
+      }
+      ProfScope ps(ctx, P_ATTN, kv_bytes, st);
+      launch_block_attention(at, st);
     }
     // x += attn @ Wo^T ; per-tile row sums of squares of x -> sk_ss
     DFL_TRY(skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_RESID, ctx->sk_o, Ly.w_o, Ly.s_o, H, NQ / 32, ctx->attn,

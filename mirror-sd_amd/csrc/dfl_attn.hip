@@ -58,10 +58,14 @@ __global__ __launch_bounds__(768) void block_attn_kernel(AttnArgs a) {
   const int wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
   const int KW = a.kw;
   const int qtl = wv / KW, kwi = wv - qtl * KW;        // query tile in group, key lane
-  const int qt = blockIdx.z * a.q_per_group + qtl;
-  const int q = lane & 31, gg = lane >> 5;
   const int ratio = a.NH / a.NKV;
   const int R = ratio * a.B;
+  const int groups = ((R + 31) / 32 + a.q_per_group - 1) / a.q_per_group;
+  const int sidx = blockIdx.z / groups;                  // sequence
+  const AttnSeq& sq = a.sq[sidx];
+  if (c >= sq.n_chunks) return;                          // this sequence has fewer chunks
+  const int qt = (blockIdx.z - sidx * groups) * a.q_per_group + qtl;
+  const int q = lane & 31, gg = lane >> 5;
   const int rq = qt * 32 + q;
   const bool row_ok = rq < R;
 
@@ -69,11 +73,12 @@ __global__ __launch_bounds__(768) void block_attn_kernel(AttnArgs a) {
   // stage's K/V loads are issued so the two latencies overlap.
   half8_t qf[8];
   bool have_q = false;
-  const uint4* qp = reinterpret_cast<const uint4*>(a.Q + ((size_t)g * R + (row_ok ? rq : 0)) * 128 +
-                                                   64 * gg);   // rows >= R: never stored
+  const uint4* qp = reinterpret_cast<const uint4*>(
+      a.Q + ((size_t)sidx * a.NH * a.B + (size_t)g * R + (row_ok ? rq : 0)) * 128 +
+      64 * gg);   // rows >= R: never stored
 
-  const int k_begin = c * a.chunk;
-  const int k_end = min(a.L, k_begin + a.chunk);
+  const int k_begin = c * sq.chunk;
+  const int k_end = min(sq.L, k_begin + sq.chunk);
 
   // Permuted key row supplied by this lane as MFMA A row i = lane % 32.
   const int i = lane & 31;
@@ -86,9 +91,9 @@ __global__ __launch_bounds__(768) void block_attn_kernel(AttnArgs a) {
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) o[dt] = (floatx16){};
 
-  const half_t* kg = a.Kc + (size_t)g * a.cap * 128;
-  const half_t* vg = a.Vt + (size_t)g * 128 * a.cap;
-  const int vlast = (a.L - 1) & ~7;   // last 8-key group holding a valid key
+  const half_t* kg = sq.Kc + (size_t)g * a.cap * 128;
+  const half_t* vg = sq.Vt + (size_t)g * 128 * a.cap;
+  const int vlast = (sq.L - 1) & ~7;   // last 8-key group holding a valid key
 
   for (int k0 = k_begin; k0 < k_end; k0 += 32 * AT_STAGE_BLOCKS) {
     const int nblk = min(AT_STAGE_BLOCKS, (k_end - k0 + 31) >> 5);
@@ -101,7 +106,7 @@ __global__ __launch_bounds__(768) void block_attn_kernel(AttnArgs a) {
       if (s < 8) {
         const int r = 4 * s + (lane >> 4);                        // key row in the block
         const int cc = (lane & 15) ^ kswz(r);
-        const int key = min(k0 + 32 * j + r, a.L - 1);
+        const int key = min(k0 + 32 * j + r, sq.L - 1);
         src = kg + (size_t)key * 128 + cc * 8;
         dst = lds + j * AT_KBLK + s * 1024;
       } else {
@@ -132,16 +137,16 @@ __global__ __launch_bounds__(768) void block_attn_kernel(AttnArgs a) {
       // Accumulator r holds key kbase + (r < 8 ? 8*gg + r : 16 + 8*gg + r - 8).
       const int kbase = k0 + 32 * j;
       float v[16];
-      if (a.ring_W > 0) {   // sink + window cache: only the valid ring rows count
+      if (sq.ring_W > 0) {   // sink + window cache: only the valid ring rows count
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int kr = kbase + (r < 8 ? 8 * gg + r : 16 + 8 * gg + (r - 8));
           bool ok = kr < k_end;
-          if (kr < a.ring_S) {
-            ok = ok && kr < a.sink_len;
+          if (kr < sq.ring_S) {
+            ok = ok && kr < sq.sink_len;
           } else {
-            const int back = (a.ring_j - 1 - (kr - a.ring_S)) % a.ring_W;
-            ok = ok && (back < 0 ? back + a.ring_W : back) < a.ring_len;
+            const int back = (sq.ring_j - 1 - (kr - sq.ring_S)) % sq.ring_W;
+            ok = ok && (back < 0 ? back + sq.ring_W : back) < sq.ring_len;
           }
           v[r] = ok ? s[r] * a.scale_log2 : -INFINITY;
         }
@@ -218,8 +223,9 @@ __global__ __launch_bounds__(768) void block_attn_kernel(AttnArgs a) {
   }
 
   if (!row_ok) return;
-  const int rowg = g * R + rq;   // = h * B + b
-  const size_t NB = (size_t)a.NH * a.B;
+  // partial row of all sequences: s * NH * B + h * B + b  (g * R + rq = h * B + b)
+  const size_t rowg = (size_t)sidx * a.NH * a.B + (size_t)g * R + rq;
+  const size_t NB = (size_t)a.n_seq * a.NH * a.B;
   float* op = a.Op + ((size_t)c * NB + rowg) * 128 + 4 * gg;
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
@@ -239,10 +245,12 @@ __global__ __launch_bounds__(768) void block_attn_kernel(AttnArgs a) {
 __global__ __launch_bounds__(128) void attn_merge_kernel(AttnArgs a) {
   __shared__ float wts[64];
   __shared__ float den_s;
-  const int rowg = blockIdx.x;   // h * B + b
+  const int rowg = blockIdx.x;   // s * NH * B + h * B + b
   const int d = threadIdx.x;
-  const size_t NB = (size_t)a.NH * a.B;
-  const int nc = a.n_chunks;
+  const int per_seq = a.NH * a.B;
+  const int sidx = rowg / per_seq;
+  const size_t NB = (size_t)a.n_seq * per_seq;
+  const int nc = a.sq[sidx].n_chunks;
   float mc = -INFINITY, lc = 0.f;
   if (d < nc) {
     mc = a.Ml[((size_t)d * NB + rowg) * 2];
@@ -264,8 +272,9 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(AttnArgs a) {
   const float* op = a.Op + (size_t)rowg * 128 + d;
 #pragma unroll 8
   for (int c = 0; c < nc; ++c) num += op[(size_t)c * NB * 128] * wts[c];
-  const int h = rowg / a.B, b = rowg - h * a.B;
-  a.O[afl_index(a.o_row0 + b, h * 128 + d, a.NH * 128)] = f2h(num / den_s);
+  const int hb = rowg - sidx * per_seq;
+  const int h = hb / a.B, b = hb - h * a.B;
+  a.O[afl_index(a.sq[sidx].o_row0 + b, h * 128 + d, a.NH * 128)] = f2h(num / den_s);
 }
 
 void launch_block_attention(const AttnArgs& a_in, hipStream_t st) {
@@ -275,14 +284,15 @@ void launch_block_attention(const AttnArgs& a_in, hipStream_t st) {
   a.q_per_group = std::min(n_qt, 8);
   // Extra waves per query tile only where the tiles alone leave the CU short of waves;
   // each takes at least one key block of the chunk.
-  const int cblocks = a.chunk / 32;
+  int cblocks = 1 << 30;
+  for (int i = 0; i < a.n_seq; ++i) cblocks = std::min(cblocks, a.sq[i].chunk / 32);
   a.kw = a.q_per_group >= 3 ? 1 : std::max(1, std::min(std::min(4, cblocks), 12 / a.q_per_group));
   const int groups = (n_qt + a.q_per_group - 1) / a.q_per_group;
   const int merge_bytes = a.q_per_group * (a.kw - 1) * AT_PART_BYTES;
   const int lds_bytes = std::max(AT_STAGE_BYTES, merge_bytes);
-  hipLaunchKernelGGL(block_attn_kernel, dim3(a.n_chunks, a.NKV, groups),
+  hipLaunchKernelGGL(block_attn_kernel, dim3(a.max_chunks, a.NKV, groups * a.n_seq),
                      dim3(64 * a.q_per_group * a.kw), lds_bytes, st, a);
-  hipLaunchKernelGGL(attn_merge_kernel, dim3(a.NH * a.B), dim3(128), 0, st, a);
+  hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_seq * a.NH * a.B), dim3(128), 0, st, a);
 }
 
 }  // namespace dfl

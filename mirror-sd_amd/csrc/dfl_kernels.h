@@ -98,56 +98,76 @@ void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* no
 void launch_apply_norm(const half_t* x, const float* ss, int ss_tiles, float eps, const half_t* g,
                        int M, int N, half_t* h, hipStream_t st);
 void launch_afl_to_rows(const half_t* x, int M, int N, half_t* h, hipStream_t st);
-// Per-head RMSNorm + neox RoPE + scatter of projections [M][N]: fp16 qkv16 (scaled and
-// rounded by the GEMM epilogue) or fp32 qkv32 (scaled and rounded here).  Rows m use position pos0 + m.  Head slots [0, NH) -> Q[h][m][d]
-// (q_rows rows per head); slots [NH, NH+NKV) -> K cache rows (cache_row0 + m);
-// [NH+NKV, NH+2NKV) -> Vt cache columns.  Column 0 of qkv16 is head slot col_slot0 (so the
-// ingest path can project only K and V).
+// Up to SEQ_MAX sequences (batched drafting) share one rope / attention launch.
+constexpr int SEQ_MAX = 8;
+
+// Where one sequence's rows go: absolute position of its first row and its K/V cache
+// (K [NKV][cap][128], Vt [NKV][128][cap]).  Without a window (ring_W == 0) row m goes to
+// cache row cache_row0 + m.  With a sink + window cache (ring_W > 0) the first sink_fill
+// rows go to cache_row0 + m (filling the sink) and later ones to ring row
+// ring_S + ((ring_j0 + m - sink_fill) mod ring_W).
+struct RopeSeq {
+  long long pos0;
+  half_t* Kc;
+  half_t* Vt;
+  int cache_row0, sink_fill, ring_j0, ring_S, ring_W;
+};
+
+// Per-head RMSNorm + neox RoPE + scatter of projections: fp16 qkv16 (scaled and rounded by
+// the GEMM epilogue) or fp32 qkv32 (scaled and rounded here), rows [n_seq * M][N], sequence
+// s owning rows s*M .. s*M + M - 1, its row m at position sq[s].pos0 + m.  Head slots
+// [0, NH) -> Q[s][h][m][d] ([n_seq][NH][M][128]); slots [NH, NH+NKV) -> K cache rows;
+// [NH+NKV, NH+2NKV) -> Vt cache columns.  Column 0 is head slot col_slot0 (so the ingest
+// path can project only K and V).
 struct QKRopeArgs {
-  const half_t* qkv16;                       // projection rows [M][N], fp16 (scaled), or
-  const float* qkv32; const half_t* oscale;  // fp32 GEMM rows [M][N] + fp16 scale per column
-  int M; int N;
+  const half_t* qkv16;                       // projection rows, fp16 (scaled), or
+  const float* qkv32; const half_t* oscale;  // fp32 GEMM rows + fp16 scale per column
+  int M; int N;                              // rows per sequence, columns
+  int n_seq;
   int col_slot0;                             // head slot of column 0
   int slot0, n_slots;                        // head slots handled (q,k,v numbering)
   int NH, NKV;
   const half_t* q_norm; const half_t* k_norm; float eps;
-  long long pos0; double log2_theta;
-  half_t* Q; int q_rows;                     // [NH][q_rows][128]
-  half_t* Kc; half_t* Vt; int cap; int cache_row0;  // K [NKV][cap][128], Vt [NKV][128][cap]
-  // sink + window cache (ring_W > 0): of the appended rows, the first sink_fill go to
-  // cache rows cache_row0 + m (filling the sink), later ones to ring row
-  // ring_S + ((ring_j0 + m - sink_fill) mod ring_W)
-  int ring_S, ring_W, ring_j0, sink_fill;
+  double log2_theta;
+  half_t* Q;
+  int cap;
+  RopeSeq sq[SEQ_MAX];
 };
 // -1: a ring row that a later row of the same launch overwrites (more than ring_W ring
 // rows appended at once keep only the newest ring_W), so it is not written at all
-DFL_DEV int cache_slot(const QKRopeArgs& a, int m) {
-  if (a.ring_W == 0 || m < a.sink_fill) return a.cache_row0 + m;
-  if (m - a.sink_fill < a.M - a.sink_fill - a.ring_W) return -1;
-  return a.ring_S + (a.ring_j0 + (m - a.sink_fill)) % a.ring_W;
+DFL_DEV int cache_slot(const RopeSeq& q, int M, int m) {
+  if (q.ring_W == 0 || m < q.sink_fill) return q.cache_row0 + m;
+  if (m - q.sink_fill < M - q.sink_fill - q.ring_W) return -1;
+  return q.ring_S + (q.ring_j0 + (m - q.sink_fill)) % q.ring_W;
 }
 void launch_qk_rope(const QKRopeArgs& a, hipStream_t st);
 // ids[m] = ~low32(keys[m]); keys[m] = 0.
 void launch_argmax_finalize(unsigned long long* keys, int M, int32_t* ids, hipStream_t st);
 
 // ---- attention (dfl_attn.hip) ----
-struct AttnArgs {
-  const half_t* Q;        // [NH][B][128]
+// One sequence of an attention launch: its cache, key range and output rows.
+// Sink + window cache (ring_W > 0): keys [0, ring_S) valid below sink_len; key ring_S + p
+// valid when (ring_j - 1 - p) mod ring_W < ring_len (the ring_len newest ring rows).
+struct AttnSeq {
   const half_t* Kc;       // [NKV][cap][128]
   const half_t* Vt;       // [NKV][128][cap]
-  int B, NH, NKV, cap, L; // L = number of valid keys
+  int L;                  // number of valid keys
   int chunk;              // keys per split (multiple of 32)
   int n_chunks;
+  int o_row0;             // first output row in O
+  int ring_S, ring_W, ring_j, ring_len, sink_len;
+};
+struct AttnArgs {
+  const half_t* Q;        // [n_seq][NH][B][128]
+  int B, NH, NKV, cap;
+  int n_seq, max_chunks;  // max_chunks = max over the sequences of n_chunks
   int q_per_group, kw;    // set by the launcher: query tiles per workgroup, waves per tile
   float scale_log2;       // head_dim^-0.5 * log2(e)
-  float* Op;              // [n_chunks][NH*B][128] unnormalised partial outputs
-  float* Ml;              // [n_chunks][NH*B][2] running (max, sum) in log2 domain
-  half_t* O;              // final output rows o_row0 .. o_row0 + B - 1 of an activation
-                          // fragment layout tile set with NH*128 columns
-  int o_row0;
-  // sink + window cache (ring_W > 0): keys [0, ring_S) valid below sink_len; key ring_S + p
-  // valid when (ring_j - 1 - p) mod ring_W < ring_len (the ring_len newest ring rows)
-  int ring_S, ring_W, ring_j, ring_len, sink_len;
+  float* Op;              // [max_chunks][n_seq*NH*B][128] unnormalised partial outputs
+  float* Ml;              // [max_chunks][n_seq*NH*B][2] running (max, sum) in log2 domain
+  half_t* O;              // output rows of an activation fragment layout tile set with
+                          // NH*128 columns
+  AttnSeq sq[SEQ_MAX];
 };
 void launch_block_attention(const AttnArgs& a, hipStream_t st);
 

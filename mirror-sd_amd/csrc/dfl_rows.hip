@@ -158,32 +158,37 @@ void launch_afl_to_rows(const half_t* x, int M, int N, half_t* h, hipStream_t st
 }
 
 
-// One wave per (row m, head slot); lane j holds head elements j and j + 64, which are
+// One wave per (sequence, row m, head slot); lane j holds head elements j and j + 64, which are
 // exactly the neox RoPE pair (dflash.py:263-275, split-half rotation), so the
 // rotation is lane-local.  Angles are computed in fp64 (pos * theta^(-j/64)).
 __global__ __launch_bounds__(256) void qk_rope_kernel(QKRopeArgs a) {
   const int lane = threadIdx.x & 63;
   const long long p = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (p >= (long long)a.M * a.n_slots) return;
-  const int m = (int)(p / a.n_slots);
-  const int slot = a.slot0 + (int)(p - (long long)m * a.n_slots);
+  const long long per_seq = (long long)a.M * a.n_slots;
+  if (p >= per_seq * a.n_seq) return;
+  const int sidx = (int)(p / per_seq);
+  const long long pr = p - (long long)sidx * per_seq;
+  const int m = (int)(pr / a.n_slots);
+  const int slot = a.slot0 + (int)(pr - (long long)m * a.n_slots);
+  const RopeSeq& sq = a.sq[sidx];
+  const size_t row = (size_t)sidx * a.M + m;
   const int c0 = (slot - a.col_slot0) * 128 + lane;
-  const int crow = slot >= a.NH ? cache_slot(a, m) : 0;
+  const int crow = slot >= a.NH ? cache_slot(sq, a.M, m) : 0;
   if (crow < 0) return;   // whole wave: one (row, head slot) per wave
   // projections scaled and rounded to fp16 (Linear output): by the GEMM epilogue (qkv16),
   // or here from the fp32 GEMM rows and the per-row scales (qkv32, oscale)
   float v0, v1;
   if (a.qkv32) {
-    v0 = h2f(f2h(a.qkv32[(size_t)m * a.N + c0] * h2f(a.oscale[c0])));
-    v1 = h2f(f2h(a.qkv32[(size_t)m * a.N + c0 + 64] * h2f(a.oscale[c0 + 64])));
+    v0 = h2f(f2h(a.qkv32[row * a.N + c0] * h2f(a.oscale[c0])));
+    v1 = h2f(f2h(a.qkv32[row * a.N + c0 + 64] * h2f(a.oscale[c0 + 64])));
   } else {
-    v0 = h2f(a.qkv16[(size_t)m * a.N + c0]);
-    v1 = h2f(a.qkv16[(size_t)m * a.N + c0 + 64]);
+    v0 = h2f(a.qkv16[row * a.N + c0]);
+    v1 = h2f(a.qkv16[row * a.N + c0 + 64]);
   }
   const int kv_slot0 = a.NH + a.NKV;
   if (slot >= kv_slot0) {   // V head: no norm, no rotation
     const int gk = slot - kv_slot0;
-    half_t* vt = a.Vt + (size_t)gk * 128 * a.cap + crow;
+    half_t* vt = sq.Vt + (size_t)gk * 128 * a.cap + crow;
     vt[(size_t)lane * a.cap] = f2h(v0);
     vt[(size_t)(lane + 64) * a.cap] = f2h(v1);
     return;
@@ -195,7 +200,7 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(QKRopeArgs a) {
   const float y0 = h2f(rms_out(v0, r, gn[lane]));
   const float y1 = h2f(rms_out(v1, r, gn[lane + 64]));
   const double inv_freq = exp2(-(double)lane * (1.0 / 64.0) * a.log2_theta);
-  const double ang = (double)(a.pos0 + m) * inv_freq;
+  const double ang = (double)(sq.pos0 + m) * inv_freq;
   double sd, cd;
   sincos(ang, &sd, &cd);
   const float c = (float)cd, sn = (float)sd;
@@ -203,17 +208,17 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(QKRopeArgs a) {
   const half_t o1 = f2h(y1 * c + y0 * sn);
   half_t* dst;
   if (is_q) {
-    dst = a.Q + ((size_t)slot * a.q_rows + m) * 128;
+    dst = a.Q + (((size_t)sidx * a.NH + slot) * a.M + m) * 128;
   } else {
     const int gk = slot - a.NH;
-    dst = a.Kc + ((size_t)gk * a.cap + crow) * 128;
+    dst = sq.Kc + ((size_t)gk * a.cap + crow) * 128;
   }
   dst[lane] = o0;
   dst[lane + 64] = o1;
 }
 
 void launch_qk_rope(const QKRopeArgs& a, hipStream_t st) {
-  const long long waves = (long long)a.M * a.n_slots;
+  const long long waves = (long long)a.M * a.n_slots * a.n_seq;
   hipLaunchKernelGGL(qk_rope_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, a);
 }
 
