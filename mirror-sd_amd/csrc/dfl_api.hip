@@ -32,6 +32,7 @@ int fail(int code, const std::string& msg) {
 constexpr int ING_MAX = 4096;      // context rows per ingest pass (at most)
 constexpr int MAX_CHUNKS = 64;     // attention key splits
 constexpr int MT_MAX = 8;          // 32-row m-tiles per M-split GEMM launch
+constexpr int LM_BLAS_MIN_ROWS = 64;   // stacked rows from which the lm_head runs on rocBLAS
 
 enum ProfCat { P_GEMM_W8 = 0, P_LM_HEAD, P_ATTN, P_QK_ROPE, P_ROWS, P_INGEST_FC, P_INGEST_KV, P_N };
 const char* const kProfNames[P_N] = {"gemm_w8a16",   "lm_head_argmax", "attention",
@@ -112,6 +113,10 @@ struct dfl_ctx {
   bool fc_loaded = false;
   half_t* final_norm = nullptr;
   uint4* w_lm = nullptr;
+  // stacked blocks (more than LM_BLAS_MIN_ROWS rows): the lm_head as a library GEMM over a
+  // row-major fp16 copy, logits in lm32 [RM][V] fp32
+  half_t* w_lm16 = nullptr;
+  float* lm32 = nullptr;
   const half_t* embed = nullptr;
   bool head_loaded = false;
   int active = 0;   // layers run per call (num_draft_layers)
@@ -448,6 +453,14 @@ int dfl_load_head(dfl_ctx* ctx, const uint16_t* final_norm, const uint16_t* embe
     if (!ctx->w_lm) DFL_TRY(ctx->alloc(&ctx->w_lm, (size_t)ctx->V * ctx->H / 8));
     launch_pack_f16(reinterpret_cast<const half_t*>(lm_head), ctx->V, ctx->H, ctx->w_lm, st);
     DFL_TRY(check_launch("pack lm_head"));
+    if (ctx->RM > LM_BLAS_MIN_ROWS) {
+      if (!ctx->w_lm16) {
+        DFL_TRY(ctx->alloc(&ctx->w_lm16, (size_t)ctx->V * ctx->H));
+        DFL_TRY(ctx->alloc(&ctx->lm32, (size_t)ctx->RM * ctx->V));
+      }
+      DFL_HIP(hipMemcpyAsync(ctx->w_lm16, lm_head, (size_t)ctx->V * ctx->H * 2,
+                             hipMemcpyDeviceToDevice, st));
+    }
   }
   ctx->head_loaded = true;
   return DFL_OK;
@@ -774,7 +787,16 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
     DFL_TRY(skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_RESID, ctx->sk_down, Ly.w_down, Ly.s_down, H, F / 32,
            ctx->act, F, M, nullptr, false, nullptr, H, ctx->x, nullptr, nullptr, st));
   }
-  if (out_logits || out_ids) {
+  if ((out_logits || out_ids) && M > LM_BLAS_MIN_ROWS && ctx->w_lm16) {
+    // stacked blocks: final norm into row-major rows, then the lm_head GEMM (fp32 logits)
+    // and a row argmax
+    ProfScope ps(ctx, P_LM_HEAD, (long long)ctx->V * H * 2, st);
+    launch_apply_norm(ctx->x, ctx->sk_ss, H / 64, ctx->cfg.rms_eps, ctx->final_norm, M, H, ctx->h,
+                      st);
+    float* lg = out_logits ? out_logits : ctx->lm32;
+    DFL_TRY(blas_gemm(ctx, ctx->V, M, H, ctx->w_lm16, H, ctx->h, H, 0.f, lg, ctx->V, st));
+    if (out_ids) launch_row_argmax(lg, M, ctx->V, out_ids, st);
+  } else if (out_logits || out_ids) {
     DFL_TRY(skgemm(ctx, P_LM_HEAD, WT_F16, EPI_ARGMAX, ctx->sk_lm, ctx->w_lm, nullptr, ctx->V, H / 16,
            ctx->x, H, M, ctx->final_norm, true, nullptr, 0, nullptr, out_logits,
            out_ids ? ctx->keys : nullptr, st));

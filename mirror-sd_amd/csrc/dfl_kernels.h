@@ -143,6 +143,8 @@ DFL_DEV int cache_slot(const RopeSeq& q, int M, int m) {
 void launch_qk_rope(const QKRopeArgs& a, hipStream_t st);
 // ids[m] = ~low32(keys[m]); keys[m] = 0.
 void launch_argmax_finalize(unsigned long long* keys, int M, int32_t* ids, hipStream_t st);
+// ids[m] = argmax of fp32 logits row m ([M][V]), lowest index on ties, -1 if none > -inf.
+void launch_row_argmax(const float* logits, int M, int V, int32_t* ids, hipStream_t st);
 
 // ---- attention (dfl_attn.hip) ----
 // One sequence of an attention launch: its cache, key range and output rows.

@@ -222,6 +222,59 @@ void launch_qk_rope(const QKRopeArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(qk_rope_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, a);
 }
 
+// ids[m] = argmax over the fp32 logits row m (lowest index on ties, NaN never chosen, -1
+// when no entry beats -inf): the lm_head argmax for stacked blocks whose logits come from
+// a library GEMM.  Each thread scans its columns in increasing order with a strict '>',
+// then the workgroup keeps the largest (order-preserving value, ~index) key.
+__global__ __launch_bounds__(256) void row_argmax_kernel(const float* __restrict__ logits, int V,
+                                                         int32_t* __restrict__ ids) {
+  __shared__ unsigned long long sm[4];
+  const int m = blockIdx.x;
+  // V % 64 == 0: rows are 16-byte aligned, read as float4 with RA_UNROLL loads in flight;
+  // a thread's columns (4 per float4, float4 i = t, t + 256, ...) are visited in order
+  constexpr int RA_UNROLL = 4;
+  const floatx4* row = reinterpret_cast<const floatx4*>(logits + (size_t)m * V);
+  const int n4 = V / 4;
+  float best = -INFINITY;
+  int bn = -1;
+  for (int i0 = threadIdx.x; i0 < n4; i0 += 256 * RA_UNROLL) {
+    floatx4 v[RA_UNROLL];
+#pragma unroll
+    for (int u = 0; u < RA_UNROLL; ++u) {
+      const int i = i0 + 256 * u;
+      v[u] = i < n4 ? row[i] : (floatx4){-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    }
+#pragma unroll
+    for (int u = 0; u < RA_UNROLL; ++u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (v[u][j] > best) {
+          best = v[u][j];
+          bn = 4 * (i0 + 256 * u) + j;
+        }
+  }
+  unsigned long long key =
+      bn < 0 ? 0ull
+             : ((unsigned long long)float_order_key(best) << 32) | (0xFFFFFFFFu - (uint32_t)bn);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const unsigned long long k2 = __shfl_xor(key, o, 64);
+    key = k2 > key ? k2 : key;
+  }
+  if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = key;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long k = sm[0];
+    for (int i = 1; i < 4; ++i) k = sm[i] > k ? sm[i] : k;
+    ids[m] = k ? (int32_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull)) : -1;
+  }
+}
+
+void launch_row_argmax(const float* logits, int M, int V, int32_t* ids, hipStream_t st) {
+  if (M <= 0) return;
+  hipLaunchKernelGGL(row_argmax_kernel, dim3(M), dim3(256), 0, st, logits, V, ids);
+}
+
 __global__ void argmax_finalize_kernel(unsigned long long* keys, int M, int32_t* ids) {
   const int m = threadIdx.x;
   if (m < M) {
