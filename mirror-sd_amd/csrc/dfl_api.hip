@@ -706,10 +706,22 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
 
   // Attention key split per sequence: about one workgroup per CU ((chunks x KV heads) ~
   // CUs) with chunks of at most 160 keys (one LDS stage) while there are at most MAX_CHUNKS.
-  auto attn_split = [&](int L, int& chunk, int& n_chunks) {
+  // Attention key split.  One sequence: about one workgroup per CU ((chunks x KV heads) ~
+  // CUs) with chunks of at most 160 keys (one LDS stage) while there are at most
+  // MAX_CHUNKS.  Several sequences in one launch: chunks in proportion to each sequence's
+  // keys, about two workgroups per CU in all; a chunk then spans several LDS stages, which
+  // keeps the per-chunk partials (the merge's input) few.
+  auto attn_split = [&](int L, long long keys_total, int n_in_launch, int& chunk,
+                        int& n_chunks) {
     const int kblocks = (L + 31) / 32;
-    const int n_split = std::max(1, std::min(std::min(MAX_CHUNKS, kblocks),
-                                              std::max((kblocks + 4) / 5, (ctx->n_cu + NKV - 1) / NKV)));
+    int n_split;
+    if (n_in_launch == 1) {
+      n_split = std::max((kblocks + 4) / 5, (ctx->n_cu + NKV - 1) / NKV);
+    } else {
+      const long long target = 2LL * ((ctx->n_cu + NKV - 1) / NKV);
+      n_split = (int)((target * L + keys_total - 1) / std::max(1LL, keys_total));
+    }
+    n_split = std::max(1, std::min(std::min(MAX_CHUNKS, kblocks), n_split));
     chunk = ((kblocks + n_split - 1) / n_split) * 32;
     n_chunks = (L + chunk - 1) / chunk;
   };
@@ -750,7 +762,12 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
       at.Op = ctx->Op;
       at.Ml = ctx->Ml;
       at.O = ctx->attn;
-      long long kv_bytes = 0;
+      long long kv_bytes = 0, keys_total = 0;
+      for (int i = 0; i < gn; ++i) {
+        SeqState after = ctx->seqs[seq0 + g0 + i];
+        after.append(B);
+        keys_total += after.key_range();
+      }
       for (int i = 0; i < gn; ++i) {
         const int sidx = seq0 + g0 + i;
         rope_seq(ctx, sidx, Ly, ctx->seqs[sidx].offset, B, q.sq[i]);
@@ -766,7 +783,7 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
         as.ring_len = std::max(0, after.len - after.sink);
         as.sink_len = std::min(after.len, after.sink);
         as.o_row0 = (g0 + i) * B;
-        attn_split(as.L, as.chunk, as.n_chunks);
+        attn_split(as.L, keys_total, gn, as.chunk, as.n_chunks);
         at.max_chunks = std::max(at.max_chunks, as.n_chunks);
         kv_bytes += 2LL * NKV * as.L * 128 * 2;
       }
