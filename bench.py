@@ -29,18 +29,20 @@ sys.path.insert(0, os.path.join(ROOT, "mirror-sd_amd"))
 
 METRIC = ("draft-block latency (us) + achieved HBM GB/s, 27B-class W8A16 block=32 ctx=4096")
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0   # dense fp16 MFMA peak of MI355X
 
 
-def algorithmic_bytes(cfg, block, ctx):
+def algorithmic_bytes(cfg, block, ctx, n_seq=1):
     """Bytes a draft block must move from HBM: int8 projection weights + fp16 scales,
-    context+block K/V read by attention, fp16 lm_head."""
+    context+block K/V read by attention, fp16 lm_head.  ``ctx`` may be a list of per-
+    sequence contexts (batched drafting: the weights stream once for all sequences)."""
     H, NH, NKV, F, D = (cfg.hidden_size, cfg.num_attention_heads, cfg.num_key_value_heads,
                         cfg.intermediate_size, cfg.head_dim)
     NQKV = (NH + 2 * NKV) * D
     per_layer_w = NQKV * H + H * NH * D + 2 * F * H + H * F
     per_layer_s = 2 * (NQKV + H + 2 * F + H)
-    L = ctx + block
-    kv = 2 * NKV * L * D * 2
+    ctxs = list(ctx) if isinstance(ctx, (list, tuple)) else [ctx]
+    kv = sum(2 * NKV * (c + block) * D * 2 for c in ctxs)
     nl = cfg.num_hidden_layers
     lm = cfg.vocab_size * H * 2
     return {"proj_weights": nl * per_layer_w, "proj_scales": nl * per_layer_s,
@@ -60,14 +62,15 @@ def traffic_per_launch(workload_name):
         return None
 
 
-def build_model(wl, seed, keep_host: bool, max_ctx: int = 0):
+def build_model(wl, seed, keep_host: bool, max_ctx: int = 0, max_seqs: int = 1):
     """Synthetic weights generated on the GPU, quantised by the library's W8A16
     quantiser and loaded.  Optionally keeps host copies for the CPU baseline."""
     import torch
     from mirror_sd_amd.dflash import DFlashDraftModel
     from mirror_sd_amd import synth
     cfg = wl.cfg
-    m = DFlashDraftModel(cfg, max_ctx=max_ctx or wl.ctx, max_block=max(wl.block, 32))
+    m = DFlashDraftModel(cfg, max_ctx=max_ctx or wl.ctx, max_block=max(wl.block, 32),
+                         max_seqs=max_seqs)
     host = {}
     names = [n for n, _, _ in synth.weight_specs(cfg)]
     gen = dict(synth.make_weights_torch(cfg, seed=seed, device="cuda",
@@ -191,11 +194,12 @@ def main():
 
     wl = workload(args.workload)
     cfg = wl.cfg
+    batched = bool(wl.seq_ctx)   # several independent sequences drafted together
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
     torch.manual_seed(args.seed)
-    want_cpu = not args.no_cpu_baseline
+    want_cpu = not args.no_cpu_baseline and not batched
     if args.copy_probe_mib > 0:
         n = (args.copy_probe_mib << 20) // 4
         src = torch.ones(n, dtype=torch.int32, device="cuda")
@@ -205,40 +209,60 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     t_setup = time.perf_counter()
-    sweep = [int(c) for c in args.sweep.split(",") if c.strip()]
+    sweep = [int(c) for c in args.sweep.split(",") if c.strip()] if not batched else []
+    n_seq = len(wl.seq_ctx) if batched else 1
     model, host = build_model(wl, args.seed, keep_host=want_cpu,
-                              max_ctx=max([wl.ctx] + sweep))
-    inp = synth.make_inputs_torch(cfg, wl.block, wl.ctx, seed=args.seed, device="cuda")
-    th, ids = inp["target_hidden"], inp["ids"]
+                              max_ctx=max([wl.ctx] + sweep), max_seqs=n_seq)
+    if batched:
+        seq_inp = [synth.make_inputs_torch(cfg, wl.block, c, seed=args.seed + 1 + i, device="cuda")
+                   for i, c in enumerate(wl.seq_ctx)]
+        ths = [d["target_hidden"] for d in seq_inp]
+        ids = torch.cat([d["ids"] for d in seq_inp]).contiguous()
+        th = ths[0]
+        del seq_inp
+    else:
+        inp = synth.make_inputs_torch(cfg, wl.block, wl.ctx, seed=args.seed, device="cuda")
+        th, ids = inp["target_hidden"], inp["ids"]
+        ths = [th]
     setup_s = time.perf_counter() - t_setup
 
     L = model._L
     ctx = model._ctx
     stream = torch.cuda.current_stream()
     sh = stream.cuda_stream
-    out_ids = torch.empty((wl.block,), dtype=torch.int32, device="cuda")
+    out_ids = torch.empty((n_seq * wl.block,), dtype=torch.int32, device="cuda")
 
     # context ingest (fc fusion + per-layer K/V), timed as its own phase after one untimed
     # ingest (the first GEMM calls load the BLAS library's kernels)
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    def ingest_all():
+        for i, t in enumerate(ths):
+            _lib.check(L.dfl_select_seq(ctx, i), "dfl_select_seq")
+            _lib.check(L.dfl_cache_reset(ctx), "dfl_cache_reset")
+            _lib.check(L.dfl_ingest_context(ctx, t.data_ptr(), t.shape[0], sh),
+                       "dfl_ingest_context")
+        _lib.check(L.dfl_select_seq(ctx, 0), "dfl_select_seq")
+
     t_first = time.perf_counter()
-    model.make_cache(0, 0)
-    _lib.check(L.dfl_ingest_context(ctx, th.data_ptr(), wl.ctx, sh), "dfl_ingest_context")
+    ingest_all()
     torch.cuda.synchronize()
     first_ingest_s = time.perf_counter() - t_first
-    model.make_cache(0, 0)
     torch.cuda.synchronize()
     ev0.record(stream)
-    _lib.check(L.dfl_ingest_context(ctx, th.data_ptr(), wl.ctx, sh), "dfl_ingest_context")
+    ingest_all()
     ev1.record(stream)
     torch.cuda.synchronize()
     ingest_ms = ev0.elapsed_time(ev1)
 
     def step():
-        rc = L.dfl_draft_block(ctx, None, ids.data_ptr(), wl.block, None, None, None,
-                               out_ids.data_ptr(), sh)
+        if batched:
+            rc = L.dfl_draft_batch(ctx, n_seq, None, ids.data_ptr(), wl.block, None, None, None,
+                                   out_ids.data_ptr(), sh)
+        else:
+            rc = L.dfl_draft_block(ctx, None, ids.data_ptr(), wl.block, None, None, None,
+                                   out_ids.data_ptr(), sh)
         if rc:
-            _lib.check(rc, "dfl_draft_block")
+            _lib.check(rc, "dfl_draft_batch" if batched else "dfl_draft_block")
 
     for _ in range(args.warmup):
         step()
@@ -271,7 +295,7 @@ def main():
     if not args.no_profile:
         ms_events, _, gprof = timed(args.steps, True)
 
-    nbytes = algorithmic_bytes(cfg, wl.block, wl.ctx)
+    nbytes = algorithmic_bytes(cfg, wl.block, list(wl.seq_ctx) if batched else wl.ctx)
     lat_us = ms_per_step * 1e3
     gbs = nbytes["total"] / (ms_per_step * 1e-3) / 1e9
 
@@ -283,9 +307,18 @@ def main():
     roofline, kernels = None, None
     if gprof and gprof.get("gemm_w8a16", {}).get("launches"):
         per_launch, avg_s, ach = rate(gprof["gemm_w8a16"])
-        roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
-                    "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-                    "traffic": traffic_per_launch(wl.name),
+        # 2 * rows flop per int8 weight byte: above the MFMA/HBM ridge the projections are
+        # bounded by the matrix cores (stacked blocks), below it by HBM (one block)
+        rows = n_seq * wl.block
+        if 2.0 * rows > MFMA_F16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9):
+            tf = 2.0 * rows * per_launch / avg_s / 1e12   # scale bytes are negligible here
+            roofline = {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                        "unit": "TFLOP/s", "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                        "hbm_gbps": round(ach, 1)}
+        else:
+            roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4)}
+        roofline.update({"traffic": traffic_per_launch(wl.name),
                     "kernel": "gsk_gemm_kernel<int8,*> (stream-K W8A16 projections "
                               "qkv/o/gate_up/down, one launch each per layer)",
                     "bytes_per_launch": per_launch, "avg_launch_us": round(avg_s * 1e6, 3),
@@ -350,15 +383,18 @@ def main():
         except Exception as e:  # report, never lose the GPU line
             cpu = {"value": None, "error": f"{type(e).__name__}: {e}"}
 
+    metric = METRIC if wl.name == "dflash_27b" else \
+        f"draft-block latency (us) + achieved HBM GB/s, {wl.description}"
     out = {
-        "metric": METRIC, "value": round(lat_us, 2), "unit": "us", "n_gpus": 1,
+        "metric": metric, "value": round(lat_us, 2), "unit": "us", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
         "data": "synthetic (seeded random-init weights, N(0,1) target_hidden)",
         "config": {"workload": wl.name, "hidden": cfg.hidden_size, "layers": cfg.num_hidden_layers,
                    "heads": cfg.num_attention_heads, "kv_heads": cfg.num_key_value_heads,
                    "ffn": cfg.intermediate_size, "vocab": cfg.vocab_size, "block": wl.block,
-                   "ctx": wl.ctx, "weights": "W8A16 (int8 + fp16 per-row scale), fp16 lm_head"},
+                   "ctx": list(wl.seq_ctx) if batched else wl.ctx, "sequences": n_seq,
+                   "weights": "W8A16 (int8 + fp16 per-row scale), fp16 lm_head"},
         "hbm_gbps": round(gbs, 1),
         "algorithmic_bytes_per_block": nbytes["total"],
         "roofline": roofline,
