@@ -182,9 +182,8 @@ def main():
     args = ap.parse_args()
 
     if args.gpus != 1:
-        print(f"bench.py: this build runs on exactly one GPU; --gpus {args.gpus} is not "
-              f"supported (the multi-GPU sharding is described, not implemented)",
-              file=sys.stderr)
+        print(f"bench.py: runs on exactly one GPU; --gpus {args.gpus} is not supported (the "
+              f"multi-GPU sharding is designed, not implemented)", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
@@ -318,11 +317,13 @@ def main():
         else:
             roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
                         "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4)}
-        roofline.update({"traffic": traffic_per_launch(wl.name),
-                    "kernel": "gsk_gemm_kernel<int8,*> (stream-K W8A16 projections "
-                              "qkv/o/gate_up/down, one launch each per layer)",
-                    "bytes_per_launch": per_launch, "avg_launch_us": round(avg_s * 1e6, 3),
-                    "launches": gprof["gemm_w8a16"]["launches"]}
+        kname = ("gsk_gemm_m_kernel<int8,RESID> (stream-K W8A16 down projection of the stacked "
+                 "rows; qkv / o / gate_up run as library GEMMs)" if rows > 64 else
+                 "gsk_gemm_kernel<int8,*> (stream-K W8A16 projections qkv/o/gate_up/down, one "
+                 "launch each per layer)")
+        roofline.update({"traffic": traffic_per_launch(wl.name), "kernel": kname,
+                         "bytes_per_launch": per_launch, "avg_launch_us": round(avg_s * 1e6, 3),
+                         "launches": gprof["gemm_w8a16"]["launches"]})
         lm = gprof.get("lm_head_argmax", {})
         if lm.get("launches"):
             per_launch, avg_s, ach = rate(lm)

@@ -32,12 +32,16 @@ int fail(int code, const std::string& msg) {
 constexpr int ING_MAX = 4096;      // context rows per ingest pass (at most)
 constexpr int MAX_CHUNKS = 64;     // attention key splits
 constexpr int MT_MAX = 8;          // 32-row m-tiles per M-split GEMM launch
-constexpr int LM_BLAS_MIN_ROWS = 64;   // stacked rows from which the lm_head runs on rocBLAS
+// Stacked blocks of more than BLAS_MIN_ROWS rows (batched drafting) are compute-bound: their
+// qkv, o, gate|up and lm_head products run as rocBLAS GEMMs over exact fp16 weight copies.
+constexpr int BLAS_MIN_ROWS = 64;
 
-enum ProfCat { P_GEMM_W8 = 0, P_LM_HEAD, P_ATTN, P_QK_ROPE, P_ROWS, P_INGEST_FC, P_INGEST_KV, P_N };
+enum ProfCat {
+  P_GEMM_W8 = 0, P_LM_HEAD, P_ATTN, P_QK_ROPE, P_ROWS, P_INGEST_FC, P_INGEST_KV, P_GEMM_BLAS, P_N
+};
 const char* const kProfNames[P_N] = {"gemm_w8a16",   "lm_head_argmax", "attention",
                                      "qk_norm_rope", "row_reduce_norm", "ingest_fc",
-                                     "ingest_kv"};
+                                     "ingest_kv",    "gemm_blas_rows"};
 
 struct ProfRec {
   int cat;
@@ -91,6 +95,9 @@ struct Layer {
   half_t *in_norm = nullptr, *post_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
   half_t *Kc = nullptr, *Vt = nullptr;   // [max_seqs][NKV][cap][128], [max_seqs][NKV][128][cap]
   half_t* w_kv16 = nullptr;              // [2*NKV*128][H] fp16 copy of the k|v int8 rows
+  // stacked blocks: exact fp16 copies [q;k;v] [NQKV][H] (w_kv16 points into it), o [H][NQ],
+  // [gate;up] [2F][H]
+  half_t *w_qkv16 = nullptr, *w_o16 = nullptr, *w_gu16 = nullptr;
   bool loaded = false;
 };
 
@@ -113,10 +120,12 @@ struct dfl_ctx {
   bool fc_loaded = false;
   half_t* final_norm = nullptr;
   uint4* w_lm = nullptr;
-  // stacked blocks (more than LM_BLAS_MIN_ROWS rows): the lm_head as a library GEMM over a
+  // stacked blocks (more than BLAS_MIN_ROWS rows): the lm_head as a library GEMM over a
   // row-major fp16 copy, logits in lm32 [RM][V] fp32
   half_t* w_lm16 = nullptr;
   float* lm32 = nullptr;
+  float* y32 = nullptr;      // [RM][max(NQKV, H, 2F)] fp32 rows of the stacked-block GEMMs
+  half_t* h2 = nullptr;      // [RM][NH*128] attention output rows (row-major)
   const half_t* embed = nullptr;
   bool head_loaded = false;
   int active = 0;   // layers run per call (num_draft_layers)
@@ -353,6 +362,12 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
     delete x;
     return r;
   }
+  if (x->RM > BLAS_MIN_ROWS &&
+      ((r = x->alloc(&x->y32, (size_t)x->RM * std::max({x->NQKV, x->H, 2 * x->F}))) ||
+       (r = x->alloc(&x->h2, (size_t)x->RM * x->NH * 128)))) {
+    delete x;
+    return r;
+  }
   *out = x;
   return DFL_OK;
 }
@@ -400,7 +415,14 @@ int dfl_load_layer_w8(dfl_ctx* ctx, int layer, const int8_t* const q[7],
     DFL_TRY(ctx->alloc(&L.post_norm, (size_t)H));
     DFL_TRY(ctx->alloc(&L.q_norm, (size_t)128));
     DFL_TRY(ctx->alloc(&L.k_norm, (size_t)128));
-    DFL_TRY(ctx->alloc(&L.w_kv16, (size_t)2 * NKV * 128 * H));
+    if (ctx->RM > BLAS_MIN_ROWS) {
+      DFL_TRY(ctx->alloc(&L.w_qkv16, (size_t)ctx->NQKV * H));
+      DFL_TRY(ctx->alloc(&L.w_o16, (size_t)H * NQ));
+      DFL_TRY(ctx->alloc(&L.w_gu16, (size_t)2 * F * H));
+      L.w_kv16 = L.w_qkv16 + (size_t)NQ * H;
+    } else {
+      DFL_TRY(ctx->alloc(&L.w_kv16, (size_t)2 * NKV * 128 * H));
+    }
   }
   auto S = [&](int i) { return reinterpret_cast<const half_t*>(scale[i]); };
   // fused QKV: row-blocks [0, NH*4) = q_proj, then k_proj, then v_proj
@@ -412,9 +434,16 @@ int dfl_load_layer_w8(dfl_ctx* ctx, int layer, const int8_t* const q[7],
   launch_pack_i8(q[4], S(4), F, H, L.w_gu, L.s_gu, 0, 2, st);
   launch_pack_i8(q[5], S(5), F, H, L.w_gu, L.s_gu, 1, 2, st);
   launch_pack_i8(q[6], S(6), H, F, L.w_down, L.s_down, 0, 1, st);
-  // exact fp16 copies of the k and v rows for the context-ingest GEMM
+  // exact fp16 copies of the k and v rows for the context-ingest GEMM (and, for stacked
+  // blocks, of every matrix but down)
   launch_i8_to_f16(q[1], (size_t)NKV * 128 * H, L.w_kv16, st);
   launch_i8_to_f16(q[2], (size_t)NKV * 128 * H, L.w_kv16 + (size_t)NKV * 128 * H, st);
+  if (L.w_qkv16) {
+    launch_i8_to_f16(q[0], (size_t)NQ * H, L.w_qkv16, st);
+    launch_i8_to_f16(q[3], (size_t)H * NQ, L.w_o16, st);
+    launch_i8_to_f16(q[4], (size_t)F * H, L.w_gu16, st);
+    launch_i8_to_f16(q[5], (size_t)F * H, L.w_gu16 + (size_t)F * H, st);
+  }
   DFL_HIP(hipMemcpyAsync(L.in_norm, in_norm, H * 2, hipMemcpyDeviceToDevice, st));
   DFL_HIP(hipMemcpyAsync(L.post_norm, post_norm, H * 2, hipMemcpyDeviceToDevice, st));
   DFL_HIP(hipMemcpyAsync(L.q_norm, q_norm, 256, hipMemcpyDeviceToDevice, st));
@@ -453,7 +482,7 @@ int dfl_load_head(dfl_ctx* ctx, const uint16_t* final_norm, const uint16_t* embe
     if (!ctx->w_lm) DFL_TRY(ctx->alloc(&ctx->w_lm, (size_t)ctx->V * ctx->H / 8));
     launch_pack_f16(reinterpret_cast<const half_t*>(lm_head), ctx->V, ctx->H, ctx->w_lm, st);
     DFL_TRY(check_launch("pack lm_head"));
-    if (ctx->RM > LM_BLAS_MIN_ROWS) {
+    if (ctx->RM > BLAS_MIN_ROWS) {
       if (!ctx->w_lm16) {
         DFL_TRY(ctx->alloc(&ctx->w_lm16, (size_t)ctx->V * ctx->H));
         DFL_TRY(ctx->alloc(&ctx->lm32, (size_t)ctx->RM * ctx->V));
@@ -695,6 +724,7 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
   hipStream_t st = (hipStream_t)stream;
   const int H = ctx->H, NH = ctx->NH, NKV = ctx->NKV, F = ctx->F, NQ = NH * 128;
   const int M = n_seq * B;
+  const bool blas = M > BLAS_MIN_ROWS && ctx->layers[0].w_qkv16;   // stacked blocks
   const float eps = ctx->cfg.rms_eps;
   // x = embedding rows (residual stream); rnorm = 1/rms(x).  Every projection whose input
   // is an RMSNorm output applies the norm on its activation load.
@@ -728,15 +758,28 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
 
   for (int l = 0; l < ctx->active; ++l) {
     Layer& Ly = ctx->layers[l];
-    // q|k|v = input_layernorm(x) @ [Wq; Wk; Wv]^T  (fp16 out)
-    DFL_TRY(skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_STORE, ctx->sk_qkv, Ly.w_qkv, Ly.s_qkv, ctx->NQKV, H / 32,
-           ctx->x, H, M, Ly.in_norm, /*rn_from_ss=*/l > 0, ctx->qkvbuf, ctx->NQKV, nullptr,
-           nullptr, nullptr, st));
+    // q|k|v = input_layernorm(x) @ [Wq; Wk; Wv]^T  (fp16 out, or fp32 rows for stacked blocks)
+    if (blas) {
+      ProfScope ps(ctx, P_GEMM_BLAS, (long long)ctx->NQKV * H * 2, st);
+      launch_apply_norm(ctx->x, l > 0 ? ctx->sk_ss : nullptr, H / 64, eps, Ly.in_norm, M, H,
+                        ctx->h, st, l > 0 ? nullptr : ctx->rnorm);
+      DFL_TRY(blas_gemm(ctx, ctx->NQKV, M, H, Ly.w_qkv16, H, ctx->h, H, 0.f, ctx->y32, ctx->NQKV,
+                        st));
+    } else {
+      DFL_TRY(skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_STORE, ctx->sk_qkv, Ly.w_qkv, Ly.s_qkv, ctx->NQKV,
+                     H / 32, ctx->x, H, M, Ly.in_norm, /*rn_from_ss=*/l > 0, ctx->qkvbuf,
+                     ctx->NQKV, nullptr, nullptr, nullptr, st));
+    }
     // Q/K norm + RoPE and attention, up to SEQ_MAX sequences per launch
     for (int g0 = 0; g0 < n_seq; g0 += SEQ_MAX) {
       const int gn = std::min(SEQ_MAX, n_seq - g0);
       QKRopeArgs q{};
-      q.qkv16 = ctx->qkvbuf + (size_t)g0 * B * ctx->NQKV;
+      if (blas) {
+        q.qkv32 = ctx->y32 + (size_t)g0 * B * ctx->NQKV;
+        q.oscale = Ly.s_qkv;
+      } else {
+        q.qkv16 = ctx->qkvbuf + (size_t)g0 * B * ctx->NQKV;
+      }
       q.M = B;
       q.N = ctx->NQKV;
       q.n_seq = gn;
@@ -762,6 +805,7 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
       at.Op = ctx->Op;
       at.Ml = ctx->Ml;
       at.O = ctx->attn;
+      at.O_rows = blas ? ctx->h2 : nullptr;
       long long kv_bytes = 0, keys_total = 0;
       for (int i = 0; i < gn; ++i) {
         SeqState after = ctx->seqs[seq0 + g0 + i];
@@ -794,17 +838,28 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
       ProfScope ps(ctx, P_ATTN, kv_bytes, st);
       launch_block_attention(at, st);
     }
-    // x += attn @ Wo^T ; per-tile row sums of squares of x -> sk_ss
-    DFL_TRY(skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_RESID, ctx->sk_o, Ly.w_o, Ly.s_o, H, NQ / 32, ctx->attn,
-           NQ, M, nullptr, false, nullptr, H, ctx->x, nullptr, nullptr, st));
-    // act = silu(gate(post_norm(x))) * up(post_norm(x))
-    DFL_TRY(skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_SWIGLU, ctx->sk_gu, Ly.w_gu, Ly.s_gu, 2 * F, H / 32,
-           ctx->x, H, M, Ly.post_norm, true, ctx->act, F, nullptr, nullptr, nullptr, st));
+    if (blas) {
+      // the same two steps as library GEMMs with the epilogues in row kernels
+      ProfScope ps(ctx, P_GEMM_BLAS, ((long long)H * NQ + 2LL * F * H) * 2, st);
+      DFL_TRY(blas_gemm(ctx, H, M, NQ, Ly.w_o16, NQ, ctx->h2, NQ, 0.f, ctx->y32, H, st));
+      launch_resid_rows(ctx->y32, M, H, Ly.s_o, ctx->x, ctx->sk_ss, st);
+      launch_apply_norm(ctx->x, ctx->sk_ss, H / 64, eps, Ly.post_norm, M, H, ctx->h, st);
+      DFL_TRY(blas_gemm(ctx, 2 * F, M, H, Ly.w_gu16, H, ctx->h, H, 0.f, ctx->y32, 2 * F, st));
+      launch_swiglu_rows(ctx->y32, M, F, Ly.s_gu, ctx->act, st);
+    } else {
+      // x += attn @ Wo^T ; per-tile row sums of squares of x -> sk_ss
+      DFL_TRY(skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_RESID, ctx->sk_o, Ly.w_o, Ly.s_o, H, NQ / 32,
+                     ctx->attn, NQ, M, nullptr, false, nullptr, H, ctx->x, nullptr, nullptr, st));
+      // act = silu(gate(post_norm(x))) * up(post_norm(x))
+      DFL_TRY(skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_SWIGLU, ctx->sk_gu, Ly.w_gu, Ly.s_gu, 2 * F,
+                     H / 32, ctx->x, H, M, Ly.post_norm, true, ctx->act, F, nullptr, nullptr,
+                     nullptr, st));
+    }
     // x += act @ Wdown^T ; per-tile row sums of squares of x -> sk_ss
     DFL_TRY(skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_RESID, ctx->sk_down, Ly.w_down, Ly.s_down, H, F / 32,
            ctx->act, F, M, nullptr, false, nullptr, H, ctx->x, nullptr, nullptr, st));
   }
-  if ((out_logits || out_ids) && M > LM_BLAS_MIN_ROWS && ctx->w_lm16) {
+  if ((out_logits || out_ids) && M > BLAS_MIN_ROWS && ctx->w_lm16) {
     // stacked blocks: final norm into row-major rows, then the lm_head GEMM (fp32 logits)
     // and a row argmax
     ProfScope ps(ctx, P_LM_HEAD, (long long)ctx->V * H * 2, st);

@@ -96,7 +96,14 @@ void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* no
 // h = fp16(fp16(x * r[m]) * g[n])  (apply_norm), or a plain copy (afl_to_rows).  r[m] =
 // 1/rms of row m from ss [M/32 m-tiles][ss_tiles][32] (row sums of squares per column tile).
 void launch_apply_norm(const half_t* x, const float* ss, int ss_tiles, float eps, const half_t* g,
-                       int M, int N, half_t* h, hipStream_t st);
+                       int M, int N, half_t* h, hipStream_t st, const float* rnorm = nullptr);
+// Epilogues of the stacked-block library GEMMs (fp32 rows y), same arithmetic as the
+// stream-K RESID / SWIGLU epilogues: x += fp16(y * s) with sums of squares into ss
+// [M/32][N/64][32]; act = swiglu(y_gate * s, y_up * s) in the fragment layout.
+void launch_resid_rows(const float* y, int M, int N, const half_t* s, half_t* x, float* ss,
+                       hipStream_t st);
+void launch_swiglu_rows(const float* y, int M, int F, const half_t* s, half_t* act,
+                        hipStream_t st);
 void launch_afl_to_rows(const half_t* x, int M, int N, half_t* h, hipStream_t st);
 // Up to SEQ_MAX sequences (batched drafting) share one rope / attention launch.
 constexpr int SEQ_MAX = 8;
@@ -168,7 +175,8 @@ struct AttnArgs {
   float* Op;              // [max_chunks][n_seq*NH*B][128] unnormalised partial outputs
   float* Ml;              // [max_chunks][n_seq*NH*B][2] running (max, sum) in log2 domain
   half_t* O;              // output rows of an activation fragment layout tile set with
-                          // NH*128 columns
+                          // NH*128 columns, or (O_rows set) row-major [rows][NH*128]
+  half_t* O_rows;
   AttnSeq sq[SEQ_MAX];
 };
 void launch_block_attention(const AttnArgs& a, hipStream_t st);

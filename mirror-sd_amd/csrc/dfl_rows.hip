@@ -61,15 +61,20 @@ void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* no
                      V, g, eps, x, h, rnorm, err);
 }
 
-// x (activation fragment layout, [M][N]) -> row-major h; with ss/g set, h = RMSNorm(x) * g
-// where 1/rms of row m comes from ss [M/32][ss_tiles][32] (per-column-tile sums of squares).
+// x (activation fragment layout, [M][N]) -> row-major h; with g set, h = RMSNorm(x) * g
+// where 1/rms of row m is rnorm[m], or comes from ss [M/32][ss_tiles][32] (per-column-tile
+// sums of squares).
 __global__ __launch_bounds__(256) void afl_rows_kernel(const half_t* __restrict__ x,
                                                        const float* __restrict__ ss, int ss_tiles,
+                                                       const float* __restrict__ rnorm,
                                                        float eps, const half_t* __restrict__ g,
                                                        int N, half_t* __restrict__ h) {
   __shared__ float rr_s;
   const int m = blockIdx.y;
-  if (ss) {
+  if (rnorm) {
+    if (threadIdx.x == 0) rr_s = rnorm[m];
+    __syncthreads();
+  } else if (ss) {
     if (threadIdx.x < 64) {
       const float* sp = ss + (size_t)(m >> 5) * ss_tiles * 32 + (m & 31);
       float tot = 0.f;
@@ -84,7 +89,7 @@ __global__ __launch_bounds__(256) void afl_rows_kernel(const half_t* __restrict_
   // 4 consecutive columns (n % 4 == 0) are 4 consecutive halves of one record
   const half4_t xv = *reinterpret_cast<const half4_t*>(x + afl_index(m, n, N));
   half4_t o = xv;
-  if (ss) {
+  if (g) {
     const float rr = rr_s;
 #pragma unroll
     for (int j = 0; j < 4; ++j) o[j] = rms_out(h2f(xv[j]), rr, g[n + j]);
@@ -93,9 +98,62 @@ __global__ __launch_bounds__(256) void afl_rows_kernel(const half_t* __restrict_
 }
 
 void launch_apply_norm(const half_t* x, const float* ss, int ss_tiles, float eps, const half_t* g,
-                       int M, int N, half_t* h, hipStream_t st) {
+                       int M, int N, half_t* h, hipStream_t st, const float* rnorm) {
   hipLaunchKernelGGL(afl_rows_kernel, dim3((N / 4 + 255) / 256, M), dim3(256), 0, st, x, ss,
-                     ss_tiles, eps, g, N, h);
+                     ss_tiles, rnorm, eps, g, N, h);
+}
+
+// RESID epilogue for fp32 library-GEMM rows y [M][N] (stacked blocks): x += fp16(y * s) in
+// place on the fragment-layout residual, with the per-(m-tile, 64-column tile) row sums of
+// squares of the new x in ss [M/32][N/64][32] -- the stream-K RESID epilogue's arithmetic.
+// One wave per (row, column tile), lane = column.
+__global__ __launch_bounds__(256) void resid_rows_kernel(const float* __restrict__ y, int M, int N,
+                                                         const half_t* __restrict__ s,
+                                                         half_t* __restrict__ x,
+                                                         float* __restrict__ ss) {
+  const int lane = threadIdx.x & 63;
+  const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int tiles = N / 64;
+  if (w >= M * tiles) return;
+  const int m = w / tiles, t = w - m * tiles;
+  const int n = t * 64 + lane;
+  const float yv = h2f(f2h(y[(size_t)m * N + n] * h2f(s[n])));
+  half_t* xp = x + afl_index(m, n, N);
+  const half_t xn = f2h(h2f(*xp) + yv);
+  *xp = xn;
+  const float tot = wave_sum(h2f(xn) * h2f(xn));
+  if (lane == 0) ss[((size_t)(m >> 5) * tiles + t) * 32 + (m & 31)] = tot;
+}
+
+void launch_resid_rows(const float* y, int M, int N, const half_t* s, half_t* x, float* ss,
+                       hipStream_t st) {
+  const int waves = M * (N / 64);
+  hipLaunchKernelGGL(resid_rows_kernel, dim3((waves + 3) / 4), dim3(256), 0, st, y, M, N, s, x, ss);
+}
+
+// SWIGLU epilogue for fp32 library-GEMM rows y [M][2F] (gate rows 0..F-1, then up rows):
+// act[m][f] = fp16(fp16(silu(g)) * u) with g = fp16(y_gate * s_gate), u = fp16(y_up * s_up),
+// the stream-K SWIGLU epilogue's rounding; scales in the packed gate|up order (gate row f at
+// 64*(f/32) + f%32, up row f 32 further).  act in the fragment layout [M][F].
+__global__ __launch_bounds__(256) void swiglu_rows_kernel(const float* __restrict__ y, int M, int F,
+                                                          const half_t* __restrict__ s,
+                                                          half_t* __restrict__ act) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)M * F) return;
+  const int m = (int)(i / F), f = (int)(i - (size_t)m * F);
+  const int si = 64 * (f >> 5) + (f & 31);
+  const float gv = h2f(f2h(y[(size_t)m * 2 * F + f] * h2f(s[si])));
+  const float uv = h2f(f2h(y[(size_t)m * 2 * F + F + f] * h2f(s[si + 32])));
+  const float sig = h2f(f2h(1.0f / (1.0f + expf(-gv))));
+  const float sil = h2f(f2h(gv * sig));
+  act[afl_index(m, f, F)] = f2h(sil * uv);
+}
+
+void launch_swiglu_rows(const float* y, int M, int F, const half_t* s, half_t* act,
+                        hipStream_t st) {
+  const size_t n = (size_t)M * F;
+  hipLaunchKernelGGL(swiglu_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, y, M,
+                     F, s, act);
 }
 
 // Row-major concatenation [rows][nf * H] of the feature tensors (the materialised
@@ -154,7 +212,7 @@ void launch_fc_norm_rows(const float* fc32, int rows, int H, const half_t* g, fl
 
 void launch_afl_to_rows(const half_t* x, int M, int N, half_t* h, hipStream_t st) {
   hipLaunchKernelGGL(afl_rows_kernel, dim3((N / 4 + 255) / 256, M), dim3(256), 0, st, x, nullptr,
-                     0, 0.f, nullptr, N, h);
+                     0, nullptr, 0.f, nullptr, N, h);
 }
 
 

@@ -122,3 +122,15 @@ def test_workload_shapes():
     assert workload("dflash_27b_ctx32768").ctx == 32768
     w = workload("qwen3_4b_layer")
     assert (w.cfg.hidden_size, w.cfg.intermediate_size, w.cfg.num_hidden_layers) == (2560, 9728, 1)
+
+
+def test_bench_compiles_and_refuses_several_gpus():
+    """bench.py parses (a subprocess compiles the whole file) and exits with a message for
+    --gpus N > 1 (one GPU per box) before touching a GPU."""
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2, r.stderr
+    assert "one GPU" in r.stderr
