@@ -29,6 +29,10 @@ GROUPS = [
     ("o / down (RESID)", r"gsk_gemm_kernel<0, 4, false, 4>"),
     ("gate|up (SWIGLU, norm-on-load)", r"gsk_gemm_kernel<0, 1, true, 4>"),
     ("lm_head (fp16, ARGMAX, norm-on-load)", r"gsk_gemm_kernel<1, 2, true, 4>"),
+    ("down, stacked rows (M-split RESID)", r"gsk_gemm_m_kernel<0, 4, false"),
+    ("stacked-row GEMMs (rocBLAS: qkv, o, gate|up, lm_head, ingest)", r"Cijk_"),
+    ("stacked-row epilogues (norm rows, RESID, SWIGLU)", r"afl_rows_kernel|resid_rows_kernel|swiglu_rows_kernel"),
+    ("row argmax (stacked lm_head)", r"row_argmax_kernel"),
     ("block attention", r"block_attn_kernel"),
     ("attention merge", r"attn_merge_kernel"),
     ("qk norm + rope", r"qk_rope_kernel"),
@@ -66,12 +70,15 @@ def main(argv=None):
     ap.add_argument("--copy-mib", type=int, default=1024)
     ap.add_argument("--workload", required=True)
     ap.add_argument("--commands", default="", help="text of the commands that made the inputs")
+    ap.add_argument("--note", default="", help="a line describing the run")
     ap.add_argument("--md", required=True)
     ap.add_argument("--json")
     a = ap.parse_args(argv)
 
     stats = read_stats(a.stats)
     out = [f"# rocprofv3 summary: {a.workload} draft block", ""]
+    if a.note:
+        out += [a.note, ""]
     if a.commands:
         out += ["Commands:", "", "```", a.commands.strip(), "```", ""]
     out += ["## Kernel durations (--kernel-trace --stats)", "",
