@@ -12,10 +12,11 @@
 //
 // Workgroup = 4 streaming waves + 1 reducer wave.  The streaming waves split each
 // segment's k-blocks, write their fp32 partial to an LDS slot (two slot sets, used by
-// alternate segments) and go straight on to the next segment.  The reducer wave loads
-// the RMSNorm gain and 1/rms rows at the start, then for each segment in turn sums the 4
-// partials in a fixed order and completes the tile, so the cross-workgroup fix-up and the
-// epilogue overlap the next segment's weight stream instead of stalling it.
+// alternate segments) and go straight on to the next segment.  The reducer wave stages
+// the RMSNorm gain and 1/rms rows in LDS at the start (its copies are issued before any
+// weight load), then for each segment in turn sums the 4 partials in a fixed order and
+// completes the tile, so the cross-workgroup fix-up and the epilogue overlap the next
+// segment's weight stream instead of stalling it.
 //
 // Completion.  A segment covering a whole tile runs the epilogue directly.  A tile split
 // across workgroups is finished by whichever arrives last: each stores its fp32 partial
@@ -92,6 +93,57 @@ DFL_DEV void store_agent(float* p, float v) {
 }
 DFL_DEV float load_agent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Norm prologue hand-off through the LDS word `ready`: the reducer wave issues the
+// prologue's loads and sets it to PRO_ISSUED, then stores the gain and 1/rms to LDS and
+// sets PRO_DONE.  The streaming waves of a NORM kernel issue no weight load before
+// PRO_ISSUED: a CU serves its vector memory requests in order, so prologue loads queued
+// behind the streaming waves' 64-128 KiB of weight loads would wait several microseconds.
+constexpr int PRO_ISSUED = 1, PRO_DONE = 2;
+DFL_DEV void mark_issued(int* ready) {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+  __hip_atomic_store(ready, PRO_ISSUED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+DFL_DEV void wait_ready(int* ready, int state) {
+  while (__hip_atomic_load(ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < state)
+    __builtin_amdgcn_s_sleep(1);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Norm prologue copies, global -> LDS with global_load_lds (16 B per lane, 1 KiB per
+// wave instruction, `bytes` a multiple of 16): the loads write LDS directly, so none of
+// them waits for another and no VGPR holds the data; the copy costs one memory latency
+// and a few instructions.  The caller waits with s_waitcnt vmcnt before reading.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+DFL_DEV void copy_to_lds(const void* src, void* lds_dst, int bytes, int lane) {
+  for (int off = 0; off < bytes; off += 1024) {
+    const int o = off + lane * 16;
+    if (o < bytes)
+      __builtin_amdgcn_global_load_lds(static_cast<const char*>(src) + o,
+                                       (lds_ptr_t)(static_cast<char*>(lds_dst) + off), 16, 0, 0);
+  }
+}
+
+// 1/rms of activation row m (lane & 31) from the per-tile sums of squares of the RESID
+// epilogue that produced X (global memory or an LDS copy): lane (m, g) adds tiles g, g+2,
+// ... with eight loads in flight.
+DFL_DEV float rn_from_ss(const float* ss, int tiles, int n, float eps, int lane) {
+  const int m = lane & 31, g = lane >> 5;
+  const float* sp = ss + m;
+  float tot = 0.f;
+  int tt = g;
+  for (; tt + 14 < tiles; tt += 16) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = sp[(size_t)(tt + 2 * j) * 32];
+    tot += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+  }
+  for (; tt < tiles; tt += 2) tot += sp[(size_t)tt * 32];
+  tot += __shfl_xor(tot, 32, 64);
+  return 1.0f / sqrtf(tot / (float)n + eps);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -205,15 +257,17 @@ DFL_DEV void stream_range(const StreamArgs& a, const half_t* gsh, const float* r
     };
 
     Stage A, B;
-    issue(A);
     if constexpr (NORM) {
-      // gain and 1/rms come from the reducer wave's prologue
-      while (__hip_atomic_load(ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
-        __builtin_amdgcn_s_sleep(1);
+      wait_ready(ready, PRO_ISSUED);
+      issue(A);
+      issue(B);   // both stages in flight while the reducer's prologue completes
+      wait_ready(ready, PRO_DONE);   // gain and 1/rms from the reducer wave's prologue
       rn = rn_lds[m];
+    } else {
+      issue(A);
     }
     for (int base = 0; base < J; base += 2 * P) {
-      issue(B);
+      if (!NORM || base > 0) issue(B);
       __builtin_amdgcn_sched_barrier(0);
       consume(A, base);
       if (base + P >= J) break;
@@ -367,24 +421,6 @@ DFL_DEV void tile_epilogue(const StreamArgs& a, int lane, int t, const floatx16&
   }
 }
 
-// 1/rms of activation row m (lane & 31) from the per-tile sums of squares of the RESID
-// epilogue that produced X: lane (m, g) adds tiles g, g+2, ... with eight loads in flight.
-DFL_DEV float rn_from_ss(const float* ss, int tiles, int n, float eps, int lane) {
-  const int m = lane & 31, g = lane >> 5;
-  const float* sp = ss + m;
-  float tot = 0.f;
-  int tt = g;
-  for (; tt + 14 < tiles; tt += 16) {
-    float v[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = sp[(size_t)(tt + 2 * j) * 32];
-    tot += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-  }
-  for (; tt < tiles; tt += 2) tot += sp[(size_t)tt * 32];
-  tot += __shfl_xor(tot, 32, 64);
-  return 1.0f / sqrtf(tot / (float)n + eps);
-}
-
 // ---------------------------------------------------------------------------------------
 // M-split mode (2 <= MT <= 8 activation m-tiles): streaming wave w owns m-tiles
 // w*MTW .. w*MTW + MTW - 1 and walks every unit of the workgroup range in order, so each
@@ -512,15 +548,18 @@ DFL_DEV void stream_range_m(const StreamArgs& a, const half_t* gsh, const float*
   };
 
   Stage A, B;
-  issue(A);
   if constexpr (NORM) {
-    while (__hip_atomic_load(ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == 0)
-      __builtin_amdgcn_s_sleep(1);
+    wait_ready(ready, PRO_ISSUED);
+    issue(A);
+    issue(B);   // both stages in flight while the reducer's prologue completes
+    wait_ready(ready, PRO_DONE);
 #pragma unroll
     for (int j = 0; j < MTW; ++j) rn[j] = rn_lds[(mt0 + min(j, nmt - 1)) * 32 + m];
+  } else {
+    issue(A);
   }
   for (int base = 0; base < J; base += 2 * P) {
-    issue(B);
+    if (!NORM || base > 0) issue(B);
     __builtin_amdgcn_sched_barrier(0);
     consume(A, base);
     if (base + P >= J) break;
@@ -551,12 +590,13 @@ DFL_DEV StreamArgs mtile_view(const StreamArgs& a, int mt) {
 // ---------------------------------------------------------------------------------------
 template <int WT, int EPI, bool NORM, int P>
 __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_gemm_kernel(StreamArgs a) {
-  constexpr int KBK = KTraits<WT>::KBK;
   __shared__ float red[2][WG_WAVES][2048];     // partial slots, two sets
   __shared__ half_t gsh[NORM ? 8192 : 8];
+  __shared__ float ss_s[NORM ? 128 * 32 : 1];  // LDS copy of ss_in (<= 128 tiles)
   __shared__ float rn_s[32];
   // arrived[p]: partials written for segments of parity p (monotonic: a set is rewritten
-  // only after its previous segment was reduced); reduced: segments summed so far
+  // only after its previous segment was reduced); reduced: segments summed so far;
+  // ready: norm prologue state (PRO_ISSUED, PRO_DONE)
   __shared__ int arrived[2], reduced, ready;
 
   const int lane = threadIdx.x & 63;
@@ -580,14 +620,17 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_gemm_kernel(StreamArg
 
   // ---- reducer wave ----
   if constexpr (NORM) {
-    const int K = a.KB * KBK;
-    for (int k = lane * 8; k < K; k += 64 * 8)
-      *reinterpret_cast<u32x4*>(gsh + k) = *reinterpret_cast<const u32x4*>(a.gnorm + k);
-    const float rn = a.ss_in ? rn_from_ss(a.ss_in, a.ss_tiles, a.ss_n, a.eps, lane)
-                             : a.rnorm[lane & 31];
+    const int K = a.KB * KTraits<WT>::KBK;
+    copy_to_lds(a.gnorm, gsh, K * 2, lane);
+    float rn = 1.0f;
+    if (a.ss_in) copy_to_lds(a.ss_in, ss_s, a.ss_tiles * 32 * 4, lane);
+    else rn = a.rnorm[lane & 31];
+    if (lane == 0) mark_issued(&ready);
+    __builtin_amdgcn_s_waitcnt(0);   // both copies have landed in LDS
+    if (a.ss_in) rn = rn_from_ss(ss_s, a.ss_tiles, a.ss_n, a.eps, lane);
     if (lane < 32) rn_s[lane] = rn;
     __builtin_amdgcn_s_waitcnt(0);
-    if (lane == 0) __hip_atomic_store(&ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (lane == 0) __hip_atomic_store(&ready, PRO_DONE, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
   int si = 0;
   for (long long u = u0; u < u1; ++si) {
@@ -656,8 +699,8 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_gemm_m_kernel(StreamA
   // ---- reducer wave ----
   if constexpr (NORM) {
     const int K = a.KB * KBK;
-    for (int k = lane * 8; k < K; k += 64 * 8)
-      *reinterpret_cast<u32x4*>(gsh + k) = *reinterpret_cast<const u32x4*>(a.gnorm + k);
+    copy_to_lds(a.gnorm, gsh, K * 2, lane);
+    if (lane == 0) mark_issued(&ready);
     for (int mt = 0; mt < a.MT; ++mt) {
       const float rn = a.ss_in ? rn_from_ss(a.ss_in + (size_t)mt * a.ss_mstride, a.ss_tiles,
                                             a.ss_n, a.eps, lane)
@@ -665,7 +708,7 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_gemm_m_kernel(StreamA
       if (lane < 32) rn_s[mt * 32 + lane] = rn;
     }
     __builtin_amdgcn_s_waitcnt(0);
-    if (lane == 0) __hip_atomic_store(&ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (lane == 0) __hip_atomic_store(&ready, PRO_DONE, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
   int si = 0;
   for (long long u = u0; u < u1; ++si) {
