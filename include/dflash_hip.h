@@ -190,7 +190,8 @@ int dfl_embed_block(dfl_ctx* ctx, const int32_t* ids, int32_t B, const void* cor
                     void* stream);
 
 /* Sticky device-side error flags (bit 0: a token id outside [0, vocab); bit 1: soft-anchor
- * logits without a single number); reading clears. */
+ * logits without a single number; bit 2: a work-queue wait of the lm_head gave up, its
+ * results are invalid); reading clears. */
 int dfl_device_errors(dfl_ctx* ctx, int32_t* flags, void* stream);
 
 #ifdef __cplusplus

@@ -140,6 +140,7 @@ struct dfl_ctx {
   float* rnorm = nullptr;        // [RM] 1/rms of the residual rows
   float* sk_ws = nullptr;        // split-tile partials
   int* sk_tile_cnt = nullptr;    // [max tiles]
+  int* dyn_next = nullptr;       // [2] work counters of the balanced lm_head (self-resetting)
   float* sk_ss = nullptr;        // [m-tiles][H/64][32] row sums of squares of x (RESID output)
   SKPlan sk_qkv, sk_o, sk_gu, sk_down, sk_lm;
   // context ingest: `ing` rows per pass; the (compute-bound) GEMMs run on rocBLAS
@@ -333,7 +334,7 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
     x->sk_o = plan(x->H, x->NH * 128 / 32);
     x->sk_gu = plan(2 * x->F, x->H / 32);
     x->sk_down = plan(x->H, x->F / 32);
-    x->sk_lm = plan(std::max(x->V, 64), x->H / 16);
+    x->sk_lm = streamk_plan_balanced(std::max(x->V, 64), x->H / 16, x->n_cu);
     size_t wsn = 0, tiles = 0;
     for (auto pr : {std::make_pair(x->sk_qkv, x->NQKV), std::make_pair(x->sk_o, x->H),
                     std::make_pair(x->sk_gu, 2 * x->F), std::make_pair(x->sk_down, x->H),
@@ -346,6 +347,7 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
     wsn *= (size_t)std::min<size_t>(MT_MAX, bm32 / 32);
     if ((r = x->alloc(&x->qkvbuf, Bm * x->NQKV)) || (r = x->alloc(&x->rnorm, bm32)) ||
         (r = x->alloc(&x->sk_ws, wsn)) || (r = x->alloc(&x->sk_tile_cnt, tiles, true)) ||
+        (r = x->alloc(&x->dyn_next, 2, true)) ||
         (r = x->alloc(&x->sk_ss, (bm32 / 32) * (size_t)(x->H / 64) * 32))) {
       delete x;
       return r;
@@ -538,6 +540,9 @@ static int skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const SKPlan& p,
     a.logits = logits ? logits + (size_t)m0 * N : nullptr;
     a.ldl = N;
     a.keys = keys ? keys + m0 : nullptr;
+    a.dyn_static = p.dyn_static;
+    a.dyn_next = ctx->dyn_next;
+    a.err = ctx->err;
     const bool ok =
         mt_n == 1 ? launch_streamk_gemm(wt, epi, gnorm != nullptr, a, p, st, ps.start(), ps.stop())
                   : launch_streamk_gemm_m(wt, epi, gnorm != nullptr, a, p, st, ps.start(), ps.stop());

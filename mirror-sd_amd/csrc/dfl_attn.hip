@@ -267,11 +267,19 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(AttnArgs a) {
     for (int o = 32; o > 0; o >>= 1) dl += __shfl_xor(dl, o, 64);
     if (d == 0) den_s = dl;
   }
-  __syncthreads();
-  float num = 0.f;
+  // every chunk's load is issued before the first product (nc <= MAX_CHUNKS = 64), in
+  // groups of 32 so that one group costs a single memory latency
   const float* op = a.Op + (size_t)rowg * 128 + d;
-#pragma unroll 8
-  for (int c = 0; c < nc; ++c) num += op[(size_t)c * NB * 128] * wts[c];
+  float num = 0.f;
+  for (int c0 = 0; c0 < nc; c0 += 32) {
+    float v[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) v[j] = c0 + j < nc ? op[(size_t)(c0 + j) * NB * 128] : 0.f;
+    if (c0 == 0) __syncthreads();   // wts complete
+#pragma unroll
+    for (int j = 0; j < 32; ++j)
+      if (c0 + j < nc) num += v[j] * wts[c0 + j];
+  }
   const int hb = rowg - sidx * per_seq;
   const int h = hb / a.B, b = hb - h * a.B;
   const int orow = a.sq[sidx].o_row0 + b;

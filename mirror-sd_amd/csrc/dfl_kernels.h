@@ -35,12 +35,24 @@ struct StreamArgs {
   float* logits;            // ARGMAX: optional [M][ldl] fp32
   int ldl;
   unsigned long long* keys; // ARGMAX: optional [M] packed (order(value) << 32 | ~index)
+  // balanced mode (SKPlan::dyn_static > 0): workgroup b first takes the whole tiles
+  // [b * dyn_static, (b + 1) * dyn_static), then half tiles of the remaining tiles from the
+  // work counter dyn_next[0]; dyn_next[1] counts finished workgroups (both zero between
+  // launches: the last workgroup resets them)
+  int dyn_static;
+  int* dyn_next;
+  int* err;                 // device error word (bit 2: a work-queue wait gave up)
 };
 struct SKPlan {
   int workers = 1;          // workgroups (one per CU)
   int seg_cap = 1;          // workspace slots per tile
+  int dyn_static = 0;       // > 0: balanced mode with this many whole tiles per workgroup
 };
 SKPlan streamk_plan(int N, int KB, int n_cu);
+// Balanced plan for a long matrix (the lm_head): most tiles statically, whole, and the
+// rest in half tiles handed out at run time, so that CUs that stream faster take more.
+// Falls back to streamk_plan when the matrix has fewer than 2 tiles per CU.
+SKPlan streamk_plan_balanced(int N, int KB, int n_cu);
 // M-split variant for 2 <= MT <= 8 m-tiles (M <= 256 rows): every weight block is read
 // once for all m-tiles.  X, out, x, ss_*, rnorm, logits, keys point at m-tile 0; m-tile mt
 // is 32*mt rows further (ss blocks ss_mstride floats further).  ws holds

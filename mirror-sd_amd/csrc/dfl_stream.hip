@@ -159,7 +159,7 @@ DFL_DEV float rn_from_ss(const float* ss, int tiles, int n, float eps, int lane)
 template <int WT, bool NORM, int P>
 DFL_DEV void stream_range(const StreamArgs& a, const half_t* gsh, const float* rn_lds,
                           int* ready, float (*red)[WG_WAVES][2048], int* arrived, int* reduced,
-                          long long u0, long long u1, int w, int lane) {
+                          long long u0, long long u1, int w, int lane, int& si) {
   constexpr int KBK = KTraits<WT>::KBK;
   constexpr int NX = KTraits<WT>::NX;
   const int m = lane & 31, g = lane >> 5;
@@ -170,7 +170,7 @@ DFL_DEV void stream_range(const StreamArgs& a, const half_t* gsh, const float* r
   const u32x4* xf = reinterpret_cast<const u32x4*>(a.X);
 
   floatx16 acc0 = (floatx16){}, acc1 = (floatx16){};
-  int si = 0;   // segments flushed so far
+  // si: segments flushed so far by this wave (continues across calls)
   auto flush = [&]() {
     // slot set si & 1 was last used by segment si - 2: wait until it has been reduced
     while (__hip_atomic_load(reduced, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < si - 1)
@@ -421,6 +421,49 @@ DFL_DEV void tile_epilogue(const StreamArgs& a, int lane, int t, const floatx16&
   }
 }
 
+// Norm prologue of the reducer wave: the gain and ss_in are copied to LDS (issued before
+// any streaming wave's weight load), then 1/rms of each activation row goes to rn_s.
+template <int WT>
+DFL_DEV void reducer_norm_prologue(const StreamArgs& a, int lane, half_t* gsh, float* ss_s,
+                                   float* rn_s, int* ready) {
+  const int K = a.KB * KTraits<WT>::KBK;
+  copy_to_lds(a.gnorm, gsh, K * 2, lane);
+  float rn = 1.0f;
+  if (a.ss_in) copy_to_lds(a.ss_in, ss_s, a.ss_tiles * 32 * 4, lane);
+  else rn = a.rnorm[lane & 31];
+  if (lane == 0) mark_issued(ready);
+  __builtin_amdgcn_s_waitcnt(0);   // both copies have landed in LDS
+  if (a.ss_in) rn = rn_from_ss(ss_s, a.ss_tiles, a.ss_n, a.eps, lane);
+  if (lane < 32) rn_s[lane] = rn;
+  __builtin_amdgcn_s_waitcnt(0);
+  if (lane == 0) __hip_atomic_store(ready, PRO_DONE, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Reducer wave, segment si (tile t): waits for the 4 streaming waves' partials, sums them
+// in a fixed order, hands the slot set back and completes the tile -- directly when the
+// segment covers it (count == 1), else as worker `slot` of the `count` sharing it.
+template <int EPI>
+DFL_DEV void reduce_segment(const StreamArgs& a, int lane, float (*red)[WG_WAVES][2048],
+                            int* arrived, int* reduced, int si, int t, int slot, int count) {
+  while (__hip_atomic_load(&arrived[si & 1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
+         WG_WAVES * ((si >> 1) + 1))
+    __builtin_amdgcn_s_sleep(1);
+  floatx16 acc0 = (floatx16){}, acc1 = (floatx16){};
+#pragma unroll 1
+  for (int j = 0; j < WG_WAVES; ++j) {
+    const float* src = red[si & 1][j];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      acc0[r] += src[r * 64 + lane];
+      acc1[r] += src[1024 + r * 64 + lane];
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);   // slot reads done before the set is handed back
+  if (lane == 0) __hip_atomic_store(reduced, si + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  const bool complete = count == 1 || finish_split_tile(a, lane, t, slot, count, acc0, acc1);
+  if (complete) tile_epilogue<EPI>(a, lane, t, acc0, acc1);
+}
+
 // ---------------------------------------------------------------------------------------
 // M-split mode (2 <= MT <= 8 activation m-tiles): streaming wave w owns m-tiles
 // w*MTW .. w*MTW + MTW - 1 and walks every unit of the workgroup range in order, so each
@@ -614,53 +657,134 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_gemm_kernel(StreamArg
   __syncthreads();
 
   if (w < WG_WAVES) {
-    stream_range<WT, NORM, P>(a, gsh, rn_s, &ready, red, arrived, &reduced, u0, u1, w, lane);
+    int si = 0;
+    stream_range<WT, NORM, P>(a, gsh, rn_s, &ready, red, arrived, &reduced, u0, u1, w, lane, si);
     return;
   }
 
   // ---- reducer wave ----
-  if constexpr (NORM) {
-    const int K = a.KB * KTraits<WT>::KBK;
-    copy_to_lds(a.gnorm, gsh, K * 2, lane);
-    float rn = 1.0f;
-    if (a.ss_in) copy_to_lds(a.ss_in, ss_s, a.ss_tiles * 32 * 4, lane);
-    else rn = a.rnorm[lane & 31];
-    if (lane == 0) mark_issued(&ready);
-    __builtin_amdgcn_s_waitcnt(0);   // both copies have landed in LDS
-    if (a.ss_in) rn = rn_from_ss(ss_s, a.ss_tiles, a.ss_n, a.eps, lane);
-    if (lane < 32) rn_s[lane] = rn;
-    __builtin_amdgcn_s_waitcnt(0);
-    if (lane == 0) __hip_atomic_store(&ready, PRO_DONE, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-  }
+  if constexpr (NORM) reducer_norm_prologue<WT>(a, lane, gsh, ss_s, rn_s, &ready);
   int si = 0;
   for (long long u = u0; u < u1; ++si) {
     const int t = (int)(u / a.KB);
     const int kbs = (int)(u - (long long)t * a.KB);
     const int kbe = (int)min((long long)a.KB, (long long)kbs + (u1 - u));
-    while (__hip_atomic_load(&arrived[si & 1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
-           WG_WAVES * ((si >> 1) + 1))
-      __builtin_amdgcn_s_sleep(1);
-    floatx16 acc0 = (floatx16){}, acc1 = (floatx16){};
-#pragma unroll 1
-    for (int j = 0; j < WG_WAVES; ++j) {
-      const float* src = red[si & 1][j];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        acc0[r] += src[r * 64 + lane];
-        acc1[r] += src[1024 + r * 64 + lane];
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(0);   // slot reads done before the set is handed back
-    if (lane == 0) __hip_atomic_store(&reduced, si + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-    bool complete = (kbs == 0 && kbe == a.KB);
-    if (!complete) {
+    int first = b, count = 1;
+    if (!(kbs == 0 && kbe == a.KB)) {
       const long long tu0 = (long long)t * a.KB;
-      const int first = worker_of(tu0, U, G);
-      const int count = worker_of(tu0 + a.KB - 1, U, G) - first + 1;
-      complete = finish_split_tile(a, lane, t, b - first, count, acc0, acc1);
+      first = worker_of(tu0, U, G);
+      count = worker_of(tu0 + a.KB - 1, U, G) - first + 1;
     }
-    if (complete) tile_epilogue<EPI>(a, lane, t, acc0, acc1);
+    reduce_segment<EPI>(a, lane, red, arrived, &reduced, si, t, b - first, count);
     u += kbe - kbs;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Balanced stream-K kernel (long matrices: the lm_head).  Streaming waves, reducer and
+// completion as in gsk_gemm_kernel, but the work is not cut into equal ranges: workgroup
+// b first streams the whole tiles [b*S, (b+1)*S) (S = dyn_static; no split, no fix-up),
+// then half tiles of tiles [G*S, N/64) taken from a device-wide counter, so CUs that get
+// more bandwidth (the XCDs differ) take more of them.  Half tile c is tile G*S + c/2,
+// k-blocks [(c&1)*KB/2, (c&1+1)*KB/2); its two halves complete through the split-tile
+// protocol as slots 0 and 1 (summed in slot order: results do not depend on which
+// workgroup took which half).
+//
+// Queue: the reducer wave takes the next chunk id before it waits for the partials of
+// the segment in flight and publishes it in an LDS ring of 4 (entry k in q_chunk[k & 3],
+// q_pub = entries published, -1 = no more), so the streaming waves find entry k + 1 there
+// when they finish chunk k.  The reducer publishes entry k + 2 only after reducing chunk
+// k, which every streaming wave has flushed, so a slot is never overwritten before all
+// have read it.  Each workgroup takes chunk ids until one is past the end, so the counter
+// has stopped moving once every workgroup has bumped dyn_next[1]; the last one resets
+// both counters to zero for the next launch.
+// ---------------------------------------------------------------------------------------
+constexpr int DYN_SPIN_LIMIT = 1 << 24;   // s_sleep rounds before a queue wait gives up
+constexpr int DYN_ERR = 4;                // device error bit: a queue wait gave up
+
+template <int WT, int EPI, bool NORM, int P>
+__global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_dyn_kernel(StreamArgs a) {
+  __shared__ float red[2][WG_WAVES][2048];
+  __shared__ half_t gsh[NORM ? 8192 : 8];
+  __shared__ float ss_s[NORM ? 128 * 32 : 1];
+  __shared__ float rn_s[32];
+  __shared__ int arrived[2], reduced, ready;
+  __shared__ int q_chunk[4], q_pub;
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int G = gridDim.x, b = blockIdx.x;
+  const int KB = a.KB, S = a.dyn_static, half = KB >> 1;
+  const int T0 = G * S;                          // first tile handed out at run time
+  const int n_chunks = 2 * ((a.N >> 6) - T0);
+  if (threadIdx.x == 0) {
+    arrived[0] = arrived[1] = 0;
+    reduced = 0;
+    ready = 0;
+    q_pub = 0;
+  }
+  __syncthreads();
+
+  if (w < WG_WAVES) {
+    int si = 0;
+    if (S > 0)
+      stream_range<WT, NORM, P>(a, gsh, rn_s, &ready, red, arrived, &reduced,
+                                (long long)b * S * KB, (long long)(b + 1) * S * KB, w, lane, si);
+    for (int k = 0;; ++k) {
+      int spins = 0;
+      while (__hip_atomic_load(&q_pub, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <= k) {
+        if (++spins > DYN_SPIN_LIMIT) {
+          if (lane == 0) atomicOr(a.err, DYN_ERR);
+          return;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      const int c = q_chunk[k & 3];
+      if (c < 0) break;
+      const long long c0 = (long long)(T0 + (c >> 1)) * KB + (long long)(c & 1) * half;
+      stream_range<WT, NORM, P>(a, gsh, rn_s, &ready, red, arrived, &reduced, c0, c0 + half, w,
+                                lane, si);
+    }
+    return;
+  }
+
+  // ---- reducer wave ----
+  if constexpr (NORM) reducer_norm_prologue<WT>(a, lane, gsh, ss_s, rn_s, &ready);
+  int n_pub = 0;
+  bool exhausted = false;
+  auto publish_next = [&]() {
+    if (exhausted) return;
+    int c = 0;
+    if (lane == 0) c = __hip_atomic_fetch_add(a.dyn_next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    c = __shfl(c, 0, 64);
+    if (c >= n_chunks) {
+      c = -1;
+      exhausted = true;
+    }
+    if (lane == 0) {
+      q_chunk[n_pub & 3] = c;
+      __hip_atomic_store(&q_pub, n_pub + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    ++n_pub;
+  };
+  int si = 0;
+  for (int i = 0; i < S; ++i, ++si) {
+    if (i == S - 1) publish_next();   // entry 0 before the last static segment's wait
+    reduce_segment<EPI>(a, lane, red, arrived, &reduced, si, b * S + i, 0, 1);
+  }
+  if (S == 0) publish_next();
+  for (int k = 0;; ++k, ++si) {
+    const int c = __shfl(q_chunk[k & 3], 0, 64);   // entry k, published by this wave
+    if (c < 0) break;
+    publish_next();                   // entry k + 1 before waiting for chunk k
+    reduce_segment<EPI>(a, lane, red, arrived, &reduced, si, T0 + (c >> 1), c & 1, 2);
+  }
+  if (lane == 0) {
+    const int prev = __hip_atomic_fetch_add(a.dyn_next + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (prev == G - 1) {
+      __hip_atomic_store(a.dyn_next, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.dyn_next + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -795,6 +919,29 @@ SKPlan streamk_plan(int N, int KB, int n_cu) {
   return p;
 }
 
+SKPlan streamk_plan_balanced(int N, int KB, int n_cu) {
+  SKPlan p = streamk_plan(N, KB, n_cu);
+  const long long nt = N / 64;
+  if (nt < 2LL * n_cu || (KB & 1)) return p;
+  p.workers = n_cu;
+  // about 86 % of the tiles statically: below the share that the slowest XCD finishes in
+  // the balanced time when the XCDs' rates differ by up to a quarter
+  // (clamped so that the static tiles never pass the last tile)
+  p.dyn_static = (int)std::min(nt / n_cu, (nt * 86 + 50LL * n_cu) / (100LL * n_cu));
+  p.seg_cap = std::max(p.seg_cap, 2);
+  return p;
+}
+
+template <int WT, int EPI, bool NORM>
+static void launch_dyn_t(const StreamArgs& a, const SKPlan& p, hipStream_t st, hipEvent_t e0,
+                         hipEvent_t e1) {
+  const dim3 grid(p.workers), block(64 * (WG_WAVES + 1));
+  if (e0 || e1)
+    hipExtLaunchKernelGGL((gsk_dyn_kernel<WT, EPI, NORM, 4>), grid, block, 0, st, e0, e1, 0, a);
+  else
+    hipLaunchKernelGGL((gsk_dyn_kernel<WT, EPI, NORM, 4>), grid, block, 0, st, a);
+}
+
 // With events, the dispatch itself records its start / end time into them (the same
 // timestamps a kernel trace reports); no marker packets are added to the stream.
 template <int WT, int EPI, bool NORM>
@@ -846,6 +993,12 @@ bool launch_streamk_gemm_m(int wt, int epi, bool norm, const StreamArgs& a, cons
 
 bool launch_streamk_gemm(int wt, int epi, bool norm, const StreamArgs& a, const SKPlan& p,
                          hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop) {
+  if (p.dyn_static > 0) {   // balanced mode: the fp16 ARGMAX lm_head only
+    if (wt != WT_F16 || epi != EPI_ARGMAX || !a.dyn_next || !a.err) return false;
+    if (norm) launch_dyn_t<WT_F16, EPI_ARGMAX, true>(a, p, st, ev_start, ev_stop);
+    else launch_dyn_t<WT_F16, EPI_ARGMAX, false>(a, p, st, ev_start, ev_stop);
+    return true;
+  }
 #define DFL_SK_CASE(W_, E_)                                        \
   if (wt == W_ && epi == E_) {                                     \
     if (norm) launch_t<W_, E_, true>(a, p, st, ev_start, ev_stop); \

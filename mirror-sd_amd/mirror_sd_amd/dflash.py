@@ -12,7 +12,7 @@ The public surface mirrors the reference:
   thread: ``prepare_forward`` / ``run_kernels`` / ``read_output`` /
   ``read_draft_tokens`` / ``set_block_size`` / ``max_ctx_len`` / ``_compute_context``
   (ane_model.py:384-430, 538-637);
-* the north-star entry point ``draft(ids, target_hidden)`` -> per-position logits and
+* the fused entry point ``draft(ids, target_hidden)`` -> per-position logits and
   argmax ids (generate.py:594-606 in one call).
 
 All arithmetic runs in libdflash_hip.so on the GPU.  Tensors are torch CUDA tensors;
@@ -444,7 +444,7 @@ class DFlashDraftModel:
 
     def draft(self, ids, target_hidden=None, cache=None, return_logits=False,
               return_hidden=False, fused_context=False):
-        """North-star entry point: block token ids [B] (+ new target_hidden rows) in,
+        """Fused entry point: block token ids [B] (+ new target_hidden rows) in,
         per-position argmax ids [B] (and fp32 logits [B, V]) out.
 
         Equivalent to the serial caller's embed -> draft -> lm_head -> argmax ->

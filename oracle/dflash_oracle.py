@@ -1,6 +1,6 @@
 """CPU oracle for the DFlash draft forward -- TEST INFRASTRUCTURE ONLY.
 
-This module is the checker, never the product: only ``tests/``,
+It checks the GPU library and is never part of it: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may import
 it.  The GPU library never routes through it.
 

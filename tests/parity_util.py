@@ -24,3 +24,15 @@ def assert_close_fp16(got, ref, cos_min=0.9995, max_abs=2e-2, what=""):
 def torch_tensors(np_tensors, device):
     import torch
     return {k: torch.from_numpy(np.ascontiguousarray(v)).to(device) for k, v in np_tensors.items()}
+
+
+def device_errors(m):
+    """The sticky device-side error flags of a DFlashDraftModel's context (reading clears)."""
+    import ctypes
+    import torch
+    from mirror_sd_amd import _lib
+    v = ctypes.c_int32(0)
+    _lib.check(m._L.dfl_device_errors(m._ctx, ctypes.byref(v),
+                                      torch.cuda.current_stream().cuda_stream),
+               "dfl_device_errors")
+    return v.value
