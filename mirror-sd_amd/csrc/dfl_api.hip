@@ -505,7 +505,8 @@ int dfl_load_head(dfl_ctx* ctx, const uint16_t* final_norm, const uint16_t* embe
 static int skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const SKPlan& p,
                    const uint4* W, const half_t* scale, int N, int KB, const half_t* X, int ldx,
                    int M, const half_t* gnorm, bool rn_from_ss, half_t* out, int ldo,
-                   half_t* xres, float* logits, unsigned long long* keys, hipStream_t st) {
+                   half_t* xres, float* logits, unsigned long long* keys, hipStream_t st,
+                   int32_t* ids = nullptr, bool* ids_done = nullptr) {
   const long long wbytes = (wt == WT_INT8) ? (long long)N * KB * 32 + 2LL * N
                                            : (long long)N * KB * 16 * 2;
   const int ss_stride = (ctx->H / 64) * 32;
@@ -543,6 +544,10 @@ static int skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const SKPlan& p,
     a.dyn_static = p.dyn_static;
     a.dyn_next = ctx->dyn_next;
     a.err = ctx->err;
+    // the balanced kernel (one m-tile) finalises the argmax ids itself
+    const bool fin = ids && keys && p.dyn_static > 0 && n_mt == 1;
+    a.ids = fin ? ids : nullptr;
+    if (ids_done) *ids_done = fin;
     const bool ok =
         mt_n == 1 ? launch_streamk_gemm(wt, epi, gnorm != nullptr, a, p, st, ps.start(), ps.stop())
                   : launch_streamk_gemm_m(wt, epi, gnorm != nullptr, a, p, st, ps.start(), ps.stop());
@@ -874,10 +879,11 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
     DFL_TRY(blas_gemm(ctx, ctx->V, M, H, ctx->w_lm16, H, ctx->h, H, 0.f, lg, ctx->V, st));
     if (out_ids) launch_row_argmax(lg, M, ctx->V, out_ids, st);
   } else if (out_logits || out_ids) {
+    bool ids_done = false;
     DFL_TRY(skgemm(ctx, P_LM_HEAD, WT_F16, EPI_ARGMAX, ctx->sk_lm, ctx->w_lm, nullptr, ctx->V, H / 16,
            ctx->x, H, M, ctx->final_norm, true, nullptr, 0, nullptr, out_logits,
-           out_ids ? ctx->keys : nullptr, st));
-    if (out_ids) {
+           out_ids ? ctx->keys : nullptr, st, out_ids, &ids_done));
+    if (out_ids && !ids_done) {
       ProfScope ps(ctx, P_ROWS, 0, st);
       launch_argmax_finalize(ctx->keys, M, out_ids, st);
     }

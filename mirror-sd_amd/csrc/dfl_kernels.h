@@ -42,6 +42,8 @@ struct StreamArgs {
   int dyn_static;
   int* dyn_next;
   int* err;                 // device error word (bit 2: a work-queue wait gave up)
+  int32_t* ids;             // balanced ARGMAX: the last workgroup turns keys [M] into ids [M]
+                            // (-1 for a row without a number) and re-arms keys to zero
 };
 struct SKPlan {
   int workers = 1;          // workgroups (one per CU)

@@ -779,9 +779,21 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_dyn_kernel(StreamArgs
     publish_next();                   // entry k + 1 before waiting for chunk k
     reduce_segment<EPI>(a, lane, red, arrived, &reduced, si, T0 + (c >> 1), c & 1, 2);
   }
-  if (lane == 0) {
-    const int prev = __hip_atomic_fetch_add(a.dyn_next + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (prev == G - 1) {
+  // this workgroup's epilogue atomics and stores are performed before it counts itself
+  // finished, so the last one to finish sees every tile's argmax key
+  __builtin_amdgcn_s_waitcnt(0);
+  int prev = 0;
+  if (lane == 0) prev = __hip_atomic_fetch_add(a.dyn_next + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  prev = __shfl(prev, 0, 64);
+  if (prev == G - 1) {
+    if (EPI == EPI_ARGMAX && a.ids && a.keys && lane < a.M) {
+      unsigned long long* kp = a.keys + lane;
+      const unsigned long long k =
+          __hip_atomic_load(kp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      a.ids[lane] = k ? (int32_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull)) : -1;
+      __hip_atomic_store(kp, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (lane == 0) {
       __hip_atomic_store(a.dyn_next, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(a.dyn_next + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
