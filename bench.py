@@ -327,7 +327,9 @@ def main():
         lm = gprof.get("lm_head_argmax", {})
         if lm.get("launches"):
             per_launch, avg_s, ach = rate(lm)
-            roofline["lm_head"] = {"kernel": "gsk_gemm_kernel<fp16,ARGMAX>", "achieved": round(ach, 1),
+            lm_name = ("rocBLAS GEMM + row argmax (stacked rows)" if rows > 64 else
+                       "gsk_dyn_kernel<fp16,ARGMAX> (balanced)")
+            roofline["lm_head"] = {"kernel": lm_name, "achieved": round(ach, 1),
                                    "frac": round(ach / HBM_PEAK_GBS, 4),
                                    "bytes_per_launch": per_launch,
                                    "avg_launch_us": round(avg_s * 1e6, 3)}

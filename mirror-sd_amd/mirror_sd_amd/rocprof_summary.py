@@ -28,7 +28,7 @@ GROUPS = [
     ("qkv (STORE, norm-on-load)", r"gsk_gemm_kernel<0, 3, true, 4>"),
     ("o / down (RESID)", r"gsk_gemm_kernel<0, 4, false, 4>"),
     ("gate|up (SWIGLU, norm-on-load)", r"gsk_gemm_kernel<0, 1, true, 4>"),
-    ("lm_head (fp16, ARGMAX, norm-on-load)", r"gsk_gemm_kernel<1, 2, true, 4>"),
+    ("lm_head (fp16, ARGMAX, norm-on-load)", r"gsk_(gemm|dyn)_kernel<1, 2, true, 4>"),
     ("down, stacked rows (M-split RESID)", r"gsk_gemm_m_kernel<0, 4, false"),
     ("stacked-row GEMMs (rocBLAS: qkv, o, gate|up, lm_head, ingest)", r"Cijk_"),
     ("stacked-row epilogues (norm rows, RESID, SWIGLU)", r"afl_rows_kernel|resid_rows_kernel|swiglu_rows_kernel"),
