@@ -138,6 +138,7 @@ struct dfl_ctx {
   int n_cu = 256;
   half_t* qkvbuf = nullptr;      // [RM][NQKV] fp16 projections
   float* rnorm = nullptr;        // [RM] 1/rms of the residual rows
+  float* rope_cs = nullptr;      // [32][64][2] RoPE cos, sin of a block's rows (one sequence)
   float* sk_ws = nullptr;        // split-tile partials
   int* sk_tile_cnt = nullptr;    // [max tiles]
   int* dyn_next = nullptr;       // [2] work counters of the balanced lm_head (self-resetting)
@@ -347,7 +348,7 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
     wsn *= (size_t)std::min<size_t>(MT_MAX, bm32 / 32);
     if ((r = x->alloc(&x->qkvbuf, Bm * x->NQKV)) || (r = x->alloc(&x->rnorm, bm32)) ||
         (r = x->alloc(&x->sk_ws, wsn)) || (r = x->alloc(&x->sk_tile_cnt, tiles, true)) ||
-        (r = x->alloc(&x->dyn_next, 2, true)) ||
+        (r = x->alloc(&x->dyn_next, 2, true)) || (r = x->alloc(&x->rope_cs, 32 * 64 * 2)) ||
         (r = x->alloc(&x->sk_ss, (bm32 / 32) * (size_t)(x->H / 64) * 32))) {
       delete x;
       return r;
@@ -506,7 +507,8 @@ static int skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const SKPlan& p,
                    const uint4* W, const half_t* scale, int N, int KB, const half_t* X, int ldx,
                    int M, const half_t* gnorm, bool rn_from_ss, half_t* out, int ldo,
                    half_t* xres, float* logits, unsigned long long* keys, hipStream_t st,
-                   int32_t* ids = nullptr, bool* ids_done = nullptr) {
+                   int32_t* ids = nullptr, bool* ids_done = nullptr,
+                   const RopeEpi* rope = nullptr) {
   const long long wbytes = (wt == WT_INT8) ? (long long)N * KB * 32 + 2LL * N
                                            : (long long)N * KB * 16 * 2;
   const int ss_stride = (ctx->H / 64) * 32;
@@ -548,6 +550,7 @@ static int skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const SKPlan& p,
     const bool fin = ids && keys && p.dyn_static > 0 && n_mt == 1;
     a.ids = fin ? ids : nullptr;
     if (ids_done) *ids_done = fin;
+    if (rope) a.rope = *rope;
     const bool ok =
         mt_n == 1 ? launch_streamk_gemm(wt, epi, gnorm != nullptr, a, p, st, ps.start(), ps.stop())
                   : launch_streamk_gemm_m(wt, epi, gnorm != nullptr, a, p, st, ps.start(), ps.stop());
@@ -735,13 +738,16 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
   const int H = ctx->H, NH = ctx->NH, NKV = ctx->NKV, F = ctx->F, NQ = NH * 128;
   const int M = n_seq * B;
   const bool blas = M > BLAS_MIN_ROWS && ctx->layers[0].w_qkv16;   // stacked blocks
+  const bool fuse_rope = !blas && n_seq == 1 && M <= 32;   // rope in the qkv epilogue
   const float eps = ctx->cfg.rms_eps;
   // x = embedding rows (residual stream); rnorm = 1/rms(x).  Every projection whose input
   // is an RMSNorm output applies the norm on its activation load.
   {
     ProfScope ps(ctx, P_ROWS, 0, st);
     launch_embed_norm(ids, ctx->embed, reinterpret_cast<const half_t*>(noise_emb), M, H, ctx->V,
-                      ctx->layers[0].in_norm, eps, ctx->x, nullptr, ctx->rnorm, ctx->err, st);
+                      ctx->layers[0].in_norm, eps, ctx->x, nullptr, ctx->rnorm, ctx->err, st,
+                      fuse_rope ? ctx->rope_cs : nullptr, ctx->seqs[seq0].offset,
+                      std::log2(ctx->cfg.rope_theta));
   }
 
   // Attention key split per sequence: about one workgroup per CU ((chunks x KV heads) ~
@@ -775,6 +781,22 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
                         ctx->h, st, l > 0 ? nullptr : ctx->rnorm);
       DFL_TRY(blas_gemm(ctx, ctx->NQKV, M, H, Ly.w_qkv16, H, ctx->h, H, 0.f, ctx->y32, ctx->NQKV,
                         st));
+    } else if (fuse_rope) {
+      // one sequence: the per-head Q/K norm, RoPE and cache scatter run in the epilogue
+      RopeEpi re{};
+      re.Q = ctx->Q;
+      re.cs = ctx->rope_cs;
+      re.q_norm = Ly.q_norm;
+      re.k_norm = Ly.k_norm;
+      re.eps = eps;
+      re.log2_theta = std::log2(ctx->cfg.rope_theta);
+      re.NH = NH;
+      re.NKV = NKV;
+      re.cap = ctx->cap;
+      rope_seq(ctx, seq0, Ly, ctx->seqs[seq0].offset, B, re.sq);
+      DFL_TRY(skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_QKROPE, ctx->sk_qkv, Ly.w_qkv, Ly.s_qkv,
+                     ctx->NQKV, H / 32, ctx->x, H, M, Ly.in_norm, /*rn_from_ss=*/l > 0, nullptr,
+                     0, nullptr, nullptr, nullptr, st, nullptr, nullptr, &re));
     } else {
       DFL_TRY(skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_STORE, ctx->sk_qkv, Ly.w_qkv, Ly.s_qkv, ctx->NQKV,
                      H / 32, ctx->x, H, M, Ly.in_norm, /*rn_from_ss=*/l > 0, ctx->qkvbuf,
@@ -841,7 +863,7 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
         at.max_chunks = std::max(at.max_chunks, as.n_chunks);
         kv_bytes += 2LL * NKV * as.L * 128 * 2;
       }
-      {
+      if (!fuse_rope) {
         ProfScope ps(ctx, P_QK_ROPE, 0, st);
         launch_qk_rope(q, st);
       }

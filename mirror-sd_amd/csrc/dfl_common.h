@@ -85,6 +85,8 @@ DFL_DEV size_t afl_index(int row, int k, int K) {
 
 DFL_DEV float h2f(half_t h) { return (float)h; }
 DFL_DEV half_t f2h(float f) { return (half_t)f; }   // round-to-nearest-even
+// RMSNorm output expression: fp16(fp16(x * r) * g)  (nn.RMSNorm, dflash.py:338-339).
+DFL_DEV half_t rms_out(float x, float r, half_t g) { return f2h(h2f(f2h(x * r)) * h2f(g)); }
 
 // Wave64 reductions via cross-lane shuffles.
 DFL_DEV float wave_sum(float v) {

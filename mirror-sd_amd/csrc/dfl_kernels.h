@@ -9,7 +9,30 @@
 namespace dfl {
 
 enum { WT_INT8 = 0, WT_F16 = 1 };
-enum { EPI_SWIGLU = 1, EPI_ARGMAX = 2, EPI_STORE = 3, EPI_RESID = 4 };
+// EPI_QKROPE: the fused q|k|v projection of one sequence (M <= 32 rows) with the per-head
+// Q/K RMSNorm, RoPE and cache scatter of qk_rope_kernel done in the epilogue (RopeEpi).
+enum { EPI_SWIGLU = 1, EPI_ARGMAX = 2, EPI_STORE = 3, EPI_RESID = 4, EPI_QKROPE = 5 };
+
+struct RopeSeq {
+  long long pos0;
+  half_t* Kc;
+  half_t* Vt;
+  int cache_row0, sink_fill, ring_j0, ring_S, ring_W;
+};
+
+// EPI_QKROPE outputs: Q [NH][M][128], the K cache rows and the Vt cache columns of the
+// sequence's rows (positions sq.pos0 + m, cache rows through cache_slot).
+struct RopeEpi {
+  half_t* Q;
+  const float* cs;          // [M][64] (cos, sin) of position pos0 + m, frequency j (embed_norm)
+  const half_t* q_norm;
+  const half_t* k_norm;
+  float eps;
+  double log2_theta;
+  int NH, NKV, cap;
+  RopeSeq sq;
+};
+
 
 // ---- stream-K weight-streaming GEMM for M <= 32 rows (dfl_stream.hip) ----
 struct StreamArgs {
@@ -44,6 +67,7 @@ struct StreamArgs {
   int* err;                 // device error word (bit 2: a work-queue wait gave up)
   int32_t* ids;             // balanced ARGMAX: the last workgroup turns keys [M] into ids [M]
                             // (-1 for a row without a number) and re-arms keys to zero
+  RopeEpi rope;             // EPI_QKROPE
 };
 struct SKPlan {
   int workers = 1;          // workgroups (one per CU)
@@ -105,7 +129,8 @@ void launch_fc_norm_rows(const float* fc32, int rows, int H, const half_t* g, fl
 void launch_i8_to_f16(const int8_t* q, size_t n, half_t* out, hipStream_t st);
 void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* noise, int B,
                        int H, int V, const half_t* g, float eps, half_t* x, half_t* h,
-                       float* rnorm, int* err, hipStream_t st);
+                       float* rnorm, int* err, hipStream_t st,
+                       float* rope_cs = nullptr, long long pos0 = 0, double log2_theta = 0.0);
 // x in the activation fragment layout (afl_index) [M][N] -> row-major h [M][N]:
 // h = fp16(fp16(x * r[m]) * g[n])  (apply_norm), or a plain copy (afl_to_rows).  r[m] =
 // 1/rms of row m from ss [M/32 m-tiles][ss_tiles][32] (row sums of squares per column tile).
@@ -127,12 +152,6 @@ constexpr int SEQ_MAX = 8;
 // cache row cache_row0 + m.  With a sink + window cache (ring_W > 0) the first sink_fill
 // rows go to cache_row0 + m (filling the sink) and later ones to ring row
 // ring_S + ((ring_j0 + m - sink_fill) mod ring_W).
-struct RopeSeq {
-  long long pos0;
-  half_t* Kc;
-  half_t* Vt;
-  int cache_row0, sink_fill, ring_j0, ring_S, ring_W;
-};
 
 // Per-head RMSNorm + neox RoPE + scatter of projections: fp16 qkv16 (scaled and rounded by
 // the GEMM epilogue) or fp32 qkv32 (scaled and rounded here), rows [n_seq * M][N], sequence

@@ -12,16 +12,23 @@ namespace dfl {
 constexpr int ROW_THREADS = 512;
 constexpr int ROW_MAXV = 16;   // hidden sizes up to 8192
 
-// RMSNorm output expression: fp16(fp16(x * r) * g)  (nn.RMSNorm, dflash.py:338-339).
-DFL_DEV half_t rms_out(float x, float r, half_t g) { return f2h(h2f(f2h(x * r)) * h2f(g)); }
-
 __global__ __launch_bounds__(ROW_THREADS) void embed_norm_kernel(
     const int32_t* __restrict__ ids, const half_t* __restrict__ embed,
     const half_t* __restrict__ noise, int H, int V, const half_t* __restrict__ g, float eps,
     half_t* __restrict__ x, half_t* __restrict__ h, float* __restrict__ rnorm,
-    int* __restrict__ err) {
+    int* __restrict__ err, float* __restrict__ rope_cs, long long pos0, double log2_theta) {
   __shared__ float sm[16];
   const int b = blockIdx.x;
+  if (rope_cs && threadIdx.x < 64) {
+    // RoPE angles of row b for the fused qkv epilogue, in fp64 as qk_rope_kernel computes
+    // them: position pos0 + b times theta^(-j/64)
+    const int j = threadIdx.x;
+    const double inv_freq = exp2(-(double)j * (1.0 / 64.0) * log2_theta);
+    double sd, cd;
+    sincos((double)(pos0 + b) * inv_freq, &sd, &cd);
+    rope_cs[2 * (b * 64 + j)] = (float)cd;
+    rope_cs[2 * (b * 64 + j) + 1] = (float)sd;
+  }
   const half_t* src = noise + (size_t)b * H;
   bool bad = false;
   if (ids) {
@@ -56,9 +63,10 @@ __global__ __launch_bounds__(ROW_THREADS) void embed_norm_kernel(
 
 void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* noise, int B,
                        int H, int V, const half_t* g, float eps, half_t* x, half_t* h,
-                       float* rnorm, int* err, hipStream_t st) {
+                       float* rnorm, int* err, hipStream_t st, float* rope_cs, long long pos0,
+                       double log2_theta) {
   hipLaunchKernelGGL(embed_norm_kernel, dim3(B), dim3(ROW_THREADS), 0, st, ids, embed, noise, H,
-                     V, g, eps, x, h, rnorm, err);
+                     V, g, eps, x, h, rnorm, err, B <= 32 ? rope_cs : nullptr, pos0, log2_theta);
 }
 
 // x (activation fragment layout, [M][N]) -> row-major h; with g set, h = RMSNorm(x) * g

@@ -384,6 +384,23 @@ DFL_DEV void tile_epilogue(const StreamArgs& a, int lane, int t, const floatx16&
       }
       *reinterpret_cast<half4_t*>(dst) = o;
     }
+  } else if constexpr (EPI == EPI_QKROPE) {
+    // a V head's tile (Q and K heads complete in qk_head_epilogue): the fp16 Linear output
+    // of row m goes to its transposed cache column, Vt[gk][d][crow], as in qk_rope_kernel
+    const RopeEpi& r = a.rope;
+    if (!row_ok) return;
+    const int crow = cache_slot(r.sq, a.M, m);
+    if (crow < 0) return;
+    half_t* vt = r.sq.Vt + (size_t)((t >> 1) - r.NH - r.NKV) * 128 * r.cap + crow;
+    const int d0 = 64 * (t & 1) + 4 * g;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int d = d0 + 8 * q + c;
+        vt[(size_t)d * r.cap] = f2h(acc0[4 * q + c] * h2f(a.scale[nb + 8 * q + c]));
+        vt[(size_t)(d + 32) * r.cap] = f2h(acc1[4 * q + c] * h2f(a.scale[nb + 32 + 8 * q + c]));
+      }
   } else {  // EPI_ARGMAX: fp16 weights, no scale
     if (row_ok && a.logits) {
       float* dst = a.logits + (size_t)m * a.ldl + nb;
@@ -462,6 +479,121 @@ DFL_DEV void reduce_segment(const StreamArgs& a, int lane, float (*red)[WG_WAVES
   if (lane == 0) __hip_atomic_store(reduced, si + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
   const bool complete = count == 1 || finish_split_tile(a, lane, t, slot, count, acc0, acc1);
   if (complete) tile_epilogue<EPI>(a, lane, t, acc0, acc1);
+}
+
+// Q or K head h of the fused qkv projection, complete: lo = d 0..63 (tile 2h), hi = d
+// 64..127 (tile 2h+1), in the accumulator layout of tile_epilogue, so lane (m, g) holds the
+// neox pair (d, d + 64) at the same register.  Per head and row: fp16 Linear output, RMSNorm
+// over the 128 d (q_norm / k_norm), split-half RoPE with the block's angle table ([m][j]
+// cos, sin, j = d mod 64), then Q[h][m] or the K cache row (qk_rope_kernel's arithmetic;
+// dflash.py:251-252, 263-275).
+DFL_DEV void qk_head_epilogue(const StreamArgs& a, int lane, int h, const floatx16& lo0,
+                              const floatx16& lo1, const floatx16& hi0, const floatx16& hi1) {
+  const RopeEpi& r = a.rope;
+  const int m = lane & 31, g = lane >> 5;
+  const int nlo = 128 * h + 4 * g;   // packed row of d = 4g (+ 32 tt + 8 q + c)
+  float vl[32], vh[32];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {   // i = 16 tt + 4 q + c: d = 32 tt + 8 q + 4 g + c
+    const int f = 32 * (i >> 4) + 8 * ((i >> 2) & 3) + (i & 3);
+    const float al = i < 16 ? lo0[i] : lo1[i - 16], ah = i < 16 ? hi0[i] : hi1[i - 16];
+    vl[i] = h2f(f2h(al * h2f(a.scale[nlo + f])));
+    vh[i] = h2f(f2h(ah * h2f(a.scale[nlo + 64 + f])));
+    ss += vl[i] * vl[i] + vh[i] * vh[i];
+  }
+  ss += __shfl_xor(ss, 32, 64);
+  if (m >= a.M) return;
+  const bool is_q = h < r.NH;
+  half_t* dst;
+  if (is_q) {
+    dst = r.Q + ((size_t)h * a.M + m) * 128;
+  } else {
+    const int crow = cache_slot(r.sq, a.M, m);
+    if (crow < 0) return;
+    dst = r.sq.Kc + ((size_t)(h - r.NH) * r.cap + crow) * 128;
+  }
+  const half_t* gn = is_q ? r.q_norm : r.k_norm;
+  const float rr = 1.0f / sqrtf(ss * (1.0f / 128.0f) + r.eps);
+#pragma unroll
+  for (int q8 = 0; q8 < 8; ++q8) {   // 4 consecutive d per (tt, q)
+    const int f0 = 32 * (q8 >> 2) + 8 * (q8 & 3) + 4 * g;
+    const floatx4* csp = reinterpret_cast<const floatx4*>(r.cs + 2 * (m * 64 + f0));
+    const floatx4 cs01 = csp[0], cs23 = csp[1];   // (cos, sin) of f0 .. f0 + 3
+    half4_t ol, oh;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int i = 4 * q8 + c, f = f0 + c;
+      const float y0 = h2f(rms_out(vl[i], rr, gn[f]));
+      const float y1 = h2f(rms_out(vh[i], rr, gn[f + 64]));
+      const floatx4& cp = c < 2 ? cs01 : cs23;
+      const float cc = cp[2 * (c & 1)], sn = cp[2 * (c & 1) + 1];
+      ol[c] = f2h(y0 * cc - y1 * sn);
+      oh[c] = f2h(y1 * cc + y0 * sn);
+    }
+    *reinterpret_cast<half4_t*>(dst + f0) = ol;
+    *reinterpret_cast<half4_t*>(dst + 64 + f0) = oh;
+  }
+}
+
+// Reducer wave, segment si of tile t of a Q/K head of the fused qkv projection: the head's
+// two tiles complete together, through the split-tile protocol with one counter (tile
+// 2h's) over the c_lo + c_hi workers of both tiles.  Every worker publishes its partial in
+// its tile's slot `slot`; the last one sums each tile's slots in slot order (the same sums
+// as a per-tile completion) and runs qk_head_epilogue.
+DFL_DEV void reduce_head(const StreamArgs& a, int lane, float (*red)[WG_WAVES][2048],
+                         int* arrived, int* reduced, int si, int t, int slot, int c_lo,
+                         int c_hi) {
+  while (__hip_atomic_load(&arrived[si & 1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
+         WG_WAVES * ((si >> 1) + 1))
+    __builtin_amdgcn_s_sleep(1);
+  floatx16 acc0 = (floatx16){}, acc1 = (floatx16){};
+#pragma unroll 1
+  for (int j = 0; j < WG_WAVES; ++j) {
+    const float* src = red[si & 1][j];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      acc0[r] += src[r * 64 + lane];
+      acc1[r] += src[1024 + r * 64 + lane];
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);   // slot reads done before the set is handed back
+  if (lane == 0) __hip_atomic_store(reduced, si + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  float* mine = a.ws + ((size_t)t * a.seg_cap + slot) * 2048;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    store_agent(mine + r * 64 + lane, acc0[r]);
+    store_agent(mine + 1024 + r * 64 + lane, acc1[r]);
+  }
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  const int t0 = t & ~1;
+  int prev = 0;
+  if (lane == 0)
+    prev = __hip_atomic_fetch_add(a.tile_cnt + t0, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  prev = __shfl(prev, 0, 64);
+  if (prev != c_lo + c_hi - 1) return;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  floatx16 lo0 = (floatx16){}, lo1 = (floatx16){}, hi0 = (floatx16){}, hi1 = (floatx16){};
+  for (int j = 0; j < c_lo; ++j) {
+    const float* src = a.ws + ((size_t)t0 * a.seg_cap + j) * 2048;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      lo0[r] += load_agent(src + r * 64 + lane);
+      lo1[r] += load_agent(src + 1024 + r * 64 + lane);
+    }
+  }
+  for (int j = 0; j < c_hi; ++j) {
+    const float* src = a.ws + ((size_t)(t0 + 1) * a.seg_cap + j) * 2048;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      hi0[r] += load_agent(src + r * 64 + lane);
+      hi1[r] += load_agent(src + 1024 + r * 64 + lane);
+    }
+  }
+  if (lane == 0) a.tile_cnt[t0] = 0;   // next use is a later launch
+  qk_head_epilogue(a, lane, t0 >> 1, lo0, lo1, hi0, hi1);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -669,6 +801,18 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_gemm_kernel(StreamArg
     const int t = (int)(u / a.KB);
     const int kbs = (int)(u - (long long)t * a.KB);
     const int kbe = (int)min((long long)a.KB, (long long)kbs + (u1 - u));
+    if constexpr (EPI == EPI_QKROPE) {
+      if ((t >> 1) < a.rope.NH + a.rope.NKV) {   // Q or K head: both tiles complete together
+        const long long h0 = (long long)(t & ~1) * a.KB;
+        const int f_lo = worker_of(h0, U, G), f_hi = worker_of(h0 + a.KB, U, G);
+        const int c_lo = worker_of(h0 + a.KB - 1, U, G) - f_lo + 1;
+        const int c_hi = worker_of(h0 + 2 * a.KB - 1, U, G) - f_hi + 1;
+        reduce_head(a, lane, red, arrived, &reduced, si, t, b - ((t & 1) ? f_hi : f_lo), c_lo,
+                    c_hi);
+        u += kbe - kbs;
+        continue;
+      }
+    }
     int first = b, count = 1;
     if (!(kbs == 0 && kbe == a.KB)) {
       const long long tu0 = (long long)t * a.KB;
@@ -1022,6 +1166,10 @@ bool launch_streamk_gemm(int wt, int epi, bool norm, const StreamArgs& a, const 
   DFL_SK_CASE(WT_INT8, EPI_SWIGLU)
   DFL_SK_CASE(WT_F16, EPI_ARGMAX)
   DFL_SK_CASE(WT_F16, EPI_STORE)
+  if (wt == WT_INT8 && epi == EPI_QKROPE && norm && a.M <= 32) {   // one sequence, one m-tile
+    launch_t<WT_INT8, EPI_QKROPE, true>(a, p, st, ev_start, ev_stop);
+    return true;
+  }
 #undef DFL_SK_CASE
   return false;
 }

@@ -25,7 +25,8 @@ import sys
 # kernel groups: (label, regex on the kernel name)
 GROUPS = [
     ("proj_gemm_w8a16", r"gsk_gemm_kernel<0, [0-9], (true|false), 4>"),
-    ("qkv (STORE, norm-on-load)", r"gsk_gemm_kernel<0, 3, true, 4>"),
+    ("qkv (norm-on-load; Q/K norm + RoPE + cache scatter in the epilogue)",
+     r"gsk_gemm_kernel<0, [35], true, 4>"),
     ("o / down (RESID)", r"gsk_gemm_kernel<0, 4, false, 4>"),
     ("gate|up (SWIGLU, norm-on-load)", r"gsk_gemm_kernel<0, 1, true, 4>"),
     ("lm_head (fp16, ARGMAX, norm-on-load)", r"gsk_(gemm|dyn)_kernel<1, 2, true, 4>"),
@@ -35,7 +36,7 @@ GROUPS = [
     ("row argmax (stacked lm_head)", r"row_argmax_kernel"),
     ("block attention", r"block_attn_kernel"),
     ("attention merge", r"attn_merge_kernel"),
-    ("qk norm + rope", r"qk_rope_kernel"),
+    ("qk norm + rope (context ingest, stacked blocks)", r"qk_rope_kernel"),
     ("embed + norm", r"embed_norm_kernel"),
     ("argmax finalize", r"argmax_finalize_kernel"),
 ]
