@@ -232,3 +232,36 @@ def test_window_cache_protocol_matches_oracle(sink, window):
                           what=f"layer {layer} values")
     if window:
         assert ocache[0].keys.shape[1] == sink + window - B   # eviction happened
+
+
+@pytest.mark.parametrize("sink,window,C", [(0, 0, 10), (4, 16, 20)])
+def test_block_rows_in_cache_match_oracle(sink, window, C):
+    """The block's own K/V rows that a cached forward appends (dflash.py:287-308: context
+    rows, then the block's rows, before the caller's trim) match the oracle's cache, row
+    order included: the per-head Q/K norm, RoPE and cache writes of the fused qkv epilogue,
+    through the ring slot map when a window is set (20 context rows + the block overflow
+    sink 4 + window 16, so the append itself evicts)."""
+    wl, cfg, t, inp, W = _full_case("tiny", seed=3)
+    B = wl.block
+    th = synth.np_normal(3, "blockrows.th", (C, 5 * cfg.hidden_size), 1.0, np.float16)
+    noise = O.embed(W, inp["ids"]).astype(np.float16)
+    m = _model(cfg, max_ctx=C + B)
+    m.load_weights(torch_tensors(t, "cuda"))
+    cache = m.make_cache(sink, window)
+    ocache = [O.OracleKVCache(sink, window) for _ in range(cfg.num_hidden_layers)]
+    ref = O.draft_forward(W, noise, th, cache=ocache, fp16=True)
+    out = m(torch.from_numpy(noise)[None], torch.from_numpy(th)[None], cache=cache)
+    torch.cuda.synchronize()
+    assert_close_fp16(out[0].float().cpu().numpy(), ref, what="forward")
+    assert cache[0].offset == ocache[0].offset == C + B
+    m._sync_cache(list(cache))
+    for layer in range(cfg.num_hidden_layers):
+        k = cache[layer].keys[0].float().cpu().numpy()
+        v = cache[layer].values[0].float().cpu().numpy()
+        assert k.shape[1] == ocache[layer].keys.shape[1], "cache length"
+        assert_close_fp16(k, ocache[layer].keys, what=f"layer {layer} keys")
+        assert_close_fp16(v, ocache[layer].values, what=f"layer {layer} values")
+        # the block's rows alone (the last B in the reference's row order)
+        assert_close_fp16(k[:, -B:], ocache[layer].keys[:, -B:], what=f"layer {layer} block keys")
+        assert_close_fp16(v[:, -B:], ocache[layer].values[:, -B:],
+                          what=f"layer {layer} block values")
