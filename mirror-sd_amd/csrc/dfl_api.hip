@@ -750,27 +750,34 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
                       std::log2(ctx->cfg.rope_theta));
   }
 
-  // Attention key split per sequence: about one workgroup per CU ((chunks x KV heads) ~
-  // CUs) with chunks of at most 160 keys (one LDS stage) while there are at most MAX_CHUNKS.
   // Attention key split.  One sequence: about one workgroup per CU ((chunks x KV heads) ~
   // CUs) with chunks of at most 160 keys (one LDS stage) while there are at most
-  // MAX_CHUNKS.  Several sequences in one launch: chunks in proportion to each sequence's
-  // keys, about two workgroups per CU in all; a chunk then spans several LDS stages, which
-  // keeps the per-chunk partials (the merge's input) few.
-  auto attn_split = [&](int L, long long keys_total, int n_in_launch, int& chunk,
-                        int& n_chunks) {
-    const int kblocks = (L + 31) / 32;
-    int n_split;
-    if (n_in_launch == 1) {
-      n_split = std::max((kblocks + 4) / 5, (ctx->n_cu + NKV - 1) / NKV);
+  // MAX_CHUNKS.  Several sequences in one launch: a chunk then spans several LDS stages,
+  // which keeps the per-chunk partials (the merge's input) few.  The launch's grid
+  // enumerates only the chunks that exist (AttnArgs::chunk0).
+  // Several sequences: one chunk length for all, the shortest (a multiple of 32 keys) that
+  // needs at most 2 * ceil(n_cu / NKV) chunks in all, so the chunk workgroups fill two per
+  // CU in a single round and none of them is longer than the others.
+  auto attn_splits = [&](const int* L, int n, int* n_split) {
+    if (n == 1) {
+      const int kblocks = (L[0] + 31) / 32;
+      n_split[0] = std::max((kblocks + 4) / 5, (ctx->n_cu + NKV - 1) / NKV);
     } else {
-      const long long target = 2LL * ((ctx->n_cu + NKV - 1) / NKV);
-      n_split = (int)((target * L + keys_total - 1) / std::max(1LL, keys_total));
+      const long long target = std::max(n, 2 * ((ctx->n_cu + NKV - 1) / NKV));
+      long long total = 0;
+      for (int i = 0; i < n; ++i) total += L[i];
+      long long kb = std::max(1LL, (total + 32 * target - 1) / (32 * target));
+      for (;; ++kb) {
+        long long need = 0;
+        for (int i = 0; i < n; ++i) need += (L[i] + 32 * kb - 1) / (32 * kb);
+        if (need <= target) break;
+      }
+      for (int i = 0; i < n; ++i) n_split[i] = (int)((L[i] + 32 * kb - 1) / (32 * kb));
     }
-    n_split = std::max(1, std::min(std::min(MAX_CHUNKS, kblocks), n_split));
-    chunk = ((kblocks + n_split - 1) / n_split) * 32;
-    n_chunks = (L + chunk - 1) / chunk;
+    for (int i = 0; i < n; ++i)
+      n_split[i] = std::max(1, std::min(std::min(MAX_CHUNKS, (L[i] + 31) / 32), n_split[i]));
   };
+
 
   for (int l = 0; l < ctx->active; ++l) {
     Layer& Ly = ctx->layers[l];
@@ -838,12 +845,15 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
       at.Ml = ctx->Ml;
       at.O = ctx->attn;
       at.O_rows = blas ? ctx->h2 : nullptr;
-      long long kv_bytes = 0, keys_total = 0;
+      long long kv_bytes = 0;
+      int Ls[SEQ_MAX], n_split[SEQ_MAX];
       for (int i = 0; i < gn; ++i) {
         SeqState after = ctx->seqs[seq0 + g0 + i];
         after.append(B);
-        keys_total += after.key_range();
+        Ls[i] = after.key_range();
       }
+      attn_splits(Ls, gn, n_split);
+      at.chunk0[0] = 0;
       for (int i = 0; i < gn; ++i) {
         const int sidx = seq0 + g0 + i;
         rope_seq(ctx, sidx, Ly, ctx->seqs[sidx].offset, B, q.sq[i]);
@@ -859,8 +869,11 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
         as.ring_len = std::max(0, after.len - after.sink);
         as.sink_len = std::min(after.len, after.sink);
         as.o_row0 = (g0 + i) * B;
-        attn_split(as.L, keys_total, gn, as.chunk, as.n_chunks);
+        const int kblocks = (as.L + 31) / 32;
+        as.chunk = ((kblocks + n_split[i] - 1) / n_split[i]) * 32;
+        as.n_chunks = (as.L + as.chunk - 1) / as.chunk;
         at.max_chunks = std::max(at.max_chunks, as.n_chunks);
+        at.chunk0[i + 1] = at.chunk0[i] + as.n_chunks;
         kv_bytes += 2LL * NKV * as.L * 128 * 2;
       }
       if (!fuse_rope) {

@@ -53,18 +53,18 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 __global__ __launch_bounds__(768) void block_attn_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
-  const int c = blockIdx.x, g = blockIdx.y;
+  const int g = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
   const int KW = a.kw;
   const int qtl = wv / KW, kwi = wv - qtl * KW;        // query tile in group, key lane
   const int ratio = a.NH / a.NKV;
   const int R = ratio * a.B;
-  const int groups = ((R + 31) / 32 + a.q_per_group - 1) / a.q_per_group;
-  const int sidx = blockIdx.z / groups;                  // sequence
+  int sidx = 0;                                          // sequence of chunk blockIdx.x
+  while (sidx + 1 < a.n_seq && (int)blockIdx.x >= a.chunk0[sidx + 1]) ++sidx;
+  const int c = blockIdx.x - a.chunk0[sidx];             // chunk within the sequence
   const AttnSeq& sq = a.sq[sidx];
-  if (c >= sq.n_chunks) return;                          // this sequence has fewer chunks
-  const int qt = (blockIdx.z - sidx * groups) * a.q_per_group + qtl;
+  const int qt = blockIdx.z * a.q_per_group + qtl;
   const int q = lane & 31, gg = lane >> 5;
   const int rq = qt * 32 + q;
   const bool row_ok = rq < R;
@@ -302,7 +302,7 @@ void launch_block_attention(const AttnArgs& a_in, hipStream_t st) {
   const int groups = (n_qt + a.q_per_group - 1) / a.q_per_group;
   const int merge_bytes = a.q_per_group * (a.kw - 1) * AT_PART_BYTES;
   const int lds_bytes = std::max(AT_STAGE_BYTES, merge_bytes);
-  hipLaunchKernelGGL(block_attn_kernel, dim3(a.max_chunks, a.NKV, groups * a.n_seq),
+  hipLaunchKernelGGL(block_attn_kernel, dim3(a.chunk0[a.n_seq], a.NKV, groups),
                      dim3(64 * a.q_per_group * a.kw), lds_bytes, st, a);
   hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_seq * a.NH * a.B), dim3(128), 0, st, a);
 }

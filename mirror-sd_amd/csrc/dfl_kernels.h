@@ -203,6 +203,8 @@ struct AttnArgs {
   const half_t* Q;        // [n_seq][NH][B][128]
   int B, NH, NKV, cap;
   int n_seq, max_chunks;  // max_chunks = max over the sequences of n_chunks
+  // grid x enumerates the chunks of all sequences: sequence s owns [chunk0[s], chunk0[s+1])
+  int chunk0[SEQ_MAX + 1];
   int q_per_group, kw;    // set by the launcher: query tiles per workgroup, waves per tile
   float scale_log2;       // head_dim^-0.5 * log2(e)
   float* Op;              // [max_chunks][n_seq*NH*B][128] unnormalised partial outputs
