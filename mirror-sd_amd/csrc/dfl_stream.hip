@@ -28,7 +28,9 @@
 //
 // Epilogues: STORE (fp16 y with the per-row scale), RESID (x += fp16(y), per-tile row sums
 // of squares for the next GEMM's 1/rms), SWIGLU (gate/up row-blocks interleaved), ARGMAX
-// (fp32 logits + packed (value, index) atomicMax per row).
+// (fp32 logits + packed (value, index) atomicMax per row), QKROPE (the fused q|k|v rows
+// of one sequence: per-head Q/K RMSNorm + RoPE and the K/V cache writes; a head's two
+// tiles complete together).
 #include "dfl_common.h"
 #include "dfl_kernels.h"
 
@@ -280,37 +282,53 @@ DFL_DEV void stream_range(const StreamArgs& a, const half_t* gsh, const float* r
   for (int t = ct; t <= t_last; ++t) flush();
 }
 
-// Cross-worker completion of tile t.  `slot` is this worker's index among the `count`
-// workers covering the tile.  Returns true (with the full sums in acc0/acc1) for the last
-// worker to arrive; the others return false after publishing their partial.
-DFL_DEV bool finish_split_tile(const StreamArgs& a, int lane, int t, int slot, int count,
-                               floatx16& acc0, floatx16& acc1) {
-  float* mine = a.ws + ((size_t)t * a.seg_cap + slot) * 2048;
+// Split-tile slot (t, slot) of the workspace: a worker's fp32 partial of tile t.
+DFL_DEV float* ws_slot(const StreamArgs& a, int t, int slot) {
+  return a.ws + ((size_t)t * a.seg_cap + slot) * 2048;
+}
+
+// Publishes this worker's partial in slot (t, slot) and bumps counter `cnt` once the
+// stores have completed (agent-coherent); returns the counter's previous value.
+DFL_DEV int publish_partial(const StreamArgs& a, int lane, int t, int slot, int* cnt,
+                            const floatx16& acc0, const floatx16& acc1) {
+  float* mine = ws_slot(a, t, slot);
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     store_agent(mine + r * 64 + lane, acc0[r]);
     store_agent(mine + 1024 + r * 64 + lane, acc1[r]);
   }
-  // the partial stores complete (agent-coherent) before the counter moves
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0);
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   int prev = 0;
-  if (lane == 0)
-    prev = __hip_atomic_fetch_add(a.tile_cnt + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (lane == 0) prev = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   prev = __shfl(prev, 0, 64);
-  if (prev != count - 1) return false;
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  acc0 = (floatx16){};
-  acc1 = (floatx16){};
+  return prev;
+}
+
+// acc += slots 0 .. count-1 of tile t, in slot order (deterministic sums).
+DFL_DEV void add_slots(const StreamArgs& a, int lane, int t, int count, floatx16& acc0,
+                       floatx16& acc1) {
   for (int j = 0; j < count; ++j) {
-    const float* src = a.ws + ((size_t)t * a.seg_cap + j) * 2048;
+    const float* src = ws_slot(a, t, j);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       acc0[r] += load_agent(src + r * 64 + lane);
       acc1[r] += load_agent(src + 1024 + r * 64 + lane);
     }
   }
+}
+
+// Cross-worker completion of tile t.  `slot` is this worker's index among the `count`
+// workers covering the tile.  Returns true (with the full sums in acc0/acc1) for the last
+// worker to arrive; the others return false after publishing their partial.
+DFL_DEV bool finish_split_tile(const StreamArgs& a, int lane, int t, int slot, int count,
+                               floatx16& acc0, floatx16& acc1) {
+  if (publish_partial(a, lane, t, slot, a.tile_cnt + t, acc0, acc1) != count - 1) return false;
+  acc0 = (floatx16){};
+  acc1 = (floatx16){};
+  add_slots(a, lane, t, count, acc0, acc1);
   if (lane == 0) a.tile_cnt[t] = 0;   // next use is a later launch
   return true;
 }
@@ -459,13 +477,13 @@ DFL_DEV void reducer_norm_prologue(const StreamArgs& a, int lane, half_t* gsh, f
 // Reducer wave, segment si (tile t): waits for the 4 streaming waves' partials, sums them
 // in a fixed order, hands the slot set back and completes the tile -- directly when the
 // segment covers it (count == 1), else as worker `slot` of the `count` sharing it.
-template <int EPI>
-DFL_DEV void reduce_segment(const StreamArgs& a, int lane, float (*red)[WG_WAVES][2048],
-                            int* arrived, int* reduced, int si, int t, int slot, int count) {
+DFL_DEV void sum_wave_partials(int lane, float (*red)[WG_WAVES][2048], int* arrived,
+                               int* reduced, int si, floatx16& acc0, floatx16& acc1) {
   while (__hip_atomic_load(&arrived[si & 1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
          WG_WAVES * ((si >> 1) + 1))
     __builtin_amdgcn_s_sleep(1);
-  floatx16 acc0 = (floatx16){}, acc1 = (floatx16){};
+  acc0 = (floatx16){};
+  acc1 = (floatx16){};
 #pragma unroll 1
   for (int j = 0; j < WG_WAVES; ++j) {
     const float* src = red[si & 1][j];
@@ -477,6 +495,13 @@ DFL_DEV void reduce_segment(const StreamArgs& a, int lane, float (*red)[WG_WAVES
   }
   __builtin_amdgcn_s_waitcnt(0);   // slot reads done before the set is handed back
   if (lane == 0) __hip_atomic_store(reduced, si + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+template <int EPI>
+DFL_DEV void reduce_segment(const StreamArgs& a, int lane, float (*red)[WG_WAVES][2048],
+                            int* arrived, int* reduced, int si, int t, int slot, int count) {
+  floatx16 acc0, acc1;
+  sum_wave_partials(lane, red, arrived, reduced, si, acc0, acc1);
   const bool complete = count == 1 || finish_split_tile(a, lane, t, slot, count, acc0, acc1);
   if (complete) tile_epilogue<EPI>(a, lane, t, acc0, acc1);
 }
@@ -544,54 +569,13 @@ DFL_DEV void qk_head_epilogue(const StreamArgs& a, int lane, int h, const floatx
 DFL_DEV void reduce_head(const StreamArgs& a, int lane, float (*red)[WG_WAVES][2048],
                          int* arrived, int* reduced, int si, int t, int slot, int c_lo,
                          int c_hi) {
-  while (__hip_atomic_load(&arrived[si & 1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
-         WG_WAVES * ((si >> 1) + 1))
-    __builtin_amdgcn_s_sleep(1);
-  floatx16 acc0 = (floatx16){}, acc1 = (floatx16){};
-#pragma unroll 1
-  for (int j = 0; j < WG_WAVES; ++j) {
-    const float* src = red[si & 1][j];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      acc0[r] += src[r * 64 + lane];
-      acc1[r] += src[1024 + r * 64 + lane];
-    }
-  }
-  __builtin_amdgcn_s_waitcnt(0);   // slot reads done before the set is handed back
-  if (lane == 0) __hip_atomic_store(reduced, si + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-  float* mine = a.ws + ((size_t)t * a.seg_cap + slot) * 2048;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    store_agent(mine + r * 64 + lane, acc0[r]);
-    store_agent(mine + 1024 + r * 64 + lane, acc1[r]);
-  }
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  floatx16 acc0, acc1;
+  sum_wave_partials(lane, red, arrived, reduced, si, acc0, acc1);
   const int t0 = t & ~1;
-  int prev = 0;
-  if (lane == 0)
-    prev = __hip_atomic_fetch_add(a.tile_cnt + t0, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  prev = __shfl(prev, 0, 64);
-  if (prev != c_lo + c_hi - 1) return;
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  if (publish_partial(a, lane, t, slot, a.tile_cnt + t0, acc0, acc1) != c_lo + c_hi - 1) return;
   floatx16 lo0 = (floatx16){}, lo1 = (floatx16){}, hi0 = (floatx16){}, hi1 = (floatx16){};
-  for (int j = 0; j < c_lo; ++j) {
-    const float* src = a.ws + ((size_t)t0 * a.seg_cap + j) * 2048;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      lo0[r] += load_agent(src + r * 64 + lane);
-      lo1[r] += load_agent(src + 1024 + r * 64 + lane);
-    }
-  }
-  for (int j = 0; j < c_hi; ++j) {
-    const float* src = a.ws + ((size_t)(t0 + 1) * a.seg_cap + j) * 2048;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      hi0[r] += load_agent(src + r * 64 + lane);
-      hi1[r] += load_agent(src + 1024 + r * 64 + lane);
-    }
-  }
+  add_slots(a, lane, t0, c_lo, lo0, lo1);
+  add_slots(a, lane, t0 + 1, c_hi, hi0, hi1);
   if (lane == 0) a.tile_cnt[t0] = 0;   // next use is a later launch
   qk_head_epilogue(a, lane, t0 >> 1, lo0, lo1, hi0, hi1);
 }
