@@ -234,17 +234,17 @@ def test_window_cache_protocol_matches_oracle(sink, window):
         assert ocache[0].keys.shape[1] == sink + window - B   # eviction happened
 
 
-@pytest.mark.parametrize("sink,window,C", [(0, 0, 10), (4, 16, 20)])
-def test_block_rows_in_cache_match_oracle(sink, window, C):
+@pytest.mark.parametrize("sink,window,C,B", [(0, 0, 10, 8), (4, 16, 20, 8), (0, 0, 9, 5)])
+def test_block_rows_in_cache_match_oracle(sink, window, C, B):
     """The block's own K/V rows that a cached forward appends (dflash.py:287-308: context
     rows, then the block's rows, before the caller's trim) match the oracle's cache, row
     order included: the per-head Q/K norm, RoPE and cache writes of the fused qkv epilogue,
     through the ring slot map when a window is set (20 context rows + the block overflow
-    sink 4 + window 16, so the append itself evicts)."""
+    sink 4 + window 16, so the append itself evicts).  A 5-row block leaves most rows of
+    the 32-row activation tile empty."""
     wl, cfg, t, inp, W = _full_case("tiny", seed=3)
-    B = wl.block
     th = synth.np_normal(3, "blockrows.th", (C, 5 * cfg.hidden_size), 1.0, np.float16)
-    noise = O.embed(W, inp["ids"]).astype(np.float16)
+    noise = O.embed(W, inp["ids"][:B]).astype(np.float16)
     m = _model(cfg, max_ctx=C + B)
     m.load_weights(torch_tensors(t, "cuda"))
     cache = m.make_cache(sink, window)
