@@ -265,3 +265,25 @@ def test_block_rows_in_cache_match_oracle(sink, window, C, B):
         assert_close_fp16(k[:, -B:], ocache[layer].keys[:, -B:], what=f"layer {layer} block keys")
         assert_close_fp16(v[:, -B:], ocache[layer].values[:, -B:],
                           what=f"layer {layer} block values")
+
+
+@pytest.mark.parametrize("B,C", [(1, 1), (1, 0), (3, 0)])
+def test_minimum_block_and_context_match_oracle(B, C):
+    """The smallest calls: a one-row block, and a block with no context rows at all (the
+    block then attends only to itself, dflash.py:287-317), with and without a cache."""
+    wl, cfg, t, inp, W = _full_case("tiny", seed=4)
+    th = synth.np_normal(4, "minimum.th", (C, 5 * cfg.hidden_size), 1.0, np.float16)
+    noise = O.embed(W, inp["ids"][:B]).astype(np.float16)
+    ref = O.draft_forward(W, noise, th, fp16=True)
+    m = _model(cfg, max_ctx=C + B + 8)
+    m.load_weights(torch_tensors(t, "cuda"))
+    ne = torch.from_numpy(noise)[None]
+    out = m(ne, torch.from_numpy(th)[None])
+    torch.cuda.synchronize()
+    assert out.shape == (1, B, cfg.hidden_size)
+    assert_close_fp16(out[0].float().cpu().numpy(), ref, what=f"B={B} C={C} cache-less")
+    cache = m.make_cache(0, 0)
+    out = m(ne, torch.from_numpy(th)[None], cache=cache)
+    torch.cuda.synchronize()
+    assert cache[0].offset == C + B
+    assert_close_fp16(out[0].float().cpu().numpy(), ref, what=f"B={B} C={C} cached")
