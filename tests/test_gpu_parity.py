@@ -287,3 +287,39 @@ def test_minimum_block_and_context_match_oracle(B, C):
     torch.cuda.synchronize()
     assert cache[0].offset == C + B
     assert_close_fp16(out[0].float().cpu().numpy(), ref, what=f"B={B} C={C} cached")
+
+
+def test_capacity_boundaries():
+    """Context rows exactly at max_ctx (the block goes into the cache's own headroom of
+    max_block rows) draft and match the oracle; one context row more is rejected before
+    anything runs; a window of exactly one block (sink 2) keeps only the block's rows past
+    the sink, as the reference's eviction does (dflash.py:179-193)."""
+    wl, cfg, t, inp, W = _full_case("tiny", seed=5)
+    B = wl.block
+    C = 12
+    th = synth.np_normal(5, "capacity.th", (C + 1, 5 * cfg.hidden_size), 1.0, np.float16)
+    noise = O.embed(W, inp["ids"]).astype(np.float16)
+    ne = torch.from_numpy(noise)[None]
+    m = _model(cfg, max_ctx=C)
+    m.load_weights(torch_tensors(t, "cuda"))
+    cache = m.make_cache(0, 0)
+    out = m(ne, torch.from_numpy(th[:C])[None], cache=cache)
+    torch.cuda.synchronize()
+    assert_close_fp16(out[0].float().cpu().numpy(), O.draft_forward(W, noise, th[:C], fp16=True),
+                      what="exactly at capacity")
+    with pytest.raises(ValueError):
+        m(ne, torch.from_numpy(th)[None], cache=m.make_cache(0, 0))
+    # sink 2 + window B: the append evicts every context row past the sink
+    cache = m.make_cache(2, B)
+    ocache = [O.OracleKVCache(2, B) for _ in range(cfg.num_hidden_layers)]
+    ref = O.draft_forward(W, noise, th[:C], cache=ocache, fp16=True)
+    out = m(ne, torch.from_numpy(th[:C])[None], cache=cache)
+    torch.cuda.synchronize()
+    assert_close_fp16(out[0].float().cpu().numpy(), ref, what="window of one block")
+    m._sync_cache(list(cache))
+    for layer in range(cfg.num_hidden_layers):
+        assert cache[layer].keys.shape[2] == ocache[layer].keys.shape[1] == 2 + B
+        assert_close_fp16(cache[layer].keys[0].float().cpu().numpy(), ocache[layer].keys,
+                          what=f"layer {layer} keys")
+        assert_close_fp16(cache[layer].values[0].float().cpu().numpy(), ocache[layer].values,
+                          what=f"layer {layer} values")
