@@ -19,16 +19,6 @@ __global__ __launch_bounds__(ROW_THREADS) void embed_norm_kernel(
     int* __restrict__ err, float* __restrict__ rope_cs, long long pos0, double log2_theta) {
   __shared__ float sm[16];
   const int b = blockIdx.x;
-  if (rope_cs && threadIdx.x < 64) {
-    // RoPE angles of row b for the fused qkv epilogue, in fp64 as qk_rope_kernel computes
-    // them: position pos0 + b times theta^(-j/64)
-    const int j = threadIdx.x;
-    const double inv_freq = exp2(-(double)j * (1.0 / 64.0) * log2_theta);
-    double sd, cd;
-    sincos((double)(pos0 + b) * inv_freq, &sd, &cd);
-    rope_cs[2 * (b * 64 + j)] = (float)cd;
-    rope_cs[2 * (b * 64 + j) + 1] = (float)sd;
-  }
   const half_t* src = noise + (size_t)b * H;
   bool bad = false;
   if (ids) {
@@ -37,6 +27,23 @@ __global__ __launch_bounds__(ROW_THREADS) void embed_norm_kernel(
     src = embed + (size_t)(bad ? 0 : id) * H;
     if (bad && threadIdx.x == 0) atomicOr(err, 1);
   }
+  half_t e[ROW_MAXV];
+#pragma unroll
+  for (int i = 0; i < ROW_MAXV; ++i) {
+    const int k = threadIdx.x + i * ROW_THREADS;
+    e[i] = (k < H && !bad) ? src[k] : (half_t)0.0f;
+  }
+  if (rope_cs && threadIdx.x < 64) {
+    // RoPE angles of row b for the fused qkv epilogue (while the row's loads are in
+    // flight), in fp64 as qk_rope_kernel computes them: position pos0 + b times
+    // theta^(-j/64)
+    const int j = threadIdx.x;
+    const double inv_freq = exp2(-(double)j * (1.0 / 64.0) * log2_theta);
+    double sd, cd;
+    sincos((double)(pos0 + b) * inv_freq, &sd, &cd);
+    rope_cs[2 * (b * 64 + j)] = (float)cd;
+    rope_cs[2 * (b * 64 + j) + 1] = (float)sd;
+  }
   float v[ROW_MAXV];
   float ss = 0.f;
 #pragma unroll
@@ -44,9 +51,8 @@ __global__ __launch_bounds__(ROW_THREADS) void embed_norm_kernel(
     const int k = threadIdx.x + i * ROW_THREADS;
     v[i] = 0.f;
     if (k < H) {
-      const half_t t = bad ? (half_t)0.0f : src[k];
-      x[afl_index(b, k, H)] = t;   // residual stream in the activation fragment layout
-      v[i] = h2f(t);
+      x[afl_index(b, k, H)] = e[i];   // residual stream in the activation fragment layout
+      v[i] = h2f(e[i]);
       ss += v[i] * v[i];
     }
   }
