@@ -751,17 +751,18 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
   }
 
   // Attention key split.  One sequence: about one workgroup per CU ((chunks x KV heads) ~
-  // CUs) with chunks of at most 160 keys (one LDS stage) while there are at most
-  // MAX_CHUNKS.  Several sequences in one launch: a chunk then spans several LDS stages,
-  // which keeps the per-chunk partials (the merge's input) few.  The launch's grid
+  // CUs).  Several sequences in one launch: two per CU.  A long chunk spans several LDS
+  // stages, which keeps the per-chunk partials (the merge's input) few.  The launch's grid
   // enumerates only the chunks that exist (AttnArgs::chunk0).
   // Several sequences: one chunk length for all, the shortest (a multiple of 32 keys) that
   // needs at most 2 * ceil(n_cu / NKV) chunks in all, so the chunk workgroups fill two per
   // CU in a single round and none of them is longer than the others.
   auto attn_splits = [&](const int* L, int n, int* n_split) {
     if (n == 1) {
-      const int kblocks = (L[0] + 31) / 32;
-      n_split[0] = std::max((kblocks + 4) / 5, (ctx->n_cu + NKV - 1) / NKV);
+      // one workgroup per CU: at long contexts a chunk spans several LDS stages, which
+      // beats twice the chunks (and partials) at two workgroups per CU (32K keys: 1154 vs
+      // 1220 us per block)
+      n_split[0] = (ctx->n_cu + NKV - 1) / NKV;
     } else {
       const long long target = std::max(n, 2 * ((ctx->n_cu + NKV - 1) / NKV));
       long long total = 0;

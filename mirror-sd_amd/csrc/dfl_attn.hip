@@ -5,8 +5,9 @@
 // Data layout: Q [NH][B][128] (the ratio*B query rows of one KV head are contiguous),
 // K cache [NKV][cap][128], V cache transposed Vt [NKV][128][cap].
 //
-// Work split.  The keys are cut into chunks of <= 160 per split so that (splits x KV
-// heads) workgroups cover the CUs in one round.  One workgroup handles (chunk, KV head,
+// Work split.  The keys are cut into chunks so that (splits x KV heads) workgroups cover
+// the CUs in one round (one per CU for one sequence, two for several); a chunk longer than
+// 160 keys spans several LDS stages.  One workgroup handles (chunk, KV head,
 // group of query tiles): its K and V are read from HBM once, through LDS, and shared by
 // every query head of the KV head.  Each 32-row query tile gets KW waves that take the
 // chunk's 32-key blocks round-robin; their (max, sum, O) states are merged in LDS at the
