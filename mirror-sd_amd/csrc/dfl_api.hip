@@ -846,6 +846,7 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
       at.Ml = ctx->Ml;
       at.O = ctx->attn;
       at.O_rows = blas ? ctx->h2 : nullptr;
+      at.n_cu = ctx->n_cu;
       long long kv_bytes = 0;
       int Ls[SEQ_MAX], n_split[SEQ_MAX];
       for (int i = 0; i < gn; ++i) {

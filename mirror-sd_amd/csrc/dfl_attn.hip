@@ -52,7 +52,10 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 }  // namespace
 
-__global__ __launch_bounds__(768) void block_attn_kernel(AttnArgs a) {
+// PIPE (one sequence, chunks of several stages, one workgroup of <= 5 waves per CU): two
+// stage buffers (160 KiB), the next stage's loads in flight while this one computes.
+template <bool PIPE>
+__global__ __launch_bounds__(PIPE ? 320 : 768) void block_attn_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
   const int g = blockIdx.y;
   const int lane = threadIdx.x & 63;
@@ -73,7 +76,6 @@ __global__ __launch_bounds__(768) void block_attn_kernel(AttnArgs a) {
   // Q fragments (step st covers d = 64*gg + 8*st + 0..7), loaded after the first
   // stage's K/V loads are issued so the two latencies overlap.
   half8_t qf[8];
-  bool have_q = false;
   const uint4* qp = reinterpret_cast<const uint4*>(
       a.Q + ((size_t)sidx * a.NH * a.B + (size_t)g * R + (row_ok ? rq : 0)) * 128 +
       64 * gg);   // rows >= R: never stored
@@ -96,10 +98,10 @@ __global__ __launch_bounds__(768) void block_attn_kernel(AttnArgs a) {
   const half_t* vg = sq.Vt + (size_t)g * 128 * a.cap;
   const int vlast = (sq.L - 1) & ~7;   // last 8-key group holding a valid key
 
-  for (int k0 = k_begin; k0 < k_end; k0 += 32 * AT_STAGE_BLOCKS) {
+  // 16 segments per key block: 8 for K (4 key rows each), 8 for Vt (16 d rows each).
+  // Keys past L are clamped to valid addresses; they are masked (K) or meet p = 0 (V).
+  auto issue_stage = [&](int k0, unsigned char* buf) {
     const int nblk = min(AT_STAGE_BLOCKS, (k_end - k0 + 31) >> 5);
-    // 16 segments per key block: 8 for K (4 key rows each), 8 for Vt (16 d rows each).
-    // Keys past L are clamped to valid addresses; they are masked (K) or meet p = 0 (V).
     for (int sgi = wv; sgi < 16 * nblk; sgi += nw) {
       const int j = sgi >> 4, s = sgi & 15;
       const half_t* src;
@@ -109,26 +111,33 @@ __global__ __launch_bounds__(768) void block_attn_kernel(AttnArgs a) {
         const int cc = (lane & 15) ^ kswz(r);
         const int key = min(k0 + 32 * j + r, sq.L - 1);
         src = kg + (size_t)key * 128 + cc * 8;
-        dst = lds + j * AT_KBLK + s * 1024;
+        dst = buf + j * AT_KBLK + s * 1024;
       } else {
         const int d = 16 * (s - 8) + (lane >> 2);
         const int cc = (lane & 3) ^ vswz(d);
         src = vg + (size_t)d * a.cap + min(k0 + 32 * j + 8 * cc, vlast);
-        dst = lds + AT_STAGE_BLOCKS * AT_KBLK + j * AT_VBLK + (s - 8) * 1024;
+        dst = buf + AT_STAGE_BLOCKS * AT_KBLK + j * AT_VBLK + (s - 8) * 1024;
       }
       __builtin_amdgcn_global_load_lds((const void*)src, (lds_ptr_t)dst, 16, 0, 0);
     }
-    if (!have_q) {
+  };
+  // One buffer: issue a stage, wait, compute, repeat.  PIPE: the buffers alternate, and the
+  // next stage is issued into the other one before this one computes.
+  int k0 = k_begin, p = 0;
+  issue_stage(k0, lds);
 #pragma unroll
-      for (int st = 0; st < 8; ++st) qf[st] = as_half8(qp[st]);
-      have_q = true;
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+  for (int st = 0; st < 8; ++st) qf[st] = as_half8(qp[st]);   // overlaps the first stage
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (;;) {
+    const int nblk = min(AT_STAGE_BLOCKS, (k_end - k0 + 31) >> 5);
+    const int kn = k0 + 32 * AT_STAGE_BLOCKS;
+    const unsigned char* buf = lds + (PIPE ? p * AT_STAGE_BYTES : 0);
+    if (PIPE && kn < k_end) issue_stage(kn, lds + (p ^ 1) * AT_STAGE_BYTES);
 
     for (int j = kwi; j < nblk; j += KW) {
-      const unsigned char* kb_lds = lds + j * AT_KBLK + koff * 256;
-      const unsigned char* vb_lds = lds + AT_STAGE_BLOCKS * AT_KBLK + j * AT_VBLK;
+      const unsigned char* kb_lds = buf + j * AT_KBLK + koff * 256;
+      const unsigned char* vb_lds = buf + AT_STAGE_BLOCKS * AT_KBLK + j * AT_VBLK;
       floatx16 s = {};
       static_for<0, 8>([&](auto st) {
         const u32x4 kf =
@@ -191,8 +200,17 @@ __global__ __launch_bounds__(768) void block_attn_kernel(AttnArgs a) {
         o[dt] = mfma32x32x16(as_half8(v2), p2, o[dt]);
       });
     }
-    __syncthreads();   // the stage buffer is reused by the next stage (or the merge)
+    if (kn >= k_end) break;
+    if (!PIPE) {
+      __syncthreads();   // every wave is done with the single buffer
+      issue_stage(kn, lds);
+    }
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's loads of the next stage have landed
+    __syncthreads();                 // everyone's, and no wave reads the buffer they reuse
+    k0 = kn;
+    p ^= 1;
   }
+  __syncthreads();   // the stage buffers are reused by the merge
 
   // Merge the KW key lanes of each query tile (fixed order), then store the partial.
   if (KW > 1) {
@@ -303,8 +321,16 @@ void launch_block_attention(const AttnArgs& a_in, hipStream_t st) {
   const int groups = (n_qt + a.q_per_group - 1) / a.q_per_group;
   const int merge_bytes = a.q_per_group * (a.kw - 1) * AT_PART_BYTES;
   const int lds_bytes = std::max(AT_STAGE_BYTES, merge_bytes);
-  hipLaunchKernelGGL(block_attn_kernel, dim3(a.chunk0[a.n_seq], a.NKV, groups),
-                     dim3(64 * a.q_per_group * a.kw), lds_bytes, st, a);
+  // two stage buffers: one sequence whose chunks span several stages, one wave per query
+  // tile and at most 5 tiles, and at most one workgroup per CU (the LDS of two buffers)
+  const bool pipe = a.n_seq == 1 && a.sq[0].chunk > 32 * AT_STAGE_BLOCKS && a.kw == 1 &&
+                    a.q_per_group <= 5 && (long long)a.chunk0[1] * a.NKV * groups <= a.n_cu;
+  if (pipe)
+    hipLaunchKernelGGL(block_attn_kernel<true>, dim3(a.chunk0[a.n_seq], a.NKV, groups),
+                       dim3(64 * a.q_per_group), 2 * AT_STAGE_BYTES, st, a);
+  else
+    hipLaunchKernelGGL(block_attn_kernel<false>, dim3(a.chunk0[a.n_seq], a.NKV, groups),
+                       dim3(64 * a.q_per_group * a.kw), lds_bytes, st, a);
   hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_seq * a.NH * a.B), dim3(128), 0, st, a);
 }
 

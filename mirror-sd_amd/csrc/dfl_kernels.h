@@ -206,6 +206,7 @@ struct AttnArgs {
   // grid x enumerates the chunks of all sequences: sequence s owns [chunk0[s], chunk0[s+1])
   int chunk0[SEQ_MAX + 1];
   int q_per_group, kw;    // set by the launcher: query tiles per workgroup, waves per tile
+  int n_cu;
   float scale_log2;       // head_dim^-0.5 * log2(e)
   float* Op;              // [max_chunks][n_seq*NH*B][128] unnormalised partial outputs
   float* Ml;              // [max_chunks][n_seq*NH*B][2] running (max, sum) in log2 domain
