@@ -22,3 +22,18 @@ def _ensure_built():
 
 
 _ensure_built()
+
+
+def pytest_terminal_summary(terminalreporter):
+    """Session total of the draft-token agreement recorded by parity_util.check_argmax."""
+    try:
+        from parity_util import ARGMAX_TOTALS
+    except ImportError:
+        return
+    n = ARGMAX_TOTALS["rows"]
+    if n:
+        a = ARGMAX_TOTALS["agree"]
+        terminalreporter.write_line(
+            f"argmax agreement over {len(ARGMAX_TOTALS['cases'])} checks: {a}/{n} = {a / n:.4f} "
+            f"(exempt: {ARGMAX_TOTALS['undecided']} oracle-undecided, {ARGMAX_TOTALS['noise']} "
+            f"within the logit noise)")

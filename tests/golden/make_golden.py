@@ -23,6 +23,12 @@ so a test can tell a change of the input recipe from a change of the results:
 
 The oracle runs in its fp16-boundary mode (the MLX rounding points) with fp32
 accumulation for the two full models, fp64 for the single layer.
+
+Every fixture with argmax ids also holds ``ids_f64`` / ``top2_val_f64``: the same forward
+with fp64 accumulation (same fp16 rounding points).  A row whose argmax differs between
+the two runs is decided by accumulation rounding alone; those rows are the only ones the
+GPU parity tests may exempt from exact argmax agreement.  ``--add-f64`` adds these arrays
+to existing fixtures without touching the rest.
 """
 
 from __future__ import annotations
@@ -77,7 +83,15 @@ def case_layer(name="qwen3_4b_layer", seed=0):
         input_digests(t, inp)
 
 
-def case_full(name, seed=0):
+def f64_outputs(W, inp):
+    """ids and top-2 logits of the fp64-accumulation run (fp16 rounding points kept)."""
+    _, logits, ids = O.draft_block(W, inp["ids"], inp["target_hidden"], fp16=True,
+                                   dtype=np.float64)
+    _, tv = top2(logits)
+    return ids.astype(np.int32), tv
+
+
+def case_full(name, seed=0, f64_only=False):
     wl = workload(name)
     cfg = wl.cfg
     t = synth.make_weights_numpy(cfg, seed=seed)
@@ -85,14 +99,17 @@ def case_full(name, seed=0):
     dig = input_digests(t, inp)
     W = O.OracleWeights(cfg, t)
     del t
+    ids64, tv64 = f64_outputs(W, inp)
+    if f64_only:
+        return dict(ids_f64=ids64, top2_val_f64=tv64), dig
     h, logits, ids = O.draft_block(W, inp["ids"], inp["target_hidden"], fp16=True,
                                    dtype=np.float32)
     ti, tv = top2(logits)
     return dict(hidden=h.astype(np.float16), ids=ids.astype(np.int32), top2_idx=ti,
-                top2_val=tv), dig
+                top2_val=tv, ids_f64=ids64, top2_val_f64=tv64), dig
 
 
-def case_batch(name="llama8b_batch", seed=0):
+def case_batch(name="llama8b_batch", seed=0, f64_only=False):
     wl = workload(name)
     cfg = wl.cfg
     t = synth.make_weights_numpy(cfg, seed=seed)
@@ -100,8 +117,13 @@ def case_batch(name="llama8b_batch", seed=0):
     dig = input_digests(t, {f"{k}.s{i}": v for i, inp in enumerate(inps) for k, v in inp.items()})
     W = O.OracleWeights(cfg, t)
     del t
-    hs, idss, tis, tvs = [], [], [], []
+    hs, idss, tis, tvs, i64s, v64s = [], [], [], [], [], []
     for inp in inps:
+        ids64, tv64 = f64_outputs(W, inp)
+        i64s.append(ids64)
+        v64s.append(tv64)
+        if f64_only:
+            continue
         h, logits, ids = O.draft_block(W, inp["ids"], inp["target_hidden"], fp16=True,
                                        dtype=np.float32)
         ti, tv = top2(logits)
@@ -109,29 +131,44 @@ def case_batch(name="llama8b_batch", seed=0):
         idss.append(ids.astype(np.int32))
         tis.append(ti)
         tvs.append(tv)
+    f64 = dict(ids_f64=np.concatenate(i64s), top2_val_f64=np.concatenate(v64s))
+    if f64_only:
+        return f64, dig
     return dict(hidden=np.concatenate(hs), ids=np.concatenate(idss), top2_idx=np.concatenate(tis),
-                top2_val=np.concatenate(tvs)), dig
+                top2_val=np.concatenate(tvs), **f64), dig
 
 
 CASES = {
-    "qwen3_4b_layer": lambda: case_layer("qwen3_4b_layer"),
-    "qwen3_8b_draft": lambda: case_full("qwen3_8b_draft"),
-    "dflash_27b": lambda: case_full("dflash_27b"),
-    **{f"dflash_27b_ctx{c}": (lambda c=c: case_full(f"dflash_27b_ctx{c}"))
+    "qwen3_4b_layer": lambda f64_only=False: case_layer("qwen3_4b_layer"),
+    "qwen3_8b_draft": lambda f64_only=False: case_full("qwen3_8b_draft", f64_only=f64_only),
+    "dflash_27b": lambda f64_only=False: case_full("dflash_27b", f64_only=f64_only),
+    **{f"dflash_27b_ctx{c}": (lambda f64_only=False, c=c:
+                              case_full(f"dflash_27b_ctx{c}", f64_only=f64_only))
        for c in (64, 2048, 16384, 32768)},
-    "llama8b_batch": lambda: case_batch("llama8b_batch"),
+    "llama8b_batch": lambda f64_only=False: case_batch("llama8b_batch", f64_only=f64_only),
 }
+ARGMAX_CASES = [n for n in CASES if n != "qwen3_4b_layer"]
 
 
 def main(argv):
-    names = argv or list(CASES)
+    add_f64 = "--add-f64" in argv
+    names = [a for a in argv if not a.startswith("--")] or \
+        (ARGMAX_CASES if add_f64 else list(CASES))
     for n in names:
         t0 = time.time()
-        out, dig = CASES[n]()
+        path = os.path.join(HERE, f"{n}.npz")
+        out, dig = CASES[n](f64_only=add_f64)
         keys = sorted(dig)
-        np.savez_compressed(os.path.join(HERE, f"{n}.npz"), **out,
-                            digest_names=np.array(keys), digest_values=np.array(
-                                [dig[k] for k in keys], dtype=np.uint32))
+        if add_f64:   # keep the stored outputs; the inputs must be the ones they came from
+            with np.load(path) as old:
+                kept = {k: old[k] for k in old.files}
+            assert dict(zip(kept["digest_names"].tolist(),
+                            kept["digest_values"].tolist())) == dig, f"{n}: inputs changed"
+            kept.update(out)
+            np.savez_compressed(path, **kept)
+        else:
+            np.savez_compressed(path, **out, digest_names=np.array(keys),
+                                digest_values=np.array([dig[k] for k in keys], dtype=np.uint32))
         print(f"{n}: {time.time() - t0:.1f} s, outputs {sorted(out)}", flush=True)
 
 

@@ -5,9 +5,10 @@ The fixtures hold the oracle's outputs for the seeded synthetic inputs of
 block 16, context 2048) and the 27B-class headline draft (5 layers, H5120, block 32,
 context 4096), so the HIP path is checked at full size without running the oracle on
 the GPU host.  Tolerances: final hidden cosine >= 0.9995 and max-abs <= 2e-2 (fp16);
-argmax identical except where the oracle's top-2 logits lie within LOGIT_TOL of each
-other and the GPU picked the runner-up; GPU logits at the oracle's top-2 indices within
-LOGIT_TOL of the oracle's values.
+argmax identical on every row except where the oracle itself is undecided (its fp32- and
+fp64-accumulation runs disagree and the GPU took one of the two ids;
+parity_util.check_argmax prints the counts); GPU logits at the oracle's top-2 indices
+within LOGIT_TOL of the oracle's values.
 """
 
 import os
@@ -18,7 +19,7 @@ import pytest
 from golden.make_golden import input_digests
 from mirror_sd_amd import synth
 from mirror_sd_amd.config import workload
-from parity_util import assert_close_fp16, device_errors, torch_tensors
+from parity_util import assert_close_fp16, check_argmax, device_errors, torch_tensors
 
 pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
@@ -70,13 +71,8 @@ def test_full_draft_matches_golden(name):
     assert_close_fp16(h.float().cpu().numpy(), g["hidden"], what=f"{name} final hidden")
     lg = logits.cpu().numpy()
     ids = ids.cpu().numpy()
-    np.testing.assert_array_equal(ids, np.argmax(lg, axis=-1))
-    got_top = np.take_along_axis(lg, g["top2_idx"].astype(np.int64), axis=-1)
-    assert np.abs(got_top - g["top2_val"]).max() < LOGIT_TOL
-    gap = g["top2_val"][:, 0] - g["top2_val"][:, 1]
-    near_tie = (gap < LOGIT_TOL) & (ids == g["top2_idx"][:, 1])
-    bad = (ids != g["ids"]) & ~near_tie
-    assert not bad.any(), f"{name}: argmax differs at rows {np.nonzero(bad)[0].tolist()}"
+    check_argmax(ids, lg, g["ids"], g["ids_f64"], name, g["top2_idx"], g["top2_val"], LOGIT_TOL,
+                 noise_rule=False)
     # the lm_head hands half tiles out at run time from self-resetting counters: later
     # launches on the same inputs give the same bits, and no queue wait gave up
     for rep in range(2):
@@ -117,15 +113,8 @@ def sweep_model():
 
 def _check_against(g, name, ids, logits, h):
     assert_close_fp16(h.float().cpu().numpy(), g["hidden"], what=f"{name} final hidden")
-    lg = logits.cpu().numpy()
-    ids = ids.cpu().numpy()
-    np.testing.assert_array_equal(ids, np.argmax(lg, axis=-1))
-    got_top = np.take_along_axis(lg, g["top2_idx"].astype(np.int64), axis=-1)
-    assert np.abs(got_top - g["top2_val"]).max() < LOGIT_TOL
-    gap = g["top2_val"][:, 0] - g["top2_val"][:, 1]
-    near_tie = (gap < LOGIT_TOL) & (ids == g["top2_idx"][:, 1])
-    bad = (ids != g["ids"]) & ~near_tie
-    assert not bad.any(), f"{name}: argmax differs at rows {np.nonzero(bad)[0].tolist()}"
+    check_argmax(ids.cpu().numpy(), logits.cpu().numpy(), g["ids"], g["ids_f64"], name,
+                 g["top2_idx"], g["top2_val"], LOGIT_TOL, noise_rule=False)
 
 
 @pytest.mark.parametrize("ctx", SWEEP)
