@@ -189,6 +189,21 @@ int dfl_embed_block(dfl_ctx* ctx, const int32_t* ids, int32_t B, const void* cor
                     int32_t logits_dtype, int32_t V, int32_t top_k, uint16_t* out_noise,
                     void* stream);
 
+/* No counterpart in the reference: the block noise embedding of dfl_embed_block for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No context is needed: the caller passes the embedding
+ * table embed [Vemb][H] fp16 (16-byte aligned rows, H % 8 == 0) and a device word err_flags
+ * that receives the same error bits as dfl_device_errors (OR'ed in; bit 0 a token id outside
+ * [0, Vemb), bit 1 soft-anchor logits without a single number).  Other arguments, checks and
+ * results as dfl_embed_block.  The soft anchor's top-k candidates go to a fixed 4 KiB device
+ * array of the library (64 scan workgroups x 8 keys, one copy per GPU, held until the process
+ * ends), so the call allocates nothing; concurrent calls on one GPU share that array and
+ * race, so a caller serialises them (one stream, or events between streams). */
+int dfl_embed_block_noalloc(const int32_t* ids, int32_t B, const uint16_t* embed, int32_t Vemb,
+                            int32_t H, const void* correction_logits, int32_t logits_dtype,
+                            int32_t V, int32_t top_k, uint16_t* out_noise, int32_t* err_flags,
+                            void* stream);
+
 /* Sticky device-side error flags (bit 0: a token id outside [0, vocab); bit 1: soft-anchor
  * logits without a single number; bit 2: a work-queue wait of the lm_head gave up, its
  * results are invalid); reading clears. */

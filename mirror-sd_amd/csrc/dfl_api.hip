@@ -4,6 +4,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -1125,6 +1126,69 @@ int dfl_embed_block(dfl_ctx* ctx, const int32_t* ids, int32_t B, const void* cor
                      top_k, ctx->sa_cand, reinterpret_cast<half_t*>(out_noise), ctx->err,
                      (hipStream_t)stream);
   return check_launch(w.c_str());
+}
+
+}  // extern "C"
+
+// Candidate keys of the allocation-free soft anchor: one fixed array per GPU (the topk scan
+// writes every entry before the embedding kernel reads it, so nothing needs clearing).
+// Host code uses the per-device address from hipGetSymbolAddress, never the array's name.
+namespace {
+constexpr int NOALLOC_MAX_DEVICES = 64;
+static __device__ __align__(256) unsigned long long scratch[SA_BLOCKS * SA_TOPK_MAX];
+std::mutex g_scratch_mu;
+unsigned long long* g_scratch_ptr[NOALLOC_MAX_DEVICES] = {};
+
+// This device's copy of `scratch`, resolved once per device (with that device current).
+int noalloc_scratch(unsigned long long** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(DFL_EHIP, std::string("hipGetDevice: ") + hipGetErrorString(e));
+  if (dev < 0 || dev >= NOALLOC_MAX_DEVICES)
+    return fail(DFL_EINVAL, "dfl_embed_block_noalloc: device index outside [0, 64)");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(DFL_EHIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<unsigned long long*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return DFL_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int dfl_embed_block_noalloc(const int32_t* ids, int32_t B, const uint16_t* embed, int32_t Vemb,
+                            int32_t H, const void* correction_logits, int32_t logits_dtype,
+                            int32_t V, int32_t top_k, uint16_t* out_noise, int32_t* err_flags,
+                            void* stream) {
+  if (!ids || !embed || !out_noise || !err_flags)
+    return fail(DFL_EINVAL, "dfl_embed_block_noalloc: null argument");
+  if (Vemb < 1 || H < 8 || H % 8 || (reinterpret_cast<uintptr_t>(embed) & 15))
+    return fail(DFL_EINVAL, "dfl_embed_block_noalloc: embedding must have >= 1 row, H a "
+                            "multiple of 8 and 16-byte alignment");
+  if (B < 1 || B > 65535)
+    return fail(DFL_EINVAL, "dfl_embed_block_noalloc: block rows must be in [1, 65535]");
+  if (correction_logits) {
+    if (logits_dtype < 0 || logits_dtype > 2)
+      return fail(DFL_EINVAL, "dfl_embed_block_noalloc: logits_dtype must be 0 (fp32), 1 (fp16) "
+                              "or 2 (bf16)");
+    if (top_k < 1 || top_k > SA_TOPK_MAX)
+      return fail(DFL_EINVAL, "dfl_embed_block_noalloc: top_k must be in [1, " +
+                                  std::to_string(SA_TOPK_MAX) + "] (the fixed candidate array "
+                                  "holds 64 x 8 keys)");
+    if (V < top_k || V > Vemb)
+      return fail(DFL_EINVAL, "dfl_embed_block_noalloc: logits length must be in [top_k, Vemb]");
+  }
+  unsigned long long* cand = nullptr;
+  DFL_TRY(noalloc_scratch(&cand));
+  launch_embed_block(ids, B, reinterpret_cast<const half_t*>(embed), Vemb, H, correction_logits,
+                     logits_dtype, V, top_k, cand, reinterpret_cast<half_t*>(out_noise),
+                     reinterpret_cast<int*>(err_flags), (hipStream_t)stream);
+  return check_launch("dfl_embed_block_noalloc");
 }
 
 int dfl_device_errors(dfl_ctx* ctx, int32_t* flags, void* stream) {

@@ -74,6 +74,9 @@ SIGNATURES = {
                                    ctypes.POINTER(c_int32)]),
     "dfl_embed_block": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p, c_int32, c_int32,
                                   c_int32, c_void_p, c_void_p]),
+    "dfl_embed_block_noalloc": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_int32, c_void_p,
+                                          c_int32, c_int32, c_int32, c_void_p, c_void_p,
+                                          c_void_p]),
     "dfl_device_errors": (c_int32, [c_void_p, ctypes.POINTER(c_int32), c_void_p]),
 }
 

@@ -71,6 +71,24 @@ def test_null_context_errors():
     assert "null" in lib.dfl_last_error().decode()
 
 
+def test_noalloc_embed_block_validates_before_device_work():
+    """dfl_embed_block_noalloc rejects bad arguments before it touches a device (these
+    pointers are never dereferenced)."""
+    lib = _lib.load()
+    fake = ctypes.c_void_p(4096)   # 16-byte aligned, never read
+    args = lambda **o: dict(dict(ids=fake, B=4, embed=fake, Vemb=1024, H=256, lg=None, dt=0,
+                                 V=0, k=8, out=fake, err=fake), **o)
+    call = lambda a: lib.dfl_embed_block_noalloc(a["ids"], a["B"], a["embed"], a["Vemb"], a["H"],
+                                                 a["lg"], a["dt"], a["V"], a["k"], a["out"],
+                                                 a["err"], None)
+    for bad, needle in [(dict(ids=None), "null"), (dict(err=None), "null"), (dict(H=100), "H"),
+                        (dict(embed=ctypes.c_void_p(4100)), "alignment"), (dict(B=0), "rows"),
+                        (dict(lg=fake, dt=3, V=64), "logits_dtype"),
+                        (dict(lg=fake, V=64, k=9), "top_k"), (dict(lg=fake, V=2048), "length")]:
+        assert call(args(**bad)) == _lib.DFL_EINVAL, bad
+        assert needle in lib.dfl_last_error().decode(), (bad, lib.dfl_last_error())
+
+
 def test_build_target_layer_ids():
     assert build_target_layer_ids(36, 5) == [1, 9, 17, 25, 33]
     assert build_target_layer_ids(36, 1) == [18]
