@@ -39,11 +39,11 @@ typedef struct dfl_ctx dfl_ctx;
 
 /* Model dimensions; field meaning follows DFlashConfig (mirror_sd/dflash.py:34-50). */
 typedef struct dfl_config {
-  int32_t hidden;          /* hidden_size                                  */
+  int32_t hidden;          /* hidden_size (multiple of 128, <= 8192)       */
   int32_t n_heads;         /* num_attention_heads                          */
   int32_t n_kv_heads;      /* num_key_value_heads (n_heads % n_kv_heads == 0) */
   int32_t head_dim;        /* head_dim; must be 128                        */
-  int32_t intermediate;    /* intermediate_size                            */
+  int32_t intermediate;    /* intermediate_size (multiple of 128)          */
   int32_t n_layers;        /* num_hidden_layers (draft layers)             */
   int32_t n_target_feat;   /* len(target_layer_ids); fc input = n_target_feat*hidden; 0 = no fc */
   int32_t vocab;           /* vocab_size of embedding / lm_head; 0 = none  */

@@ -275,12 +275,12 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
   *out = nullptr;
   const dfl_config& c = *cfg;
   if (c.head_dim != 128) return fail(DFL_EINVAL, "dfl_create: head_dim must be 128");
-  if (c.hidden <= 0 || c.hidden % 64 || c.hidden > 8192)
-    return fail(DFL_EINVAL, "dfl_create: hidden must be a positive multiple of 64, <= 8192");
+  if (c.hidden <= 0 || c.hidden % 128 || c.hidden > 8192)
+    return fail(DFL_EINVAL, "dfl_create: hidden must be a positive multiple of 128, <= 8192");
   if (c.n_heads <= 0 || c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads)
     return fail(DFL_EINVAL, "dfl_create: n_heads must be a positive multiple of n_kv_heads");
-  if (c.intermediate <= 0 || c.intermediate % 32 || c.intermediate > 8192 * 8)
-    return fail(DFL_EINVAL, "dfl_create: intermediate must be a positive multiple of 32");
+  if (c.intermediate <= 0 || c.intermediate % 128 || c.intermediate > 8192 * 8)
+    return fail(DFL_EINVAL, "dfl_create: intermediate must be a positive multiple of 128");
   if (c.n_layers <= 0) return fail(DFL_EINVAL, "dfl_create: n_layers must be positive");
   if (c.vocab < 0 || c.vocab % 64) return fail(DFL_EINVAL, "dfl_create: vocab must be a multiple of 64");
   if (c.max_block <= 0 || c.max_block > 256)
@@ -341,7 +341,8 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
     for (auto pr : {std::make_pair(x->sk_qkv, x->NQKV), std::make_pair(x->sk_o, x->H),
                     std::make_pair(x->sk_gu, 2 * x->F), std::make_pair(x->sk_down, x->H),
                     std::make_pair(x->sk_lm, std::max(x->V, 64))}) {
-      wsn = std::max(wsn, (size_t)(pr.second / 64) * pr.first.seg_cap * 2048);
+      wsn = std::max(wsn, (size_t)(pr.second / 64) *
+                              std::max(pr.first.seg_cap, pr.first.sk_seg_cap) * 2048);
       tiles = std::max(tiles, (size_t)(pr.second / 64));
     }
     const size_t bm32 = ((Bm + 31) / 32) * 32;
@@ -534,7 +535,10 @@ static int skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const SKPlan& p,
     a.ss_mstride = ss_stride;
     a.gnorm = gnorm;
     a.ws = ctx->sk_ws;
-    a.seg_cap = p.seg_cap;
+    // one m-tile: the hybrid plan when it has whole tiles per workgroup; the M-split kernel
+    // keeps the contiguous partition
+    a.dp = mt_n == 1 ? p.dp : 0;
+    a.seg_cap = a.dp > 0 ? p.sk_seg_cap : p.seg_cap;
     a.tile_cnt = ctx->sk_tile_cnt;
     a.out = out ? out + (size_t)m0 * ldo : nullptr;
     a.ldo = ldo;

@@ -67,12 +67,16 @@ struct StreamArgs {
   int* err;                 // device error word (bit 2: a work-queue wait gave up)
   int32_t* ids;             // balanced ARGMAX: the last workgroup turns keys [M] into ids [M]
                             // (-1 for a row without a number) and re-arms keys to zero
+  int dp;                   // hybrid plan (SKPlan::dp): whole tiles per workgroup
   RopeEpi rope;             // EPI_QKROPE
 };
 struct SKPlan {
   int workers = 1;          // workgroups (one per CU)
-  int seg_cap = 1;          // workspace slots per tile
+  int seg_cap = 1;          // workspace slots per tile (contiguous partition)
   int dyn_static = 0;       // > 0: balanced mode with this many whole tiles per workgroup
+  int dp = 0;               // > 0: hybrid plan, whole tiles per workgroup after the split
+                            // units of the first N/64 - dp * workers tiles
+  int sk_seg_cap = 0;       // hybrid plan: workspace slots per split tile
 };
 SKPlan streamk_plan(int N, int KB, int n_cu);
 // Balanced plan for a long matrix (the lm_head): most tiles statically, whole, and the

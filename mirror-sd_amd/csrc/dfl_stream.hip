@@ -149,19 +149,21 @@ DFL_DEV float rn_from_ss(const float* ss, int tiles, int n, float eps, int lane)
 }
 
 // ---------------------------------------------------------------------------------------
-// Streaming wave w takes units u0 + w, u0 + w + WG_WAVES, ... of the workgroup's range
-// [u0, u1) (unit = 64-row wave-tile t x k-block kb, u = t * KB + kb), crossing tile
-// boundaries in one continuous load pipeline.  Two register stages of P units alternate
-// (sched_barrier keeps each stage's loads issued ahead of use); loads past the wave's last
-// unit repeat its address and are not consumed.  Every tile the range touches is one
-// segment: when the wave leaves a tile it hands its fp32 partial (two 32x32 accumulators,
-// zero if it had no unit there) to the reducer wave through LDS slot set (segment & 1),
-// while the next tile's loads are already in flight.
+// Streaming wave w walks the workgroup's work list -- units [u0, u1), then [v0, v1) (unit
+// = 64-row wave-tile t x k-block kb, u = t * KB + kb) -- taking every WG_WAVES-th unit of
+// the concatenation (w, w + WG_WAVES, ...) in one continuous load pipeline.  Two register
+// stages of P units alternate (sched_barrier keeps each stage's loads issued ahead of use);
+// loads past the wave's last unit repeat its address and are not consumed.  Every tile a
+// range touches is one segment, numbered in list order; when the wave leaves a segment it
+// hands its fp32 partial (two 32x32 accumulators, zero if it had no unit there) to the
+// reducer wave through LDS slot set (segment & 1), while the next units' loads are already
+// in flight.
 // ---------------------------------------------------------------------------------------
 template <int WT, bool NORM, int P>
 DFL_DEV void stream_range(const StreamArgs& a, const half_t* gsh, const float* rn_lds,
                           int* ready, float (*red)[WG_WAVES][2048], int* arrived, int* reduced,
-                          long long u0, long long u1, int w, int lane, int& si) {
+                          long long u0, long long u1, long long v0, long long v1, int w,
+                          int lane, int& si) {
   constexpr int KBK = KTraits<WT>::KBK;
   constexpr int NX = KTraits<WT>::NX;
   const int m = lane & 31, g = lane >> 5;
@@ -190,18 +192,34 @@ DFL_DEV void stream_range(const StreamArgs& a, const half_t* gsh, const float* r
     ++si;
   };
 
-  const int t_first = (int)(u0 / KB);
-  const int t_last = (int)((u1 - 1) / KB);
-  const long long g0 = u0 + w;
-  const int J = g0 < u1 ? (int)((u1 - g0 + WG_WAVES - 1) / WG_WAVES) : 0;
-  int ct = (int)(min(g0, u1 - 1) / KB);          // consume cursor: tile of the next unit
-  for (int t = t_first; t < ct; ++t) flush();   // leading tiles without a unit of this wave
+  const int len1 = (int)(u1 - u0), len = len1 + (int)(v1 - v0);
+  const int nseg1 = len1 > 0 ? (int)((u1 - 1) / KB - u0 / KB + 1) : 0;
+  const int nseg = nseg1 + (v1 > v0 ? (int)((v1 - 1) / KB - v0 / KB + 1) : 0);
+  const int J = w < len ? (len - w + WG_WAVES - 1) / WG_WAVES : 0;
+  // units of this wave in the first range; its first unit of the second range is list
+  // position w + WG_WAVES * J1
+  const int J1 = w < len1 ? (len1 - w + WG_WAVES - 1) / WG_WAVES : 0;
+  int cs = 0;   // consume cursor: segment of the next unit (segments before it are flushed)
   if (J > 0) {
-    // issue cursor (t, kb) of the next unit to load; advanced by WG_WAVES (< KB) units
-    int it = ct, ikb = (int)(g0 - (long long)ct * KB), issued = 0;
+    // issue cursor: tile it, k-block ikb, segment isg of the next unit (KB >= WG_WAVES);
+    // the second range starts at (it2, ikb2, isg2)
+    int it, ikb, isg, it2 = 0, ikb2 = 0, isg2 = 0;
+    {
+      const long long ua = w < len1 ? u0 + w : v0 + (w - len1);
+      it = (int)(ua / KB);
+      ikb = (int)(ua - (long long)it * KB);
+      isg = w < len1 ? it - (int)(u0 / KB) : nseg1 + it - (int)(v0 / KB);
+      if (J1 > 0 && J1 < J) {
+        const long long ub = v0 + (w + WG_WAVES * J1 - len1);
+        it2 = (int)(ub / KB);
+        ikb2 = (int)(ub - (long long)it2 * KB);
+        isg2 = nseg1 + it2 - (int)(v0 / KB);
+      }
+    }
+    int issued = 0;
     struct Stage {
       u32x4 w0[P], w1[P], x[P][NX];
-      int kb[P], t[P];
+      int kb[P], sg[P];
     };
     auto issue = [&](Stage& st) {
       static_for<0, P>([&](auto s) {
@@ -209,7 +227,7 @@ DFL_DEV void stream_range(const StreamArgs& a, const half_t* gsh, const float* r
         st.w0[s] = load_stream(wp);
         st.w1[s] = load_stream(wp + (size_t)KB * 64);
         st.kb[s] = ikb;
-        st.t[s] = it;
+        st.sg[s] = isg;
         if constexpr (WT == WT_INT8) {
           st.x[s][0] = xf[(size_t)(2 * ikb) * 64 + lane];
           st.x[s][NX - 1] = xf[(size_t)(2 * ikb + 1) * 64 + lane];
@@ -217,10 +235,17 @@ DFL_DEV void stream_range(const StreamArgs& a, const half_t* gsh, const float* r
           st.x[s][0] = xf[(size_t)((ikb >> 1) * 2 + g) * 64 + m + 32 * (ikb & 1)];
         }
         if (++issued < J) {
-          ikb += WG_WAVES;
-          while (ikb >= KB) {   // KB may be smaller than WG_WAVES
-            ikb -= KB;
-            ++it;
+          if (issued == J1) {   // into the second range
+            it = it2;
+            ikb = ikb2;
+            isg = isg2;
+          } else {
+            ikb += WG_WAVES;
+            if (ikb >= KB) {
+              ikb -= KB;
+              ++it;
+              ++isg;
+            }
           }
         }
       });
@@ -229,9 +254,9 @@ DFL_DEV void stream_range(const StreamArgs& a, const half_t* gsh, const float* r
     auto consume = [&](const Stage& st, int base) {
       static_for<0, P>([&](auto s) {
         if (base + (int)s < J) {
-          while (ct < st.t[s]) {   // left a tile (or tiles): hand over its partial
+          while (cs < st.sg[s]) {   // left a segment (or segments): hand over its partial
             flush();
-            ++ct;
+            ++cs;
           }
           u32x4 xa = st.x[s][0], xb = st.x[s][NX - 1];
           if constexpr (NORM) {
@@ -278,8 +303,8 @@ DFL_DEV void stream_range(const StreamArgs& a, const half_t* gsh, const float* r
       consume(B, base + P);
     }
   }
-  // the tile of the last unit, then trailing tiles without a unit of this wave
-  for (int t = ct; t <= t_last; ++t) flush();
+  // the segment of the last unit, then trailing segments without a unit of this wave
+  for (; cs < nseg; ++cs) flush();
 }
 
 // Split-tile slot (t, slot) of the workspace: a worker's fp32 partial of tile t.
@@ -333,12 +358,47 @@ DFL_DEV bool finish_split_tile(const StreamArgs& a, int lane, int t, int slot, i
   return true;
 }
 
-// Epilogue of a completed tile t for the 32 activation rows held by this wave.
+// Global inputs of a tile's epilogue, loaded ahead of it (before the reducer waits for
+// the streaming waves' partials) so that completing the launch's last tiles costs no load
+// latency: the per-row scales of the lane's 32 rows and, for RESID, its residual values.
+struct EpiIn {
+  half4_t s0[4], s1[4];   // scale[nb + 8q + 0..3], scale[nb + 32 + 8q + 0..3]
+  half4_t xv[2][4];       // RESID: x row m, columns nb + 32 tt + 8 q + 0..3
+};
+
+template <int EPI>
+DFL_DEV EpiIn epi_prefetch(const StreamArgs& a, int lane, int t) {
+  EpiIn in;
+  const int m = lane & 31, g = lane >> 5;
+  const int nb = (2 * t) * 32 + 4 * g;
+  if (a.scale) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      in.s0[q] = *reinterpret_cast<const half4_t*>(a.scale + nb + 8 * q);
+      in.s1[q] = *reinterpret_cast<const half4_t*>(a.scale + nb + 32 + 8 * q);
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) in.s0[q] = in.s1[q] = (half4_t){1, 1, 1, 1};
+  }
+  if constexpr (EPI == EPI_RESID) {
+    // x is an AFL tile [32][N] (32 rows always allocated)
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        in.xv[tt][q] = *reinterpret_cast<const half4_t*>(a.x + afl_offset(m, nb + 32 * tt + 8 * q));
+  }
+  return in;
+}
+
+// Epilogue of a completed tile t for the 32 activation rows held by this wave, with its
+// global inputs from epi_prefetch (EPI_STORE, EPI_RESID, EPI_SWIGLU).
 // Row n of the packed matrix in accumulator r of block tt: n = (2t+tt)*32 + 8*(r/4)
 // + 4*g + (r%4), activation row m = lane % 32.
 template <int EPI>
 DFL_DEV void tile_epilogue(const StreamArgs& a, int lane, int t, const floatx16& acc0,
-                           const floatx16& acc1) {
+                           const floatx16& acc1, const EpiIn& in) {
   const int m = lane & 31, g = lane >> 5;
   const bool row_ok = m < a.M;
   const int nb = (2 * t) * 32 + 4 * g;
@@ -349,11 +409,9 @@ DFL_DEV void tile_epilogue(const StreamArgs& a, int lane, int t, const floatx16&
     for (int q = 0; q < 4; ++q) {
       half4_t o0, o1;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {   // fp16 weights carry no scale
-        const float s0 = a.scale ? h2f(a.scale[nb + 8 * q + c]) : 1.0f;
-        const float s1 = a.scale ? h2f(a.scale[nb + 32 + 8 * q + c]) : 1.0f;
-        o0[c] = f2h(acc0[4 * q + c] * s0);
-        o1[c] = f2h(acc1[4 * q + c] * s1);
+      for (int c = 0; c < 4; ++c) {   // fp16 weights carry no scale (in.s = 1)
+        o0[c] = f2h(acc0[4 * q + c] * h2f(in.s0[q][c]));
+        o1[c] = f2h(acc1[4 * q + c] * h2f(in.s1[q][c]));
       }
       *reinterpret_cast<half4_t*>(dst + 8 * q) = o0;
       *reinterpret_cast<half4_t*>(dst + 32 + 8 * q) = o1;
@@ -368,11 +426,11 @@ DFL_DEV void tile_epilogue(const StreamArgs& a, int lane, int t, const floatx16&
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
           half_t* xp = a.x + afl_offset(m, nb + 32 * tt + 8 * q);
-          half4_t xv = *reinterpret_cast<const half4_t*>(xp);
+          half4_t xv = in.xv[tt][q];
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
             const float acc = tt ? acc1[4 * q + c] : acc0[4 * q + c];
-            const float y = h2f(f2h(acc * h2f(a.scale[nb + 32 * tt + 8 * q + c])));
+            const float y = h2f(f2h(acc * h2f(tt ? in.s1[q][c] : in.s0[q][c])));
             const half_t xn = f2h(h2f(xv[c]) + y);
             xv[c] = xn;
             ss += h2f(xn) * h2f(xn);
@@ -386,7 +444,6 @@ DFL_DEV void tile_epilogue(const StreamArgs& a, int lane, int t, const floatx16&
   } else if constexpr (EPI == EPI_SWIGLU) {
     if (!row_ok) return;
     // out is an AFL tile [32][N/2]: columns 32t + 8q + 4g + (0..3) of row m
-    const half_t* sg = a.scale + nb;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       half_t* dst = a.out + afl_offset(m, t * 32 + 8 * q + 4 * g);
@@ -394,8 +451,8 @@ DFL_DEV void tile_epilogue(const StreamArgs& a, int lane, int t, const floatx16&
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int r = 4 * q + c;
-        const float gv = h2f(f2h(acc0[r] * h2f(sg[8 * q + c])));
-        const float uv = h2f(f2h(acc1[r] * h2f(sg[32 + 8 * q + c])));
+        const float gv = h2f(f2h(acc0[r] * h2f(in.s0[q][c])));
+        const float uv = h2f(f2h(acc1[r] * h2f(in.s1[q][c])));
         const float sig = h2f(f2h(1.0f / (1.0f + expf(-gv))));
         const float sil = h2f(f2h(gv * sig));
         o[c] = f2h(sil * uv);
@@ -416,8 +473,8 @@ DFL_DEV void tile_epilogue(const StreamArgs& a, int lane, int t, const floatx16&
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int d = d0 + 8 * q + c;
-        vt[(size_t)d * r.cap] = f2h(acc0[4 * q + c] * h2f(a.scale[nb + 8 * q + c]));
-        vt[(size_t)(d + 32) * r.cap] = f2h(acc1[4 * q + c] * h2f(a.scale[nb + 32 + 8 * q + c]));
+        vt[(size_t)d * r.cap] = f2h(acc0[4 * q + c] * h2f(in.s0[q][c]));
+        vt[(size_t)(d + 32) * r.cap] = f2h(acc1[4 * q + c] * h2f(in.s1[q][c]));
       }
   } else {  // EPI_ARGMAX: fp16 weights, no scale
     if (row_ok && a.logits) {
@@ -454,6 +511,13 @@ DFL_DEV void tile_epilogue(const StreamArgs& a, int lane, int t, const floatx16&
       }
     }
   }
+}
+
+// The epilogue with its inputs loaded on the spot.
+template <int EPI>
+DFL_DEV void tile_epilogue(const StreamArgs& a, int lane, int t, const floatx16& acc0,
+                           const floatx16& acc1) {
+  tile_epilogue<EPI>(a, lane, t, acc0, acc1, epi_prefetch<EPI>(a, lane, t));
 }
 
 // Norm prologue of the reducer wave: the gain and ss_in are copied to LDS (issued before
@@ -500,10 +564,11 @@ DFL_DEV void sum_wave_partials(int lane, float (*red)[WG_WAVES][2048], int* arri
 template <int EPI>
 DFL_DEV void reduce_segment(const StreamArgs& a, int lane, float (*red)[WG_WAVES][2048],
                             int* arrived, int* reduced, int si, int t, int slot, int count) {
+  const EpiIn in = epi_prefetch<EPI>(a, lane, t);   // in flight while the partials arrive
   floatx16 acc0, acc1;
   sum_wave_partials(lane, red, arrived, reduced, si, acc0, acc1);
   const bool complete = count == 1 || finish_split_tile(a, lane, t, slot, count, acc0, acc1);
-  if (complete) tile_epilogue<EPI>(a, lane, t, acc0, acc1);
+  if (complete) tile_epilogue<EPI>(a, lane, t, acc0, acc1, in);
 }
 
 // Q or K head h of the fused qkv projection, complete: lo = d 0..63 (tile 2h), hi = d
@@ -762,9 +827,15 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_gemm_kernel(StreamArg
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int G = gridDim.x;
   const int b = blockIdx.x;
-  const long long U = (long long)(a.N >> 6) * a.KB;
+  // Work list: the split (stream-K) units of tiles [0, T - dp*G), an equal contiguous range
+  // per workgroup, first; then dp whole tiles of its own.  Split tiles are completed by
+  // cross-workgroup fix-ups while the whole tiles stream, so the launch ends on local
+  // epilogues only.  dp == 0: one stream-K range over the whole matrix.
+  const int T = a.N >> 6, dp = a.dp;
+  const long long U = (long long)(T - dp * G) * a.KB;   // split units
   const long long u0 = (long long)b * U / G, u1 = (long long)(b + 1) * U / G;
-  if (u0 >= u1) return;   // (the plan never makes more workgroups than units)
+  const long long v0 = (long long)(T - dp * G + dp * b) * a.KB, v1 = v0 + (long long)dp * a.KB;
+  if (u0 >= u1 && v0 >= v1) return;   // (the plan never makes more workgroups than units)
   if (threadIdx.x == 0) {
     arrived[0] = arrived[1] = 0;
     reduced = 0;
@@ -774,7 +845,8 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_gemm_kernel(StreamArg
 
   if (w < WG_WAVES) {
     int si = 0;
-    stream_range<WT, NORM, P>(a, gsh, rn_s, &ready, red, arrived, &reduced, u0, u1, w, lane, si);
+    stream_range<WT, NORM, P>(a, gsh, rn_s, &ready, red, arrived, &reduced, u0, u1, v0, v1, w,
+                              lane, si);
     return;
   }
 
@@ -806,6 +878,8 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_gemm_kernel(StreamArg
     reduce_segment<EPI>(a, lane, red, arrived, &reduced, si, t, b - first, count);
     u += kbe - kbs;
   }
+  for (long long u = v0; u < v1; u += a.KB, ++si)   // whole tiles: local epilogues
+    reduce_segment<EPI>(a, lane, red, arrived, &reduced, si, (int)(u / a.KB), 0, 1);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -857,7 +931,8 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_dyn_kernel(StreamArgs
     int si = 0;
     if (S > 0)
       stream_range<WT, NORM, P>(a, gsh, rn_s, &ready, red, arrived, &reduced,
-                                (long long)b * S * KB, (long long)(b + 1) * S * KB, w, lane, si);
+                                (long long)b * S * KB, (long long)(b + 1) * S * KB, 0, 0, w,
+                                lane, si);
     for (int k = 0;; ++k) {
       int spins = 0;
       while (__hip_atomic_load(&q_pub, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <= k) {
@@ -870,8 +945,8 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_dyn_kernel(StreamArgs
       const int c = q_chunk[k & 3];
       if (c < 0) break;
       const long long c0 = (long long)(T0 + (c >> 1)) * KB + (long long)(c & 1) * half;
-      stream_range<WT, NORM, P>(a, gsh, rn_s, &ready, red, arrived, &reduced, c0, c0 + half, w,
-                                lane, si);
+      stream_range<WT, NORM, P>(a, gsh, rn_s, &ready, red, arrived, &reduced, c0, c0 + half, 0,
+                                0, w, lane, si);
     }
     return;
   }
@@ -1047,7 +1122,10 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_gemm_m_kernel(StreamA
 SKPlan streamk_plan(int N, int KB, int n_cu) {
   // One workgroup per CU.  When there are fewer wave-tiles than CUs the worker count is
   // the largest multiple of the tile count that fits, so every tile is split into the
-  // same number of equal k-ranges (no worker straddles two tiles).
+  // same number of equal k-ranges (no worker straddles two tiles).  With at least one
+  // tile per CU, each workgroup also gets dp = tiles / CUs whole tiles, streamed after its
+  // share of the remaining tiles' split units (hybrid plan; the M-split kernel keeps the
+  // contiguous partition, whose slot count is seg_cap).
   SKPlan p;
   const long long nt = N / 64;
   const long long U = nt * KB;
@@ -1056,11 +1134,19 @@ SKPlan streamk_plan(int N, int KB, int n_cu) {
   p.workers = (int)std::max(1LL, std::min(W, U));
   const long long per = std::max(1LL, U / p.workers);
   p.seg_cap = (int)((KB + per - 1) / per + 1);
+  if (nt >= n_cu) {
+    p.dp = (int)(nt / n_cu);
+    const long long S = (nt - (long long)p.dp * n_cu) * KB;
+    const long long sper = std::max(1LL, S / n_cu);
+    p.sk_seg_cap = S > 0 ? (int)((KB + sper - 1) / sper + 1) : 1;
+  }
   return p;
 }
 
 SKPlan streamk_plan_balanced(int N, int KB, int n_cu) {
   SKPlan p = streamk_plan(N, KB, n_cu);
+  p.dp = 0;
+  p.sk_seg_cap = 0;
   const long long nt = N / 64;
   if (nt < 2LL * n_cu || (KB & 1)) return p;
   p.workers = n_cu;

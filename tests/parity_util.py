@@ -45,10 +45,14 @@ def device_errors(m):
 #    points) pick different ids, and the GPU picked one of the two;
 #  * "noise": the GPU picked the oracle's runner-up and the oracle's top-2 gap is below
 #    NOISE_SIGMAS x sigma, sigma being the RMS of (GPU logit - oracle logit) over every
-#    row's oracle top-2 entries in the same case -- the measured logit noise that decides
-#    such a row (the logits themselves stay within logit_tol of the oracle's).
-# The full-size workloads use the first rule only; the second serves the small random test
-# models (vocab 1024), whose logits crowd together.  Everything else must agree.  Every call records its counts; conftest prints the session
+#    row's oracle top-2 entries in the same case.  That logit noise comes from fp32
+#    summation order flipping fp16 roundings through the layers (the oracle's own fp32 and
+#    fp64 runs differ by up to 2.6e-3 in a gap); at the full-size shapes sigma is about
+#    3e-3, so the gap of two logits carries noise ~ sqrt(2) sigma and a row whose gap is
+#    4 sigma (2.8 x that) or more flips with probability below 0.3 % -- such rows must
+#    agree.  Any change of summation order (a different split of a projection over the
+#    CUs) re-draws the rows below the threshold, so they cannot be held to exact agreement.
+# Everything else must agree.  Every call records its counts; conftest prints the session
 # total, raw agreement included.
 ARGMAX_TOTALS = {"rows": 0, "agree": 0, "undecided": 0, "noise": 0, "cases": []}
 NOISE_SIGMAS = 4.0
@@ -58,7 +62,7 @@ def check_argmax(ids, logits, ref_ids, alt_ids, what, ref_top2_idx, ref_top2_val
                  logit_tol=2e-2, noise_rule=True):
     """Assert the GPU ids against the oracle's (fp32-accumulation ``ref_ids`` with its top-2
     indices / logits, fp64 ``alt_ids``); returns (agree, rows, exempt).  ``noise_rule``
-    False (the full-size fixtures) exempts oracle-undecided rows only."""
+    False exempts oracle-undecided rows only."""
     ids = np.asarray(ids).reshape(-1)
     ref_ids = np.asarray(ref_ids).reshape(-1)
     alt_ids = np.asarray(alt_ids).reshape(-1)
@@ -80,8 +84,9 @@ def check_argmax(ids, logits, ref_ids, alt_ids, what, ref_top2_idx, ref_top2_val
     n, n_agree = ids.size, int(agree.sum())
     n_und, n_noise = int(undecided.sum()), int(noise.sum())
     print(f"{what}: argmax agreement {n_agree}/{n} ({n_agree / n:.4f}); exempt "
-          f"{n_und} oracle-undecided, {n_noise} below {NOISE_SIGMAS:g} sigma = {tau:.2e} "
-          f"(logit error rms {sigma:.2e}, max {emax:.2e})", flush=True)
+          f"{n_und} oracle-undecided, {n_noise} of {int((gap < tau).sum())} rows with a top-2 "
+          f"gap below {NOISE_SIGMAS:g} sigma = {tau:.2e} (logit error rms {sigma:.2e}, max "
+          f"{emax:.2e})", flush=True)
     ARGMAX_TOTALS["rows"] += n
     ARGMAX_TOTALS["agree"] += n_agree
     ARGMAX_TOTALS["undecided"] += n_und

@@ -112,6 +112,5 @@ def test_batch_full_matches_golden():
     M = ids_b.size
     assert_close_fp16(h.float().cpu().numpy().reshape(M, -1), g["hidden"], what=f"{name} hidden")
     check_argmax(ids.cpu().numpy().reshape(M), logits.cpu().numpy().reshape(M, -1), g["ids"],
-                 g["ids_f64"], name, g["top2_idx"], g["top2_val"], LOGIT_TOL,
-                 noise_rule=False)
+                 g["ids_f64"], name, g["top2_idx"], g["top2_val"], LOGIT_TOL)
     m.close()

@@ -6,9 +6,9 @@ block 16, context 2048) and the 27B-class headline draft (5 layers, H5120, block
 context 4096), so the HIP path is checked at full size without running the oracle on
 the GPU host.  Tolerances: final hidden cosine >= 0.9995 and max-abs <= 2e-2 (fp16);
 argmax identical on every row except where the oracle itself is undecided (its fp32- and
-fp64-accumulation runs disagree and the GPU took one of the two ids;
-parity_util.check_argmax prints the counts); GPU logits at the oracle's top-2 indices
-within LOGIT_TOL of the oracle's values.
+fp64-accumulation runs disagree, or its top-2 gap lies within 4 x the measured logit noise;
+parity_util.check_argmax states the rule and prints the counts); GPU logits at the
+oracle's top-2 indices within LOGIT_TOL of the oracle's values.
 """
 
 import os
@@ -71,8 +71,7 @@ def test_full_draft_matches_golden(name):
     assert_close_fp16(h.float().cpu().numpy(), g["hidden"], what=f"{name} final hidden")
     lg = logits.cpu().numpy()
     ids = ids.cpu().numpy()
-    check_argmax(ids, lg, g["ids"], g["ids_f64"], name, g["top2_idx"], g["top2_val"], LOGIT_TOL,
-                 noise_rule=False)
+    check_argmax(ids, lg, g["ids"], g["ids_f64"], name, g["top2_idx"], g["top2_val"], LOGIT_TOL)
     # the lm_head hands half tiles out at run time from self-resetting counters: later
     # launches on the same inputs give the same bits, and no queue wait gave up
     for rep in range(2):
@@ -114,7 +113,7 @@ def sweep_model():
 def _check_against(g, name, ids, logits, h):
     assert_close_fp16(h.float().cpu().numpy(), g["hidden"], what=f"{name} final hidden")
     check_argmax(ids.cpu().numpy(), logits.cpu().numpy(), g["ids"], g["ids_f64"], name,
-                 g["top2_idx"], g["top2_val"], LOGIT_TOL, noise_rule=False)
+                 g["top2_idx"], g["top2_val"], LOGIT_TOL)
 
 
 @pytest.mark.parametrize("ctx", SWEEP)
