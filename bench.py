@@ -9,6 +9,10 @@ the resident context K/V plus the block -> final norm -> lm_head -> argmax ids. 
 context (fc fusion + per-layer K/V of 4096 rows) is ingested once before timing and
 reported as its own phase.  Weights and inputs are synthetic (seeded, random-init).
 
+After the headline, the same run times the block step at resident contexts 64, 2048,
+16384 and 32768 (``context_sweep``) and the batched-drafting workload (LLaMA-3.1-8B-class,
+8 sequences x 32 rows, ragged contexts: ``batched``); both are extra keys, never ``value``.
+
 Prints ONE JSON line.  ``value`` is the mean draft-block latency in microseconds over
 the timed steps (inputs resident in HBM).  ``roofline`` describes the W8A16 projection
 GEMM kernel, timed live with HIP events on the library's stream in a separate pass of
@@ -163,52 +167,17 @@ def cpu_baseline(wl, model, host, ids, max_seconds=12.0, max_blocks=8):
                       f"dequantised W8A16 weights, context K/V precomputed)"}
 
 
-def main():
-    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="dflash_27b")
-    ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--profile-steps", type=int, default=5)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-profile", action="store_true")
-    ap.add_argument("--sweep", default="",
-                    help="comma-separated contexts: after the headline, time the block step "
-                         "at each of these context lengths too (context-sweep report)")
-    ap.add_argument("--copy-probe-mib", type=int, default=0,
-                    help="run a plain device copy of this many MiB 3 times first (a known-size "
-                         "kernel for scaling FETCH_SIZE / WRITE_SIZE counter readings)")
-    args = ap.parse_args()
-
-    if args.gpus != 1:
-        print(f"bench.py: runs on exactly one GPU; --gpus {args.gpus} is not supported (the "
-              f"multi-GPU sharding is designed, not implemented)", file=sys.stderr)
-        sys.exit(2)
-
-    import numpy as np
+def run_workload(wl, args, sweep, want_cpu):
+    """Build the model of workload ``wl``, ingest its context(s), time ``args.steps`` draft
+    blocks (after ``args.warmup``), profile the kernels and optionally sweep the resident
+    context length.  Returns the measurement dict (the JSON line's fields)."""
     import torch
-    from mirror_sd_amd.config import workload
     from mirror_sd_amd import synth, _lib
 
-    wl = workload(args.workload)
     cfg = wl.cfg
     batched = bool(wl.seq_ctx)   # several independent sequences drafted together
-    if not torch.cuda.is_available():
-        print("bench.py: no GPU visible", file=sys.stderr)
-        sys.exit(1)
     torch.manual_seed(args.seed)
-    want_cpu = not args.no_cpu_baseline and not batched
-    if args.copy_probe_mib > 0:
-        n = (args.copy_probe_mib << 20) // 4
-        src = torch.ones(n, dtype=torch.int32, device="cuda")
-        dst = torch.empty_like(src)
-        for _ in range(3):   # elementwise kernel: reads n*4 bytes, writes n*4 bytes
-            torch.bitwise_not(src, out=dst)
-        torch.cuda.synchronize()
-        del src, dst
     t_setup = time.perf_counter()
-    sweep = [int(c) for c in args.sweep.split(",") if c.strip()] if not batched else []
     n_seq = len(wl.seq_ctx) if batched else 1
     model, host = build_model(wl, args.seed, keep_host=want_cpu,
                               max_ctx=max([wl.ctx] + sweep), max_seqs=n_seq)
@@ -217,12 +186,10 @@ def main():
                    for i, c in enumerate(wl.seq_ctx)]
         ths = [d["target_hidden"] for d in seq_inp]
         ids = torch.cat([d["ids"] for d in seq_inp]).contiguous()
-        th = ths[0]
         del seq_inp
     else:
         inp = synth.make_inputs_torch(cfg, wl.block, wl.ctx, seed=args.seed, device="cuda")
-        th, ids = inp["target_hidden"], inp["ids"]
-        ths = [th]
+        ths, ids = [inp["target_hidden"]], inp["ids"]
     setup_s = time.perf_counter() - t_setup
 
     L = model._L
@@ -385,30 +352,119 @@ def main():
             cpu = cpu_baseline(wl, model, host, ids)
         except Exception as e:  # report, never lose the GPU line
             cpu = {"value": None, "error": f"{type(e).__name__}: {e}"}
+    model.close()
+    del model, host, ths
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return {"lat_us": lat_us, "ms_per_step": ms_per_step, "wall_s": wall_s, "gbs": gbs,
+            "nbytes": nbytes, "roofline": roofline, "kernels": kernels, "cpu": cpu,
+            "ingest_ms": ingest_ms, "first_ingest_s": first_ingest_s, "setup_s": setup_s,
+            "ms_events": ms_events, "context_sweep": context_sweep, "first_ids": first_ids,
+            "n_seq": n_seq, "batched": batched}
 
-    metric = METRIC if wl.name == "dflash_27b" else \
+
+# The context sweep of the headline draft (contexts 64 .. 32768; 4096 is the headline itself)
+# and the batched-drafting workload run by default after the headline, as extra keys.
+DEFAULT_SWEEP = "64,2048,16384,32768"
+EXTRA_WORKLOAD = "llama8b_batch"
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="dflash_27b")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--profile-steps", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-profile", action="store_true")
+    ap.add_argument("--sweep", default=None,
+                    help="comma-separated contexts: after the headline, time the block step "
+                         f"at each of these context lengths too (default for the headline "
+                         f"workload: {DEFAULT_SWEEP}; '' for none)")
+    ap.add_argument("--no-extra", action="store_true",
+                    help=f"skip the batched-drafting workload ({EXTRA_WORKLOAD}) that the "
+                         "headline run reports as an extra key")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="run a plain device copy of this many MiB 3 times first (a known-size "
+                         "kernel for scaling FETCH_SIZE / WRITE_SIZE counter readings)")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: runs on exactly one GPU; --gpus {args.gpus} is not supported (the "
+              f"multi-GPU sharding is designed, not implemented)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from mirror_sd_amd.config import workload
+
+    wl = workload(args.workload)
+    cfg = wl.cfg
+    batched = bool(wl.seq_ctx)
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    headline = wl.name == "dflash_27b"
+    want_cpu = not args.no_cpu_baseline and not batched
+    if args.copy_probe_mib > 0:
+        n = (args.copy_probe_mib << 20) // 4
+        src = torch.ones(n, dtype=torch.int32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):   # elementwise kernel: reads n*4 bytes, writes n*4 bytes
+            torch.bitwise_not(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
+    sweep_arg = args.sweep if args.sweep is not None else (DEFAULT_SWEEP if headline else "")
+    sweep = [int(c) for c in sweep_arg.split(",") if c.strip()] if not batched else []
+    r = run_workload(wl, args, sweep, want_cpu)
+
+    extra = None
+    if headline and not args.no_extra:
+        # the batched drafting workload (8 sequences x 32 rows, ragged contexts): stacked
+        # M = 256 projections, MFMA-bound
+        xw = workload(EXTRA_WORKLOAD)
+        x = run_workload(xw, args, [], False)
+        tokens = x["n_seq"] * xw.block
+        extra = {"workload": xw.name, "config": {"hidden": xw.cfg.hidden_size,
+                                                  "layers": xw.cfg.num_hidden_layers,
+                                                  "ffn": xw.cfg.intermediate_size,
+                                                  "vocab": xw.cfg.vocab_size,
+                                                  "sequences": x["n_seq"], "block": xw.block,
+                                                  "ctx": list(xw.seq_ctx)},
+                 "block_us": round(x["lat_us"], 2),
+                 "draft_tokens_per_s": round(tokens / (x["ms_per_step"] * 1e-3), 1),
+                 "hbm_gbps": round(x["gbs"], 1),
+                 "algorithmic_bytes_per_block": x["nbytes"]["total"],
+                 "roofline": x["roofline"], "kernels": x["kernels"],
+                 "context_ingest_ms": round(x["ingest_ms"], 3)}
+        print(f"{xw.name}: block {x['lat_us']:.1f} us", file=sys.stderr, flush=True)
+
+    metric = METRIC if headline else \
         f"draft-block latency (us) + achieved HBM GB/s, {wl.description}"
     out = {
-        "metric": metric, "value": round(lat_us, 2), "unit": "us", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
+        "metric": metric, "value": round(r["lat_us"], 2), "unit": "us", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(r["ms_per_step"], 5),
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
         "data": "synthetic (seeded random-init weights, N(0,1) target_hidden)",
         "config": {"workload": wl.name, "hidden": cfg.hidden_size, "layers": cfg.num_hidden_layers,
                    "heads": cfg.num_attention_heads, "kv_heads": cfg.num_key_value_heads,
                    "ffn": cfg.intermediate_size, "vocab": cfg.vocab_size, "block": wl.block,
-                   "ctx": list(wl.seq_ctx) if batched else wl.ctx, "sequences": n_seq,
+                   "ctx": list(wl.seq_ctx) if batched else wl.ctx, "sequences": r["n_seq"],
                    "weights": "W8A16 (int8 + fp16 per-row scale), fp16 lm_head"},
-        "hbm_gbps": round(gbs, 1),
-        "algorithmic_bytes_per_block": nbytes["total"],
-        "roofline": roofline,
-        "cpu_baseline": cpu,
-        "phases": {"context_ingest_ms": round(ingest_ms, 3),
-                   "first_ingest_s": round(first_ingest_s, 3), "setup_s": round(setup_s, 1),
-                   "ms_per_step_with_gemm_events": (round(ms_events, 5) if ms_events else None),
-                   "wall_ms_per_step": round(wall_s * 1e3 / args.steps, 4)},
-        "kernels": kernels,
-        "context_sweep": context_sweep,
-        "draft_ids_head": first_ids[:4],
+        "hbm_gbps": round(r["gbs"], 1),
+        "algorithmic_bytes_per_block": r["nbytes"]["total"],
+        "roofline": r["roofline"],
+        "cpu_baseline": r["cpu"],
+        "phases": {"context_ingest_ms": round(r["ingest_ms"], 3),
+                   "first_ingest_s": round(r["first_ingest_s"], 3), "setup_s": round(r["setup_s"], 1),
+                   "ms_per_step_with_gemm_events": (round(r["ms_events"], 5) if r["ms_events"]
+                                                    else None),
+                   "wall_ms_per_step": round(r["wall_s"] * 1e3 / args.steps, 4)},
+        "kernels": r["kernels"],
+        "context_sweep": r["context_sweep"],
+        "batched": extra,
+        "draft_ids_head": r["first_ids"][:4],
     }
     print(json.dumps(out), flush=True)
 
