@@ -9,6 +9,9 @@ the resident context K/V plus the block -> final norm -> lm_head -> argmax ids. 
 context (fc fusion + per-layer K/V of 4096 rows) is ingested once before timing and
 reported as its own phase.  Weights and inputs are synthetic (seeded, random-init).
 
+``steady_step`` times the decode-loop step: 16 or 32 new context rows ingested (the
+per-step path) and then the block, next to the ingest alone.
+
 After the headline, the same run times the block step at resident contexts 64, 2048,
 16384 and 32768 (``context_sweep``) and the batched-drafting workload (LLaMA-3.1-8B-class,
 8 sequences x 32 rows, ragged contexts: ``batched``); both are extra keys, never ``value``.
@@ -321,6 +324,49 @@ def run_workload(wl, args, sweep, want_cpu):
                 ent["bytes_per_launch"] = r["bytes"] / r["launches"]
             kernels[name] = ent
 
+    steady = None
+    if not batched and args.steady:
+        # the decode-loop step: k new context rows ingested (the per-step stream-K path),
+        # then the block; and the ingest alone (its rows trimmed again)
+        steady = {}
+        for k in (16, 32):
+            rows = synth.make_inputs_torch(cfg, wl.block, k, seed=args.seed + 7,
+                                           device="cuda")["target_hidden"]
+            def ingest_k():
+                _lib.check(L.dfl_ingest_context(ctx, rows.data_ptr(), k, sh), "dfl_ingest_context")
+            def ingest_only():
+                ingest_k()
+                _lib.check(L.dfl_cache_trim(ctx, k), "dfl_cache_trim")
+            for _ in range(args.warmup):
+                ingest_only()
+            torch.cuda.synchronize()
+            ev0.record(stream)
+            for _ in range(args.steps):
+                ingest_only()
+            ev1.record(stream)
+            torch.cuda.synchronize()
+            ing_us = ev0.elapsed_time(ev1) * 1e3 / args.steps
+            n_app = 0
+            for _ in range(args.warmup):
+                ingest_k()
+                step()
+                n_app += k
+            torch.cuda.synchronize()
+            ev0.record(stream)
+            for _ in range(args.steps):
+                ingest_k()
+                step()
+                n_app += k
+            ev1.record(stream)
+            torch.cuda.synchronize()
+            step_us = ev0.elapsed_time(ev1) * 1e3 / args.steps
+            _lib.check(L.dfl_cache_trim(ctx, n_app), "dfl_cache_trim")   # back to the context
+            steady[str(k)] = {"step_us": round(step_us, 2), "ingest_us": round(ing_us, 2),
+                              "context_rows": f"{wl.ctx} + {k} per step"}
+            print(f"steady step, {k} new rows: {step_us:.1f} us (ingest {ing_us:.1f} us)",
+                  file=sys.stderr, flush=True)
+            del rows
+
     context_sweep = None
     if sweep:
         # the block step against other resident context lengths (same weights)
@@ -359,7 +405,8 @@ def run_workload(wl, args, sweep, want_cpu):
     return {"lat_us": lat_us, "ms_per_step": ms_per_step, "wall_s": wall_s, "gbs": gbs,
             "nbytes": nbytes, "roofline": roofline, "kernels": kernels, "cpu": cpu,
             "ingest_ms": ingest_ms, "first_ingest_s": first_ingest_s, "setup_s": setup_s,
-            "ms_events": ms_events, "context_sweep": context_sweep, "first_ids": first_ids,
+            "ms_events": ms_events, "context_sweep": context_sweep, "steady": steady,
+            "first_ids": first_ids,
             "n_seq": n_seq, "batched": batched}
 
 
@@ -383,6 +430,8 @@ def main():
                     help="comma-separated contexts: after the headline, time the block step "
                          f"at each of these context lengths too (default for the headline "
                          f"workload: {DEFAULT_SWEEP}; '' for none)")
+    ap.add_argument("--no-steady", dest="steady", action="store_false",
+                    help="skip the decode-loop step timing (16 / 32 new context rows + block)")
     ap.add_argument("--no-extra", action="store_true",
                     help=f"skip the batched-drafting workload ({EXTRA_WORKLOAD}) that the "
                          "headline run reports as an extra key")
@@ -462,6 +511,7 @@ def main():
                                                     else None),
                    "wall_ms_per_step": round(r["wall_s"] * 1e3 / args.steps, 4)},
         "kernels": r["kernels"],
+        "steady_step": r["steady"],
         "context_sweep": r["context_sweep"],
         "batched": extra,
         "draft_ids_head": r["first_ids"][:4],

@@ -12,6 +12,7 @@
 
 #include "dflash_hip.h"
 #include "dfl_kernels.h"
+#include "dfl_check.h"
 
 using namespace dfl;
 
@@ -31,6 +32,10 @@ int fail(int code, const std::string& msg) {
   } while (0)
 
 constexpr int ING_MAX = 4096;      // context rows per ingest pass (at most)
+// Ingest calls of at most SMALL_ING rows (the per-step context of a decode loop: acceptance
+// + 1 rows) run on the stream-K kernels, which stream each weight once at HBM rate; larger
+// (prompt) ingests are compute-bound and run on rocBLAS.
+constexpr int SMALL_ING = 64;
 constexpr int MAX_CHUNKS = 64;     // attention key splits
 constexpr int MT_MAX = 8;          // 32-row m-tiles per M-split GEMM launch
 // Stacked blocks of more than BLAS_MIN_ROWS rows (batched drafting) are compute-bound: their
@@ -137,6 +142,7 @@ struct dfl_ctx {
   int* err = nullptr;
   // stream-K GEMM state (block step)
   int n_cu = 256;
+  int lds_max = 0;               // LDS bytes per workgroup of the device
   half_t* qkvbuf = nullptr;      // [RM][NQKV] fp16 projections
   float* rnorm = nullptr;        // [RM] 1/rms of the residual rows
   float* rope_cs = nullptr;      // [32][64][2] RoPE cos, sin of a block's rows (one sequence)
@@ -151,6 +157,15 @@ struct dfl_ctx {
   float* fc32 = nullptr;      // [ing][H] fc GEMM rows (fp32)
   half_t* xn = nullptr;       // [ing][H] hidden_norm(fc) rows (fp16, row-major)
   float* kv32 = nullptr;      // [ing][2*NKV*128] K|V GEMM rows (fp32)
+  // per-step ingest of up to SMALL_ING rows on the stream-K kernels (no library GEMM): the
+  // fc weight packed in fp16 blocks, input / normed rows in activation fragment layout,
+  // fp16 fc and K|V rows
+  uint4* w_fc_pk = nullptr;   // packed fc [H][NF*H] (KB = NF*H/16)
+  half_t* si_in = nullptr;    // [SMALL_ING/32][32][max(NF,1)*H] fragment-layout input rows
+  half_t* si_fc = nullptr;    // [SMALL_ING][H] fc rows (fp16)
+  half_t* si_xn = nullptr;    // [SMALL_ING/32][32][H] fragment-layout hidden_norm rows
+  half_t* si_kv = nullptr;    // [SMALL_ING][2*NKV*128] K|V rows (fp16, scaled)
+  SKPlan sk_fc, sk_kv;
   std::vector<void*> allocs;
   int prof = 0;   // 0 off, 1 every kernel group, 2 stream-K GEMM launches only
   std::vector<ProfRec> recs;
@@ -254,6 +269,11 @@ static int setup_ingest(dfl_ctx* x) {
   x->ing = std::max(32, std::min(ING_MAX, ((x->cfg.max_ctx + 31) / 32) * 32));
   int r = DFL_OK;
   if ((r = x->alloc(&x->kv32, (size_t)x->ing * Nkv))) return r;
+  if ((r = x->alloc(&x->si_in, (size_t)SMALL_ING * std::max(x->NF, 1) * H, true)) ||
+      (r = x->alloc(&x->si_fc, (size_t)SMALL_ING * H)) ||
+      (r = x->alloc(&x->si_xn, (size_t)SMALL_ING * H, true)) ||
+      (r = x->alloc(&x->si_kv, (size_t)SMALL_ING * Nkv)))
+    return r;
   if (x->NF > 0 && ((r = x->alloc(&x->fc32, (size_t)x->ing * H)) ||
                     (r = x->alloc(&x->xn, (size_t)x->ing * H))))
     return r;
@@ -326,28 +346,41 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
     return r;
   }
   {
-    int dev = 0, ncu = 0;
+    int dev = 0, ncu = 0, lds = 0;
     if (hipGetDevice(&dev) == hipSuccess &&
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
         ncu > 0)
       x->n_cu = ncu;
+    // the attention's LDS stage needs 80 KiB per workgroup (160 KiB for two stage buffers)
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
+        lds < 80 * 1024) {
+      delete x;
+      return fail(DFL_EINVAL, "dfl_create: the device offers " + std::to_string(lds) +
+                                  " bytes of LDS per workgroup; the attention kernel needs 81920");
+    }
+    x->lds_max = lds;
     auto plan = [&](int N, int KB) { return streamk_plan(N, KB, x->n_cu); };
     x->sk_qkv = plan(x->NQKV, x->H / 32);
     x->sk_o = plan(x->H, x->NH * 128 / 32);
     x->sk_gu = plan(2 * x->F, x->H / 32);
     x->sk_down = plan(x->H, x->F / 32);
     x->sk_lm = streamk_plan_balanced(std::max(x->V, 64), x->H / 16, x->n_cu);
+    x->sk_fc = streamk_plan(x->H, std::max(x->NF, 1) * x->H / 16, x->n_cu);
+    x->sk_kv = plan(2 * x->NKV * 128, x->H / 32);
     size_t wsn = 0, tiles = 0;
     for (auto pr : {std::make_pair(x->sk_qkv, x->NQKV), std::make_pair(x->sk_o, x->H),
                     std::make_pair(x->sk_gu, 2 * x->F), std::make_pair(x->sk_down, x->H),
-                    std::make_pair(x->sk_lm, std::max(x->V, 64))}) {
+                    std::make_pair(x->sk_lm, std::max(x->V, 64)), std::make_pair(x->sk_fc, x->H),
+                    std::make_pair(x->sk_kv, 2 * x->NKV * 128)}) {
       wsn = std::max(wsn, (size_t)(pr.second / 64) *
                               std::max(pr.first.seg_cap, pr.first.sk_seg_cap) * 2048);
       tiles = std::max(tiles, (size_t)(pr.second / 64));
     }
     const size_t bm32 = ((Bm + 31) / 32) * 32;
-    // split-tile partials hold one 32x64 slot per m-tile of a launch
-    wsn *= (size_t)std::min<size_t>(MT_MAX, bm32 / 32);
+    // split-tile partials hold one 32x64 slot per m-tile of a launch (the per-step ingest's
+    // fc and K|V launches take up to SMALL_ING / 32 m-tiles)
+    wsn *= (size_t)std::min<size_t>(MT_MAX, std::max<size_t>(bm32 / 32, SMALL_ING / 32));
     if ((r = x->alloc(&x->qkvbuf, Bm * x->NQKV)) || (r = x->alloc(&x->rnorm, bm32)) ||
         (r = x->alloc(&x->sk_ws, wsn)) || (r = x->alloc(&x->sk_tile_cnt, tiles, true)) ||
         (r = x->alloc(&x->dyn_next, 2, true)) || (r = x->alloc(&x->rope_cs, 32 * 64 * 2)) ||
@@ -470,6 +503,10 @@ int dfl_load_fc(dfl_ctx* ctx, const uint16_t* fc_weight, const uint16_t* hidden_
   }
   DFL_HIP(hipMemcpyAsync(ctx->w_fc, fc_weight, (size_t)ctx->H * K * 2, hipMemcpyDeviceToDevice, st));
   DFL_HIP(hipMemcpyAsync(ctx->hidden_norm, hidden_norm, ctx->H * 2, hipMemcpyDeviceToDevice, st));
+  // the same weight in the stream-K fp16 block layout, for per-step ingests
+  if (!ctx->w_fc_pk) DFL_TRY(ctx->alloc(&ctx->w_fc_pk, (size_t)ctx->H * K / 8));
+  launch_pack_f16(reinterpret_cast<const half_t*>(fc_weight), ctx->H, K, ctx->w_fc_pk, st);
+  DFL_TRY(check_launch("pack fc"));
   ctx->fc_loaded = true;
   return DFL_OK;
 }
@@ -556,11 +593,28 @@ static int skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const SKPlan& p,
     a.ids = fin ? ids : nullptr;
     if (ids_done) *ids_done = fin;
     if (rope) a.rope = *rope;
+    if (const char* why = check_stream_args(wt, epi, gnorm != nullptr, a, p, mt_n > 1))
+      return fail(DFL_EINVAL, std::string("stream-K GEMM launch refused: ") + why);
     const bool ok =
         mt_n == 1 ? launch_streamk_gemm(wt, epi, gnorm != nullptr, a, p, st, ps.start(), ps.stop())
                   : launch_streamk_gemm_m(wt, epi, gnorm != nullptr, a, p, st, ps.start(), ps.stop());
     if (!ok) return fail(DFL_EINVAL, "no GEMM kernel for this weight type / epilogue");
   }
+  return DFL_OK;
+}
+
+// The rope / attention launchers with their argument checks reported as DFL_EINVAL.
+static int qk_rope(const QKRopeArgs& q, hipStream_t st) {
+  if (const char* why = check_qk_rope_args(q))
+    return fail(DFL_EINVAL, std::string("Q/K norm + RoPE launch refused: ") + why);
+  launch_qk_rope(q, st);
+  return DFL_OK;
+}
+
+static int block_attention(const AttnArgs& at, hipStream_t st) {
+  if (const char* why = check_attn_args(at))
+    return fail(DFL_EINVAL, std::string("attention launch refused: ") + why);
+  launch_block_attention(at, st);
   return DFL_OK;
 }
 
@@ -615,8 +669,70 @@ static int ingest_kv_rows(dfl_ctx* ctx, const half_t* rows_src, int ld, int rows
     q.cap = ctx->cap;
     rope_seq(ctx, ctx->cur, L, ctx->sq().offset + r0, rows, q.sq[0]);
     ProfScope ps(ctx, P_INGEST_KV, 0, st);
-    launch_qk_rope(q, st);
+    DFL_TRY(qk_rope(q, st));
   }
+  return DFL_OK;
+}
+
+// Per-step ingest of C <= SMALL_ING context rows on the stream-K kernels: the rows (or the
+// tapped layers' features) into fragment layout; unless already fused, fc as an fp16 STORE
+// GEMM (each fc weight byte read once) and hidden_norm; then per layer the K|V rows of the
+// packed W8A16 qkv matrix as an int8 STORE GEMM (the Linear's scale and fp16 rounding in
+// its epilogue) and k_norm + RoPE into the cache.  Same arithmetic as the library path.
+static int ingest_small(dfl_ctx* ctx, const half_t* in, int C, bool fused, const FeatPtrs* feats,
+                        hipStream_t st) {
+  const int H = ctx->H, NH = ctx->NH, NKV = ctx->NKV, Nkv = 2 * NKV * 128;
+  FeatPtrs f{};
+  if (feats) {
+    f = *feats;
+  } else {   // one row-major buffer: feature j is columns [j*H, (j+1)*H) of each row
+    f.n = fused ? 1 : ctx->NF;
+    f.ld = (long long)f.n * H;
+    for (int j = 0; j < f.n; ++j) f.p[j] = in + (size_t)j * H;
+  }
+  const half_t* xsrc = ctx->si_in;   // fused rows: already the attention's context rows
+  {
+    ProfScope ps(ctx, P_INGEST_FC, 0, st);
+    launch_feats_to_afl(f, C, H, ctx->si_in, st);
+  }
+  if (!fused) {
+    const int K = ctx->NF * H;
+    DFL_TRY(skgemm(ctx, P_INGEST_FC, WT_F16, EPI_STORE, ctx->sk_fc, ctx->w_fc_pk, nullptr, H,
+                   K / 16, ctx->si_in, K, C, nullptr, false, ctx->si_fc, H, nullptr, nullptr,
+                   nullptr, st));
+    ProfScope ps(ctx, P_INGEST_FC, 0, st);
+    launch_rows_norm_afl(ctx->si_fc, H, C, H, ctx->hidden_norm, ctx->cfg.rms_eps, ctx->si_xn, st);
+    xsrc = ctx->si_xn;
+  }
+  const int KB = H / 32;
+  for (int l = 0; l < ctx->active; ++l) {
+    Layer& L = ctx->layers[l];
+    // the K|V rows start at packed row-block NH*128/32 of the qkv matrix
+    const uint4* w_kv = L.w_qkv + (size_t)(NH * 128 / 32) * KB * 64;
+    DFL_TRY(skgemm(ctx, P_INGEST_KV, WT_INT8, EPI_STORE, ctx->sk_kv, w_kv, L.s_qkv + NH * 128,
+                   Nkv, KB, xsrc, H, C, nullptr, false, ctx->si_kv, Nkv, nullptr, nullptr,
+                   nullptr, st));
+    QKRopeArgs q{};
+    q.qkv16 = ctx->si_kv;
+    q.M = C;
+    q.N = Nkv;
+    q.n_seq = 1;
+    q.col_slot0 = NH;
+    q.slot0 = NH;
+    q.n_slots = 2 * NKV;
+    q.NH = NH;
+    q.NKV = NKV;
+    q.q_norm = L.q_norm;
+    q.k_norm = L.k_norm;
+    q.eps = ctx->cfg.rms_eps;
+    q.log2_theta = std::log2(ctx->cfg.rope_theta);
+    q.Q = nullptr;
+    q.cap = ctx->cap;
+    rope_seq(ctx, ctx->cur, L, ctx->sq().offset, C, q.sq[0]);
+    ProfScope ps(ctx, P_INGEST_KV, 0, st);
+    DFL_TRY(qk_rope(q, st));
+  }
+  ctx->sq().append(C);
   return DFL_OK;
 }
 
@@ -636,6 +752,19 @@ static int ingest(dfl_ctx* ctx, const uint16_t* src, int C, bool fused, void* st
   const int K = ctx->NF * H;
   const half_t* in = reinterpret_cast<const half_t*>(src);
   ctx->sq().last_block = 0;
+  // per-step context rows: stream-K kernels (16-byte aligned rows; else the library path)
+  bool aligned = true;
+  if (feats) {
+    for (int j = 0; j < feats->n; ++j) aligned &= !(reinterpret_cast<uintptr_t>(feats->p[j]) & 15);
+  } else {
+    aligned = !(reinterpret_cast<uintptr_t>(in) & 15);
+  }
+  if (C > 0 && C <= SMALL_ING && aligned && (fused || ctx->w_fc_pk)) {
+    DFL_TRY(ingest_small(ctx, in, C, fused, feats, st));
+    DFL_TRY(check_launch("ingest"));
+    ctx->sq().offset += C;
+    return DFL_OK;
+  }
   for (int r0 = 0; r0 < C; r0 += ctx->ing) {
     const int rows = std::min(ctx->ing, C - r0);
     if (fused) {
@@ -852,6 +981,7 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
       at.O = ctx->attn;
       at.O_rows = blas ? ctx->h2 : nullptr;
       at.n_cu = ctx->n_cu;
+      at.lds_max = ctx->lds_max;
       long long kv_bytes = 0;
       int Ls[SEQ_MAX], n_split[SEQ_MAX];
       for (int i = 0; i < gn; ++i) {
@@ -885,10 +1015,10 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
       }
       if (!fuse_rope) {
         ProfScope ps(ctx, P_QK_ROPE, 0, st);
-        launch_qk_rope(q, st);
+        DFL_TRY(qk_rope(q, st));
       }
       ProfScope ps(ctx, P_ATTN, kv_bytes, st);
-      launch_block_attention(at, st);
+      DFL_TRY(block_attention(at, st));
     }
     if (blas) {
       // the same two steps as library GEMMs with the epilogues in row kernels

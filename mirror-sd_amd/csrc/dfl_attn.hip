@@ -29,6 +29,7 @@
 // needs as its B fragment, so P never goes through LDS.
 #include "dfl_common.h"
 #include "dfl_kernels.h"
+#include "dfl_check.h"
 
 #include <algorithm>
 
@@ -308,7 +309,8 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(AttnArgs a) {
     a.O[afl_index(orow, h * 128 + d, a.NH * 128)] = f2h(num / den_s);
 }
 
-void launch_block_attention(const AttnArgs& a_in, hipStream_t st) {
+bool launch_block_attention(const AttnArgs& a_in, hipStream_t st) {
+  if (check_attn_args(a_in)) return false;
   AttnArgs a = a_in;
   const int R = (a.NH / a.NKV) * a.B;
   const int n_qt = (R + 31) / 32;
@@ -324,7 +326,8 @@ void launch_block_attention(const AttnArgs& a_in, hipStream_t st) {
   // two stage buffers: one sequence whose chunks span several stages, one wave per query
   // tile and at most 5 tiles, and at most one workgroup per CU (the LDS of two buffers)
   const bool pipe = a.n_seq == 1 && a.sq[0].chunk > 32 * AT_STAGE_BLOCKS && a.kw == 1 &&
-                    a.q_per_group <= 5 && (long long)a.chunk0[1] * a.NKV * groups <= a.n_cu;
+                    a.q_per_group <= 5 && (long long)a.chunk0[1] * a.NKV * groups <= a.n_cu &&
+                    a.lds_max >= 2 * AT_STAGE_BYTES;
   if (pipe)
     hipLaunchKernelGGL(block_attn_kernel<true>, dim3(a.chunk0[a.n_seq], a.NKV, groups),
                        dim3(64 * a.q_per_group), 2 * AT_STAGE_BYTES, st, a);
@@ -332,6 +335,7 @@ void launch_block_attention(const AttnArgs& a_in, hipStream_t st) {
     hipLaunchKernelGGL(block_attn_kernel<false>, dim3(a.chunk0[a.n_seq], a.NKV, groups),
                        dim3(64 * a.q_per_group * a.kw), lds_bytes, st, a);
   hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_seq * a.NH * a.B), dim3(128), 0, st, a);
+  return true;
 }
 
 }  // namespace dfl

@@ -1,0 +1,99 @@
+// Host-side consistency checks of the kernel launch argument structs.  Each returns nullptr
+// when the struct is consistent with what its kernel assumes, else a short reason; the
+// launchers refuse (launch nothing) on a reason, and the C ABI reports it as DFL_EINVAL.
+// Pure host code: a host test can exercise every rule without a GPU.
+#pragma once
+
+#include "dfl_kernels.h"
+
+namespace dfl {
+
+constexpr int CHECK_WG_WAVES = 4;   // streaming waves of a stream-K workgroup (unit walk stride)
+constexpr int CHECK_MAX_CHUNKS = 64;
+
+inline const char* check_stream_args(int wt, int epi, bool norm, const StreamArgs& a,
+                                     const SKPlan& p, bool m_split) {
+  if (wt != WT_INT8 && wt != WT_F16) return "unknown weight type";
+  if (!a.W) return "null weight matrix";
+  if (a.N <= 0 || a.N % 64) return "N must be a positive multiple of 64";
+  if (a.KB < CHECK_WG_WAVES) return "fewer k-blocks than streaming waves";
+  if (!a.X) return "null activations";
+  if (a.M < 1) return "no activation rows";
+  if (m_split ? (a.MT < 2 || a.MT > 8 || a.M > 32 * a.MT) : (a.M > 32))
+    return "activation rows exceed the kernel's m-tiles";
+  if (p.workers < 1 || a.seg_cap < 1 || !a.ws || !a.tile_cnt)
+    return "missing split-tile workspace";
+  if (wt == WT_INT8 && !a.scale) return "int8 weights without per-row scales";
+  if (norm) {
+    const int K = a.KB * (wt == WT_INT8 ? 32 : 16);
+    if (!a.gnorm || K > 8192) return "norm-on-load needs a gain of at most 8192 entries";
+    if (!a.ss_in && !a.rnorm) return "norm-on-load needs row sums or 1/rms rows";
+    if (a.ss_in && (a.ss_tiles < 1 || a.ss_tiles > 128 || a.ss_n < 1))
+      return "row-sum tiles outside [1, 128]";
+  }
+  switch (epi) {
+    case EPI_STORE:
+      if (!a.out || a.ldo < a.N) return "STORE without an output of N columns";
+      break;
+    case EPI_RESID:
+      if (!a.x || !a.ss_part) return "RESID without residual rows and row sums";
+      break;
+    case EPI_SWIGLU:
+      if (!a.out || wt != WT_INT8) return "SWIGLU needs int8 weights and an output";
+      break;
+    case EPI_ARGMAX:
+      if (wt != WT_F16 || (!a.keys && !a.logits)) return "ARGMAX needs fp16 weights and keys or logits";
+      break;
+    case EPI_QKROPE: {
+      const RopeEpi& r = a.rope;
+      if (m_split || a.M > 32 || !norm) return "QKROPE is the single-tile normed qkv kernel";
+      if (a.N != (r.NH + 2 * r.NKV) * 128 || r.NH < 1 || r.NKV < 1)
+        return "QKROPE rows are not the q|k|v heads";
+      if (!r.Q || !r.cs || !r.q_norm || !r.k_norm || !r.sq.Kc || !r.sq.Vt || r.cap < 1)
+        return "QKROPE outputs or tables missing";
+      break;
+    }
+    default:
+      return "unknown epilogue";
+  }
+  if (p.dyn_static > 0 && (!a.dyn_next || !a.err || (a.KB & 1) || epi != EPI_ARGMAX))
+    return "balanced plan needs work counters, an error word and an even k-block count";
+  if (a.dp > 0 && ((long long)a.dp * p.workers > a.N / 64 || m_split))
+    return "hybrid plan with more whole tiles than the matrix has";
+  return nullptr;
+}
+
+inline const char* check_qk_rope_args(const QKRopeArgs& a) {
+  if ((a.qkv16 == nullptr) == (a.qkv32 == nullptr)) return "pass exactly one of qkv16 / qkv32";
+  if (a.qkv32 && !a.oscale) return "fp32 rows without per-column scales";
+  if (a.M < 1 || a.n_seq < 1 || a.n_seq > SEQ_MAX) return "rows or sequences out of range";
+  if (a.NH < 1 || a.NKV < 1 || a.n_slots < 1 || a.slot0 < a.col_slot0 ||
+      a.slot0 + a.n_slots > a.NH + 2 * a.NKV)
+    return "head slots outside the q|k|v heads";
+  if ((long long)(a.slot0 + a.n_slots - a.col_slot0) * 128 > a.N) return "slots past the row width";
+  if (a.slot0 < a.NH && !a.Q) return "Q slots without a Q output";
+  if (!a.q_norm || !a.k_norm || a.cap < 1) return "missing norms or cache capacity";
+  if (a.slot0 + a.n_slots > a.NH)
+    for (int s = 0; s < a.n_seq; ++s)
+      if (!a.sq[s].Kc || !a.sq[s].Vt) return "K/V slots without cache pointers";
+  return nullptr;
+}
+
+inline const char* check_attn_args(const AttnArgs& a) {
+  if (!a.Q || !a.Op || !a.Ml || (!a.O && !a.O_rows)) return "missing attention buffers";
+  if (a.B < 1 || a.NH < 1 || a.NKV < 1 || a.NH % a.NKV) return "bad head counts or block rows";
+  if (a.n_seq < 1 || a.n_seq > SEQ_MAX) return "sequences out of range";
+  if (a.max_chunks < 1 || a.max_chunks > CHECK_MAX_CHUNKS) return "chunk count out of range";
+  if (a.chunk0[0] != 0) return "chunk table does not start at 0";
+  for (int s = 0; s < a.n_seq; ++s) {
+    const AttnSeq& q = a.sq[s];
+    if (!q.Kc || !q.Vt || q.L < 1 || q.L > a.cap) return "sequence keys out of range";
+    if (q.chunk < 32 || q.chunk % 32 || q.n_chunks < 1 || q.n_chunks > a.max_chunks ||
+        (long long)q.chunk * q.n_chunks < q.L || (long long)q.chunk * (q.n_chunks - 1) >= q.L)
+      return "key chunks do not tile the keys";
+    if (a.chunk0[s + 1] != a.chunk0[s] + q.n_chunks) return "chunk table inconsistent";
+  }
+  return nullptr;
+}
+
+}  // namespace dfl

@@ -130,6 +130,12 @@ struct FeatPtrs {
 void launch_concat_feats(const FeatPtrs& f, int rows, int H, half_t* out, hipStream_t st);
 void launch_fc_norm_rows(const float* fc32, int rows, int H, const half_t* g, float eps,
                          half_t* xn, hipStream_t st);
+// Stream-K ingest inputs: concat_j(f_j) rows (f.n features of H columns, H % 8 == 0) into
+// activation fragment layout tiles [ceil(rows/32)][32][f.n*H], padding rows zero; and
+// hidden_norm of fp16 rows x [rows][H] (row stride ld) into tiles [ceil(rows/32)][32][H].
+void launch_feats_to_afl(const FeatPtrs& f, int rows, int H, half_t* afl, hipStream_t st);
+void launch_rows_norm_afl(const half_t* x, int ld, int rows, int H, const half_t* g, float eps,
+                          half_t* afl, hipStream_t st);
 void launch_i8_to_f16(const int8_t* q, size_t n, half_t* out, hipStream_t st);
 void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* noise, int B,
                        int H, int V, const half_t* g, float eps, half_t* x, half_t* h,
@@ -184,7 +190,8 @@ DFL_DEV int cache_slot(const RopeSeq& q, int M, int m) {
   if (m - q.sink_fill < M - q.sink_fill - q.ring_W) return -1;
   return q.ring_S + (q.ring_j0 + (m - q.sink_fill)) % q.ring_W;
 }
-void launch_qk_rope(const QKRopeArgs& a, hipStream_t st);
+// Returns false (and launches nothing) when the struct fails check_qk_rope_args.
+bool launch_qk_rope(const QKRopeArgs& a, hipStream_t st);
 // ids[m] = ~low32(keys[m]); keys[m] = 0.
 void launch_argmax_finalize(unsigned long long* keys, int M, int32_t* ids, hipStream_t st);
 // ids[m] = argmax of fp32 logits row m ([M][V]), lowest index on ties, -1 if none > -inf.
@@ -211,6 +218,7 @@ struct AttnArgs {
   int chunk0[SEQ_MAX + 1];
   int q_per_group, kw;    // set by the launcher: query tiles per workgroup, waves per tile
   int n_cu;
+  int lds_max;            // the device's LDS bytes per workgroup (two stage buffers need 160 KiB)
   float scale_log2;       // head_dim^-0.5 * log2(e)
   float* Op;              // [max_chunks][n_seq*NH*B][128] unnormalised partial outputs
   float* Ml;              // [max_chunks][n_seq*NH*B][2] running (max, sum) in log2 domain
@@ -219,6 +227,7 @@ struct AttnArgs {
   half_t* O_rows;
   AttnSeq sq[SEQ_MAX];
 };
-void launch_block_attention(const AttnArgs& a, hipStream_t st);
+// Returns false (and launches nothing) when the struct fails check_attn_args.
+bool launch_block_attention(const AttnArgs& a, hipStream_t st);
 
 }  // namespace dfl

@@ -6,6 +6,7 @@
 // RMSNorm, RoPE and residual add produces an fp16 tensor; internal math is fp32.
 #include "dfl_common.h"
 #include "dfl_kernels.h"
+#include "dfl_check.h"
 
 namespace dfl {
 
@@ -188,6 +189,71 @@ void launch_concat_feats(const FeatPtrs& f, int rows, int H, half_t* out, hipStr
                      f, H, out);
 }
 
+// Context rows into activation fragment layout tiles for the stream-K ingest GEMMs: row r,
+// column k of concat_j(f_j) (feature j gives columns [j*H, (j+1)*H), read through its row
+// stride) goes to afl_index(r, k, K), K = f.n * H; rows in [rows, 32 * tiles) are zero.
+// One thread per 8 consecutive columns (16 bytes, contiguous in both layouts).
+__global__ __launch_bounds__(256) void feats_to_afl_kernel(FeatPtrs f, int H, int rows,
+                                                           half_t* __restrict__ afl) {
+  const int r = blockIdx.y;
+  const int K = f.n * H;
+  const int k = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (k >= K) return;
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (r < rows) {
+    const int j = k / H;
+    v = *reinterpret_cast<const u32x4*>(f.p[j] + (size_t)r * f.ld + (k - j * H));
+  }
+  *reinterpret_cast<u32x4*>(afl + afl_index(r, k, K)) = v;
+}
+
+void launch_feats_to_afl(const FeatPtrs& f, int rows, int H, half_t* afl, hipStream_t st) {
+  const int tiles = (rows + 31) / 32;
+  if (tiles == 0) return;
+  hipLaunchKernelGGL(feats_to_afl_kernel, dim3((f.n * H / 8 + 255) / 256, 32 * tiles), dim3(256),
+                     0, st, f, H, rows, afl);
+}
+
+// hidden_norm of fp16 rows (the ingest's fc output): x [rows][H] (row stride ld) ->
+// fp16(fp16(x * r) * g) into activation fragment layout tiles [tiles][32][H]; rows in
+// [rows, 32 * tiles) are zero.
+__global__ __launch_bounds__(ROW_THREADS) void rows_norm_afl_kernel(
+    const half_t* __restrict__ x, int ld, int rows, int H, const half_t* __restrict__ g,
+    float eps, half_t* __restrict__ afl) {
+  __shared__ float red[16];
+  const int r = blockIdx.x;
+  if (r >= rows) {   // padding row: zero
+    for (int k = threadIdx.x; k < H; k += ROW_THREADS) afl[afl_index(r, k, H)] = (half_t)0.0f;
+    return;
+  }
+  float v[ROW_MAXV];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < ROW_MAXV; ++i) {
+    const int k = threadIdx.x + i * ROW_THREADS;
+    v[i] = 0.f;
+    if (k < H) {
+      v[i] = h2f(x[(size_t)r * ld + k]);
+      ss += v[i] * v[i];
+    }
+  }
+  ss = block_sum(ss, red);
+  const float rr = 1.0f / sqrtf(ss / (float)H + eps);
+#pragma unroll
+  for (int i = 0; i < ROW_MAXV; ++i) {
+    const int k = threadIdx.x + i * ROW_THREADS;
+    if (k < H) afl[afl_index(r, k, H)] = rms_out(v[i], rr, g[k]);
+  }
+}
+
+void launch_rows_norm_afl(const half_t* x, int ld, int rows, int H, const half_t* g, float eps,
+                          half_t* afl, hipStream_t st) {
+  const int tiles = (rows + 31) / 32;
+  if (tiles == 0) return;
+  hipLaunchKernelGGL(rows_norm_afl_kernel, dim3(32 * tiles), dim3(ROW_THREADS), 0, st, x, ld, rows,
+                     H, g, eps, afl);
+}
+
 // hidden_norm(fc(.)) for the ingest: fc32 [rows][H] fp32 GEMM rows, rounded to fp16 (the
 // Linear output), then RMSNorm (fp16(fp16(x * r) * g)) into row-major fp16 xn [rows][H].
 __global__ __launch_bounds__(ROW_THREADS) void fc_norm_rows_kernel(const float* __restrict__ fc32,
@@ -289,9 +355,11 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(QKRopeArgs a) {
   dst[lane + 64] = o1;
 }
 
-void launch_qk_rope(const QKRopeArgs& a, hipStream_t st) {
+bool launch_qk_rope(const QKRopeArgs& a, hipStream_t st) {
+  if (check_qk_rope_args(a)) return false;
   const long long waves = (long long)a.M * a.n_slots * a.n_seq;
   hipLaunchKernelGGL(qk_rope_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, a);
+  return true;
 }
 
 // ids[m] = argmax over the fp32 logits row m (lowest index on ties, NaN never chosen, -1

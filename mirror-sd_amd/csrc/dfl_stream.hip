@@ -33,6 +33,7 @@
 // tiles complete together).
 #include "dfl_common.h"
 #include "dfl_kernels.h"
+#include "dfl_check.h"
 
 #include <hip/hip_ext.h>
 
@@ -1202,6 +1203,7 @@ static void launch_m_t(const StreamArgs& a, const SKPlan& p, hipStream_t st, hip
 
 bool launch_streamk_gemm_m(int wt, int epi, bool norm, const StreamArgs& a, const SKPlan& p,
                            hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop) {
+  if (check_stream_args(wt, epi, norm, a, p, true)) return false;
 #define DFL_SKM_CASE(W_, E_)                                         \
   if (wt == W_ && epi == E_) {                                       \
     if (norm) launch_m_t<W_, E_, true>(a, p, st, ev_start, ev_stop); \
@@ -1219,6 +1221,7 @@ bool launch_streamk_gemm_m(int wt, int epi, bool norm, const StreamArgs& a, cons
 
 bool launch_streamk_gemm(int wt, int epi, bool norm, const StreamArgs& a, const SKPlan& p,
                          hipStream_t st, hipEvent_t ev_start, hipEvent_t ev_stop) {
+  if (check_stream_args(wt, epi, norm, a, p, false)) return false;
   if (p.dyn_static > 0) {   // balanced mode: the fp16 ARGMAX lm_head only
     if (wt != WT_F16 || epi != EPI_ARGMAX || !a.dyn_next || !a.err) return false;
     if (norm) launch_dyn_t<WT_F16, EPI_ARGMAX, true>(a, p, st, ev_start, ev_stop);

@@ -1,0 +1,83 @@
+// Host test of the launch-argument checks (dfl_check.h): one valid struct per launcher,
+// then one rule broken at a time; prints "ok" or the failing case.  Built and run by
+// tests/test_host.py::test_launch_argument_checks (no GPU needed).
+#include <cstdio>
+#include <cstring>
+
+#include "dfl_check.h"
+
+using namespace dfl;
+
+static int fails = 0;
+static void expect(const char* got, const char* needle, const char* what) {
+  const bool ok = needle ? (got && std::strstr(got, needle)) : !got;
+  if (!ok) {
+    std::printf("FAIL %s: got '%s', want '%s'\n", what, got ? got : "(accepted)",
+                needle ? needle : "(accepted)");
+    ++fails;
+  }
+}
+
+int main() {
+  static char dummy[64];
+  void* P = dummy;
+  StreamArgs a{};
+  a.W = (const uint4*)P; a.scale = (const half_t*)P; a.N = 5120; a.KB = 160;
+  a.X = (const half_t*)P; a.ldx = 5120; a.M = 32; a.MT = 1; a.ws = (float*)P; a.seg_cap = 3;
+  a.tile_cnt = (int*)P; a.x = (half_t*)P; a.ss_part = (float*)P; a.out = (half_t*)P; a.ldo = 5120;
+  SKPlan p{};
+  p.workers = 240;
+  a.gnorm = (const half_t*)P; a.ss_in = (const float*)P; a.ss_tiles = 80; a.ss_n = 5120;
+  expect(check_stream_args(WT_INT8, EPI_RESID, false, a, p, false), nullptr, "valid RESID");
+  expect(check_stream_args(WT_INT8, EPI_STORE, true, a, p, false), nullptr, "valid STORE+norm");
+  { StreamArgs b = a; b.M = 33; expect(check_stream_args(WT_INT8, EPI_RESID, false, b, p, false), "m-tiles", "M > 32"); }
+  { StreamArgs b = a; b.M = 65; b.MT = 2; expect(check_stream_args(WT_INT8, EPI_RESID, false, b, p, true), "m-tiles", "M > 32 MT"); }
+  { StreamArgs b = a; b.N = 5000; expect(check_stream_args(WT_INT8, EPI_RESID, false, b, p, false), "multiple of 64", "N"); }
+  { StreamArgs b = a; b.KB = 2; expect(check_stream_args(WT_INT8, EPI_RESID, false, b, p, false), "k-blocks", "KB"); }
+  { StreamArgs b = a; b.scale = nullptr; expect(check_stream_args(WT_INT8, EPI_RESID, false, b, p, false), "scales", "scale"); }
+  { StreamArgs b = a; b.x = nullptr; expect(check_stream_args(WT_INT8, EPI_RESID, false, b, p, false), "RESID", "x"); }
+  { StreamArgs b = a; b.out = nullptr; expect(check_stream_args(WT_INT8, EPI_STORE, false, b, p, false), "STORE", "out"); }
+  { StreamArgs b = a; b.ldo = 100; expect(check_stream_args(WT_INT8, EPI_STORE, false, b, p, false), "STORE", "ldo"); }
+  { StreamArgs b = a; b.gnorm = nullptr; expect(check_stream_args(WT_INT8, EPI_SWIGLU, true, b, p, false), "gain", "gain"); }
+  { StreamArgs b = a; b.ss_in = nullptr; b.rnorm = nullptr; expect(check_stream_args(WT_INT8, EPI_SWIGLU, true, b, p, false), "row sums", "rows"); }
+  { StreamArgs b = a; b.ss_tiles = 200; expect(check_stream_args(WT_INT8, EPI_SWIGLU, true, b, p, false), "tiles", "ss tiles"); }
+  { StreamArgs b = a; expect(check_stream_args(WT_INT8, EPI_ARGMAX, false, b, p, false), "ARGMAX", "argmax int8"); }
+  { StreamArgs b = a; b.keys = nullptr; b.logits = nullptr; expect(check_stream_args(WT_F16, EPI_ARGMAX, false, b, p, false), "ARGMAX", "argmax outputs"); }
+  { StreamArgs b = a; expect(check_stream_args(WT_INT8, EPI_QKROPE, true, b, p, false), "QKROPE", "qkrope rows"); }
+  { StreamArgs b = a; b.dp = 2; expect(check_stream_args(WT_INT8, EPI_RESID, false, b, p, false), "hybrid", "dp"); }
+  { StreamArgs b = a; SKPlan q = p; q.dyn_static = 2; expect(check_stream_args(WT_F16, EPI_STORE, false, b, q, false), "balanced", "dyn"); }
+  { StreamArgs b = a; b.ws = nullptr; expect(check_stream_args(WT_INT8, EPI_RESID, false, b, p, false), "workspace", "ws"); }
+  { StreamArgs b = a; expect(check_stream_args(7, EPI_RESID, false, b, p, false), "weight type", "wt"); }
+  { StreamArgs b = a; expect(check_stream_args(WT_INT8, 42, false, b, p, false), "epilogue", "epi"); }
+
+  QKRopeArgs q{};
+  q.qkv16 = (const half_t*)P; q.M = 32; q.N = 7168; q.n_seq = 1; q.col_slot0 = 0; q.slot0 = 0;
+  q.n_slots = 56; q.NH = 40; q.NKV = 8; q.q_norm = (const half_t*)P; q.k_norm = (const half_t*)P;
+  q.Q = (half_t*)P; q.cap = 4128; q.sq[0].Kc = (half_t*)P; q.sq[0].Vt = (half_t*)P;
+  expect(check_qk_rope_args(q), nullptr, "valid rope");
+  { QKRopeArgs b = q; b.qkv32 = (const float*)P; expect(check_qk_rope_args(b), "exactly one", "both inputs"); }
+  { QKRopeArgs b = q; b.qkv16 = nullptr; expect(check_qk_rope_args(b), "exactly one", "no input"); }
+  { QKRopeArgs b = q; b.qkv16 = nullptr; b.qkv32 = (const float*)P; expect(check_qk_rope_args(b), "scales", "fp32 no scale"); }
+  { QKRopeArgs b = q; b.Q = nullptr; expect(check_qk_rope_args(b), "Q output", "no Q"); }
+  { QKRopeArgs b = q; b.n_slots = 57; expect(check_qk_rope_args(b), "slots", "slots"); }
+  { QKRopeArgs b = q; b.N = 2048; expect(check_qk_rope_args(b), "row width", "width"); }
+  { QKRopeArgs b = q; b.n_seq = 9; expect(check_qk_rope_args(b), "range", "n_seq"); }
+  { QKRopeArgs b = q; b.sq[0].Kc = nullptr; expect(check_qk_rope_args(b), "cache", "cache"); }
+  { QKRopeArgs b = q; b.Q = nullptr; b.col_slot0 = 40; b.slot0 = 40; b.n_slots = 16; b.N = 2048; expect(check_qk_rope_args(b), nullptr, "valid K|V only"); }
+
+  AttnArgs t{};
+  t.Q = (const half_t*)P; t.B = 32; t.NH = 40; t.NKV = 8; t.cap = 4128; t.n_seq = 1;
+  t.max_chunks = 26; t.chunk0[0] = 0; t.chunk0[1] = 26; t.Op = (float*)P; t.Ml = (float*)P;
+  t.O = (half_t*)P; t.sq[0].Kc = (const half_t*)P; t.sq[0].Vt = (const half_t*)P; t.sq[0].L = 4128;
+  t.sq[0].chunk = 160; t.sq[0].n_chunks = 26;
+  expect(check_attn_args(t), nullptr, "valid attention");
+  { AttnArgs b = t; b.sq[0].chunk = 150; expect(check_attn_args(b), "chunks", "chunk not 32x"); }
+  { AttnArgs b = t; b.sq[0].n_chunks = 25; b.chunk0[1] = 25; b.max_chunks = 25; expect(check_attn_args(b), "chunks", "chunks short"); }
+  { AttnArgs b = t; b.chunk0[1] = 20; expect(check_attn_args(b), "table", "chunk table"); }
+  { AttnArgs b = t; b.sq[0].L = 5000; expect(check_attn_args(b), "keys", "L > cap"); }
+  { AttnArgs b = t; b.NH = 41; expect(check_attn_args(b), "head counts", "ratio"); }
+  { AttnArgs b = t; b.O = nullptr; expect(check_attn_args(b), "buffers", "no output"); }
+  { AttnArgs b = t; b.max_chunks = 65; expect(check_attn_args(b), "chunk count", "max chunks"); }
+  if (fails == 0) std::printf("ok\n");
+  return fails ? 1 : 0;
+}

@@ -16,6 +16,10 @@ so a test can tell a change of the input recipe from a change of the results:
                   same outputs for 32 rows.
   dflash_27b_ctxN the 27B-class draft at context N in {64, 2048, 16384, 32768} (the context
                   sweep; N = 4096 is dflash_27b): same weights (seed 0), inputs of N rows.
+  dflash_27b_steady  the 27B-class draft in a decode loop: context rows 0..4096, then 1,
+                  16 and 32 more rows; after each of those ingests a block of 32 is drafted.
+                  One fixture entry per step (prefix s0, s1, s2), each the oracle's single
+                  pass over that step's context prefix (4097, 4113, 4145 rows).
   llama8b_batch   5 layers, H4096, 32/8, FFN 14336, V128256, theta 5e5; 8 independent
                   sequences x block 32 with contexts [4146, 4443, 6312, 7812, 779, 1619, 6833,
                   7798]; each sequence run through the single-sequence oracle; outputs stacked
@@ -109,6 +113,39 @@ def case_full(name, seed=0, f64_only=False):
                 top2_val=tv, ids_f64=ids64, top2_val_f64=tv64), dig
 
 
+STEADY_BASE, STEADY_STEPS = 4096, (1, 16, 32)
+
+
+def case_steady(name="dflash_27b_steady", seed=0, f64_only=False):
+    """The decode-loop protocol: the context grows by STEADY_STEPS rows after a 4096-row
+    prefix; a draft after each step equals a single pass over the prefix (context K/V
+    depend only on the fused context rows and their positions)."""
+    wl = workload("dflash_27b")
+    cfg = wl.cfg
+    total = STEADY_BASE + sum(STEADY_STEPS)
+    t = synth.make_weights_numpy(cfg, seed=seed)
+    inp = synth.make_inputs_numpy(cfg, wl.block, total, seed=seed)
+    dig = input_digests(t, inp)
+    W = O.OracleWeights(cfg, t)
+    del t
+    out = {}
+    n = STEADY_BASE
+    for i, k in enumerate(STEADY_STEPS):
+        n += k
+        sub = {"ids": inp["ids"], "target_hidden": inp["target_hidden"][:n]}
+        ids64, tv64 = f64_outputs(W, sub)
+        out[f"s{i}_ids_f64"], out[f"s{i}_top2_val_f64"] = ids64, tv64
+        if f64_only:
+            continue
+        h, logits, ids = O.draft_block(W, sub["ids"], sub["target_hidden"], fp16=True,
+                                       dtype=np.float32)
+        ti, tv = top2(logits)
+        out.update({f"s{i}_hidden": h.astype(np.float16), f"s{i}_ids": ids.astype(np.int32),
+                    f"s{i}_top2_idx": ti, f"s{i}_top2_val": tv})
+        print(f"{name}: step {i} ({n} context rows) done", flush=True)
+    return out, dig
+
+
 def case_batch(name="llama8b_batch", seed=0, f64_only=False):
     wl = workload(name)
     cfg = wl.cfg
@@ -146,6 +183,7 @@ CASES = {
                               case_full(f"dflash_27b_ctx{c}", f64_only=f64_only))
        for c in (64, 2048, 16384, 32768)},
     "llama8b_batch": lambda f64_only=False: case_batch("llama8b_batch", f64_only=f64_only),
+    "dflash_27b_steady": lambda f64_only=False: case_steady(f64_only=f64_only),
 }
 ARGMAX_CASES = [n for n in CASES if n != "qwen3_4b_layer"]
 

@@ -145,3 +145,43 @@ def test_context_sweep_matches_golden(sweep_model, ctx):
                                     want_ids=True)
         torch.cuda.synchronize()
         _check_against(g, name + " (chunked ingest)", ids2, lg2, h2)
+
+
+def test_decode_loop_matches_golden():
+    """The 27B-class draft in a decode loop: 4096 context rows ingested at once (library
+    GEMMs), then 1, 16 and 32 more rows per step (the stream-K per-step ingest), a block of
+    32 drafted after each step against the oracle's single pass over the same prefix."""
+    from golden.make_golden import STEADY_BASE, STEADY_STEPS
+    from mirror_sd_amd import _lib
+    from mirror_sd_amd.dflash import DFlashDraftModel
+    name = "dflash_27b_steady"
+    g = load(name)
+    wl = workload("dflash_27b")
+    total = STEADY_BASE + sum(STEADY_STEPS)
+    print(f"case {name}: generating inputs", flush=True)
+    t = synth.make_weights_numpy(wl.cfg, seed=0)
+    inp = synth.make_inputs_numpy(wl.cfg, wl.block, total, seed=0)
+    assert input_digests(t, inp) == dict(zip(g["digest_names"].tolist(),
+                                             g["digest_values"].tolist()))
+    m = DFlashDraftModel(wl.cfg, max_ctx=total)
+    m.load_weights(torch_tensors(t, "cuda"))
+    del t
+    torch.cuda.empty_cache()
+    th = torch.from_numpy(inp["target_hidden"]).cuda()
+    ids = torch.from_numpy(inp["ids"])
+    _lib.check(m._L.dfl_cache_reset(m._ctx), "dfl_cache_reset")
+    m._gen += 1
+    m._ingest(th[:STEADY_BASE])
+    n = STEADY_BASE
+    for i, k in enumerate(STEADY_STEPS):
+        print(f"case {name}: step {i}, {k} new rows", flush=True)
+        m._ingest(th[n:n + k])
+        n += k
+        h, _, lg, idg = m._draft(ids=ids, want_logits=True, want_ids=True)
+        torch.cuda.synchronize()
+        assert_close_fp16(h.float().cpu().numpy(), g[f"s{i}_hidden"], what=f"{name} step {i} hidden")
+        check_argmax(idg.cpu().numpy(), lg.cpu().numpy(), g[f"s{i}_ids"], g[f"s{i}_ids_f64"],
+                     f"{name} step {i} ({n} context rows)", g[f"s{i}_top2_idx"],
+                     g[f"s{i}_top2_val"], LOGIT_TOL)
+    assert device_errors(m) == 0
+    m.close()

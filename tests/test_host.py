@@ -89,6 +89,24 @@ def test_noalloc_embed_block_validates_before_device_work():
         assert needle in lib.dfl_last_error().decode(), (bad, lib.dfl_last_error())
 
 
+def test_launch_argument_checks(tmp_path):
+    """The host-side checks of the kernel launch structs (dfl_check.h) refuse each kind of
+    inconsistent argument: built with hipcc as a host program and run on the CPU."""
+    import shutil
+    import subprocess
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(hipcc):
+        pytest.skip("hipcc not available")
+    exe = str(tmp_path / "check_args_host")
+    csrc = os.path.join(ROOT, "mirror-sd_amd", "csrc")
+    r = subprocess.run([hipcc, "--offload-arch=gfx950", "-std=c++17", "-O1", "-I", csrc,
+                        os.path.join(ROOT, "tests", "check_args_host.hip"), "-o", exe],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0 and r.stdout.strip() == "ok", r.stdout + r.stderr
+
+
 def test_build_target_layer_ids():
     assert build_target_layer_ids(36, 5) == [1, 9, 17, 25, 33]
     assert build_target_layer_ids(36, 1) == [18]
