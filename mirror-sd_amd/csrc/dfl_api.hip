@@ -3,6 +3,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -575,6 +576,8 @@ static int skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const SKPlan& p,
     // one m-tile: the hybrid plan when it has whole tiles per workgroup; the M-split kernel
     // keeps the contiguous partition
     a.dp = mt_n == 1 ? p.dp : 0;
+    // test hook of the balanced kernel's bounded work-queue wait (its give-up path)
+    a.dyn_test_timeout = p.dyn_static > 0 && std::getenv("DFL_TEST_QUEUE_TIMEOUT") != nullptr;
     a.seg_cap = a.dp > 0 ? p.sk_seg_cap : p.seg_cap;
     a.tile_cnt = ctx->sk_tile_cnt;
     a.out = out ? out + (size_t)m0 * ldo : nullptr;

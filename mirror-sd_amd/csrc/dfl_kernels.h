@@ -68,6 +68,7 @@ struct StreamArgs {
   int32_t* ids;             // balanced ARGMAX: the last workgroup turns keys [M] into ids [M]
                             // (-1 for a row without a number) and re-arms keys to zero
   int dp;                   // hybrid plan (SKPlan::dp): whole tiles per workgroup
+  int dyn_test_timeout;     // balanced mode: force the work-queue wait to give up (test hook)
   RopeEpi rope;             // EPI_QKROPE
 };
 struct SKPlan {

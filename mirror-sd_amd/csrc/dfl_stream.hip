@@ -164,7 +164,7 @@ template <int WT, bool NORM, int P>
 DFL_DEV void stream_range(const StreamArgs& a, const half_t* gsh, const float* rn_lds,
                           int* ready, float (*red)[WG_WAVES][2048], int* arrived, int* reduced,
                           long long u0, long long u1, long long v0, long long v1, int w,
-                          int lane, int& si) {
+                          int lane, int& si, const int* abort = nullptr) {
   constexpr int KBK = KTraits<WT>::KBK;
   constexpr int NX = KTraits<WT>::NX;
   const int m = lane & 31, g = lane >> 5;
@@ -177,8 +177,10 @@ DFL_DEV void stream_range(const StreamArgs& a, const half_t* gsh, const float* r
   floatx16 acc0 = (floatx16){}, acc1 = (floatx16){};
   // si: segments flushed so far by this wave (continues across calls)
   auto flush = [&]() {
-    // slot set si & 1 was last used by segment si - 2: wait until it has been reduced
-    while (__hip_atomic_load(reduced, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < si - 1)
+    // slot set si & 1 was last used by segment si - 2: wait until it has been reduced (or
+    // the workgroup aborted: its results are invalid, every wave just runs to its end)
+    while (__hip_atomic_load(reduced, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < si - 1 &&
+           !(abort && __hip_atomic_load(abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)))
       __builtin_amdgcn_s_sleep(1);
     float* dst = red[si & 1][w];
 #pragma unroll
@@ -543,9 +545,11 @@ DFL_DEV void reducer_norm_prologue(const StreamArgs& a, int lane, half_t* gsh, f
 // in a fixed order, hands the slot set back and completes the tile -- directly when the
 // segment covers it (count == 1), else as worker `slot` of the `count` sharing it.
 DFL_DEV void sum_wave_partials(int lane, float (*red)[WG_WAVES][2048], int* arrived,
-                               int* reduced, int si, floatx16& acc0, floatx16& acc1) {
+                               int* reduced, int si, floatx16& acc0, floatx16& acc1,
+                               const int* abort = nullptr) {
   while (__hip_atomic_load(&arrived[si & 1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
-         WG_WAVES * ((si >> 1) + 1))
+             WG_WAVES * ((si >> 1) + 1) &&
+         !(abort && __hip_atomic_load(abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)))
     __builtin_amdgcn_s_sleep(1);
   acc0 = (floatx16){};
   acc1 = (floatx16){};
@@ -564,10 +568,11 @@ DFL_DEV void sum_wave_partials(int lane, float (*red)[WG_WAVES][2048], int* arri
 
 template <int EPI>
 DFL_DEV void reduce_segment(const StreamArgs& a, int lane, float (*red)[WG_WAVES][2048],
-                            int* arrived, int* reduced, int si, int t, int slot, int count) {
+                            int* arrived, int* reduced, int si, int t, int slot, int count,
+                            const int* abort = nullptr) {
   const EpiIn in = epi_prefetch<EPI>(a, lane, t);   // in flight while the partials arrive
   floatx16 acc0, acc1;
-  sum_wave_partials(lane, red, arrived, reduced, si, acc0, acc1);
+  sum_wave_partials(lane, red, arrived, reduced, si, acc0, acc1, abort);
   const bool complete = count == 1 || finish_split_tile(a, lane, t, slot, count, acc0, acc1);
   if (complete) tile_epilogue<EPI>(a, lane, t, acc0, acc1, in);
 }
@@ -904,6 +909,10 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_gemm_kernel(StreamArg
 // ---------------------------------------------------------------------------------------
 constexpr int DYN_SPIN_LIMIT = 1 << 24;   // s_sleep rounds before a queue wait gives up
 constexpr int DYN_ERR = 4;                // device error bit: a queue wait gave up
+// With StreamArgs::dyn_test_timeout set, the queue wait's condition is never met and it gives
+// up after this many rounds: the host forces the give-up path (its test), every wave still
+// ends normally.
+constexpr int DYN_TEST_SPIN_LIMIT = 256;
 
 template <int WT, int EPI, bool NORM, int P>
 __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_dyn_kernel(StreamArgs a) {
@@ -913,6 +922,9 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_dyn_kernel(StreamArgs
   __shared__ float rn_s[32];
   __shared__ int arrived[2], reduced, ready;
   __shared__ int q_chunk[4], q_pub;
+  // abort: set by a streaming wave whose queue wait gave up; every other wait of the
+  // workgroup then stops waiting, so all waves run to their end (results invalid, DYN_ERR set)
+  __shared__ int abort;
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -925,6 +937,7 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_dyn_kernel(StreamArgs
     reduced = 0;
     ready = 0;
     q_pub = 0;
+    abort = 0;
   }
   __syncthreads();
 
@@ -933,12 +946,18 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_dyn_kernel(StreamArgs
     if (S > 0)
       stream_range<WT, NORM, P>(a, gsh, rn_s, &ready, red, arrived, &reduced,
                                 (long long)b * S * KB, (long long)(b + 1) * S * KB, 0, 0, w,
-                                lane, si);
+                                lane, si, &abort);
+    const int limit = a.dyn_test_timeout ? DYN_TEST_SPIN_LIMIT : DYN_SPIN_LIMIT;
     for (int k = 0;; ++k) {
       int spins = 0;
-      while (__hip_atomic_load(&q_pub, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <= k) {
-        if (++spins > DYN_SPIN_LIMIT) {
-          if (lane == 0) atomicOr(a.err, DYN_ERR);
+      while (__hip_atomic_load(&q_pub, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <= k ||
+             a.dyn_test_timeout) {
+        if (++spins > limit ||
+            __hip_atomic_load(&abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) {
+          if (lane == 0) {
+            atomicOr(a.err, DYN_ERR);
+            __hip_atomic_store(&abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          }
           return;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -947,7 +966,7 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_dyn_kernel(StreamArgs
       if (c < 0) break;
       const long long c0 = (long long)(T0 + (c >> 1)) * KB + (long long)(c & 1) * half;
       stream_range<WT, NORM, P>(a, gsh, rn_s, &ready, red, arrived, &reduced, c0, c0 + half, 0,
-                                0, w, lane, si);
+                                0, w, lane, si, &abort);
     }
     return;
   }
@@ -974,14 +993,14 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_dyn_kernel(StreamArgs
   int si = 0;
   for (int i = 0; i < S; ++i, ++si) {
     if (i == S - 1) publish_next();   // entry 0 before the last static segment's wait
-    reduce_segment<EPI>(a, lane, red, arrived, &reduced, si, b * S + i, 0, 1);
+    reduce_segment<EPI>(a, lane, red, arrived, &reduced, si, b * S + i, 0, 1, &abort);
   }
   if (S == 0) publish_next();
   for (int k = 0;; ++k, ++si) {
     const int c = __shfl(q_chunk[k & 3], 0, 64);   // entry k, published by this wave
     if (c < 0) break;
     publish_next();                   // entry k + 1 before waiting for chunk k
-    reduce_segment<EPI>(a, lane, red, arrived, &reduced, si, T0 + (c >> 1), c & 1, 2);
+    reduce_segment<EPI>(a, lane, red, arrived, &reduced, si, T0 + (c >> 1), c & 1, 2, &abort);
   }
   // this workgroup's epilogue atomics and stores are performed before it counts itself
   // finished, so the last one to finish sees every tile's argmax key

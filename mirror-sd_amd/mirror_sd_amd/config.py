@@ -203,3 +203,12 @@ def workload(name: str) -> Workload:
         cfg = _draft_cfg(256, 4, 2, 512, 2, vocab=1024, block=8)
         return Workload(name, cfg, block=8, ctx=24, description="test shape")
     raise KeyError(name)
+
+
+def require_unscaled_rope(cfg) -> None:
+    """Raise NotImplementedError for a rope_scaling other than the default: the reference
+    scales RoPE through mlx_lm's initialize_rope (mirror_sd/dflash.py:254-262); only
+    unscaled neox RoPE is implemented here."""
+    rs = getattr(cfg, "rope_scaling", None)
+    if rs is not None and (rs.get("rope_type", rs.get("type")) not in (None, "default")):
+        raise NotImplementedError(f"rope_scaling {rs!r}: only unscaled RoPE is implemented")

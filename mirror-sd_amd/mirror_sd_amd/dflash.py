@@ -25,7 +25,7 @@ import ctypes
 from typing import Dict, List, Optional
 
 from . import _lib
-from .config import DFlashConfig
+from .config import DFlashConfig, require_unscaled_rope
 from .synth import PROJ_NAMES, proj_key
 
 __all__ = ["DFlashDraftModel", "DFlashKVCache", "sample"]
@@ -111,6 +111,7 @@ class DFlashDraftModel:
     def __init__(self, config: DFlashConfig, max_ctx: int = 8192, max_block: Optional[int] = None,
                  device=None, n_target_feat: Optional[int] = None, max_seqs: int = 1):
         import torch
+        require_unscaled_rope(config)
         self.config = config
         self.block_size = config.block_size
         self.mask_token_id = config.mask_token_id

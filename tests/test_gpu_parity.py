@@ -325,3 +325,74 @@ def test_capacity_boundaries():
                           what=f"layer {layer} keys")
         assert_close_fp16(cache[layer].values[0].float().cpu().numpy(), ocache[layer].values,
                           what=f"layer {layer} values")
+
+
+def test_lm_head_queue_give_up_reports_error_and_recovers(monkeypatch):
+    """The balanced lm_head's bounded work-queue wait: forced to give up from the host
+    (DFL_TEST_QUEUE_TIMEOUT makes its wait condition unsatisfiable for a few hundred
+    rounds), every wave still ends, device error bit 2 is set, and the next call -- its
+    self-resetting counters re-armed -- gives the same results as before."""
+    from parity_util import device_errors
+    cfg = DFlashConfig(hidden_size=256, num_hidden_layers=1, intermediate_size=512,
+                       num_attention_heads=4, num_key_value_heads=2, head_dim=128,
+                       vocab_size=65536, block_size=8, mask_token_id=65535)
+    t = synth.make_weights_numpy(cfg, seed=5)
+    inp = synth.make_inputs_numpy(cfg, 8, 16, seed=5)
+    m = _model(cfg, max_ctx=16)
+    m.load_weights(torch_tensors(t, "cuda"))
+    ids, lg = m.draft(torch.from_numpy(inp["ids"]), torch.from_numpy(inp["target_hidden"]),
+                      return_logits=True)
+    torch.cuda.synchronize()
+    assert device_errors(m) == 0
+    ids, lg = ids.cpu().numpy(), lg.cpu().numpy()
+    monkeypatch.setenv("DFL_TEST_QUEUE_TIMEOUT", "1")
+    m.draft(torch.from_numpy(inp["ids"]), torch.from_numpy(inp["target_hidden"]))
+    torch.cuda.synchronize()
+    assert device_errors(m) & 4
+    monkeypatch.delenv("DFL_TEST_QUEUE_TIMEOUT")
+    for _ in range(2):
+        ids2, lg2 = m.draft(torch.from_numpy(inp["ids"]), torch.from_numpy(inp["target_hidden"]),
+                            return_logits=True)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(ids2.cpu().numpy(), ids)
+        np.testing.assert_array_equal(lg2.cpu().numpy(), lg)
+    assert device_errors(m) == 0
+    m.close()
+
+
+@pytest.mark.parametrize("n_heads", [24, 32])
+def test_two_stage_attention_with_sink_window_matches_oracle(n_heads):
+    """Long single-sequence contexts run the attention with two LDS stage buffers (chunks of
+    more than 160 keys, one workgroup per CU): here with 3 and 4 query tiles per KV head
+    (24 / 32 query heads over 8 KV heads, block 32) and a sink + window ring whose chunks
+    span several stages, against the oracle's windowed cache over two steps (the second
+    evicts middle rows; 64 + 6400 keys are live)."""
+    cfg = DFlashConfig(hidden_size=256, num_hidden_layers=1, intermediate_size=512,
+                       num_attention_heads=n_heads, num_key_value_heads=8, head_dim=128,
+                       vocab_size=1024, block_size=32, mask_token_id=1023)
+    B, sink, window = 32, 64, 6400
+    steps = (4000, 3000)
+    t = synth.make_weights_numpy(cfg, seed=11)
+    W = O.OracleWeights(cfg, t)
+    ids = np.array([7] + [1023] * (B - 1), dtype=np.int32)
+    noise = O.embed(W, ids).astype(np.float16)
+    th_all = synth.np_normal(11, "twostage.th", (sum(steps), 5 * cfg.hidden_size), 1.0,
+                             np.float16)
+    m = _model(cfg, max_ctx=sum(steps) + B)
+    m.load_weights(torch_tensors(t, "cuda"))
+    cache = m.make_cache(sink, window)
+    ocache = [O.OracleKVCache(sink, window)]
+    ne = torch.from_numpy(noise)[None]
+    r0 = 0
+    for i, C in enumerate(steps):
+        print(f"two-stage attention: {n_heads} heads, step {i}, {C} rows", flush=True)
+        th = th_all[r0:r0 + C]
+        r0 += C
+        ref = O.draft_forward(W, noise, th, cache=ocache, fp16=True)
+        out = m(ne, torch.from_numpy(th)[None], cache=cache)
+        torch.cuda.synchronize()
+        assert_close_fp16(out[0].float().cpu().numpy(), ref, what=f"step {i}")
+        for c in cache:
+            c.trim(B)
+        ocache[0].trim(B)
+    assert ocache[0].keys.shape[1] == sink + window - B   # eviction happened

@@ -170,3 +170,16 @@ def test_bench_compiles_and_refuses_several_gpus():
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2, r.stderr
     assert "one GPU" in r.stderr
+
+
+def test_model_refuses_scaled_rope():
+    """A config carrying a non-default rope_scaling is refused by the model itself, not only
+    by the loader (the reference applies the scaling in initialize_rope, dflash.py:254-262)."""
+    from mirror_sd_amd.dflash import DFlashDraftModel
+    cfg = DFlashConfig.from_dict({"hidden_size": 256, "num_hidden_layers": 1,
+                                  "rope_scaling": {"rope_type": "yarn", "factor": 4.0}})
+    with pytest.raises(NotImplementedError):
+        DFlashDraftModel(cfg, max_ctx=16)
+    cfg = DFlashConfig.from_dict({"hidden_size": 256, "rope_scaling": {"rope_type": "default"}})
+    from mirror_sd_amd.config import require_unscaled_rope
+    require_unscaled_rope(cfg)   # the default type is plain RoPE
