@@ -42,12 +42,27 @@ def common_flags(debug: bool):
     return f
 
 
+# The packed-FP32 guard (-target-feature -packed-fp32-ops) reaches hipcc's host (x86) pass
+# too, which reports it as an unknown feature on every compile; hipcc cannot scope -Xclang
+# arguments to the device pass (-Xarch_device refuses them), so that one line is dropped and
+# every other compiler message is shown.
+_HOST_FEATURE_NOTE = "'-packed-fp32-ops' is not a recognized feature for this target"
+
+
+def compiler_messages(text: str) -> str:
+    return "\n".join(l for l in text.splitlines()
+                     if l.strip() and _HOST_FEATURE_NOTE not in l and "--hip-link" not in l)
+
+
 def compile_one(src: str, debug: bool) -> str:
     obj = os.path.join(BUILD, os.path.basename(src).replace(".hip", ".o"))
     cmd = [hipcc(), *common_flags(debug), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    msgs = compiler_messages(r.stdout + "\n" + r.stderr)
+    if msgs:
+        print(f"{os.path.basename(src)}:\n{msgs}", file=sys.stderr)
     return obj
 
 
