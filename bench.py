@@ -274,35 +274,41 @@ def run_workload(wl, args, sweep, want_cpu):
         return per_launch, avg_s, per_launch / avg_s / 1e9
 
     roofline, kernels = None, None
-    if gprof and gprof.get("gemm_w8a16", {}).get("launches"):
-        per_launch, avg_s, ach = rate(gprof["gemm_w8a16"])
+    rows = n_seq * wl.block
+    stacked = rows > 64
+    gkey = "gemm_tile_rows" if stacked else "gemm_w8a16"
+    if gprof and gprof.get(gkey, {}).get("launches"):
+        per_launch, avg_s, ach = rate(gprof[gkey])
         # 2 * rows flop per int8 weight byte: above the MFMA/HBM ridge the projections are
         # bounded by the matrix cores (stacked blocks), below it by HBM (one block)
-        rows = n_seq * wl.block
         if 2.0 * rows > MFMA_F16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9):
-            tf = 2.0 * rows * per_launch / avg_s / 1e12   # scale bytes are negligible here
+            tf = 2.0 * rows * per_launch / avg_s / 1e12
             roofline = {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_F16_PEAK_TFLOPS,
                         "unit": "TFLOP/s", "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
                         "hbm_gbps": round(ach, 1)}
         else:
             roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
                         "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4)}
-        kname = ("gsk_gemm_m_kernel<int8,RESID> (stream-K W8A16 down projection of the stacked "
-                 "rows; qkv / o / gate_up run as library GEMMs)" if rows > 64 else
+        kname = ("tile_gemm_kernel<int8> (LDS-staged MFMA tile GEMM of the stacked rows: qkv, "
+                 "o, gate_up, down)" if stacked else
                  "gsk_gemm_kernel<int8,*> (stream-K W8A16 projections qkv/o/gate_up/down, one "
                  "launch each per layer)")
         roofline.update({"traffic": traffic_per_launch(wl.name), "kernel": kname,
                          "bytes_per_launch": per_launch, "avg_launch_us": round(avg_s * 1e6, 3),
-                         "launches": gprof["gemm_w8a16"]["launches"]})
+                         "launches": gprof[gkey]["launches"]})
         lm = gprof.get("lm_head_argmax", {})
         if lm.get("launches"):
             per_launch, avg_s, ach = rate(lm)
-            lm_name = ("rocBLAS GEMM + row argmax (stacked rows)" if rows > 64 else
+            lm_name = ("tile_gemm_kernel<fp16> (stacked rows; row argmax after)" if stacked else
                        "gsk_dyn_kernel<fp16,ARGMAX> (balanced)")
             roofline["lm_head"] = {"kernel": lm_name, "achieved": round(ach, 1),
                                    "frac": round(ach / HBM_PEAK_GBS, 4),
                                    "bytes_per_launch": per_launch,
                                    "avg_launch_us": round(avg_s * 1e6, 3)}
+            if stacked:   # fp16 weights: rows flop per weight byte
+                tf = rows * per_launch / avg_s / 1e12
+                roofline["lm_head"].update({"tflops": round(tf, 1),
+                                            "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
     if not args.no_profile and args.profile_steps > 0:
         # per-group breakdown; groups other than the GEMMs are bracketed by marker events,
         # which add a few microseconds of dispatch latency each

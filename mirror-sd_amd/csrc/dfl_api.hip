@@ -14,6 +14,7 @@
 #include "dflash_hip.h"
 #include "dfl_kernels.h"
 #include "dfl_check.h"
+#include "dfl_tile_plan.h"
 
 using namespace dfl;
 
@@ -35,20 +36,22 @@ int fail(int code, const std::string& msg) {
 constexpr int ING_MAX = 4096;      // context rows per ingest pass (at most)
 // Ingest calls of at most SMALL_ING rows (the per-step context of a decode loop: acceptance
 // + 1 rows) run on the stream-K kernels, which stream each weight once at HBM rate; larger
-// (prompt) ingests are compute-bound and run on rocBLAS.
+// (prompt) ingests are compute-bound: their K|V rows run on the tile GEMM (MFMA) over the
+// packed int8 qkv matrix, the fc on rocBLAS over the fp16 fc weight.
 constexpr int SMALL_ING = 64;
 constexpr int MAX_CHUNKS = 64;     // attention key splits
 constexpr int MT_MAX = 8;          // 32-row m-tiles per M-split GEMM launch
-// Stacked blocks of more than BLAS_MIN_ROWS rows (batched drafting) are compute-bound: their
-// qkv, o, gate|up and lm_head products run as rocBLAS GEMMs over exact fp16 weight copies.
-constexpr int BLAS_MIN_ROWS = 64;
+// Stacked blocks of more than STACK_MIN_ROWS rows (batched drafting) are compute-bound: their
+// projections and the lm_head run on the tile GEMM (MFMA, LDS-staged) over the packed weights,
+// with the epilogues in row kernels.
+constexpr int STACK_MIN_ROWS = 64;
 
 enum ProfCat {
-  P_GEMM_W8 = 0, P_LM_HEAD, P_ATTN, P_QK_ROPE, P_ROWS, P_INGEST_FC, P_INGEST_KV, P_GEMM_BLAS, P_N
+  P_GEMM_W8 = 0, P_LM_HEAD, P_ATTN, P_QK_ROPE, P_ROWS, P_INGEST_FC, P_INGEST_KV, P_GEMM_TILE, P_N
 };
 const char* const kProfNames[P_N] = {"gemm_w8a16",   "lm_head_argmax", "attention",
                                      "qk_norm_rope", "row_reduce_norm", "ingest_fc",
-                                     "ingest_kv",    "gemm_blas_rows"};
+                                     "ingest_kv",    "gemm_tile_rows"};
 
 struct ProfRec {
   int cat;
@@ -101,10 +104,6 @@ struct Layer {
   half_t *s_qkv = nullptr, *s_o = nullptr, *s_gu = nullptr, *s_down = nullptr;
   half_t *in_norm = nullptr, *post_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
   half_t *Kc = nullptr, *Vt = nullptr;   // [max_seqs][NKV][cap][128], [max_seqs][NKV][128][cap]
-  half_t* w_kv16 = nullptr;              // [2*NKV*128][H] fp16 copy of the k|v int8 rows
-  // stacked blocks: exact fp16 copies [q;k;v] [NQKV][H] (w_kv16 points into it), o [H][NQ],
-  // [gate;up] [2F][H]
-  half_t *w_qkv16 = nullptr, *w_o16 = nullptr, *w_gu16 = nullptr;
   bool loaded = false;
 };
 
@@ -127,15 +126,13 @@ struct dfl_ctx {
   bool fc_loaded = false;
   half_t* final_norm = nullptr;
   uint4* w_lm = nullptr;
-  // stacked blocks (more than BLAS_MIN_ROWS rows): the lm_head as a library GEMM over a
-  // row-major fp16 copy, logits in lm32 [RM][V] fp32
-  half_t* w_lm16 = nullptr;
+  // stacked blocks (more than STACK_MIN_ROWS rows): lm_head logits lm32 [RM][V] fp32
   float* lm32 = nullptr;
   float* y32 = nullptr;      // [RM][max(NQKV, H, 2F)] fp32 rows of the stacked-block GEMMs
-  half_t* h2 = nullptr;      // [RM][NH*128] attention output rows (row-major)
   const half_t* embed = nullptr;
   bool head_loaded = false;
   int active = 0;   // layers run per call (num_draft_layers)
+  // x, attn, act and h (the normed rows of stacked blocks) in the activation fragment layout
   half_t *x = nullptr, *h = nullptr, *Q = nullptr, *attn = nullptr, *act = nullptr;
   float *Op = nullptr, *Ml = nullptr;
   unsigned long long* keys = nullptr;
@@ -152,11 +149,11 @@ struct dfl_ctx {
   int* dyn_next = nullptr;       // [2] work counters of the balanced lm_head (self-resetting)
   float* sk_ss = nullptr;        // [m-tiles][H/64][32] row sums of squares of x (RESID output)
   SKPlan sk_qkv, sk_o, sk_gu, sk_down, sk_lm;
-  // context ingest: `ing` rows per pass; the (compute-bound) GEMMs run on rocBLAS
+  // context ingest: `ing` rows per pass (compute-bound: fc on rocBLAS, K|V on the tile GEMM)
   int ing = 0;
   rocblas_handle blas = nullptr;
   float* fc32 = nullptr;      // [ing][H] fc GEMM rows (fp32)
-  half_t* xn = nullptr;       // [ing][H] hidden_norm(fc) rows (fp16, row-major)
+  half_t* xn = nullptr;       // [ing/32][32][H] hidden_norm(fc) (or fused) rows, fragment layout
   float* kv32 = nullptr;      // [ing][2*NKV*128] K|V GEMM rows (fp32)
   // per-step ingest of up to SMALL_ING rows on the stream-K kernels (no library GEMM): the
   // fc weight packed in fp16 blocks, input / normed rows in activation fragment layout,
@@ -275,9 +272,8 @@ static int setup_ingest(dfl_ctx* x) {
       (r = x->alloc(&x->si_xn, (size_t)SMALL_ING * H, true)) ||
       (r = x->alloc(&x->si_kv, (size_t)SMALL_ING * Nkv)))
     return r;
-  if (x->NF > 0 && ((r = x->alloc(&x->fc32, (size_t)x->ing * H)) ||
-                    (r = x->alloc(&x->xn, (size_t)x->ing * H))))
-    return r;
+  if ((r = x->alloc(&x->xn, (size_t)x->ing * H))) return r;
+  if (x->NF > 0 && (r = x->alloc(&x->fc32, (size_t)x->ing * H))) return r;
   if (rocblas_create_handle(&x->blas) != rocblas_status_success)
     return fail(DFL_EHIP, "dfl_create: rocblas_create_handle failed");
   unsigned char* ws = nullptr;
@@ -336,7 +332,7 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
   int r = DFL_OK;
   // x / attn / act are 32-row tiles in the activation fragment layout (zero padded rows)
   const size_t Bt = ((Bm + 31) / 32) * 32;
-  if ((r = x->alloc(&x->x, Bt * x->H, true)) || (r = x->alloc(&x->h, Bm * x->H)) ||
+  if ((r = x->alloc(&x->x, Bt * x->H, true)) || (r = x->alloc(&x->h, Bt * x->H, true)) ||
       (r = x->alloc(&x->Q, (size_t)x->NH * Bm * 128)) ||
       (r = x->alloc(&x->attn, Bt * x->NH * 128, true)) || (r = x->alloc(&x->act, Bt * x->F, true)) ||
       (r = x->alloc(&x->Op, (size_t)MAX_CHUNKS * x->NH * Bm * 128)) ||
@@ -401,9 +397,8 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
     delete x;
     return r;
   }
-  if (x->RM > BLAS_MIN_ROWS &&
-      ((r = x->alloc(&x->y32, (size_t)x->RM * std::max({x->NQKV, x->H, 2 * x->F}))) ||
-       (r = x->alloc(&x->h2, (size_t)x->RM * x->NH * 128)))) {
+  if (x->RM > STACK_MIN_ROWS &&
+      (r = x->alloc(&x->y32, (size_t)x->RM * std::max({x->NQKV, x->H, 2 * x->F})))) {
     delete x;
     return r;
   }
@@ -454,14 +449,6 @@ int dfl_load_layer_w8(dfl_ctx* ctx, int layer, const int8_t* const q[7],
     DFL_TRY(ctx->alloc(&L.post_norm, (size_t)H));
     DFL_TRY(ctx->alloc(&L.q_norm, (size_t)128));
     DFL_TRY(ctx->alloc(&L.k_norm, (size_t)128));
-    if (ctx->RM > BLAS_MIN_ROWS) {
-      DFL_TRY(ctx->alloc(&L.w_qkv16, (size_t)ctx->NQKV * H));
-      DFL_TRY(ctx->alloc(&L.w_o16, (size_t)H * NQ));
-      DFL_TRY(ctx->alloc(&L.w_gu16, (size_t)2 * F * H));
-      L.w_kv16 = L.w_qkv16 + (size_t)NQ * H;
-    } else {
-      DFL_TRY(ctx->alloc(&L.w_kv16, (size_t)2 * NKV * 128 * H));
-    }
   }
   auto S = [&](int i) { return reinterpret_cast<const half_t*>(scale[i]); };
   // fused QKV: row-blocks [0, NH*4) = q_proj, then k_proj, then v_proj
@@ -473,16 +460,6 @@ int dfl_load_layer_w8(dfl_ctx* ctx, int layer, const int8_t* const q[7],
   launch_pack_i8(q[4], S(4), F, H, L.w_gu, L.s_gu, 0, 2, st);
   launch_pack_i8(q[5], S(5), F, H, L.w_gu, L.s_gu, 1, 2, st);
   launch_pack_i8(q[6], S(6), H, F, L.w_down, L.s_down, 0, 1, st);
-  // exact fp16 copies of the k and v rows for the context-ingest GEMM (and, for stacked
-  // blocks, of every matrix but down)
-  launch_i8_to_f16(q[1], (size_t)NKV * 128 * H, L.w_kv16, st);
-  launch_i8_to_f16(q[2], (size_t)NKV * 128 * H, L.w_kv16 + (size_t)NKV * 128 * H, st);
-  if (L.w_qkv16) {
-    launch_i8_to_f16(q[0], (size_t)NQ * H, L.w_qkv16, st);
-    launch_i8_to_f16(q[3], (size_t)H * NQ, L.w_o16, st);
-    launch_i8_to_f16(q[4], (size_t)F * H, L.w_gu16, st);
-    launch_i8_to_f16(q[5], (size_t)F * H, L.w_gu16 + (size_t)F * H, st);
-  }
   DFL_HIP(hipMemcpyAsync(L.in_norm, in_norm, H * 2, hipMemcpyDeviceToDevice, st));
   DFL_HIP(hipMemcpyAsync(L.post_norm, post_norm, H * 2, hipMemcpyDeviceToDevice, st));
   DFL_HIP(hipMemcpyAsync(L.q_norm, q_norm, 256, hipMemcpyDeviceToDevice, st));
@@ -525,14 +502,8 @@ int dfl_load_head(dfl_ctx* ctx, const uint16_t* final_norm, const uint16_t* embe
     if (!ctx->w_lm) DFL_TRY(ctx->alloc(&ctx->w_lm, (size_t)ctx->V * ctx->H / 8));
     launch_pack_f16(reinterpret_cast<const half_t*>(lm_head), ctx->V, ctx->H, ctx->w_lm, st);
     DFL_TRY(check_launch("pack lm_head"));
-    if (ctx->RM > BLAS_MIN_ROWS) {
-      if (!ctx->w_lm16) {
-        DFL_TRY(ctx->alloc(&ctx->w_lm16, (size_t)ctx->V * ctx->H));
-        DFL_TRY(ctx->alloc(&ctx->lm32, (size_t)ctx->RM * ctx->V));
-      }
-      DFL_HIP(hipMemcpyAsync(ctx->w_lm16, lm_head, (size_t)ctx->V * ctx->H * 2,
-                             hipMemcpyDeviceToDevice, st));
-    }
+    if (ctx->RM > STACK_MIN_ROWS && !ctx->lm32)
+      DFL_TRY(ctx->alloc(&ctx->lm32, (size_t)ctx->RM * ctx->V));
   }
   ctx->head_loaded = true;
   return DFL_OK;
@@ -621,6 +592,30 @@ static int block_attention(const AttnArgs& at, hipStream_t st) {
   return DFL_OK;
 }
 
+// Tile GEMM Y[M][ldy] = X . W^T (fp32) for more than STACK_MIN_ROWS rows (X in the
+// fragment layout), with its argument checks reported as DFL_EINVAL.
+static int tgemm(dfl_ctx* ctx, int cat, int wt, const uint4* W, int N, int K, const half_t* X,
+                 int M, float* Y, int ldy, hipStream_t st) {
+  const TilePlan p = tile_plan(M, N, K, wt, ctx->n_cu);
+  TileArgs a{};
+  a.W = W;
+  a.N = N;
+  a.K = K;
+  a.X = X;
+  a.M = M;
+  a.Y = Y;
+  a.ldy = ldy;
+  if (const char* why = check_tile_args(wt, a, p))
+    return fail(DFL_EINVAL, std::string("tile GEMM launch refused: ") + why);
+  if (tile_lds_bytes(wt, p) > (size_t)ctx->lds_max)
+    return fail(DFL_EINVAL, "tile GEMM: the device's LDS per workgroup is too small");
+  const long long wbytes = (long long)N * K * (wt == WT_INT8 ? 1 : 2);
+  ProfScope ps(ctx, cat, wbytes, st, /*attached=*/true);
+  if (!launch_tile_gemm(wt, a, p, st, ps.start(), ps.stop()))
+    return fail(DFL_EINVAL, "no tile GEMM kernel for this shape");
+  return DFL_OK;
+}
+
 static int layers_ready(dfl_ctx* ctx, const char* who) {
   for (int l = 0; l < ctx->active; ++l)
     if (!ctx->layers[l].loaded)
@@ -640,19 +635,18 @@ static void rope_seq(dfl_ctx* ctx, int seq, const Layer& L, long long pos0, int 
   r.ring_W = q.window;
 }
 
-// Per-layer K/V of `rows` fused context rows (row-major fp16, row stride ld): the K|V
-// projection on rocBLAS (fp32 rows), then per-row scale + fp16 rounding, k_norm + RoPE on K,
-// appended at cache row len + r0 with absolute position offset + r0.
-static int ingest_kv_rows(dfl_ctx* ctx, const half_t* rows_src, int ld, int rows, int r0,
-                          hipStream_t st) {
+// Per-layer K/V of `rows` fused context rows (fragment-layout tiles xa): the K|V rows of the
+// packed W8A16 qkv matrix on the tile GEMM (fp32 integer-weight sums), then per-row scale +
+// fp16 rounding, k_norm + RoPE on K, appended at cache row len + r0 with absolute position
+// offset + r0.
+static int ingest_kv_rows(dfl_ctx* ctx, const half_t* xa, int rows, int r0, hipStream_t st) {
   const int H = ctx->H, NH = ctx->NH, NKV = ctx->NKV;
   const int Nkv = 2 * NKV * 128;
   for (int l = 0; l < ctx->active; ++l) {
     Layer& L = ctx->layers[l];
-    {
-      ProfScope ps(ctx, P_INGEST_KV, 0, st);
-      DFL_TRY(blas_gemm(ctx, Nkv, rows, H, L.w_kv16, H, rows_src, ld, 0.f, ctx->kv32, Nkv, st));
-    }
+    // the K|V rows start at packed row-block NH*128/32 of the qkv matrix
+    const uint4* w_kv = L.w_qkv + (size_t)(NH * 128 / 32) * (H / 32) * 64;
+    DFL_TRY(tgemm(ctx, P_INGEST_KV, WT_INT8, w_kv, Nkv, H, xa, rows, ctx->kv32, Nkv, st));
     QKRopeArgs q{};
     q.qkv32 = ctx->kv32;
     q.oscale = L.s_qkv + NH * 128;   // scales of the k|v rows, in row order
@@ -771,7 +765,15 @@ static int ingest(dfl_ctx* ctx, const uint16_t* src, int C, bool fused, void* st
   for (int r0 = 0; r0 < C; r0 += ctx->ing) {
     const int rows = std::min(ctx->ing, C - r0);
     if (fused) {
-      DFL_TRY(ingest_kv_rows(ctx, in + (size_t)r0 * H, H, rows, r0, st));
+      FeatPtrs f{};
+      f.n = 1;
+      f.ld = H;
+      f.p[0] = in + (size_t)r0 * H;
+      {
+        ProfScope ps(ctx, P_INGEST_KV, 0, st);
+        launch_feats_to_afl(f, rows, H, ctx->xn, st);
+      }
+      DFL_TRY(ingest_kv_rows(ctx, ctx->xn, rows, r0, st));
     } else {
       // hidden_norm(fc(target_hidden)): fc output rounded to fp16 (Linear), then RMSNorm.
       // Tapped-layer features: fc(concat(f_j)) = sum_j f_j W_fc[:, jH:(j+1)H]^T.
@@ -788,7 +790,7 @@ static int ingest(dfl_ctx* ctx, const uint16_t* src, int C, bool fused, void* st
         }
         launch_fc_norm_rows(ctx->fc32, rows, H, ctx->hidden_norm, ctx->cfg.rms_eps, ctx->xn, st);
       }
-      DFL_TRY(ingest_kv_rows(ctx, ctx->xn, H, rows, r0, st));
+      DFL_TRY(ingest_kv_rows(ctx, ctx->xn, rows, r0, st));
     }
     ctx->sq().append(rows);
   }
@@ -874,8 +876,8 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
   hipStream_t st = (hipStream_t)stream;
   const int H = ctx->H, NH = ctx->NH, NKV = ctx->NKV, F = ctx->F, NQ = NH * 128;
   const int M = n_seq * B;
-  const bool blas = M > BLAS_MIN_ROWS && ctx->layers[0].w_qkv16;   // stacked blocks
-  const bool fuse_rope = !blas && n_seq == 1 && M <= 32;   // rope in the qkv epilogue
+  const bool stacked = M > STACK_MIN_ROWS;   // compute-bound: tile GEMMs + row epilogues
+  const bool fuse_rope = !stacked && n_seq == 1 && M <= 32;   // rope in the qkv epilogue
   const float eps = ctx->cfg.rms_eps;
   // x = embedding rows (residual stream); rnorm = 1/rms(x).  Every projection whose input
   // is an RMSNorm output applies the norm on its activation load.
@@ -920,12 +922,14 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
   for (int l = 0; l < ctx->active; ++l) {
     Layer& Ly = ctx->layers[l];
     // q|k|v = input_layernorm(x) @ [Wq; Wk; Wv]^T  (fp16 out, or fp32 rows for stacked blocks)
-    if (blas) {
-      ProfScope ps(ctx, P_GEMM_BLAS, (long long)ctx->NQKV * H * 2, st);
-      launch_apply_norm(ctx->x, l > 0 ? ctx->sk_ss : nullptr, H / 64, eps, Ly.in_norm, M, H,
-                        ctx->h, st, l > 0 ? nullptr : ctx->rnorm);
-      DFL_TRY(blas_gemm(ctx, ctx->NQKV, M, H, Ly.w_qkv16, H, ctx->h, H, 0.f, ctx->y32, ctx->NQKV,
-                        st));
+    if (stacked) {
+      {
+        ProfScope ps(ctx, P_ROWS, 0, st);
+        launch_apply_norm(ctx->x, l > 0 ? ctx->sk_ss : nullptr, H / 64, eps, Ly.in_norm, M, H,
+                          ctx->h, st, l > 0 ? nullptr : ctx->rnorm, /*h_afl=*/true);
+      }
+      DFL_TRY(tgemm(ctx, P_GEMM_TILE, WT_INT8, Ly.w_qkv, ctx->NQKV, H, ctx->h, M, ctx->y32,
+                    ctx->NQKV, st));
     } else if (fuse_rope) {
       // one sequence: the per-head Q/K norm, RoPE and cache scatter run in the epilogue
       RopeEpi re{};
@@ -951,7 +955,7 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
     for (int g0 = 0; g0 < n_seq; g0 += SEQ_MAX) {
       const int gn = std::min(SEQ_MAX, n_seq - g0);
       QKRopeArgs q{};
-      if (blas) {
+      if (stacked) {
         q.qkv32 = ctx->y32 + (size_t)g0 * B * ctx->NQKV;
         q.oscale = Ly.s_qkv;
       } else {
@@ -982,7 +986,6 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
       at.Op = ctx->Op;
       at.Ml = ctx->Ml;
       at.O = ctx->attn;
-      at.O_rows = blas ? ctx->h2 : nullptr;
       at.n_cu = ctx->n_cu;
       at.lds_max = ctx->lds_max;
       long long kv_bytes = 0;
@@ -1023,14 +1026,25 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
       ProfScope ps(ctx, P_ATTN, kv_bytes, st);
       DFL_TRY(block_attention(at, st));
     }
-    if (blas) {
-      // the same two steps as library GEMMs with the epilogues in row kernels
-      ProfScope ps(ctx, P_GEMM_BLAS, ((long long)H * NQ + 2LL * F * H) * 2, st);
-      DFL_TRY(blas_gemm(ctx, H, M, NQ, Ly.w_o16, NQ, ctx->h2, NQ, 0.f, ctx->y32, H, st));
-      launch_resid_rows(ctx->y32, M, H, Ly.s_o, ctx->x, ctx->sk_ss, st);
-      launch_apply_norm(ctx->x, ctx->sk_ss, H / 64, eps, Ly.post_norm, M, H, ctx->h, st);
-      DFL_TRY(blas_gemm(ctx, 2 * F, M, H, Ly.w_gu16, H, ctx->h, H, 0.f, ctx->y32, 2 * F, st));
-      launch_swiglu_rows(ctx->y32, M, F, Ly.s_gu, ctx->act, st);
+    if (stacked) {
+      // the same steps as tile GEMMs with the epilogues in row kernels
+      DFL_TRY(tgemm(ctx, P_GEMM_TILE, WT_INT8, Ly.w_o, H, NQ, ctx->attn, M, ctx->y32, H, st));
+      {
+        ProfScope ps(ctx, P_ROWS, 0, st);
+        launch_resid_rows(ctx->y32, M, H, Ly.s_o, ctx->x, ctx->sk_ss, st);
+        launch_apply_norm(ctx->x, ctx->sk_ss, H / 64, eps, Ly.post_norm, M, H, ctx->h, st,
+                          nullptr, /*h_afl=*/true);
+      }
+      DFL_TRY(tgemm(ctx, P_GEMM_TILE, WT_INT8, Ly.w_gu, 2 * F, H, ctx->h, M, ctx->y32, 2 * F, st));
+      {
+        ProfScope ps(ctx, P_ROWS, 0, st);
+        launch_swiglu_rows(ctx->y32, M, F, Ly.s_gu, ctx->act, st);
+      }
+      DFL_TRY(tgemm(ctx, P_GEMM_TILE, WT_INT8, Ly.w_down, H, F, ctx->act, M, ctx->y32, H, st));
+      {
+        ProfScope ps(ctx, P_ROWS, 0, st);
+        launch_resid_rows(ctx->y32, M, H, Ly.s_down, ctx->x, ctx->sk_ss, st);
+      }
     } else {
       // x += attn @ Wo^T ; per-tile row sums of squares of x -> sk_ss
       DFL_TRY(skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_RESID, ctx->sk_o, Ly.w_o, Ly.s_o, H, NQ / 32,
@@ -1039,20 +1053,26 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
       DFL_TRY(skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_SWIGLU, ctx->sk_gu, Ly.w_gu, Ly.s_gu, 2 * F,
                      H / 32, ctx->x, H, M, Ly.post_norm, true, ctx->act, F, nullptr, nullptr,
                      nullptr, st));
+      // x += act @ Wdown^T ; per-tile row sums of squares of x -> sk_ss
+      DFL_TRY(skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_RESID, ctx->sk_down, Ly.w_down, Ly.s_down, H,
+                     F / 32, ctx->act, F, M, nullptr, false, nullptr, H, ctx->x, nullptr, nullptr,
+                     st));
     }
-    // x += act @ Wdown^T ; per-tile row sums of squares of x -> sk_ss
-    DFL_TRY(skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_RESID, ctx->sk_down, Ly.w_down, Ly.s_down, H, F / 32,
-           ctx->act, F, M, nullptr, false, nullptr, H, ctx->x, nullptr, nullptr, st));
   }
-  if ((out_logits || out_ids) && M > BLAS_MIN_ROWS && ctx->w_lm16) {
-    // stacked blocks: final norm into row-major rows, then the lm_head GEMM (fp32 logits)
-    // and a row argmax
-    ProfScope ps(ctx, P_LM_HEAD, (long long)ctx->V * H * 2, st);
-    launch_apply_norm(ctx->x, ctx->sk_ss, H / 64, ctx->cfg.rms_eps, ctx->final_norm, M, H, ctx->h,
-                      st);
+  if ((out_logits || out_ids) && stacked) {
+    // stacked blocks: final norm into fragment-layout rows, then the lm_head tile GEMM (fp32
+    // logits) and a row argmax
+    {
+      ProfScope ps(ctx, P_ROWS, 0, st);
+      launch_apply_norm(ctx->x, ctx->sk_ss, H / 64, ctx->cfg.rms_eps, ctx->final_norm, M, H,
+                        ctx->h, st, nullptr, /*h_afl=*/true);
+    }
     float* lg = out_logits ? out_logits : ctx->lm32;
-    DFL_TRY(blas_gemm(ctx, ctx->V, M, H, ctx->w_lm16, H, ctx->h, H, 0.f, lg, ctx->V, st));
-    if (out_ids) launch_row_argmax(lg, M, ctx->V, out_ids, st);
+    DFL_TRY(tgemm(ctx, P_LM_HEAD, WT_F16, ctx->w_lm, ctx->V, H, ctx->h, M, lg, ctx->V, st));
+    if (out_ids) {
+      ProfScope ps(ctx, P_ROWS, 0, st);
+      launch_row_argmax(lg, M, ctx->V, out_ids, st);
+    }
   } else if (out_logits || out_ids) {
     bool ids_done = false;
     DFL_TRY(skgemm(ctx, P_LM_HEAD, WT_F16, EPI_ARGMAX, ctx->sk_lm, ctx->w_lm, nullptr, ctx->V, H / 16,

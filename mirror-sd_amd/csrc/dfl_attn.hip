@@ -303,10 +303,7 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(AttnArgs a) {
   const int hb = rowg - sidx * per_seq;
   const int h = hb / a.B, b = hb - h * a.B;
   const int orow = a.sq[sidx].o_row0 + b;
-  if (a.O_rows)
-    a.O_rows[(size_t)orow * a.NH * 128 + h * 128 + d] = f2h(num / den_s);
-  else
-    a.O[afl_index(orow, h * 128 + d, a.NH * 128)] = f2h(num / den_s);
+  a.O[afl_index(orow, h * 128 + d, a.NH * 128)] = f2h(num / den_s);
 }
 
 bool launch_block_attention(const AttnArgs& a_in, hipStream_t st) {

@@ -80,7 +80,7 @@ inline const char* check_qk_rope_args(const QKRopeArgs& a) {
 }
 
 inline const char* check_attn_args(const AttnArgs& a) {
-  if (!a.Q || !a.Op || !a.Ml || (!a.O && !a.O_rows)) return "missing attention buffers";
+  if (!a.Q || !a.Op || !a.Ml || !a.O) return "missing attention buffers";
   if (a.B < 1 || a.NH < 1 || a.NKV < 1 || a.NH % a.NKV) return "bad head counts or block rows";
   if (a.n_seq < 1 || a.n_seq > SEQ_MAX) return "sequences out of range";
   if (a.max_chunks < 1 || a.max_chunks > CHECK_MAX_CHUNKS) return "chunk count out of range";
@@ -93,6 +93,23 @@ inline const char* check_attn_args(const AttnArgs& a) {
       return "key chunks do not tile the keys";
     if (a.chunk0[s + 1] != a.chunk0[s] + q.n_chunks) return "chunk table inconsistent";
   }
+  return nullptr;
+}
+
+inline const char* check_tile_args(int wt, const TileArgs& a, const TilePlan& p) {
+  if (wt != WT_INT8 && wt != WT_F16) return "unknown weight type";
+  if (!a.W || !a.X || !a.Y) return "null weights, activations or output";
+  if (p.mtw < 1 || p.mtw > 2 || (p.rbw != 1 && p.rbw != 2 && p.rbw != 4) || p.wn < 1 ||
+      p.wn > 2 || (p.kc != 32 && p.kc != 64))
+    return "unknown tile shape";
+  if (a.M < 1 || a.N < 1 || a.K < 64 || a.K % 64 || a.K % p.kc)
+    return "M, N >= 1 and K a positive multiple of 64 and of the stage's k";
+  if (a.N % (32 * p.rbw * p.wn)) return "N is not a multiple of the tile's columns";
+  if (a.ldy < a.N) return "output row shorter than N";
+  if (p.tiles_n != a.N / (32 * p.rbw * p.wn) || (long long)p.tiles_m * 128 * p.mtw < a.M ||
+      (long long)p.tiles_m * 128 * p.mtw >= (long long)a.M + 128 * p.mtw)
+    return "tile counts do not cover the product";
+  if ((long long)p.tiles_m * p.tiles_n > 0x7fffffffLL) return "too many tiles";
   return nullptr;
 }
 

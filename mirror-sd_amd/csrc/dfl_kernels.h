@@ -98,6 +98,31 @@ bool launch_streamk_gemm(int wt, int epi, bool norm, const StreamArgs& a, const 
                          hipStream_t st, hipEvent_t ev_start = nullptr,
                          hipEvent_t ev_stop = nullptr);
 
+// ---- tile GEMM for stacked rows, M > 64 (dfl_tile.hip) ----
+// Y[M][ldy] (fp32, columns [0, N)) = X . W^T with X in the activation fragment layout
+// (ceil(M/32) tiles of 32 x K) and W packed blocks (int8: unscaled integer-weight sums).
+struct TileArgs {
+  const uint4* W;           // packed weight blocks, N rows
+  int N, K;                 // N % (32 * rb) == 0, K % 64 == 0
+  const half_t* X;          // fragment-layout tiles, ceil(M/32) of them
+  int M;
+  float* Y;                 // row-major fp32 [M][ldy]
+  int ldy;
+  int tiles_m, tiles_n;     // set by the launcher from the plan
+};
+struct TilePlan {
+  int mtw = 0;              // m-tiles per wave: 1 (128-row workgroup tile) or 2 (256 rows)
+  int rbw = 0;              // weight row-blocks (32 columns) per wave: 1, 2 or 4
+  int wn = 0;               // wave columns: 1 (4 waves) or 2 (8 waves)
+  int kc = 0;               // k per LDS stage: 32 or 64
+  int tiles_m = 0, tiles_n = 0;
+};
+// (tile_plan / tile_lds_bytes: dfl_tile_plan.h)
+// Returns false (and launches nothing) when the arguments fail check_tile_args.
+// ev_start / ev_stop (optional) receive the kernel's own start and end timestamps.
+bool launch_tile_gemm(int wt, const TileArgs& a, const TilePlan& p, hipStream_t st,
+                      hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
+
 // ---- pack / quantise (dfl_pack.hip) ----
 // Symmetric per-row int8 quantisation of w [oc][ic] fp32.
 void launch_quantize_w8(const float* w, int64_t oc, int64_t ic, int8_t* q, half_t* s,
@@ -129,6 +154,7 @@ struct FeatPtrs {
   long long ld;
 };
 void launch_concat_feats(const FeatPtrs& f, int rows, int H, half_t* out, hipStream_t st);
+// hidden_norm of the fp32 fc rows (rounded to fp16 first) into fragment-layout tiles xn.
 void launch_fc_norm_rows(const float* fc32, int rows, int H, const half_t* g, float eps,
                          half_t* xn, hipStream_t st);
 // Stream-K ingest inputs: concat_j(f_j) rows (f.n features of H columns, H % 8 == 0) into
@@ -137,19 +163,21 @@ void launch_fc_norm_rows(const float* fc32, int rows, int H, const half_t* g, fl
 void launch_feats_to_afl(const FeatPtrs& f, int rows, int H, half_t* afl, hipStream_t st);
 void launch_rows_norm_afl(const half_t* x, int ld, int rows, int H, const half_t* g, float eps,
                           half_t* afl, hipStream_t st);
-void launch_i8_to_f16(const int8_t* q, size_t n, half_t* out, hipStream_t st);
 void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* noise, int B,
                        int H, int V, const half_t* g, float eps, half_t* x, half_t* h,
                        float* rnorm, int* err, hipStream_t st,
                        float* rope_cs = nullptr, long long pos0 = 0, double log2_theta = 0.0);
-// x in the activation fragment layout (afl_index) [M][N] -> row-major h [M][N]:
-// h = fp16(fp16(x * r[m]) * g[n])  (apply_norm), or a plain copy (afl_to_rows).  r[m] =
-// 1/rms of row m from ss [M/32 m-tiles][ss_tiles][32] (row sums of squares per column tile).
+// x in the activation fragment layout (afl_index) [M][N] -> h [M][N], row-major or (h_afl)
+// fragment layout: h = fp16(fp16(x * r[m]) * g[n])  (apply_norm), or a plain row-major copy
+// (afl_to_rows).  r[m] = 1/rms of row m from ss [M/32 m-tiles][ss_tiles][32] (row sums of
+// squares per column tile), or rnorm[m].
 void launch_apply_norm(const half_t* x, const float* ss, int ss_tiles, float eps, const half_t* g,
-                       int M, int N, half_t* h, hipStream_t st, const float* rnorm = nullptr);
-// Epilogues of the stacked-block library GEMMs (fp32 rows y), same arithmetic as the
+                       int M, int N, half_t* h, hipStream_t st, const float* rnorm = nullptr,
+                       bool h_afl = false);
+// Epilogues of the stacked-block tile GEMMs (fp32 rows y), same arithmetic as the
 // stream-K RESID / SWIGLU epilogues: x += fp16(y * s) with sums of squares into ss
-// [M/32][N/64][32]; act = swiglu(y_gate * s, y_up * s) in the fragment layout.
+// [M/32][N/64][32]; act = swiglu(y_gate * s, y_up * s) (y in the packed gate|up column
+// order) in the fragment layout.
 void launch_resid_rows(const float* y, int M, int N, const half_t* s, half_t* x, float* ss,
                        hipStream_t st);
 void launch_swiglu_rows(const float* y, int M, int F, const half_t* s, half_t* act,
@@ -224,8 +252,7 @@ struct AttnArgs {
   float* Op;              // [max_chunks][n_seq*NH*B][128] unnormalised partial outputs
   float* Ml;              // [max_chunks][n_seq*NH*B][2] running (max, sum) in log2 domain
   half_t* O;              // output rows of an activation fragment layout tile set with
-                          // NH*128 columns, or (O_rows set) row-major [rows][NH*128]
-  half_t* O_rows;
+                          // NH*128 columns
   AttnSeq sq[SEQ_MAX];
 };
 // Returns false (and launches nothing) when the struct fails check_attn_args.

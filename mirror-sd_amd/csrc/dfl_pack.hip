@@ -73,27 +73,6 @@ __global__ __launch_bounds__(64) void pack_f16_kernel(const half_t* __restrict__
   dst[((size_t)rb * KB + kb) * 64 + l] = *reinterpret_cast<const uint4*>(src);
 }
 
-// int8 -> fp16, exact (|q| <= 127 has at most 7 significant bits): the fp16 copy of a W8A16
-// matrix that the context-ingest GEMMs multiply, scales applied to their fp32 output.
-__global__ __launch_bounds__(256) void i8_to_f16_kernel(const int8_t* __restrict__ q, size_t n,
-                                                        half_t* __restrict__ out) {
-  const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 8;
-  if (i >= n) return;
-  const int2 v = *reinterpret_cast<const int2*>(q + i);   // n % 8 == 0
-  half8_t o;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    o[j] = (half_t)(float)(int8_t)(v.x >> (8 * j));
-    o[4 + j] = (half_t)(float)(int8_t)(v.y >> (8 * j));
-  }
-  *reinterpret_cast<half8_t*>(out + i) = o;
-}
-
-void launch_i8_to_f16(const int8_t* q, size_t n, half_t* out, hipStream_t st) {
-  hipLaunchKernelGGL(i8_to_f16_kernel, dim3((unsigned)((n / 8 + 255) / 256)), dim3(256), 0, st, q,
-                     n, out);
-}
-
 void launch_pack_f16(const half_t* w, int rows, int K, uint4* dst, hipStream_t st) {
   hipLaunchKernelGGL(pack_f16_kernel, dim3(K / 16, rows / 32), dim3(64), 0, st, w, K, dst);
 }

@@ -76,14 +76,14 @@ void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* no
                      V, g, eps, x, h, rnorm, err, B <= 32 ? rope_cs : nullptr, pos0, log2_theta);
 }
 
-// x (activation fragment layout, [M][N]) -> row-major h; with g set, h = RMSNorm(x) * g
-// where 1/rms of row m is rnorm[m], or comes from ss [M/32][ss_tiles][32] (per-column-tile
-// sums of squares).
+// x (activation fragment layout, [M][N]) -> h, row-major or (h_afl) in the fragment layout;
+// with g set, h = RMSNorm(x) * g where 1/rms of row m is rnorm[m], or comes from ss
+// [M/32][ss_tiles][32] (per-column-tile sums of squares).
 __global__ __launch_bounds__(256) void afl_rows_kernel(const half_t* __restrict__ x,
                                                        const float* __restrict__ ss, int ss_tiles,
                                                        const float* __restrict__ rnorm,
                                                        float eps, const half_t* __restrict__ g,
-                                                       int N, half_t* __restrict__ h) {
+                                                       int N, half_t* __restrict__ h, bool h_afl) {
   __shared__ float rr_s;
   const int m = blockIdx.y;
   if (rnorm) {
@@ -109,16 +109,16 @@ __global__ __launch_bounds__(256) void afl_rows_kernel(const half_t* __restrict_
 #pragma unroll
     for (int j = 0; j < 4; ++j) o[j] = rms_out(h2f(xv[j]), rr, g[n + j]);
   }
-  *reinterpret_cast<half4_t*>(h + (size_t)m * N + n) = o;
+  *reinterpret_cast<half4_t*>(h + (h_afl ? afl_index(m, n, N) : (size_t)m * N + n)) = o;
 }
 
 void launch_apply_norm(const half_t* x, const float* ss, int ss_tiles, float eps, const half_t* g,
-                       int M, int N, half_t* h, hipStream_t st, const float* rnorm) {
+                       int M, int N, half_t* h, hipStream_t st, const float* rnorm, bool h_afl) {
   hipLaunchKernelGGL(afl_rows_kernel, dim3((N / 4 + 255) / 256, M), dim3(256), 0, st, x, ss,
-                     ss_tiles, rnorm, eps, g, N, h);
+                     ss_tiles, rnorm, eps, g, N, h, h_afl);
 }
 
-// RESID epilogue for fp32 library-GEMM rows y [M][N] (stacked blocks): x += fp16(y * s) in
+// RESID epilogue for fp32 tile-GEMM rows y [M][N] (stacked blocks): x += fp16(y * s) in
 // place on the fragment-layout residual, with the per-(m-tile, 64-column tile) row sums of
 // squares of the new x in ss [M/32][N/64][32] -- the stream-K RESID epilogue's arithmetic.
 // One wave per (row, column tile), lane = column.
@@ -146,10 +146,10 @@ void launch_resid_rows(const float* y, int M, int N, const half_t* s, half_t* x,
   hipLaunchKernelGGL(resid_rows_kernel, dim3((waves + 3) / 4), dim3(256), 0, st, y, M, N, s, x, ss);
 }
 
-// SWIGLU epilogue for fp32 library-GEMM rows y [M][2F] (gate rows 0..F-1, then up rows):
+// SWIGLU epilogue for fp32 tile-GEMM rows y [M][2F] in the packed gate|up column order
+// (gate row f at column 64*(f/32) + f%32, up row f 32 further, as the scales):
 // act[m][f] = fp16(fp16(silu(g)) * u) with g = fp16(y_gate * s_gate), u = fp16(y_up * s_up),
-// the stream-K SWIGLU epilogue's rounding; scales in the packed gate|up order (gate row f at
-// 64*(f/32) + f%32, up row f 32 further).  act in the fragment layout [M][F].
+// the stream-K SWIGLU epilogue's rounding.  act in the fragment layout [M][F].
 __global__ __launch_bounds__(256) void swiglu_rows_kernel(const float* __restrict__ y, int M, int F,
                                                           const half_t* __restrict__ s,
                                                           half_t* __restrict__ act) {
@@ -157,8 +157,8 @@ __global__ __launch_bounds__(256) void swiglu_rows_kernel(const float* __restric
   if (i >= (size_t)M * F) return;
   const int m = (int)(i / F), f = (int)(i - (size_t)m * F);
   const int si = 64 * (f >> 5) + (f & 31);
-  const float gv = h2f(f2h(y[(size_t)m * 2 * F + f] * h2f(s[si])));
-  const float uv = h2f(f2h(y[(size_t)m * 2 * F + F + f] * h2f(s[si + 32])));
+  const float gv = h2f(f2h(y[(size_t)m * 2 * F + si] * h2f(s[si])));
+  const float uv = h2f(f2h(y[(size_t)m * 2 * F + si + 32] * h2f(s[si + 32])));
   const float sig = h2f(f2h(1.0f / (1.0f + expf(-gv))));
   const float sil = h2f(f2h(gv * sig));
   act[afl_index(m, f, F)] = f2h(sil * uv);
@@ -202,7 +202,15 @@ __global__ __launch_bounds__(256) void feats_to_afl_kernel(FeatPtrs f, int H, in
   u32x4 v = {0u, 0u, 0u, 0u};
   if (r < rows) {
     const int j = k / H;
-    v = *reinterpret_cast<const u32x4*>(f.p[j] + (size_t)r * f.ld + (k - j * H));
+    const half_t* src = f.p[j] + (size_t)r * f.ld + (k - j * H);
+    if (!(reinterpret_cast<uintptr_t>(src) & 15)) {
+      v = *reinterpret_cast<const u32x4*>(src);
+    } else {   // a caller's buffer without 16-byte alignment: 2-byte loads
+      half8_t h;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) h[i] = src[i];
+      v = __builtin_bit_cast(u32x4, h);
+    }
   }
   *reinterpret_cast<u32x4*>(afl + afl_index(r, k, K)) = v;
 }
@@ -255,7 +263,8 @@ void launch_rows_norm_afl(const half_t* x, int ld, int rows, int H, const half_t
 }
 
 // hidden_norm(fc(.)) for the ingest: fc32 [rows][H] fp32 GEMM rows, rounded to fp16 (the
-// Linear output), then RMSNorm (fp16(fp16(x * r) * g)) into row-major fp16 xn [rows][H].
+// Linear output), then RMSNorm (fp16(fp16(x * r) * g)) into fragment-layout tiles xn
+// [ceil(rows/32)][32][H] (the K|V tile GEMM's input).
 __global__ __launch_bounds__(ROW_THREADS) void fc_norm_rows_kernel(const float* __restrict__ fc32,
                                                                    int H, const half_t* __restrict__ g,
                                                                    float eps,
@@ -279,7 +288,7 @@ __global__ __launch_bounds__(ROW_THREADS) void fc_norm_rows_kernel(const float* 
 #pragma unroll
   for (int i = 0; i < ROW_MAXV; ++i) {
     const int k = threadIdx.x + i * ROW_THREADS;
-    if (k < H) xn[(size_t)r * H + k] = rms_out(v[i], rr, g[k]);
+    if (k < H) xn[afl_index(r, k, H)] = rms_out(v[i], rr, g[k]);
   }
 }
 
@@ -292,7 +301,7 @@ void launch_fc_norm_rows(const float* fc32, int rows, int H, const half_t* g, fl
 
 void launch_afl_to_rows(const half_t* x, int M, int N, half_t* h, hipStream_t st) {
   hipLaunchKernelGGL(afl_rows_kernel, dim3((N / 4 + 255) / 256, M), dim3(256), 0, st, x, nullptr,
-                     0, nullptr, 0.f, nullptr, N, h);
+                     0, nullptr, 0.f, nullptr, N, h, false);
 }
 
 

@@ -1,0 +1,320 @@
+// Tile GEMM for stacked activation rows (M > 64): the compute-bound projection shapes.
+//
+//   Y[M][N] (fp32, row-major) = X[M][K] . W[N][K]^T
+//
+// X is in the activation fragment layout (32-row tiles of 1 KiB records, afl_offset) and
+// W in the packed 1 KiB blocks of the stream-K kernel (int8 [32 rows][32 k], or fp16
+// [32 rows][16 k]), so the same weight bytes serve both kernels and no fp16 copy of an
+// int8 matrix exists.  For int8 weights Y holds the exact-integer-weight sums; the per-row
+// scale and the fp16 rounding of the Linear are applied by the consumer (the same
+// epilogue arithmetic as the stream-K kernel).
+//
+// At M = 256 an int8 weight byte feeds 512 flop, above the MI355X ridge (~312 flop/B), so
+// these shapes are MFMA-bound rather than HBM-bound; what bounds them in practice is the
+// global -> LDS copy rate (about 14 TB/s over the chip), so the larger the workgroup tile,
+// the fewer bytes per flop.  A workgroup of 4 * WN waves (WN = 1 or 2 wave columns)
+// computes a BM x BN output tile: BM = 128 * MTW rows (wave row wm owns m-tiles
+// [wm*MTW, (wm+1)*MTW)), BN = 32 * RBW * WN columns (wave column wn owns row-blocks
+// [wn*RBW, (wn+1)*RBW)).  K is walked in stages of KC (32 or 64): each stage's X records
+// (BM/32 tiles x KC/16 KiB, contiguous per tile) and weight blocks (contiguous per
+// row-block) are copied global -> LDS with global_load_lds (1 KiB per wave instruction,
+// no VGPR staging), the copies spread over the waves, into a ring of 3 to 8 stage buffers
+// (as many as 160 KiB holds), all but three in flight.  The compute waves work per k-block
+// of 32: the next block's fragments are read from LDS (lane-linear 16-byte reads,
+// conflict-free) while the current block is multiplied; int8 blocks are dequantised
+// exactly in registers (dequant_i8x16).
+//
+// Output lane layout of v_mfma_f32_32x32x16_f16 with A = X (rows m) and B = W (columns
+// n): accumulator r of lane l is Y[8*(r/4) + 4*(l/32) + r%4][l%32], so each store
+// instruction writes 128 contiguous bytes of two rows.
+#include <hip/hip_ext.h>
+
+#include <algorithm>
+
+#include "dfl_check.h"
+#include "dfl_common.h"
+#include "dfl_kernels.h"
+#include "dfl_tile_plan.h"
+
+namespace dfl {
+
+namespace {
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+
+template <int WT, int MTW, int RBW, int WN, int KC>
+struct TgShape {
+  static constexpr int NW = TG_WM * WN;                      // compute waves
+  static constexpr bool LOADER = tile_loader(WN);            // + a loader wave
+  static constexpr int MT = TG_WM * MTW;                     // m-tiles per workgroup
+  static constexpr int RB = RBW * WN;                        // row-blocks per workgroup
+  static constexpr int KBS = KC / 32;                        // k-blocks of 32 per stage
+  static constexpr int XREC = 2 * KBS;                       // X records per tile and stage
+  static constexpr int X_BYTES = MT * XREC * 1024;
+  static constexpr int WBLK = WT == WT_INT8 ? KBS : 2 * KBS;  // weight blocks per row-block
+  static constexpr int W_BLOCKS = RB * WBLK;
+  static constexpr int STAGE = X_BYTES + W_BLOCKS * 1024;
+  static constexpr int IPS = STAGE / 1024;                   // copies per stage
+  // copies per issuing wave (at least): all of them for the loader
+  static constexpr int PER_WAVE_MIN = LOADER ? IPS : IPS / NW;
+  static constexpr int STAGES = tile_stages(WT, MTW, RBW, WN, KC);
+  static constexpr int LDS = STAGES * STAGE;
+  static_assert(STAGE == tile_stage_bytes(WT, MTW, RBW, WN, KC), "stage size");
+  static_assert((STAGES - 3) * (LOADER ? IPS : (IPS + NW - 1) / NW) < 64 && STAGES >= 3,
+                "vmcnt range");
+  static_assert(LDS <= TG_LDS_BUDGET, "LDS budget");
+  static constexpr int NACC = MTW * RBW >= 4 ? 1 : 2;        // independent MFMA chains
+};
+
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt
+// left at "no wait").
+template <int N>
+DFL_DEV void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+DFL_DEV void tg_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+DFL_DEV u32x4 lds_read16(const unsigned char* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+// Fragments of one k-block (32 k) for one wave: its X fragments and raw weight blocks.
+template <int WT, int MTW, int RBW>
+struct TgFrag {
+  static constexpr int NQ = WT == WT_INT8 ? 1 : 2;   // weight blocks per row-block and k-block
+  half8_t x[NQ][MTW][WT == WT_INT8 ? 2 : 1];
+  u32x4 w[NQ][RBW];
+};
+
+// Reads k-block kbl of the stage at xs for the wave at (wm, wn).
+template <class S, int WT, int MTW, int RBW>
+DFL_DEV void tg_read_frags(TgFrag<WT, MTW, RBW>& f, const unsigned char* xs, int kbl, int wm,
+                           int wn, int lane) {
+  const unsigned char* ws = xs + S::X_BYTES;
+  if constexpr (WT == WT_INT8) {
+    static_for<0, RBW>([&](auto r) {
+      const int rb = wn * RBW + r;
+      f.w[0][r] = lds_read16(ws + (rb * S::WBLK + kbl) * 1024 + lane * 16);
+    });
+    static_for<0, MTW>([&](auto t) {
+      const int mtl = wm * MTW + t;
+      f.x[0][t][0] = as_half8(lds_read16(xs + (mtl * S::XREC + 2 * kbl + 0) * 1024 + lane * 16));
+      f.x[0][t][1] = as_half8(lds_read16(xs + (mtl * S::XREC + 2 * kbl + 1) * 1024 + lane * 16));
+    });
+  } else {
+    // fp16 block q = 2*kbl + qq holds, for lane l, k = 16*q + 8*(l/32) + 0..7; the matching
+    // activation halves sit in record (kbl, h = l/32) at lane position l%32 + 32*qq
+    const int g = lane >> 5;
+    static_for<0, 2>([&](auto qq) {
+      static_for<0, RBW>([&](auto r) {
+        const int rb = wn * RBW + r;
+        f.w[qq][r] = lds_read16(ws + (rb * S::WBLK + 2 * kbl + qq) * 1024 + lane * 16);
+      });
+      static_for<0, MTW>([&](auto t) {
+        const int mtl = wm * MTW + t;
+        f.x[qq][t][0] = as_half8(lds_read16(xs + (mtl * S::XREC + 2 * kbl + g) * 1024 +
+                                            ((lane & 31) + 32 * qq) * 16));
+      });
+    });
+  }
+}
+
+template <int WT, int MTW, int RBW, int NACC>
+DFL_DEV void tg_mfma(const TgFrag<WT, MTW, RBW>& f, floatx16 (&acc)[RBW][MTW][NACC]) {
+  if constexpr (WT == WT_INT8) {
+    static_for<0, RBW>([&](auto r) {
+      half8_t lo, hi;
+      dequant_i8x16(f.w[0][r], lo, hi);
+      static_for<0, MTW>([&](auto t) {
+        acc[r][t][0] = mfma32x32x16(f.x[0][t][0], lo, acc[r][t][0]);
+        acc[r][t][NACC - 1] = mfma32x32x16(f.x[0][t][1], hi, acc[r][t][NACC - 1]);
+      });
+    });
+  } else {
+    static_for<0, 2>([&](auto qq) {
+      static_for<0, RBW>([&](auto r) {
+        static_for<0, MTW>([&](auto t) {
+          constexpr int c = NACC == 1 ? 0 : (int)qq;
+          acc[r][t][c] = mfma32x32x16(f.x[qq][t][0], as_half8(f.w[qq][r]), acc[r][t][c]);
+        });
+      });
+    });
+  }
+}
+
+// Barriers: before B(t) every issuing wave waits for its own copies of stage t + 1, so
+// after B(t) stage t + 1 is in LDS; B(t) also orders every read of stage t - 1 (consumed by
+// MFMAs before B(t)) before the copies of stage t + STAGES - 1 that refill its buffer,
+// issued right after B(t).  B(-1) precedes the first read.  Every wave passes B(-1) ..
+// B(nst - 2).
+template <int WT, int MTW, int RBW, int WN, int KC>
+__global__ __launch_bounds__(64 * (TG_WM * WN + (tile_loader(WN) ? 1 : 0))) void tile_gemm_kernel(
+    TileArgs a) {
+  using S = TgShape<WT, MTW, RBW, WN, KC>;
+  extern __shared__ __attribute__((aligned(1024))) unsigned char tg_lds[];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int wm = wv % TG_WM, wn = wv / TG_WM;
+
+  // XCD-aware tile order: consecutive workgroups go to different XCDs, so tile t is run by
+  // workgroup b with t = (b % 8) * (G / 8) + b / 8; the tiles of one m-tile row (sharing X)
+  // then run on one XCD and share its L2.
+  const int G = gridDim.x;
+  const int b = blockIdx.x;
+  const int tile = (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
+  const int tm = tile / a.tiles_n;
+  const int tn = tile - tm * a.tiles_n;
+  const int mt0 = tm * S::MT;                  // first m-tile of this workgroup
+  const int nb0 = tn * S::RB;                  // first weight row-block
+  const int K = a.K;
+  const int nst = K / KC;
+  const int MTt = (a.M + 31) >> 5;             // m-tiles present in X
+  const int KBW = WT == WT_INT8 ? K / 32 : K / 16;   // weight blocks per row-block
+
+  // copy i of a stage (X records first, then weight blocks) is issued by the loader, or by
+  // compute wave i % NW
+  constexpr int ISSUERS = S::LOADER ? 1 : S::NW;
+  const int iw = S::LOADER ? 0 : wv;
+  auto issue_stage = [&](int s) __attribute__((always_inline)) {
+    unsigned char* buf = tg_lds + (s % S::STAGES) * S::STAGE;
+#pragma unroll
+    for (int j = 0; j < (S::IPS + ISSUERS - 1) / ISSUERS; ++j) {
+      const int i = iw + ISSUERS * j;
+      if (i < S::MT * S::XREC) {
+        const int mtl = i / S::XREC, rec = i % S::XREC;
+        const int mg = min(mt0 + mtl, MTt - 1);   // rows past M: any valid tile (never stored)
+        const half_t* src =
+            a.X + (size_t)mg * 32 * K + ((size_t)(S::XREC * s + rec) * 64 + lane) * 8;
+        __builtin_amdgcn_global_load_lds((const void*)src, (lds_ptr_t)(buf + i * 1024), 16, 0, 0);
+      } else if (i < S::IPS) {
+        const int wi = i - S::MT * S::XREC;
+        const int r = wi / S::WBLK, q = wi % S::WBLK;
+        const uint4* src = a.W + ((size_t)(nb0 + r) * KBW + (size_t)S::WBLK * s + q) * 64 + lane;
+        __builtin_amdgcn_global_load_lds((const void*)src, (lds_ptr_t)(buf + i * 1024), 16, 0, 0);
+      }
+    }
+  };
+  // before B(t): this wave's copies of stage t + 1 have landed; stages up to t + STAGES - 2
+  // were issued, so STAGES - 3 of them may stay in flight (all landed near the end)
+  auto wait_stage = [&](int t) __attribute__((always_inline)) {
+    if (t + S::STAGES - 2 <= nst - 1) wait_vmcnt<(S::STAGES - 3) * S::PER_WAVE_MIN>();
+    else wait_vmcnt<0>();
+  };
+
+  floatx16 acc[RBW][MTW][S::NACC];
+  static_for<0, RBW>([&](auto r) {
+    static_for<0, MTW>([&](auto t) {
+      static_for<0, S::NACC>([&](auto c) { acc[r][t][c] = (floatx16){}; });
+    });
+  });
+
+  if constexpr (S::LOADER) {
+    if (wv == S::NW) {
+      // ---- loader wave: the copies and the waits; the compute waves only pass barriers ----
+      for (int t = 0; t < S::STAGES - 2 && t < nst; ++t) issue_stage(t);
+      for (int t = -1; t <= nst - 2; ++t) {
+        wait_stage(t);
+        tg_barrier();   // B(t)
+        if (t + S::STAGES - 1 < nst) issue_stage(t + S::STAGES - 1);
+      }
+      return;
+    }
+    tg_barrier();   // B(-1)
+  } else {
+    for (int t = 0; t < S::STAGES - 2 && t < nst; ++t) issue_stage(t);
+    wait_stage(-1);
+    tg_barrier();   // B(-1)
+    if (S::STAGES - 2 < nst) issue_stage(S::STAGES - 2);
+  }
+
+  // k-blocks u = 0 .. nkb-1 (stage u / KBS); f0 / f1 alternate
+  const int nkb = K / 32;
+  TgFrag<WT, MTW, RBW> f0, f1;
+  tg_read_frags<S>(f0, tg_lds, 0, wm, wn, lane);
+  // before reading k-block u + 1: a new stage needs B(stage - 1) and refills
+  auto next = [&](int u, TgFrag<WT, MTW, RBW>& f) __attribute__((always_inline)) {
+    const int v = u + 1;
+    const int sv = v / S::KBS;
+    if (v % S::KBS == 0) {
+      if constexpr (!S::LOADER) wait_stage(sv - 1);
+      tg_barrier();   // B(sv - 1)
+      if constexpr (!S::LOADER)
+        if (sv - 1 + S::STAGES - 1 < nst) issue_stage(sv - 1 + S::STAGES - 1);
+    }
+    tg_read_frags<S>(f, tg_lds + (sv % S::STAGES) * S::STAGE, v % S::KBS, wm, wn, lane);
+  };
+  for (int u = 0; u < nkb; u += 2) {   // nkb is even (K % 64 == 0)
+    next(u, f1);
+    tg_mfma<WT, MTW, RBW, S::NACC>(f0, acc);
+    if (u + 2 < nkb) next(u + 1, f0);
+    tg_mfma<WT, MTW, RBW, S::NACC>(f1, acc);
+  }
+
+  // epilogue: fp32 rows, m < M only
+  const int g = lane >> 5;
+  const int n_lane = (nb0 + wn * RBW) * 32 + (lane & 31);
+  static_for<0, MTW>([&](auto t) {
+    const int mbase = (mt0 + wm * MTW + t) * 32 + 4 * g;
+    static_for<0, RBW>([&](auto r) {
+      floatx16 v = acc[r][t][0];
+      if constexpr (S::NACC == 2) v += acc[r][t][1];
+      float* yc = a.Y + n_lane + 32 * r;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int m = mbase + 8 * (i >> 2) + (i & 3);
+        if (m < a.M) yc[(size_t)m * a.ldy] = v[i];
+      }
+    });
+  });
+}
+
+template <int WT, int MTW, int RBW, int WN, int KC>
+void launch_tile(const TileArgs& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+  using S = TgShape<WT, MTW, RBW, WN, KC>;
+  const dim3 grid(a.tiles_m * a.tiles_n), block(64 * (S::NW + (S::LOADER ? 1 : 0)));
+  if (e0 && e1)
+    hipExtLaunchKernelGGL((tile_gemm_kernel<WT, MTW, RBW, WN, KC>), grid, block, S::LDS, st, e0,
+                          e1, 0, a);
+  else
+    hipLaunchKernelGGL((tile_gemm_kernel<WT, MTW, RBW, WN, KC>), grid, block, S::LDS, st, a);
+}
+
+template <int I>
+bool launch_shape_i(int wt, const TileArgs& a, const TilePlan& p, hipStream_t st, hipEvent_t e0,
+                    hipEvent_t e1) {
+  if constexpr (I < (int)(sizeof(kTileShapes) / sizeof(kTileShapes[0]))) {
+    constexpr TileShape s = kTileShapes[I];
+    if (wt == s.wt && p.mtw == s.mtw && p.rbw == s.rbw && p.wn == s.wn && p.kc == s.kc) {
+      launch_tile<s.wt, s.mtw, s.rbw, s.wn, s.kc>(a, st, e0, e1);
+      return true;
+    }
+    return launch_shape_i<I + 1>(wt, a, p, st, e0, e1);
+  }
+  return false;
+}
+
+}  // namespace
+
+bool launch_tile_gemm(int wt, const TileArgs& a0, const TilePlan& p, hipStream_t st,
+                      hipEvent_t ev_start, hipEvent_t ev_stop) {
+  if (check_tile_args(wt, a0, p)) return false;
+  TileArgs a = a0;
+  a.tiles_m = p.tiles_m;
+  a.tiles_n = p.tiles_n;
+  return launch_shape_i<0>(wt, a, p, st, ev_start, ev_stop);
+}
+
+}  // namespace dfl

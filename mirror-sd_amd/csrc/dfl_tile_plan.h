@@ -1,0 +1,94 @@
+// Host-side planning of the tile GEMM (dfl_tile.hip): the workgroup tile shape of an
+// M x N x K product and its LDS size.  Pure host code, so a host test can check plans
+// without a GPU.
+#pragma once
+
+#include <algorithm>
+#include <cstddef>
+
+#include "dfl_kernels.h"
+
+namespace dfl {
+
+constexpr int TG_WM = 4;                   // wave rows of a workgroup (m direction)
+constexpr int TG_LDS_BUDGET = 160 * 1024;  // one workgroup per CU
+
+// The tile shapes the library instantiates: mtw m-tiles (32 rows) and rbw weight
+// row-blocks (32 columns) per wave, wn wave columns (4 * wn waves), kc k per LDS stage.
+struct TileShape {
+  int wt, mtw, rbw, wn, kc;
+};
+constexpr TileShape kTileShapes[] = {
+    {WT_INT8, 1, 1, 1, 64},   // 128 x 32
+    {WT_INT8, 1, 2, 1, 64},   // 128 x 64
+    {WT_INT8, 2, 4, 1, 64},   // 256 x 128
+    {WT_INT8, 2, 4, 2, 32},   // 256 x 256
+    {WT_F16, 2, 2, 1, 64},    // 256 x 64
+    {WT_F16, 2, 4, 1, 32},    // 256 x 128
+    {WT_F16, 2, 4, 2, 32},    // 256 x 256
+};
+
+constexpr int tile_waves(int wn) { return TG_WM * wn; }
+// The 4-wave shapes (wn == 1) add a loader wave that issues every global -> LDS copy (the
+// compute waves never stall on a full memory queue); the 8-wave shapes have no room for a
+// ninth wave's registers, so their compute waves issue the copies themselves.
+constexpr bool tile_loader(int wn) { return wn == 1; }
+// Bytes of one stage: the X records of the workgroup's m-tiles (2 KiB per tile and k-block
+// of 32) and its weight blocks (1 KiB per row-block and 32 (int8) or 16 (fp16) k).
+constexpr int tile_stage_bytes(int wt, int mtw, int rbw, int wn, int kc) {
+  return TG_WM * mtw * (kc / 32) * 2048 + rbw * wn * (kc / (wt == WT_INT8 ? 32 : 16)) * 1024;
+}
+// Stage buffers: as many as fit the LDS budget, at most 8, at most 3 more than a wave's
+// vmcnt field (6 bits) counts in stages of its share of the copies, at least 3.  All but
+// three of them are in flight while the compute waves read one and multiply another.
+constexpr int tile_stages(int wt, int mtw, int rbw, int wn, int kc) {
+  const int sb = tile_stage_bytes(wt, mtw, rbw, wn, kc);
+  const int per_wave =
+      tile_loader(wn) ? sb / 1024 : (sb / 1024 + tile_waves(wn) - 1) / tile_waves(wn);
+  const int by_lds = TG_LDS_BUDGET / sb;
+  const int by_cnt = 3 + 63 / (per_wave > 0 ? per_wave : 1);
+  const int s = by_lds < by_cnt ? by_lds : by_cnt;
+  return s < 3 ? 3 : (s > 8 ? 8 : s);
+}
+
+// Estimated cycles of one k-block (32 k) of a workgroup: the larger of the MFMA time of a
+// SIMD (32 cycles per 32x32x16 MFMA, wn waves per SIMD) and the copy time of the block's X
+// and weight bytes at the copy rate measured for global -> LDS traffic (about 24 B per
+// cycle and CU, 14 TB/s over the chip).
+inline double tile_kblock_cycles(const TileShape& s) {
+  const double mfma = 32.0 * 2 * s.mtw * s.rbw * s.wn;
+  const double bytes = TG_WM * s.mtw * 2048.0 + s.rbw * s.wn * 1024.0 * (s.wt == WT_INT8 ? 1 : 2);
+  return std::max(mfma, bytes / 24.0);
+}
+
+// The instantiated shape with the least estimated time: rounds of one workgroup per CU x
+// k-blocks x cycles per k-block.
+inline TilePlan tile_plan(int M, int N, int K, int wt, int n_cu) {
+  TilePlan best{};
+  double best_t = 1e300;
+  for (const TileShape& s : kTileShapes) {
+    if (s.wt != wt || K % s.kc) continue;
+    const int bm = 32 * TG_WM * s.mtw, bn = 32 * s.rbw * s.wn;
+    if (N % bn) continue;
+    const long long tiles = (long long)((M + bm - 1) / bm) * (N / bn);
+    const long long rounds = (tiles + n_cu - 1) / n_cu;
+    const double t = (double)rounds * (K / 32) * tile_kblock_cycles(s);
+    if (t < best_t * 0.999) {
+      best_t = t;
+      best.mtw = s.mtw;
+      best.rbw = s.rbw;
+      best.wn = s.wn;
+      best.kc = s.kc;
+      best.tiles_m = (M + bm - 1) / bm;
+      best.tiles_n = N / bn;
+    }
+  }
+  return best;
+}
+
+inline size_t tile_lds_bytes(int wt, const TilePlan& p) {
+  return (size_t)tile_stages(wt, p.mtw, p.rbw, p.wn, p.kc) *
+         tile_stage_bytes(wt, p.mtw, p.rbw, p.wn, p.kc);
+}
+
+}  // namespace dfl

@@ -30,8 +30,11 @@ GROUPS = [
     ("o / down (RESID)", r"gsk_gemm_kernel<0, 4, false, 4>"),
     ("gate|up (SWIGLU, norm-on-load)", r"gsk_gemm_kernel<0, 1, true, 4>"),
     ("lm_head (fp16, ARGMAX, norm-on-load)", r"gsk_(gemm|dyn)_kernel<1, 2, true, 4>"),
-    ("down, stacked rows (M-split RESID)", r"gsk_gemm_m_kernel<0, 4, false"),
-    ("stacked-row GEMMs (rocBLAS: qkv, o, gate|up, lm_head, ingest)", r"Cijk_"),
+    ("M-split stream-K (stacked rows up to 64)", r"gsk_gemm_m_kernel"),
+    ("tile GEMM int8 (stacked rows: qkv, o, gate|up, down; prompt-sized ingest K|V)",
+     r"tile_gemm_kernel<0,"),
+    ("tile GEMM fp16 (stacked rows: lm_head)", r"tile_gemm_kernel<1,"),
+    ("library GEMM (rocBLAS: prompt-sized ingest fc)", r"Cijk_"),
     ("stacked-row epilogues (norm rows, RESID, SWIGLU)", r"afl_rows_kernel|resid_rows_kernel|swiglu_rows_kernel"),
     ("row argmax (stacked lm_head)", r"row_argmax_kernel"),
     ("block attention", r"block_attn_kernel"),

@@ -5,6 +5,7 @@
 #include <cstring>
 
 #include "dfl_check.h"
+#include "dfl_tile_plan.h"
 
 using namespace dfl;
 
@@ -78,6 +79,36 @@ int main() {
   { AttnArgs b = t; b.NH = 41; expect(check_attn_args(b), "head counts", "ratio"); }
   { AttnArgs b = t; b.O = nullptr; expect(check_attn_args(b), "buffers", "no output"); }
   { AttnArgs b = t; b.max_chunks = 65; expect(check_attn_args(b), "chunk count", "max chunks"); }
+  // tile GEMM: every plan of the shapes the library multiplies covers its product, passes
+  // the checks and fits 160 KiB of LDS; then one rule broken at a time
+  const int shapes[][3] = {{256, 6144, 4096}, {256, 4096, 4096}, {256, 28672, 4096},
+                           {256, 4096, 14336}, {256, 128256, 4096}, {4096, 2048, 5120},
+                           {4096, 2048, 4096}, {65, 7168, 5120}, {96, 34816, 5120},
+                           {200, 5120, 17408}, {100, 1024, 256}, {128, 512, 256}};
+  for (const auto& sh : shapes)
+    for (int wt = 0; wt < 2; ++wt) {
+      const TilePlan tp = tile_plan(sh[0], sh[1], sh[2], wt, 256);
+      TileArgs ta{};
+      ta.W = (const uint4*)P; ta.X = (const half_t*)P; ta.Y = (float*)P;
+      ta.M = sh[0]; ta.N = sh[1]; ta.K = sh[2]; ta.ldy = sh[1];
+      char what[96];
+      std::snprintf(what, sizeof what, "tile plan %dx%dx%d wt %d", sh[0], sh[1], sh[2], wt);
+      expect(check_tile_args(wt, ta, tp), nullptr, what);
+      if (tile_lds_bytes(wt, tp) > 160 * 1024) expect("LDS", nullptr, what);
+    }
+  {
+    TileArgs ta{};
+    ta.W = (const uint4*)P; ta.X = (const half_t*)P; ta.Y = (float*)P;
+    ta.M = 256; ta.N = 4096; ta.K = 4096; ta.ldy = 4096;
+    const TilePlan tp = tile_plan(256, 4096, 4096, WT_INT8, 256);
+    { TileArgs b = ta; b.K = 4000; expect(check_tile_args(WT_INT8, b, tp), "multiple of 64", "tile K"); }
+    { TileArgs b = ta; b.ldy = 100; expect(check_tile_args(WT_INT8, b, tp), "output row", "tile ldy"); }
+    { TileArgs b = ta; b.Y = nullptr; expect(check_tile_args(WT_INT8, b, tp), "null", "tile Y"); }
+    { TileArgs b = ta; b.M = 1000; expect(check_tile_args(WT_INT8, b, tp), "cover", "tile M"); }
+    { TilePlan q = tp; q.rbw = 3; expect(check_tile_args(WT_INT8, ta, q), "shape", "tile rbw"); }
+    { TilePlan q = tp; q.tiles_n += 1; expect(check_tile_args(WT_INT8, ta, q), "cover", "tile n"); }
+    { TileArgs b = ta; b.N = 4010; expect(check_tile_args(WT_INT8, b, tp), "multiple", "tile N"); }
+  }
   if (fails == 0) std::printf("ok\n");
   return fails ? 1 : 0;
 }
