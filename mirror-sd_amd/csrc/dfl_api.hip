@@ -126,9 +126,8 @@ struct dfl_ctx {
   bool fc_loaded = false;
   half_t* final_norm = nullptr;
   uint4* w_lm = nullptr;
-  // stacked blocks (more than STACK_MIN_ROWS rows): lm_head logits lm32 [RM][V] fp32
-  float* lm32 = nullptr;
   float* y32 = nullptr;      // [RM][max(NQKV, H, 2F)] fp32 rows of the stacked-block GEMMs
+  unsigned long long* lm_parts = nullptr;   // [V/32][RM] stacked lm_head argmax partial keys
   const half_t* embed = nullptr;
   bool head_loaded = false;
   int active = 0;   // layers run per call (num_draft_layers)
@@ -147,7 +146,7 @@ struct dfl_ctx {
   float* sk_ws = nullptr;        // split-tile partials
   int* sk_tile_cnt = nullptr;    // [max tiles]
   int* dyn_next = nullptr;       // [2] work counters of the balanced lm_head (self-resetting)
-  float* sk_ss = nullptr;        // [m-tiles][H/64][32] row sums of squares of x (RESID output)
+  float* sk_ss = nullptr;        // [m-tiles][H/64 or H/32][32] row sums of squares of x (RESID)
   SKPlan sk_qkv, sk_o, sk_gu, sk_down, sk_lm;
   // context ingest: `ing` rows per pass (compute-bound: fc on rocBLAS, K|V on the tile GEMM)
   int ing = 0;
@@ -381,7 +380,7 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
     if ((r = x->alloc(&x->qkvbuf, Bm * x->NQKV)) || (r = x->alloc(&x->rnorm, bm32)) ||
         (r = x->alloc(&x->sk_ws, wsn)) || (r = x->alloc(&x->sk_tile_cnt, tiles, true)) ||
         (r = x->alloc(&x->dyn_next, 2, true)) || (r = x->alloc(&x->rope_cs, 32 * 64 * 2)) ||
-        (r = x->alloc(&x->sk_ss, (bm32 / 32) * (size_t)(x->H / 64) * 32))) {
+        (r = x->alloc(&x->sk_ss, (bm32 / 32) * (size_t)(x->H / 32) * 32))) {
       delete x;
       return r;
     }
@@ -502,8 +501,8 @@ int dfl_load_head(dfl_ctx* ctx, const uint16_t* final_norm, const uint16_t* embe
     if (!ctx->w_lm) DFL_TRY(ctx->alloc(&ctx->w_lm, (size_t)ctx->V * ctx->H / 8));
     launch_pack_f16(reinterpret_cast<const half_t*>(lm_head), ctx->V, ctx->H, ctx->w_lm, st);
     DFL_TRY(check_launch("pack lm_head"));
-    if (ctx->RM > STACK_MIN_ROWS && !ctx->lm32)
-      DFL_TRY(ctx->alloc(&ctx->lm32, (size_t)ctx->RM * ctx->V));
+    if (ctx->RM > STACK_MIN_ROWS && !ctx->lm_parts)
+      DFL_TRY(ctx->alloc(&ctx->lm_parts, (size_t)(ctx->V / 32) * ctx->RM));
   }
   ctx->head_loaded = true;
   return DFL_OK;
@@ -592,28 +591,42 @@ static int block_attention(const AttnArgs& at, hipStream_t st) {
   return DFL_OK;
 }
 
-// Tile GEMM Y[M][ldy] = X . W^T (fp32) for more than STACK_MIN_ROWS rows (X in the
-// fragment layout), with its argument checks reported as DFL_EINVAL.
-static int tgemm(dfl_ctx* ctx, int cat, int wt, const uint4* W, int N, int K, const half_t* X,
-                 int M, float* Y, int ldy, hipStream_t st) {
-  const TilePlan p = tile_plan(M, N, K, wt, ctx->n_cu);
-  TileArgs a{};
+// Tile GEMM of more than STACK_MIN_ROWS rows (X in the fragment layout) with epilogue epi
+// (the TileArgs outputs e), its argument checks reported as DFL_EINVAL.
+// n_parts (ARGMAX): receives the number of partial key rows written (one per wave column).
+static int tgemm(dfl_ctx* ctx, int cat, int wt, int epi, const uint4* W, int N, int K,
+                 const half_t* X, int M, const TileArgs& e, hipStream_t st,
+                 int* n_parts = nullptr) {
+  const TilePlan p = tile_plan(M, N, K, wt, ctx->n_cu, epi == TG_SWIGLU);
+  if (n_parts) *n_parts = N / (32 * p.rbw);
+  TileArgs a = e;
   a.W = W;
   a.N = N;
   a.K = K;
   a.X = X;
   a.M = M;
-  a.Y = Y;
-  a.ldy = ldy;
-  if (const char* why = check_tile_args(wt, a, p))
+  if (const char* why = check_tile_args(wt, epi, a, p))
     return fail(DFL_EINVAL, std::string("tile GEMM launch refused: ") + why);
   if (tile_lds_bytes(wt, p) > (size_t)ctx->lds_max)
     return fail(DFL_EINVAL, "tile GEMM: the device's LDS per workgroup is too small");
   const long long wbytes = (long long)N * K * (wt == WT_INT8 ? 1 : 2);
   ProfScope ps(ctx, cat, wbytes, st, /*attached=*/true);
-  if (!launch_tile_gemm(wt, a, p, st, ps.start(), ps.stop()))
-    return fail(DFL_EINVAL, "no tile GEMM kernel for this shape");
+  if (!launch_tile_gemm(wt, epi, a, p, st, ps.start(), ps.stop()))
+    return fail(DFL_EINVAL, "no tile GEMM kernel for this shape and epilogue");
   return DFL_OK;
+}
+static TileArgs tile_f32(float* Y, int ldy) {
+  TileArgs e{};
+  e.Y = Y;
+  e.ldy = ldy;
+  return e;
+}
+static TileArgs tile_resid(const half_t* scale, half_t* x, float* ss) {
+  TileArgs e{};
+  e.scale = scale;
+  e.x = x;
+  e.ss = ss;
+  return e;
 }
 
 static int layers_ready(dfl_ctx* ctx, const char* who) {
@@ -646,7 +659,8 @@ static int ingest_kv_rows(dfl_ctx* ctx, const half_t* xa, int rows, int r0, hipS
     Layer& L = ctx->layers[l];
     // the K|V rows start at packed row-block NH*128/32 of the qkv matrix
     const uint4* w_kv = L.w_qkv + (size_t)(NH * 128 / 32) * (H / 32) * 64;
-    DFL_TRY(tgemm(ctx, P_INGEST_KV, WT_INT8, w_kv, Nkv, H, xa, rows, ctx->kv32, Nkv, st));
+    DFL_TRY(tgemm(ctx, P_INGEST_KV, WT_INT8, TG_F32, w_kv, Nkv, H, xa, rows, tile_f32(ctx->kv32, Nkv),
+                  st));
     QKRopeArgs q{};
     q.qkv32 = ctx->kv32;
     q.oscale = L.s_qkv + NH * 128;   // scales of the k|v rows, in row order
@@ -925,11 +939,11 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
     if (stacked) {
       {
         ProfScope ps(ctx, P_ROWS, 0, st);
-        launch_apply_norm(ctx->x, l > 0 ? ctx->sk_ss : nullptr, H / 64, eps, Ly.in_norm, M, H,
+        launch_apply_norm(ctx->x, l > 0 ? ctx->sk_ss : nullptr, H / 32, eps, Ly.in_norm, M, H,
                           ctx->h, st, l > 0 ? nullptr : ctx->rnorm, /*h_afl=*/true);
       }
-      DFL_TRY(tgemm(ctx, P_GEMM_TILE, WT_INT8, Ly.w_qkv, ctx->NQKV, H, ctx->h, M, ctx->y32,
-                    ctx->NQKV, st));
+      DFL_TRY(tgemm(ctx, P_GEMM_TILE, WT_INT8, TG_F32, Ly.w_qkv, ctx->NQKV, H, ctx->h, M,
+                    tile_f32(ctx->y32, ctx->NQKV), st));
     } else if (fuse_rope) {
       // one sequence: the per-head Q/K norm, RoPE and cache scatter run in the epilogue
       RopeEpi re{};
@@ -1027,24 +1041,21 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
       DFL_TRY(block_attention(at, st));
     }
     if (stacked) {
-      // the same steps as tile GEMMs with the epilogues in row kernels
-      DFL_TRY(tgemm(ctx, P_GEMM_TILE, WT_INT8, Ly.w_o, H, NQ, ctx->attn, M, ctx->y32, H, st));
+      // the same steps as tile GEMMs with the RESID / SWIGLU epilogues fused; the RMSNorm
+      // of a GEMM's input is a row kernel (row sums of squares per 32-column tile)
+      DFL_TRY(tgemm(ctx, P_GEMM_TILE, WT_INT8, TG_RESID, Ly.w_o, H, NQ, ctx->attn, M,
+                    tile_resid(Ly.s_o, ctx->x, ctx->sk_ss), st));
       {
         ProfScope ps(ctx, P_ROWS, 0, st);
-        launch_resid_rows(ctx->y32, M, H, Ly.s_o, ctx->x, ctx->sk_ss, st);
-        launch_apply_norm(ctx->x, ctx->sk_ss, H / 64, eps, Ly.post_norm, M, H, ctx->h, st,
+        launch_apply_norm(ctx->x, ctx->sk_ss, H / 32, eps, Ly.post_norm, M, H, ctx->h, st,
                           nullptr, /*h_afl=*/true);
       }
-      DFL_TRY(tgemm(ctx, P_GEMM_TILE, WT_INT8, Ly.w_gu, 2 * F, H, ctx->h, M, ctx->y32, 2 * F, st));
-      {
-        ProfScope ps(ctx, P_ROWS, 0, st);
-        launch_swiglu_rows(ctx->y32, M, F, Ly.s_gu, ctx->act, st);
-      }
-      DFL_TRY(tgemm(ctx, P_GEMM_TILE, WT_INT8, Ly.w_down, H, F, ctx->act, M, ctx->y32, H, st));
-      {
-        ProfScope ps(ctx, P_ROWS, 0, st);
-        launch_resid_rows(ctx->y32, M, H, Ly.s_down, ctx->x, ctx->sk_ss, st);
-      }
+      TileArgs sw{};
+      sw.scale = Ly.s_gu;
+      sw.out = ctx->act;
+      DFL_TRY(tgemm(ctx, P_GEMM_TILE, WT_INT8, TG_SWIGLU, Ly.w_gu, 2 * F, H, ctx->h, M, sw, st));
+      DFL_TRY(tgemm(ctx, P_GEMM_TILE, WT_INT8, TG_RESID, Ly.w_down, H, F, ctx->act, M,
+                    tile_resid(Ly.s_down, ctx->x, ctx->sk_ss), st));
     } else {
       // x += attn @ Wo^T ; per-tile row sums of squares of x -> sk_ss
       DFL_TRY(skgemm(ctx, P_GEMM_W8, WT_INT8, EPI_RESID, ctx->sk_o, Ly.w_o, Ly.s_o, H, NQ / 32,
@@ -1059,19 +1070,24 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
                      st));
     }
   }
+  // row sums of squares of x: per 64 columns (stream-K RESID) or 32 (tile RESID)
+  const int ss_tiles = stacked ? H / 32 : H / 64;
   if ((out_logits || out_ids) && stacked) {
-    // stacked blocks: final norm into fragment-layout rows, then the lm_head tile GEMM (fp32
-    // logits) and a row argmax
+    // stacked blocks: final norm into fragment-layout rows, then the lm_head tile GEMM with
+    // the argmax keys (and the fp32 logits if asked for)
     {
       ProfScope ps(ctx, P_ROWS, 0, st);
-      launch_apply_norm(ctx->x, ctx->sk_ss, H / 64, ctx->cfg.rms_eps, ctx->final_norm, M, H,
+      launch_apply_norm(ctx->x, ctx->sk_ss, ss_tiles, ctx->cfg.rms_eps, ctx->final_norm, M, H,
                         ctx->h, st, nullptr, /*h_afl=*/true);
     }
-    float* lg = out_logits ? out_logits : ctx->lm32;
-    DFL_TRY(tgemm(ctx, P_LM_HEAD, WT_F16, ctx->w_lm, ctx->V, H, ctx->h, M, lg, ctx->V, st));
+    TileArgs lm = tile_f32(out_logits, ctx->V);
+    lm.keys = out_ids ? ctx->lm_parts : nullptr;
+    int parts = 0;
+    DFL_TRY(tgemm(ctx, P_LM_HEAD, WT_F16, out_ids ? TG_ARGMAX : TG_F32, ctx->w_lm, ctx->V, H,
+                  ctx->h, M, lm, st, &parts));
     if (out_ids) {
       ProfScope ps(ctx, P_ROWS, 0, st);
-      launch_row_argmax(lg, M, ctx->V, out_ids, st);
+      launch_argmax_parts(ctx->lm_parts, parts, M, out_ids, st);
     }
   } else if (out_logits || out_ids) {
     bool ids_done = false;
@@ -1085,7 +1101,7 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
   }
   if (out_hidden) {
     ProfScope ps(ctx, P_ROWS, 0, st);
-    launch_apply_norm(ctx->x, ctx->sk_ss, H / 64, ctx->cfg.rms_eps, ctx->final_norm, M, H,
+    launch_apply_norm(ctx->x, ctx->sk_ss, ss_tiles, ctx->cfg.rms_eps, ctx->final_norm, M, H,
                       reinterpret_cast<half_t*>(out_hidden), st);
   }
   if (out_prenorm) {

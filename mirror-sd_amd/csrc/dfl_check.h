@@ -96,16 +96,33 @@ inline const char* check_attn_args(const AttnArgs& a) {
   return nullptr;
 }
 
-inline const char* check_tile_args(int wt, const TileArgs& a, const TilePlan& p) {
+inline const char* check_tile_args(int wt, int epi, const TileArgs& a, const TilePlan& p) {
   if (wt != WT_INT8 && wt != WT_F16) return "unknown weight type";
-  if (!a.W || !a.X || !a.Y) return "null weights, activations or output";
+  if (!a.W || !a.X) return "null weights or activations";
+  switch (epi) {
+    case TG_F32:
+      if (!a.Y) return "F32 epilogue without an output";
+      break;
+    case TG_RESID:
+      if (wt != WT_INT8 || !a.scale || !a.x || !a.ss) return "RESID needs int8 weights, scales, x and row sums";
+      break;
+    case TG_SWIGLU:
+      if (wt != WT_INT8 || !a.scale || !a.out || p.rbw % 2)
+        return "SWIGLU needs int8 weights, scales, an output and gate|up pairs in each wave";
+      break;
+    case TG_ARGMAX:
+      if (wt != WT_F16 || !a.keys) return "ARGMAX needs fp16 weights and keys";
+      break;
+    default:
+      return "unknown epilogue";
+  }
   if (p.mtw < 1 || p.mtw > 2 || (p.rbw != 1 && p.rbw != 2 && p.rbw != 4) || p.wn < 1 ||
       p.wn > 2 || (p.kc != 32 && p.kc != 64))
     return "unknown tile shape";
   if (a.M < 1 || a.N < 1 || a.K < 64 || a.K % 64 || a.K % p.kc)
     return "M, N >= 1 and K a positive multiple of 64 and of the stage's k";
   if (a.N % (32 * p.rbw * p.wn)) return "N is not a multiple of the tile's columns";
-  if (a.ldy < a.N) return "output row shorter than N";
+  if (a.Y && a.ldy < a.N) return "output row shorter than N";
   if (p.tiles_n != a.N / (32 * p.rbw * p.wn) || (long long)p.tiles_m * 128 * p.mtw < a.M ||
       (long long)p.tiles_m * 128 * p.mtw >= (long long)a.M + 128 * p.mtw)
     return "tile counts do not cover the product";

@@ -101,13 +101,24 @@ bool launch_streamk_gemm(int wt, int epi, bool norm, const StreamArgs& a, const 
 // ---- tile GEMM for stacked rows, M > 64 (dfl_tile.hip) ----
 // Y[M][ldy] (fp32, columns [0, N)) = X . W^T with X in the activation fragment layout
 // (ceil(M/32) tiles of 32 x K) and W packed blocks (int8: unscaled integer-weight sums).
+// Tile GEMM epilogues: TG_F32 stores Y; TG_RESID, TG_SWIGLU and TG_ARGMAX do what the
+// stream-K RESID / SWIGLU / ARGMAX epilogues do (same arithmetic and rounding points), with
+// RESID's row sums of squares per 32-column tile.
+enum { TG_F32 = 0, TG_RESID = 1, TG_SWIGLU = 2, TG_ARGMAX = 3 };
 struct TileArgs {
   const uint4* W;           // packed weight blocks, N rows
   int N, K;                 // N % (32 * rb) == 0, K % 64 == 0
   const half_t* X;          // fragment-layout tiles, ceil(M/32) of them
   int M;
-  float* Y;                 // row-major fp32 [M][ldy]
+  float* Y;                 // TG_F32 (and optionally TG_ARGMAX): row-major fp32 [M][ldy]
   int ldy;
+  const half_t* scale;      // RESID / SWIGLU: [N] per-row scales of the int8 weights
+  half_t* x;                // RESID: fragment-layout residual [M][N], updated in place
+  float* ss;                // RESID: [ceil(M/32)][N/32][32] row sums of squares of the new x
+  half_t* out;              // SWIGLU: fragment-layout act [M][N/2] (N in packed gate|up order)
+  unsigned long long* keys; // ARGMAX: [N/32/rbw][M] per-wave-column best keys (packed
+                            // order(value) << 32 | ~index, 0 = none), reduced by
+                            // launch_argmax_parts
   int tiles_m, tiles_n;     // set by the launcher from the plan
 };
 struct TilePlan {
@@ -120,7 +131,7 @@ struct TilePlan {
 // (tile_plan / tile_lds_bytes: dfl_tile_plan.h)
 // Returns false (and launches nothing) when the arguments fail check_tile_args.
 // ev_start / ev_stop (optional) receive the kernel's own start and end timestamps.
-bool launch_tile_gemm(int wt, const TileArgs& a, const TilePlan& p, hipStream_t st,
+bool launch_tile_gemm(int wt, int epi, const TileArgs& a, const TilePlan& p, hipStream_t st,
                       hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
 
 // ---- pack / quantise (dfl_pack.hip) ----
@@ -174,14 +185,6 @@ void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* no
 void launch_apply_norm(const half_t* x, const float* ss, int ss_tiles, float eps, const half_t* g,
                        int M, int N, half_t* h, hipStream_t st, const float* rnorm = nullptr,
                        bool h_afl = false);
-// Epilogues of the stacked-block tile GEMMs (fp32 rows y), same arithmetic as the
-// stream-K RESID / SWIGLU epilogues: x += fp16(y * s) with sums of squares into ss
-// [M/32][N/64][32]; act = swiglu(y_gate * s, y_up * s) (y in the packed gate|up column
-// order) in the fragment layout.
-void launch_resid_rows(const float* y, int M, int N, const half_t* s, half_t* x, float* ss,
-                       hipStream_t st);
-void launch_swiglu_rows(const float* y, int M, int F, const half_t* s, half_t* act,
-                        hipStream_t st);
 void launch_afl_to_rows(const half_t* x, int M, int N, half_t* h, hipStream_t st);
 // Up to SEQ_MAX sequences (batched drafting) share one rope / attention launch.
 constexpr int SEQ_MAX = 8;
@@ -223,8 +226,9 @@ DFL_DEV int cache_slot(const RopeSeq& q, int M, int m) {
 bool launch_qk_rope(const QKRopeArgs& a, hipStream_t st);
 // ids[m] = ~low32(keys[m]); keys[m] = 0.
 void launch_argmax_finalize(unsigned long long* keys, int M, int32_t* ids, hipStream_t st);
-// ids[m] = argmax of fp32 logits row m ([M][V]), lowest index on ties, -1 if none > -inf.
-void launch_row_argmax(const float* logits, int M, int V, int32_t* ids, hipStream_t st);
+// ids[m] from the largest of parts[p][m], p < P (the tile GEMM's ARGMAX keys); -1 if none.
+void launch_argmax_parts(const unsigned long long* parts, int P, int M, int32_t* ids,
+                         hipStream_t st);
 
 // ---- attention (dfl_attn.hip) ----
 // One sequence of an attention launch: its cache, key range and output rows.

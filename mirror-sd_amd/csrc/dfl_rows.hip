@@ -118,59 +118,6 @@ void launch_apply_norm(const half_t* x, const float* ss, int ss_tiles, float eps
                      ss_tiles, rnorm, eps, g, N, h, h_afl);
 }
 
-// RESID epilogue for fp32 tile-GEMM rows y [M][N] (stacked blocks): x += fp16(y * s) in
-// place on the fragment-layout residual, with the per-(m-tile, 64-column tile) row sums of
-// squares of the new x in ss [M/32][N/64][32] -- the stream-K RESID epilogue's arithmetic.
-// One wave per (row, column tile), lane = column.
-__global__ __launch_bounds__(256) void resid_rows_kernel(const float* __restrict__ y, int M, int N,
-                                                         const half_t* __restrict__ s,
-                                                         half_t* __restrict__ x,
-                                                         float* __restrict__ ss) {
-  const int lane = threadIdx.x & 63;
-  const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int tiles = N / 64;
-  if (w >= M * tiles) return;
-  const int m = w / tiles, t = w - m * tiles;
-  const int n = t * 64 + lane;
-  const float yv = h2f(f2h(y[(size_t)m * N + n] * h2f(s[n])));
-  half_t* xp = x + afl_index(m, n, N);
-  const half_t xn = f2h(h2f(*xp) + yv);
-  *xp = xn;
-  const float tot = wave_sum(h2f(xn) * h2f(xn));
-  if (lane == 0) ss[((size_t)(m >> 5) * tiles + t) * 32 + (m & 31)] = tot;
-}
-
-void launch_resid_rows(const float* y, int M, int N, const half_t* s, half_t* x, float* ss,
-                       hipStream_t st) {
-  const int waves = M * (N / 64);
-  hipLaunchKernelGGL(resid_rows_kernel, dim3((waves + 3) / 4), dim3(256), 0, st, y, M, N, s, x, ss);
-}
-
-// SWIGLU epilogue for fp32 tile-GEMM rows y [M][2F] in the packed gate|up column order
-// (gate row f at column 64*(f/32) + f%32, up row f 32 further, as the scales):
-// act[m][f] = fp16(fp16(silu(g)) * u) with g = fp16(y_gate * s_gate), u = fp16(y_up * s_up),
-// the stream-K SWIGLU epilogue's rounding.  act in the fragment layout [M][F].
-__global__ __launch_bounds__(256) void swiglu_rows_kernel(const float* __restrict__ y, int M, int F,
-                                                          const half_t* __restrict__ s,
-                                                          half_t* __restrict__ act) {
-  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (size_t)M * F) return;
-  const int m = (int)(i / F), f = (int)(i - (size_t)m * F);
-  const int si = 64 * (f >> 5) + (f & 31);
-  const float gv = h2f(f2h(y[(size_t)m * 2 * F + si] * h2f(s[si])));
-  const float uv = h2f(f2h(y[(size_t)m * 2 * F + si + 32] * h2f(s[si + 32])));
-  const float sig = h2f(f2h(1.0f / (1.0f + expf(-gv))));
-  const float sil = h2f(f2h(gv * sig));
-  act[afl_index(m, f, F)] = f2h(sil * uv);
-}
-
-void launch_swiglu_rows(const float* y, int M, int F, const half_t* s, half_t* act,
-                        hipStream_t st) {
-  const size_t n = (size_t)M * F;
-  hipLaunchKernelGGL(swiglu_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, y, M,
-                     F, s, act);
-}
-
 // Row-major concatenation [rows][nf * H] of the feature tensors (the materialised
 // extract_context_feature).
 __global__ __launch_bounds__(256) void concat_feats_kernel(FeatPtrs f, int H,
@@ -371,59 +318,6 @@ bool launch_qk_rope(const QKRopeArgs& a, hipStream_t st) {
   return true;
 }
 
-// ids[m] = argmax over the fp32 logits row m (lowest index on ties, NaN never chosen, -1
-// when no entry beats -inf): the lm_head argmax for stacked blocks whose logits come from
-// a library GEMM.  Each thread scans its columns in increasing order with a strict '>',
-// then the workgroup keeps the largest (order-preserving value, ~index) key.
-__global__ __launch_bounds__(256) void row_argmax_kernel(const float* __restrict__ logits, int V,
-                                                         int32_t* __restrict__ ids) {
-  __shared__ unsigned long long sm[4];
-  const int m = blockIdx.x;
-  // V % 64 == 0: rows are 16-byte aligned, read as float4 with RA_UNROLL loads in flight;
-  // a thread's columns (4 per float4, float4 i = t, t + 256, ...) are visited in order
-  constexpr int RA_UNROLL = 4;
-  const floatx4* row = reinterpret_cast<const floatx4*>(logits + (size_t)m * V);
-  const int n4 = V / 4;
-  float best = -INFINITY;
-  int bn = -1;
-  for (int i0 = threadIdx.x; i0 < n4; i0 += 256 * RA_UNROLL) {
-    floatx4 v[RA_UNROLL];
-#pragma unroll
-    for (int u = 0; u < RA_UNROLL; ++u) {
-      const int i = i0 + 256 * u;
-      v[u] = i < n4 ? row[i] : (floatx4){-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-    }
-#pragma unroll
-    for (int u = 0; u < RA_UNROLL; ++u)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (v[u][j] > best) {
-          best = v[u][j];
-          bn = 4 * (i0 + 256 * u) + j;
-        }
-  }
-  unsigned long long key =
-      bn < 0 ? 0ull
-             : ((unsigned long long)float_order_key(best) << 32) | (0xFFFFFFFFu - (uint32_t)bn);
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const unsigned long long k2 = __shfl_xor(key, o, 64);
-    key = k2 > key ? k2 : key;
-  }
-  if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = key;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    unsigned long long k = sm[0];
-    for (int i = 1; i < 4; ++i) k = sm[i] > k ? sm[i] : k;
-    ids[m] = k ? (int32_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull)) : -1;
-  }
-}
-
-void launch_row_argmax(const float* logits, int M, int V, int32_t* ids, hipStream_t st) {
-  if (M <= 0) return;
-  hipLaunchKernelGGL(row_argmax_kernel, dim3(M), dim3(256), 0, st, logits, V, ids);
-}
-
 __global__ void argmax_finalize_kernel(unsigned long long* keys, int M, int32_t* ids) {
   const int m = threadIdx.x;
   if (m < M) {
@@ -431,6 +325,31 @@ __global__ void argmax_finalize_kernel(unsigned long long* keys, int M, int32_t*
     ids[m] = k ? (int32_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull)) : -1;
     keys[m] = 0ull;
   }
+}
+
+// One wave per row: the largest of the P partial keys (fixed tree order), as an id.
+__global__ __launch_bounds__(256) void argmax_parts_kernel(const unsigned long long* parts, int P,
+                                                           int M, int32_t* ids) {
+  const int lane = threadIdx.x & 63;
+  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= M) return;
+  unsigned long long k = 0ull;
+  for (int p = lane; p < P; p += 64) {
+    const unsigned long long v = parts[(size_t)p * M + m];
+    k = v > k ? v : k;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const unsigned long long k2 = __shfl_xor(k, o, 64);
+    k = k2 > k ? k2 : k;
+  }
+  if (lane == 0) ids[m] = k ? (int32_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull)) : -1;
+}
+
+void launch_argmax_parts(const unsigned long long* parts, int P, int M, int32_t* ids,
+                         hipStream_t st) {
+  if (M <= 0) return;
+  hipLaunchKernelGGL(argmax_parts_kernel, dim3((M + 3) / 4), dim3(256), 0, st, parts, P, M, ids);
 }
 
 void launch_argmax_finalize(unsigned long long* keys, int M, int32_t* ids, hipStream_t st) {

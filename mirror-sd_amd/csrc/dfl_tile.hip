@@ -160,7 +160,7 @@ DFL_DEV void tg_mfma(const TgFrag<WT, MTW, RBW>& f, floatx16 (&acc)[RBW][MTW][NA
 // MFMAs before B(t)) before the copies of stage t + STAGES - 1 that refill its buffer,
 // issued right after B(t).  B(-1) precedes the first read.  Every wave passes B(-1) ..
 // B(nst - 2).
-template <int WT, int MTW, int RBW, int WN, int KC>
+template <int WT, int EPI, int MTW, int RBW, int WN, int KC>
 __global__ __launch_bounds__(64 * (TG_WM * WN + (tile_loader(WN) ? 1 : 0))) void tile_gemm_kernel(
     TileArgs a) {
   using S = TgShape<WT, MTW, RBW, WN, KC>;
@@ -263,58 +263,176 @@ __global__ __launch_bounds__(64 * (TG_WM * WN + (tile_loader(WN) ? 1 : 0))) void
     tg_mfma<WT, MTW, RBW, S::NACC>(f1, acc);
   }
 
-  // epilogue: fp32 rows, m < M only
+  // epilogue, rows m < M only.  Lane l holds, in register i of block (r, t), row
+  // mbase(t) + 8*(i/4) + (i%4) and column n_lane + 32*r.
   const int g = lane >> 5;
   const int n_lane = (nb0 + wn * RBW) * 32 + (lane & 31);
-  static_for<0, MTW>([&](auto t) {
-    const int mbase = (mt0 + wm * MTW + t) * 32 + 4 * g;
-    static_for<0, RBW>([&](auto r) {
-      floatx16 v = acc[r][t][0];
-      if constexpr (S::NACC == 2) v += acc[r][t][1];
-      float* yc = a.Y + n_lane + 32 * r;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int m = mbase + 8 * (i >> 2) + (i & 3);
-        if (m < a.M) yc[(size_t)m * a.ldy] = v[i];
-      }
+  floatx16 v[RBW][MTW];
+  static_for<0, RBW>([&](auto r) {
+    static_for<0, MTW>([&](auto t) {
+      v[r][t] = acc[r][t][0];
+      if constexpr (S::NACC == 2) v[r][t] += acc[r][t][1];
     });
   });
+  auto row_of = [&](int t, int i) __attribute__((always_inline)) {
+    return (mt0 + wm * MTW + t) * 32 + 4 * g + 8 * (i >> 2) + (i & 3);
+  };
+  if constexpr (EPI == TG_F32 || EPI == TG_ARGMAX) {
+    if (a.Y) {
+      static_for<0, MTW>([&](auto t) {
+        static_for<0, RBW>([&](auto r) {
+          float* yc = a.Y + n_lane + 32 * r;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int m = row_of(t, i);
+            if (m < a.M) yc[(size_t)m * a.ldy] = v[r][t][i];
+          }
+        });
+      });
+    }
+  }
+  if constexpr (EPI == TG_RESID) {
+    // x += fp16(y * s) in place; row sums of squares of the new x per 32-column tile
+    const int ncol = a.N >> 5;
+    static_for<0, MTW>([&](auto t) {
+      static_for<0, RBW>([&](auto r) {
+        const int n = n_lane + 32 * r;
+        const float s = h2f(a.scale[n]);
+        float sq[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int m = row_of(t, i);
+          sq[i] = 0.f;
+          if (m < a.M) {
+            half_t* xp = a.x + afl_index(m, n, a.N);
+            const half_t xn = f2h(h2f(*xp) + h2f(f2h(v[r][t][i] * s)));
+            *xp = xn;
+            sq[i] = h2f(xn) * h2f(xn);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+#pragma unroll
+          for (int o = 16; o > 0; o >>= 1) sq[i] += __shfl_xor(sq[i], o, 64);
+        if ((lane & 31) == 0) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int m = row_of(t, i);
+            if (m < a.M) a.ss[((size_t)(m >> 5) * ncol + (n >> 5)) * 32 + (m & 31)] = sq[i];
+          }
+        }
+      });
+    });
+  }
+  if constexpr (EPI == TG_SWIGLU) {
+    // packed gate|up: row-block 2j holds gate rows [32j, 32j+32), 2j+1 the matching up rows
+    const int F = a.N >> 1;
+    static_for<0, MTW>([&](auto t) {
+      static_for<0, RBW / 2>([&](auto j) {
+        const int ng = n_lane + 64 * j;
+        const int f = (ng >> 6) * 32 + (lane & 31);
+        const float sg = h2f(a.scale[ng]), su = h2f(a.scale[ng + 32]);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int m = row_of(t, i);
+          if (m < a.M) {
+            const float gv = h2f(f2h(v[2 * j][t][i] * sg));
+            const float uv = h2f(f2h(v[2 * j + 1][t][i] * su));
+            const float sig = h2f(f2h(1.0f / (1.0f + expf(-gv))));
+            const float sil = h2f(f2h(gv * sig));
+            a.out[afl_index(m, f, F)] = f2h(sil * uv);
+          }
+        }
+      });
+    });
+  }
+  if constexpr (EPI == TG_ARGMAX) {
+    // per row: the wave's best column (increasing n, strict '>': lowest index on ties; NaN
+    // never chosen), then the best of the 32 lanes as (order-preserving value << 32 |
+    // ~index), stored in the wave column's own slot (no atomics: each row key would
+    // otherwise take one atomic from every column tile)
+    unsigned long long* part = a.keys + (size_t)(nb0 / RBW + wn) * a.M;
+    static_for<0, MTW>([&](auto t) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float best = -INFINITY;
+        int bn = -1;
+        static_for<0, RBW>([&](auto r) {
+          if (v[r][t][i] > best) {
+            best = v[r][t][i];
+            bn = n_lane + 32 * r;
+          }
+        });
+        unsigned long long key =
+            bn < 0 ? 0ull
+                   : ((unsigned long long)float_order_key(best) << 32) | (0xFFFFFFFFu - (uint32_t)bn);
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) {
+          const unsigned long long k2 = __shfl_xor(key, o, 64);
+          key = k2 > key ? k2 : key;
+        }
+        const int m = row_of(t, i);
+        if ((lane & 31) == 0 && m < a.M) part[m] = key;
+      }
+    });
+  }
 }
 
-template <int WT, int MTW, int RBW, int WN, int KC>
+template <int WT, int EPI, int MTW, int RBW, int WN, int KC>
 void launch_tile(const TileArgs& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   using S = TgShape<WT, MTW, RBW, WN, KC>;
   const dim3 grid(a.tiles_m * a.tiles_n), block(64 * (S::NW + (S::LOADER ? 1 : 0)));
   if (e0 && e1)
-    hipExtLaunchKernelGGL((tile_gemm_kernel<WT, MTW, RBW, WN, KC>), grid, block, S::LDS, st, e0,
-                          e1, 0, a);
+    hipExtLaunchKernelGGL((tile_gemm_kernel<WT, EPI, MTW, RBW, WN, KC>), grid, block, S::LDS, st,
+                          e0, e1, 0, a);
   else
-    hipLaunchKernelGGL((tile_gemm_kernel<WT, MTW, RBW, WN, KC>), grid, block, S::LDS, st, a);
+    hipLaunchKernelGGL((tile_gemm_kernel<WT, EPI, MTW, RBW, WN, KC>), grid, block, S::LDS, st, a);
 }
 
+// The epilogues each weight type has: int8 F32 / RESID / SWIGLU (gate|up pairs), fp16 F32 /
+// ARGMAX.
 template <int I>
-bool launch_shape_i(int wt, const TileArgs& a, const TilePlan& p, hipStream_t st, hipEvent_t e0,
-                    hipEvent_t e1) {
+bool launch_shape_i(int wt, int epi, const TileArgs& a, const TilePlan& p, hipStream_t st,
+                    hipEvent_t e0, hipEvent_t e1) {
   if constexpr (I < (int)(sizeof(kTileShapes) / sizeof(kTileShapes[0]))) {
     constexpr TileShape s = kTileShapes[I];
     if (wt == s.wt && p.mtw == s.mtw && p.rbw == s.rbw && p.wn == s.wn && p.kc == s.kc) {
-      launch_tile<s.wt, s.mtw, s.rbw, s.wn, s.kc>(a, st, e0, e1);
-      return true;
+      if (epi == TG_F32) {
+        launch_tile<s.wt, TG_F32, s.mtw, s.rbw, s.wn, s.kc>(a, st, e0, e1);
+        return true;
+      }
+      if constexpr (s.wt == WT_INT8) {
+        if (epi == TG_RESID) {
+          launch_tile<s.wt, TG_RESID, s.mtw, s.rbw, s.wn, s.kc>(a, st, e0, e1);
+          return true;
+        }
+        if constexpr (s.rbw % 2 == 0)
+          if (epi == TG_SWIGLU) {
+            launch_tile<s.wt, TG_SWIGLU, s.mtw, s.rbw, s.wn, s.kc>(a, st, e0, e1);
+            return true;
+          }
+      } else {
+        if (epi == TG_ARGMAX) {
+          launch_tile<s.wt, TG_ARGMAX, s.mtw, s.rbw, s.wn, s.kc>(a, st, e0, e1);
+          return true;
+        }
+      }
+      return false;
     }
-    return launch_shape_i<I + 1>(wt, a, p, st, e0, e1);
+    return launch_shape_i<I + 1>(wt, epi, a, p, st, e0, e1);
   }
   return false;
 }
 
 }  // namespace
 
-bool launch_tile_gemm(int wt, const TileArgs& a0, const TilePlan& p, hipStream_t st,
+bool launch_tile_gemm(int wt, int epi, const TileArgs& a0, const TilePlan& p, hipStream_t st,
                       hipEvent_t ev_start, hipEvent_t ev_stop) {
-  if (check_tile_args(wt, a0, p)) return false;
+  if (check_tile_args(wt, epi, a0, p)) return false;
   TileArgs a = a0;
   a.tiles_m = p.tiles_m;
   a.tiles_n = p.tiles_n;
-  return launch_shape_i<0>(wt, a, p, st, ev_start, ev_stop);
+  return launch_shape_i<0>(wt, epi, a, p, st, ev_start, ev_stop);
 }
 
 }  // namespace dfl

@@ -62,12 +62,13 @@ inline double tile_kblock_cycles(const TileShape& s) {
 }
 
 // The instantiated shape with the least estimated time: rounds of one workgroup per CU x
-// k-blocks x cycles per k-block.
-inline TilePlan tile_plan(int M, int N, int K, int wt, int n_cu) {
+// k-blocks x cycles per k-block.  pairs: each wave must hold gate|up row-block pairs
+// (SWIGLU), i.e. an even rbw.
+inline TilePlan tile_plan(int M, int N, int K, int wt, int n_cu, bool pairs = false) {
   TilePlan best{};
   double best_t = 1e300;
   for (const TileShape& s : kTileShapes) {
-    if (s.wt != wt || K % s.kc) continue;
+    if (s.wt != wt || K % s.kc || (pairs && s.rbw % 2)) continue;
     const int bm = 32 * TG_WM * s.mtw, bn = 32 * s.rbw * s.wn;
     if (N % bn) continue;
     const long long tiles = (long long)((M + bm - 1) / bm) * (N / bn);

@@ -35,8 +35,7 @@ GROUPS = [
      r"tile_gemm_kernel<0,"),
     ("tile GEMM fp16 (stacked rows: lm_head)", r"tile_gemm_kernel<1,"),
     ("library GEMM (rocBLAS: prompt-sized ingest fc)", r"Cijk_"),
-    ("stacked-row epilogues (norm rows, RESID, SWIGLU)", r"afl_rows_kernel|resid_rows_kernel|swiglu_rows_kernel"),
-    ("row argmax (stacked lm_head)", r"row_argmax_kernel"),
+    ("RMSNorm rows (stacked blocks)", r"afl_rows_kernel"),
     ("block attention", r"block_attn_kernel"),
     ("attention merge", r"attn_merge_kernel"),
     ("qk norm + rope (context ingest, stacked blocks)", r"qk_rope_kernel"),

@@ -86,28 +86,39 @@ int main() {
                            {4096, 2048, 4096}, {65, 7168, 5120}, {96, 34816, 5120},
                            {200, 5120, 17408}, {100, 1024, 256}, {128, 512, 256}};
   for (const auto& sh : shapes)
-    for (int wt = 0; wt < 2; ++wt) {
-      const TilePlan tp = tile_plan(sh[0], sh[1], sh[2], wt, 256);
-      TileArgs ta{};
-      ta.W = (const uint4*)P; ta.X = (const half_t*)P; ta.Y = (float*)P;
-      ta.M = sh[0]; ta.N = sh[1]; ta.K = sh[2]; ta.ldy = sh[1];
-      char what[96];
-      std::snprintf(what, sizeof what, "tile plan %dx%dx%d wt %d", sh[0], sh[1], sh[2], wt);
-      expect(check_tile_args(wt, ta, tp), nullptr, what);
-      if (tile_lds_bytes(wt, tp) > 160 * 1024) expect("LDS", nullptr, what);
-    }
+    for (int wt = 0; wt < 2; ++wt)
+      for (int epi = 0; epi < 4; ++epi) {
+        if ((epi == TG_RESID || epi == TG_SWIGLU) && wt != WT_INT8) continue;
+        if (epi == TG_ARGMAX && wt != WT_F16) continue;
+        const TilePlan tp = tile_plan(sh[0], sh[1], sh[2], wt, 256, epi == TG_SWIGLU);
+        TileArgs ta{};
+        ta.W = (const uint4*)P; ta.X = (const half_t*)P; ta.Y = (float*)P;
+        ta.M = sh[0]; ta.N = sh[1]; ta.K = sh[2]; ta.ldy = sh[1];
+        ta.scale = (const half_t*)P; ta.x = (half_t*)P; ta.ss = (float*)P; ta.out = (half_t*)P;
+        ta.keys = (unsigned long long*)P;
+        char what[96];
+        std::snprintf(what, sizeof what, "tile plan %dx%dx%d wt %d epi %d", sh[0], sh[1], sh[2], wt, epi);
+        expect(check_tile_args(wt, epi, ta, tp), nullptr, what);
+        if (tile_lds_bytes(wt, tp) > 160 * 1024) expect("LDS", nullptr, what);
+      }
   {
     TileArgs ta{};
     ta.W = (const uint4*)P; ta.X = (const half_t*)P; ta.Y = (float*)P;
     ta.M = 256; ta.N = 4096; ta.K = 4096; ta.ldy = 4096;
     const TilePlan tp = tile_plan(256, 4096, 4096, WT_INT8, 256);
-    { TileArgs b = ta; b.K = 4000; expect(check_tile_args(WT_INT8, b, tp), "multiple of 64", "tile K"); }
-    { TileArgs b = ta; b.ldy = 100; expect(check_tile_args(WT_INT8, b, tp), "output row", "tile ldy"); }
-    { TileArgs b = ta; b.Y = nullptr; expect(check_tile_args(WT_INT8, b, tp), "null", "tile Y"); }
-    { TileArgs b = ta; b.M = 1000; expect(check_tile_args(WT_INT8, b, tp), "cover", "tile M"); }
-    { TilePlan q = tp; q.rbw = 3; expect(check_tile_args(WT_INT8, ta, q), "shape", "tile rbw"); }
-    { TilePlan q = tp; q.tiles_n += 1; expect(check_tile_args(WT_INT8, ta, q), "cover", "tile n"); }
-    { TileArgs b = ta; b.N = 4010; expect(check_tile_args(WT_INT8, b, tp), "multiple", "tile N"); }
+    { TileArgs b = ta; b.K = 4000; expect(check_tile_args(WT_INT8, TG_F32, b, tp), "multiple of 64", "tile K"); }
+    { TileArgs b = ta; b.ldy = 100; expect(check_tile_args(WT_INT8, TG_F32, b, tp), "output row", "tile ldy"); }
+    { TileArgs b = ta; b.Y = nullptr; expect(check_tile_args(WT_INT8, TG_F32, b, tp), "output", "tile Y"); }
+    { TileArgs b = ta; b.M = 1000; expect(check_tile_args(WT_INT8, TG_F32, b, tp), "cover", "tile M"); }
+    { TilePlan q = tp; q.rbw = 3; expect(check_tile_args(WT_INT8, TG_F32, ta, q), "shape", "tile rbw"); }
+    { TilePlan q = tp; q.tiles_n += 1; expect(check_tile_args(WT_INT8, TG_F32, ta, q), "cover", "tile n"); }
+    { TileArgs b = ta; b.N = 4010; expect(check_tile_args(WT_INT8, TG_F32, b, tp), "multiple", "tile N"); }
+    { expect(check_tile_args(WT_INT8, TG_RESID, ta, tp), "RESID", "tile resid args"); }
+    { expect(check_tile_args(WT_F16, TG_ARGMAX, ta, tp), "ARGMAX", "tile argmax keys"); }
+    { TileArgs b = ta; b.scale = (const half_t*)P; b.out = (half_t*)P;
+      TilePlan q = tp; q.rbw = 1;   // no gate|up pairs in a wave
+      expect(check_tile_args(WT_INT8, TG_SWIGLU, b, q), "pairs", "tile swiglu pairs"); }
+    { expect(check_tile_args(WT_INT8, 9, ta, tp), "epilogue", "tile epi"); }
   }
   if (fails == 0) std::printf("ok\n");
   return fails ? 1 : 0;
