@@ -31,10 +31,13 @@ GROUPS = [
     ("gate|up (SWIGLU, norm-on-load)", r"gsk_gemm_kernel<0, 1, true, 4>"),
     ("lm_head (fp16, ARGMAX, norm-on-load)", r"gsk_(gemm|dyn)_kernel<1, 2, true, 4>"),
     ("M-split stream-K (stacked rows up to 64)", r"gsk_gemm_m_kernel"),
-    ("tile GEMM int8 (stacked rows: qkv, o, gate|up, down; prompt-sized ingest K|V)",
-     r"tile_gemm_kernel<0,"),
-    ("tile GEMM fp16 (stacked rows: lm_head)", r"tile_gemm_kernel<1,"),
+    ("tile GEMM int8, fp32 rows (stacked qkv; prompt-sized ingest K|V)", r"tile_gemm_kernel<0, 0,"),
+    ("tile GEMM int8, RESID (stacked o, down)", r"tile_gemm_kernel<0, 1,"),
+    ("tile GEMM int8, SWIGLU (stacked gate|up)", r"tile_gemm_kernel<0, 2,"),
+    ("tile GEMM fp16, ARGMAX (stacked lm_head)", r"tile_gemm_kernel<1, 3,"),
+    ("argmax of the partial keys (stacked lm_head)", r"argmax_parts_kernel"),
     ("library GEMM (rocBLAS: prompt-sized ingest fc)", r"Cijk_"),
+    ("fc rows: fp16 rounding + hidden_norm (prompt-sized ingest)", r"fc_norm_rows_kernel"),
     ("RMSNorm rows (stacked blocks)", r"afl_rows_kernel"),
     ("block attention", r"block_attn_kernel"),
     ("attention merge", r"attn_merge_kernel"),
