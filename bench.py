@@ -182,8 +182,10 @@ def run_workload(wl, args, sweep, want_cpu):
     torch.manual_seed(args.seed)
     t_setup = time.perf_counter()
     n_seq = len(wl.seq_ctx) if batched else 1
+    # room for the swept contexts and for the rows the decode-loop steps append
+    steady_rows = 0 if batched or not args.steady else (args.warmup + args.steps) * 32
     model, host = build_model(wl, args.seed, keep_host=want_cpu,
-                              max_ctx=max([wl.ctx] + sweep), max_seqs=n_seq)
+                              max_ctx=max([wl.ctx + steady_rows] + sweep), max_seqs=n_seq)
     if batched:
         seq_inp = [synth.make_inputs_torch(cfg, wl.block, c, seed=args.seed + 1 + i, device="cuda")
                    for i, c in enumerate(wl.seq_ctx)]

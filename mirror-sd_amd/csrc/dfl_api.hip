@@ -161,8 +161,13 @@ struct dfl_ctx {
   half_t* si_in = nullptr;    // [SMALL_ING/32][32][max(NF,1)*H] fragment-layout input rows
   half_t* si_fc = nullptr;    // [SMALL_ING][H] fc rows (fp16)
   half_t* si_xn = nullptr;    // [SMALL_ING/32][32][H] fragment-layout hidden_norm rows
-  half_t* si_kv = nullptr;    // [SMALL_ING][2*NKV*128] K|V rows (fp16, scaled)
-  SKPlan sk_fc, sk_kv;
+  half_t* si_kv = nullptr;    // [SMALL_ING][NL*2*NKV*128] K|V rows of every layer (fp16, scaled)
+  // the K|V rows of every layer side by side ([NL*2*NKV*128][H] packed int8 + scales), so
+  // that one launch projects a per-step ingest's rows for all layers (a copy of 2*NKV*128
+  // of each layer's NQKV qkv rows)
+  uint4* w_kv_all = nullptr;
+  half_t* s_kv_all = nullptr;
+  SKPlan sk_fc;
   std::vector<void*> allocs;
   int prof = 0;   // 0 off, 1 every kernel group, 2 stream-K GEMM launches only
   std::vector<ProfRec> recs;
@@ -269,7 +274,9 @@ static int setup_ingest(dfl_ctx* x) {
   if ((r = x->alloc(&x->si_in, (size_t)SMALL_ING * std::max(x->NF, 1) * H, true)) ||
       (r = x->alloc(&x->si_fc, (size_t)SMALL_ING * H)) ||
       (r = x->alloc(&x->si_xn, (size_t)SMALL_ING * H, true)) ||
-      (r = x->alloc(&x->si_kv, (size_t)SMALL_ING * Nkv)))
+      (r = x->alloc(&x->si_kv, (size_t)SMALL_ING * x->NL * Nkv)) ||
+      (r = x->alloc(&x->w_kv_all, (size_t)x->NL * Nkv * H / 16)) ||
+      (r = x->alloc(&x->s_kv_all, (size_t)x->NL * Nkv)))
     return r;
   if ((r = x->alloc(&x->xn, (size_t)x->ing * H))) return r;
   if (x->NF > 0 && (r = x->alloc(&x->fc32, (size_t)x->ing * H))) return r;
@@ -363,12 +370,16 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
     x->sk_down = plan(x->H, x->F / 32);
     x->sk_lm = streamk_plan_balanced(std::max(x->V, 64), x->H / 16, x->n_cu);
     x->sk_fc = streamk_plan(x->H, std::max(x->NF, 1) * x->H / 16, x->n_cu);
-    x->sk_kv = plan(2 * x->NKV * 128, x->H / 32);
+    std::vector<std::pair<SKPlan, int>> plans = {
+        {x->sk_qkv, x->NQKV}, {x->sk_o, x->H}, {x->sk_gu, 2 * x->F}, {x->sk_down, x->H},
+        {x->sk_lm, std::max(x->V, 64)}, {x->sk_fc, x->H}};
+    // the per-step ingest's K|V rows of the first `active` layers, any active count
+    for (int nl = 1; nl <= x->NL; ++nl) {
+      const int n = nl * 2 * x->NKV * 128;
+      plans.push_back({plan(n, x->H / 32), n});
+    }
     size_t wsn = 0, tiles = 0;
-    for (auto pr : {std::make_pair(x->sk_qkv, x->NQKV), std::make_pair(x->sk_o, x->H),
-                    std::make_pair(x->sk_gu, 2 * x->F), std::make_pair(x->sk_down, x->H),
-                    std::make_pair(x->sk_lm, std::max(x->V, 64)), std::make_pair(x->sk_fc, x->H),
-                    std::make_pair(x->sk_kv, 2 * x->NKV * 128)}) {
+    for (const auto& pr : plans) {
       wsn = std::max(wsn, (size_t)(pr.second / 64) *
                               std::max(pr.first.seg_cap, pr.first.sk_seg_cap) * 2048);
       tiles = std::max(tiles, (size_t)(pr.second / 64));
@@ -459,6 +470,11 @@ int dfl_load_layer_w8(dfl_ctx* ctx, int layer, const int8_t* const q[7],
   launch_pack_i8(q[4], S(4), F, H, L.w_gu, L.s_gu, 0, 2, st);
   launch_pack_i8(q[5], S(5), F, H, L.w_gu, L.s_gu, 1, 2, st);
   launch_pack_i8(q[6], S(6), H, F, L.w_down, L.s_down, 0, 1, st);
+  // the k|v rows again in the all-layer matrix (row-blocks of layer l at l * 2*NKV*4)
+  launch_pack_i8(q[1], S(1), NKV * 128, H, ctx->w_kv_all, ctx->s_kv_all, layer * 2 * NKV * 4, 1,
+                 st);
+  launch_pack_i8(q[2], S(2), NKV * 128, H, ctx->w_kv_all, ctx->s_kv_all,
+                 layer * 2 * NKV * 4 + NKV * 4, 1, st);
   DFL_HIP(hipMemcpyAsync(L.in_norm, in_norm, H * 2, hipMemcpyDeviceToDevice, st));
   DFL_HIP(hipMemcpyAsync(L.post_norm, post_norm, H * 2, hipMemcpyDeviceToDevice, st));
   DFL_HIP(hipMemcpyAsync(L.q_norm, q_norm, 256, hipMemcpyDeviceToDevice, st));
@@ -715,31 +731,37 @@ static int ingest_small(dfl_ctx* ctx, const half_t* in, int C, bool fused, const
     launch_rows_norm_afl(ctx->si_fc, H, C, H, ctx->hidden_norm, ctx->cfg.rms_eps, ctx->si_xn, st);
     xsrc = ctx->si_xn;
   }
+  // the K|V rows of all active layers in one GEMM (the all-layer matrix), then k_norm + RoPE
+  // and the cache writes for up to SEQ_MAX layers per launch
   const int KB = H / 32;
-  for (int l = 0; l < ctx->active; ++l) {
-    Layer& L = ctx->layers[l];
-    // the K|V rows start at packed row-block NH*128/32 of the qkv matrix
-    const uint4* w_kv = L.w_qkv + (size_t)(NH * 128 / 32) * KB * 64;
-    DFL_TRY(skgemm(ctx, P_INGEST_KV, WT_INT8, EPI_STORE, ctx->sk_kv, w_kv, L.s_qkv + NH * 128,
-                   Nkv, KB, xsrc, H, C, nullptr, false, ctx->si_kv, Nkv, nullptr, nullptr,
-                   nullptr, st));
+  const int Nall = ctx->active * Nkv;
+  DFL_TRY(skgemm(ctx, P_INGEST_KV, WT_INT8, EPI_STORE, streamk_plan(Nall, KB, ctx->n_cu),
+                 ctx->w_kv_all, ctx->s_kv_all, Nall, KB, xsrc, H, C, nullptr, false, ctx->si_kv,
+                 Nall, nullptr, nullptr, nullptr, st));
+  for (int l0 = 0; l0 < ctx->active; l0 += SEQ_MAX) {
+    const int nl = std::min(SEQ_MAX, ctx->active - l0);
     QKRopeArgs q{};
-    q.qkv16 = ctx->si_kv;
+    q.qkv16 = ctx->si_kv + (size_t)l0 * Nkv;
     q.M = C;
-    q.N = Nkv;
-    q.n_seq = 1;
+    q.N = Nall;
+    q.n_seq = nl;
+    q.layer_cols = Nkv;
     q.col_slot0 = NH;
     q.slot0 = NH;
     q.n_slots = 2 * NKV;
     q.NH = NH;
     q.NKV = NKV;
-    q.q_norm = L.q_norm;
-    q.k_norm = L.k_norm;
+    q.q_norm = ctx->layers[l0].q_norm;
+    q.k_norm = ctx->layers[l0].k_norm;
     q.eps = ctx->cfg.rms_eps;
     q.log2_theta = std::log2(ctx->cfg.rope_theta);
     q.Q = nullptr;
     q.cap = ctx->cap;
-    rope_seq(ctx, ctx->cur, L, ctx->sq().offset, C, q.sq[0]);
+    for (int i = 0; i < nl; ++i) {
+      const Layer& L = ctx->layers[l0 + i];
+      q.k_norm_s[i] = L.k_norm;
+      rope_seq(ctx, ctx->cur, L, ctx->sq().offset, C, q.sq[i]);
+    }
     ProfScope ps(ctx, P_INGEST_KV, 0, st);
     DFL_TRY(qk_rope(q, st));
   }

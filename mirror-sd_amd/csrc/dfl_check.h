@@ -70,7 +70,16 @@ inline const char* check_qk_rope_args(const QKRopeArgs& a) {
   if (a.NH < 1 || a.NKV < 1 || a.n_slots < 1 || a.slot0 < a.col_slot0 ||
       a.slot0 + a.n_slots > a.NH + 2 * a.NKV)
     return "head slots outside the q|k|v heads";
-  if ((long long)(a.slot0 + a.n_slots - a.col_slot0) * 128 > a.N) return "slots past the row width";
+  if (a.layer_cols) {
+    if (a.qkv32 || a.slot0 < a.NH) return "layer mode takes fp16 K|V rows only";
+    if ((long long)(a.slot0 + a.n_slots - a.col_slot0) * 128 > a.layer_cols ||
+        (long long)a.n_seq * a.layer_cols > a.N)
+      return "slots past the row width";
+    for (int s = 0; s < a.n_seq; ++s)
+      if (!a.k_norm_s[s]) return "layer mode without a per-layer k_norm";
+  } else if ((long long)(a.slot0 + a.n_slots - a.col_slot0) * 128 > a.N) {
+    return "slots past the row width";
+  }
   if (a.slot0 < a.NH && !a.Q) return "Q slots without a Q output";
   if (!a.q_norm || !a.k_norm || a.cap < 1) return "missing norms or cache capacity";
   if (a.slot0 + a.n_slots > a.NH)

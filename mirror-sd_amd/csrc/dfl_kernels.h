@@ -214,6 +214,11 @@ struct QKRopeArgs {
   half_t* Q;
   int cap;
   RopeSeq sq[SEQ_MAX];
+  // layer mode (layer_cols > 0): the entries are layers of one sequence sharing the rows;
+  // entry s reads columns [s * layer_cols, ...) of each row (N is the row stride) and uses
+  // the k_norm gain k_norm_s[s]
+  int layer_cols;
+  const half_t* k_norm_s[SEQ_MAX];
 };
 // -1: a ring row that a later row of the same launch overwrites (more than ring_W ring
 // rows appended at once keep only the newest ring_W), so it is not written at all

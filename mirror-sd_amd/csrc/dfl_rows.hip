@@ -265,8 +265,8 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(QKRopeArgs a) {
   const int m = (int)(pr / a.n_slots);
   const int slot = a.slot0 + (int)(pr - (long long)m * a.n_slots);
   const RopeSeq& sq = a.sq[sidx];
-  const size_t row = (size_t)sidx * a.M + m;
-  const int c0 = (slot - a.col_slot0) * 128 + lane;
+  const size_t row = a.layer_cols ? (size_t)m : (size_t)sidx * a.M + m;
+  const int c0 = (a.layer_cols ? sidx * a.layer_cols : 0) + (slot - a.col_slot0) * 128 + lane;
   const int crow = slot >= a.NH ? cache_slot(sq, a.M, m) : 0;
   if (crow < 0) return;   // whole wave: one (row, head slot) per wave
   // projections scaled and rounded to fp16 (Linear output): by the GEMM epilogue (qkv16),
@@ -288,7 +288,7 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(QKRopeArgs a) {
     return;
   }
   const bool is_q = slot < a.NH;
-  const half_t* gn = is_q ? a.q_norm : a.k_norm;
+  const half_t* gn = is_q ? a.q_norm : (a.layer_cols ? a.k_norm_s[sidx] : a.k_norm);
   const float ss = wave_sum(v0 * v0 + v1 * v1);
   const float r = 1.0f / sqrtf(ss * (1.0f / 128.0f) + a.eps);
   const float y0 = h2f(rms_out(v0, r, gn[lane]));

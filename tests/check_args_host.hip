@@ -65,6 +65,16 @@ int main() {
   { QKRopeArgs b = q; b.n_seq = 9; expect(check_qk_rope_args(b), "range", "n_seq"); }
   { QKRopeArgs b = q; b.sq[0].Kc = nullptr; expect(check_qk_rope_args(b), "cache", "cache"); }
   { QKRopeArgs b = q; b.Q = nullptr; b.col_slot0 = 40; b.slot0 = 40; b.n_slots = 16; b.N = 2048; expect(check_qk_rope_args(b), nullptr, "valid K|V only"); }
+  {   // layer mode: 5 layers' K|V rows side by side
+    QKRopeArgs b = q; b.Q = nullptr; b.col_slot0 = 40; b.slot0 = 40; b.n_slots = 16; b.N = 5 * 2048;
+    b.n_seq = 5; b.layer_cols = 2048;
+    for (int i = 0; i < 5; ++i) { b.k_norm_s[i] = (const half_t*)P; b.sq[i].Kc = (half_t*)P; b.sq[i].Vt = (half_t*)P; }
+    expect(check_qk_rope_args(b), nullptr, "valid layer mode");
+    { QKRopeArgs c = b; c.N = 4 * 2048; expect(check_qk_rope_args(c), "row width", "layer mode width"); }
+    { QKRopeArgs c = b; c.k_norm_s[3] = nullptr; expect(check_qk_rope_args(c), "k_norm", "layer mode norm"); }
+    { QKRopeArgs c = b; c.slot0 = 0; c.col_slot0 = 0; c.n_slots = 56; c.Q = (half_t*)P;
+      expect(check_qk_rope_args(c), "K|V rows only", "layer mode Q"); }
+  }
 
   AttnArgs t{};
   t.Q = (const half_t*)P; t.B = 32; t.NH = 40; t.NKV = 8; t.cap = 4128; t.n_seq = 1;
