@@ -41,8 +41,9 @@ def _oracle_both(W, inp):
                                        ((5, 9, 2, 30, 12, 7, 1, 18, 22, 3), 8)])  # 80 rows
 def test_batch_small_matches_oracle_and_single_sequence(seq_ctx, B):
     """Stacked rows below one m-tile (stream-K GEMMs throughout), and 80, 128 and 192 rows
-    (library GEMMs for qkv / o / gate|up / lm_head, M-split stream-K for down); 10
-    sequences take two rope / attention launches (8 + 2)."""
+    (tile GEMMs with fused RESID / SWIGLU / ARGMAX epilogues; 80 rows leave a partial
+    m-tile whose rows the epilogues must skip); 10 sequences take two rope / attention
+    launches (8 + 2)."""
     from mirror_sd_amd.dflash import DFlashDraftModel
     wl = workload("tiny")
     cfg = wl.cfg
@@ -64,7 +65,7 @@ def test_batch_small_matches_oracle_and_single_sequence(seq_ctx, B):
         check_argmax(ids[i], logits[i], ids_ref, ids64, f"batch {seq_ctx} sequence {i}", ti, tv,
                      LOGIT_TOL)
     # the same sequences drafted one at a time through the single-sequence entry point
-    # (stream-K GEMMs; the stacked path above may use library GEMMs, so the two agree to
+    # (stream-K GEMMs; the stacked path above may use tile GEMMs, so the two agree to
     # fp32 summation order: hidden within 1e-5 of cosine, ids as against the oracle)
     for i, inp in enumerate(inps):
         m.select_seq(i)

@@ -182,6 +182,35 @@ def test_qwen3_8b_shape_one_layer_matches_oracle():
                  ti, np.take_along_axis(logits_ref, ti, -1))
 
 
+@pytest.mark.parametrize("ctx", [24, 100])
+def test_fewer_draft_layers_match_oracle(ctx):
+    """num_draft_layers = 1 of 2 (dflash.py:382): the context ingest projects the K|V rows of
+    the active layers only (one all-layer launch up to 64 rows, the tile GEMM per layer
+    above), and the draft runs one layer before the final norm and lm_head."""
+    cfg = workload("tiny").cfg.copy()
+    t = synth.make_weights_numpy(cfg, seed=5)
+    inp = synth.make_inputs_numpy(cfg, 8, ctx, seed=5)
+    cfg1 = cfg.copy()
+    cfg1.num_hidden_layers = 1
+    W = O.OracleWeights(cfg1, t)
+    h_ref, logits_ref, ids_ref = O.draft_block(W, inp["ids"], inp["target_hidden"], fp16=True,
+                                               dtype=np.float32)
+    _, _, ids64 = O.draft_block(W, inp["ids"], inp["target_hidden"], fp16=True)
+    m = _model(cfg, max_ctx=ctx)
+    m.load_weights(torch_tensors(t, "cuda"))
+    m.num_draft_layers = 1
+    ids, logits, h = m.draft(torch.from_numpy(inp["ids"]), torch.from_numpy(inp["target_hidden"]),
+                             return_logits=True, return_hidden=True)
+    torch.cuda.synchronize()
+    assert_close_fp16(h.float().cpu().numpy(), h_ref, what=f"one of two layers, ctx {ctx}")
+    lg = logits.cpu().numpy()
+    assert np.abs(lg - logits_ref).max() < 5e-2
+    ti = np.argsort(-logits_ref, axis=-1, kind="stable")[:, :2]
+    check_argmax(ids.cpu().numpy(), lg, ids_ref, ids64, f"one of two layers, ctx {ctx}", ti,
+                 np.take_along_axis(logits_ref, ti, -1), 5e-2)
+    m.close()
+
+
 def test_bad_token_id_rejected():
     wl, cfg, t, inp, W = _full_case("tiny")
     m = _model(cfg, max_ctx=wl.ctx)
