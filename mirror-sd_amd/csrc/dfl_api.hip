@@ -127,6 +127,8 @@ struct dfl_ctx {
   half_t* final_norm = nullptr;
   uint4* w_lm = nullptr;
   float* y32 = nullptr;      // [RM][max(NQKV, H, 2F)] fp32 rows of the stacked-block GEMMs
+  float* tile_ws = nullptr;  // split-K planes of the stacked-block tile GEMMs
+  size_t tile_ws_floats = 0;
   unsigned long long* lm_parts = nullptr;   // [V/32][RM] stacked lm_head argmax partial keys
   const half_t* embed = nullptr;
   bool head_loaded = false;
@@ -407,10 +409,22 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
     delete x;
     return r;
   }
-  if (x->RM > STACK_MIN_ROWS &&
-      (r = x->alloc(&x->y32, (size_t)x->RM * std::max({x->NQKV, x->H, 2 * x->F})))) {
-    delete x;
-    return r;
+  if (x->RM > STACK_MIN_ROWS) {
+    // split-K planes: the largest plan of the stacked qkv / o / down products over every
+    // row count up to RM
+    for (int M = 32; M <= ((x->RM + 31) / 32) * 32; M += 32)
+      for (auto nk : {std::make_pair(x->NQKV, x->H), std::make_pair(x->H, x->NH * 128),
+                      std::make_pair(x->H, x->F)}) {
+        const TilePlan p = tile_plan(std::min(M, x->RM), nk.first, nk.second, WT_INT8, x->n_cu,
+                                     false, true);
+        x->tile_ws_floats =
+            std::max(x->tile_ws_floats, (size_t)p.splits * std::min(M, x->RM) * nk.first);
+      }
+    if ((r = x->alloc(&x->y32, (size_t)x->RM * std::max({x->NQKV, x->H, 2 * x->F}))) ||
+        (r = x->alloc(&x->tile_ws, x->tile_ws_floats))) {
+      delete x;
+      return r;
+    }
   }
   *out = x;
   return DFL_OK;
@@ -609,11 +623,16 @@ static int block_attention(const AttnArgs& at, hipStream_t st) {
 
 // Tile GEMM of more than STACK_MIN_ROWS rows (X in the fragment layout) with epilogue epi
 // (the TileArgs outputs e), its argument checks reported as DFL_EINVAL.
+// Split-K (F32 and RESID epilogues of stacked blocks, when the plan finds it faster): the
+// GEMM writes fp32 planes into tile_ws and launch_tile_reduce applies the epilogue.
 // n_parts (ARGMAX): receives the number of partial key rows written (one per wave column).
 static int tgemm(dfl_ctx* ctx, int cat, int wt, int epi, const uint4* W, int N, int K,
                  const half_t* X, int M, const TileArgs& e, hipStream_t st,
                  int* n_parts = nullptr) {
-  const TilePlan p = tile_plan(M, N, K, wt, ctx->n_cu, epi == TG_SWIGLU);
+  const bool split_ok = (epi == TG_F32 || epi == TG_RESID) && ctx->tile_ws && M <= ctx->RM;
+  TilePlan p = tile_plan(M, N, K, wt, ctx->n_cu, epi == TG_SWIGLU, split_ok);
+  if (p.splits > 1 && (size_t)p.splits * M * N > ctx->tile_ws_floats)
+    p = tile_plan(M, N, K, wt, ctx->n_cu, epi == TG_SWIGLU);   // planes do not fit: no split
   if (n_parts) *n_parts = N / (32 * p.rbw);
   TileArgs a = e;
   a.W = W;
@@ -621,14 +640,32 @@ static int tgemm(dfl_ctx* ctx, int cat, int wt, int epi, const uint4* W, int N, 
   a.K = K;
   a.X = X;
   a.M = M;
-  if (const char* why = check_tile_args(wt, epi, a, p))
+  TileArgs g = a;   // the GEMM's own arguments: F32 planes when split
+  if (p.splits > 1) {
+    g = TileArgs{};
+    g.W = W;
+    g.N = N;
+    g.K = K;
+    g.X = X;
+    g.M = M;
+    g.Y = ctx->tile_ws;
+    g.ldy = N;
+  }
+  const int gepi = p.splits > 1 ? TG_F32 : epi;
+  if (const char* why = check_tile_args(wt, gepi, g, p))
     return fail(DFL_EINVAL, std::string("tile GEMM launch refused: ") + why);
+  if (p.splits > 1)
+    if (const char* why = check_tile_reduce_args(epi, a, ctx->tile_ws, p.splits))
+      return fail(DFL_EINVAL, std::string("tile GEMM reduction refused: ") + why);
   if (tile_lds_bytes(wt, p) > (size_t)ctx->lds_max)
     return fail(DFL_EINVAL, "tile GEMM: the device's LDS per workgroup is too small");
   const long long wbytes = (long long)N * K * (wt == WT_INT8 ? 1 : 2);
+  // the attached events span the GEMM and, when split, its reduction
   ProfScope ps(ctx, cat, wbytes, st, /*attached=*/true);
-  if (!launch_tile_gemm(wt, epi, a, p, st, ps.start(), ps.stop()))
+  if (!launch_tile_gemm(wt, gepi, g, p, st, ps.start(), p.splits > 1 ? nullptr : ps.stop()))
     return fail(DFL_EINVAL, "no tile GEMM kernel for this shape and epilogue");
+  if (p.splits > 1 && !launch_tile_reduce(epi, a, ctx->tile_ws, p.splits, st, ps.stop()))
+    return fail(DFL_EINVAL, "tile GEMM reduction refused");
   return DFL_OK;
 }
 static TileArgs tile_f32(float* Y, int ldy) {

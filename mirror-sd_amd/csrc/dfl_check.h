@@ -135,7 +135,23 @@ inline const char* check_tile_args(int wt, int epi, const TileArgs& a, const Til
   if (p.tiles_n != a.N / (32 * p.rbw * p.wn) || (long long)p.tiles_m * 128 * p.mtw < a.M ||
       (long long)p.tiles_m * 128 * p.mtw >= (long long)a.M + 128 * p.mtw)
     return "tile counts do not cover the product";
-  if ((long long)p.tiles_m * p.tiles_n > 0x7fffffffLL) return "too many tiles";
+  if (p.splits < 1 || p.splits > a.K / 64) return "split-K factor outside [1, K/64]";
+  if (p.splits > 1 && epi != TG_F32) return "split-K writes F32 planes only";
+  if ((long long)p.tiles_m * p.tiles_n * p.splits > 0x7fffffffLL) return "too many tiles";
+  return nullptr;
+}
+
+inline const char* check_tile_reduce_args(int epi, const TileArgs& a, const float* parts,
+                                          int splits) {
+  if (!parts || splits < 1) return "no split-K planes";
+  if (a.M < 1 || a.N < 64 || a.N % 64) return "N must be a positive multiple of 64";
+  if (epi == TG_F32) {
+    if (!a.Y || a.ldy < a.N) return "F32 reduction without an output of N columns";
+  } else if (epi == TG_RESID) {
+    if (!a.x || !a.ss || !a.scale) return "RESID reduction needs x, row sums and scales";
+  } else {
+    return "the reduction has F32 and RESID epilogues only";
+  }
   return nullptr;
 }
 

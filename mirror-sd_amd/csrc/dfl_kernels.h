@@ -120,6 +120,7 @@ struct TileArgs {
                             // order(value) << 32 | ~index, 0 = none), reduced by
                             // launch_argmax_parts
   int tiles_m, tiles_n;     // set by the launcher from the plan
+  int splits;               // split-K: F32 sums of split s into plane s of Y ([splits][M][ldy])
 };
 struct TilePlan {
   int mtw = 0;              // m-tiles per wave: 1 (128-row workgroup tile) or 2 (256 rows)
@@ -127,8 +128,14 @@ struct TilePlan {
   int wn = 0;               // wave columns: 1 (4 waves) or 2 (8 waves)
   int kc = 0;               // k per LDS stage: 32 or 64
   int tiles_m = 0, tiles_n = 0;
+  int splits = 1;           // split-K factor (F32 planes, then launch_tile_reduce)
 };
 // (tile_plan / tile_lds_bytes: dfl_tile_plan.h)
+// The split-K planes parts [splits][M][N] summed in plane order, with epilogue TG_F32 (into
+// a.Y, row stride a.ldy) or TG_RESID (a.x, a.ss, a.scale as the RESID epilogue).  Returns
+// false (and launches nothing) when the arguments fail check_tile_reduce_args.
+bool launch_tile_reduce(int epi, const TileArgs& a, const float* parts, int splits,
+                        hipStream_t st, hipEvent_t ev_stop = nullptr);
 // Returns false (and launches nothing) when the arguments fail check_tile_args.
 // ev_start / ev_stop (optional) receive the kernel's own start and end timestamps.
 bool launch_tile_gemm(int wt, int epi, const TileArgs& a, const TilePlan& p, hipStream_t st,

@@ -174,13 +174,22 @@ __global__ __launch_bounds__(64 * (TG_WM * WN + (tile_loader(WN) ? 1 : 0))) void
   // then run on one XCD and share its L2.
   const int G = gridDim.x;
   const int b = blockIdx.x;
-  const int tile = (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
+  const int gt = (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
+  // split-K (a.splits > 1): workgroup gt takes k-split gt / tiles of tile gt % tiles (the
+  // workgroups of one split, which read the same X k-slice, neighbour each other) and writes
+  // its fp32 sums into plane split of Y (reduced by tile_reduce_kernel)
+  const int tiles = a.tiles_m * a.tiles_n;
+  const int sp = gt / tiles;
+  const int tile = gt - sp * tiles;
   const int tm = tile / a.tiles_n;
   const int tn = tile - tm * a.tiles_n;
   const int mt0 = tm * S::MT;                  // first m-tile of this workgroup
   const int nb0 = tn * S::RB;                  // first weight row-block
   const int K = a.K;
-  const int nst = K / KC;
+  // this split's stages [st0, st0 + nst), in whole 64-k steps (an even number of k-blocks)
+  const int npair = K / 64;
+  const int st0 = (int)((long long)sp * npair / a.splits) * (64 / KC);
+  const int nst = (int)((long long)(sp + 1) * npair / a.splits) * (64 / KC) - st0;
   const int MTt = (a.M + 31) >> 5;             // m-tiles present in X
   const int KBW = WT == WT_INT8 ? K / 32 : K / 16;   // weight blocks per row-block
 
@@ -188,8 +197,9 @@ __global__ __launch_bounds__(64 * (TG_WM * WN + (tile_loader(WN) ? 1 : 0))) void
   // compute wave i % NW
   constexpr int ISSUERS = S::LOADER ? 1 : S::NW;
   const int iw = S::LOADER ? 0 : wv;
-  auto issue_stage = [&](int s) __attribute__((always_inline)) {
-    unsigned char* buf = tg_lds + (s % S::STAGES) * S::STAGE;
+  auto issue_stage = [&](int ls) __attribute__((always_inline)) {
+    unsigned char* buf = tg_lds + (ls % S::STAGES) * S::STAGE;
+    const int s = st0 + ls;   // stage of K
 #pragma unroll
     for (int j = 0; j < (S::IPS + ISSUERS - 1) / ISSUERS; ++j) {
       const int i = iw + ISSUERS * j;
@@ -240,8 +250,8 @@ __global__ __launch_bounds__(64 * (TG_WM * WN + (tile_loader(WN) ? 1 : 0))) void
     if (S::STAGES - 2 < nst) issue_stage(S::STAGES - 2);
   }
 
-  // k-blocks u = 0 .. nkb-1 (stage u / KBS); f0 / f1 alternate
-  const int nkb = K / 32;
+  // k-blocks u = 0 .. nkb-1 of this split (local stage u / KBS); f0 / f1 alternate
+  const int nkb = nst * S::KBS;
   TgFrag<WT, MTW, RBW> f0, f1;
   tg_read_frags<S>(f0, tg_lds, 0, wm, wn, lane);
   // before reading k-block u + 1: a new stage needs B(stage - 1) and refills
@@ -256,7 +266,7 @@ __global__ __launch_bounds__(64 * (TG_WM * WN + (tile_loader(WN) ? 1 : 0))) void
     }
     tg_read_frags<S>(f, tg_lds + (sv % S::STAGES) * S::STAGE, v % S::KBS, wm, wn, lane);
   };
-  for (int u = 0; u < nkb; u += 2) {   // nkb is even (K % 64 == 0)
+  for (int u = 0; u < nkb; u += 2) {   // nkb is even (whole 64-k steps)
     next(u, f1);
     tg_mfma<WT, MTW, RBW, S::NACC>(f0, acc);
     if (u + 2 < nkb) next(u + 1, f0);
@@ -279,9 +289,10 @@ __global__ __launch_bounds__(64 * (TG_WM * WN + (tile_loader(WN) ? 1 : 0))) void
   };
   if constexpr (EPI == TG_F32 || EPI == TG_ARGMAX) {
     if (a.Y) {
+      float* yplane = a.Y + (size_t)sp * a.M * a.ldy;
       static_for<0, MTW>([&](auto t) {
         static_for<0, RBW>([&](auto r) {
-          float* yc = a.Y + n_lane + 32 * r;
+          float* yc = yplane + n_lane + 32 * r;
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             const int m = row_of(t, i);
@@ -381,8 +392,8 @@ __global__ __launch_bounds__(64 * (TG_WM * WN + (tile_loader(WN) ? 1 : 0))) void
 template <int WT, int EPI, int MTW, int RBW, int WN, int KC>
 void launch_tile(const TileArgs& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   using S = TgShape<WT, MTW, RBW, WN, KC>;
-  const dim3 grid(a.tiles_m * a.tiles_n), block(64 * (S::NW + (S::LOADER ? 1 : 0)));
-  if (e0 && e1)
+  const dim3 grid(a.tiles_m * a.tiles_n * a.splits), block(64 * (S::NW + (S::LOADER ? 1 : 0)));
+  if (e0 || e1)
     hipExtLaunchKernelGGL((tile_gemm_kernel<WT, EPI, MTW, RBW, WN, KC>), grid, block, S::LDS, st,
                           e0, e1, 0, a);
   else
@@ -426,12 +437,58 @@ bool launch_shape_i(int wt, int epi, const TileArgs& a, const TilePlan& p, hipSt
 
 }  // namespace
 
+namespace {
+
+// Sum of the split-K planes y[s][M][N] (s < S, fixed order) with the epilogue: TG_F32 into
+// out_y [M][N], or TG_RESID (x += fp16(sum * scale), row sums of squares per 32 columns).
+// One thread per column of a row; a wave covers 64 columns (two 32-column tiles).
+__global__ __launch_bounds__(256) void tile_reduce_kernel(TileArgs a, const float* __restrict__ y,
+                                                          int S, int epi) {
+  const int lane = threadIdx.x & 63;
+  const long long w = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int wpr = a.N >> 6;   // waves per row
+  if (w >= (long long)a.M * wpr) return;
+  const int m = (int)(w / wpr);
+  const int n = (int)(w - (long long)m * wpr) * 64 + lane;
+  const size_t plane = (size_t)a.M * a.N;
+  const float* src = y + (size_t)m * a.N + n;
+  float v = src[0];
+  for (int s = 1; s < S; ++s) v += src[s * plane];
+  if (epi == TG_F32) {
+    a.Y[(size_t)m * a.ldy + n] = v;
+    return;
+  }
+  half_t* xp = a.x + afl_index(m, n, a.N);
+  const half_t xn = f2h(h2f(*xp) + h2f(f2h(v * h2f(a.scale[n]))));
+  *xp = xn;
+  float sq = h2f(xn) * h2f(xn);
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) sq += __shfl_xor(sq, o, 64);
+  if ((lane & 31) == 0) a.ss[((size_t)(m >> 5) * (a.N >> 5) + (n >> 5)) * 32 + (m & 31)] = sq;
+}
+
+}  // namespace
+
+bool launch_tile_reduce(int epi, const TileArgs& a, const float* parts, int splits,
+                        hipStream_t st, hipEvent_t ev_stop) {
+  if (check_tile_reduce_args(epi, a, parts, splits)) return false;
+  const long long waves = (long long)a.M * (a.N / 64);
+  const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+  if (ev_stop)
+    hipExtLaunchKernelGGL(tile_reduce_kernel, grid, block, 0, st, nullptr, ev_stop, 0, a, parts,
+                          splits, epi);
+  else
+    hipLaunchKernelGGL(tile_reduce_kernel, grid, block, 0, st, a, parts, splits, epi);
+  return true;
+}
+
 bool launch_tile_gemm(int wt, int epi, const TileArgs& a0, const TilePlan& p, hipStream_t st,
                       hipEvent_t ev_start, hipEvent_t ev_stop) {
   if (check_tile_args(wt, epi, a0, p)) return false;
   TileArgs a = a0;
   a.tiles_m = p.tiles_m;
   a.tiles_n = p.tiles_n;
+  a.splits = p.splits;
   return launch_shape_i<0>(wt, epi, a, p, st, ev_start, ev_stop);
 }
 

@@ -61,10 +61,14 @@ inline double tile_kblock_cycles(const TileShape& s) {
   return std::max(mfma, bytes / 24.0);
 }
 
-// The instantiated shape with the least estimated time: rounds of one workgroup per CU x
-// k-blocks x cycles per k-block.  pairs: each wave must hold gate|up row-block pairs
-// (SWIGLU), i.e. an even rbw.
-inline TilePlan tile_plan(int M, int N, int K, int wt, int n_cu, bool pairs = false) {
+// The instantiated shape (and split-K factor) with the least estimated time, in cycles of
+// 2.4 GHz: rounds of one workgroup per CU x k-blocks x cycles per k-block.  A split-K
+// (allowed with split) runs fewer k-blocks per workgroup on larger tiles, so less X per
+// flop, but each workgroup writes its fp32 tile (at about 21 B per cycle) and a reduction
+// launch reads every plane (at about 2 KB per cycle over the chip, plus 3 us).  pairs:
+// each wave must hold gate|up row-block pairs (SWIGLU), i.e. an even rbw.
+inline TilePlan tile_plan(int M, int N, int K, int wt, int n_cu, bool pairs = false,
+                          bool split = false) {
   TilePlan best{};
   double best_t = 1e300;
   for (const TileShape& s : kTileShapes) {
@@ -72,16 +76,22 @@ inline TilePlan tile_plan(int M, int N, int K, int wt, int n_cu, bool pairs = fa
     const int bm = 32 * TG_WM * s.mtw, bn = 32 * s.rbw * s.wn;
     if (N % bn) continue;
     const long long tiles = (long long)((M + bm - 1) / bm) * (N / bn);
-    const long long rounds = (tiles + n_cu - 1) / n_cu;
-    const double t = (double)rounds * (K / 32) * tile_kblock_cycles(s);
-    if (t < best_t * 0.999) {
-      best_t = t;
-      best.mtw = s.mtw;
-      best.rbw = s.rbw;
-      best.wn = s.wn;
-      best.kc = s.kc;
-      best.tiles_m = (M + bm - 1) / bm;
-      best.tiles_n = N / bn;
+    for (int sp = 1; sp <= (split ? 16 : 1) && sp <= K / 64; sp *= 2) {
+      if (sp > 1 && tiles * sp > n_cu) break;
+      const long long rounds = (tiles * sp + n_cu - 1) / n_cu;
+      double t = (double)rounds * ((double)K / 32 / sp) * tile_kblock_cycles(s);
+      if (sp > 1)
+        t += (double)bm * bn * 4 / 21.0 + (double)(sp + 1) * M * N * 4 / 2083.0 + 7200.0;
+      if (t < best_t * 0.999) {
+        best_t = t;
+        best.mtw = s.mtw;
+        best.rbw = s.rbw;
+        best.wn = s.wn;
+        best.kc = s.kc;
+        best.tiles_m = (M + bm - 1) / bm;
+        best.tiles_n = N / bn;
+        best.splits = sp;
+      }
     }
   }
   return best;

@@ -129,6 +129,22 @@ int main() {
       TilePlan q = tp; q.rbw = 1;   // no gate|up pairs in a wave
       expect(check_tile_args(WT_INT8, TG_SWIGLU, b, q), "pairs", "tile swiglu pairs"); }
     { expect(check_tile_args(WT_INT8, 9, ta, tp), "epilogue", "tile epi"); }
+    // split-K: the small-N stacked products split; the planes go through the F32 epilogue
+    // only; the reduction's own rules
+    const TilePlan sp = tile_plan(256, 4096, 14336, WT_INT8, 256, false, true);
+    { TileArgs b = ta; b.K = 14336;
+      if (sp.splits < 2) expect("no split", nullptr, "down 256 rows splits");
+      if (sp.tiles_m * sp.tiles_n * sp.splits > 256) expect("over-subscribed", nullptr, "split grid");
+      expect(check_tile_args(WT_INT8, TG_F32, b, sp), nullptr, "split plan F32");
+      b.scale = (const half_t*)P; b.x = (half_t*)P; b.ss = (float*)P;
+      expect(check_tile_args(WT_INT8, TG_RESID, b, sp), "split-K", "split plan RESID"); }
+    { TilePlan q = tp; q.splits = 65; expect(check_tile_args(WT_INT8, TG_F32, ta, q), "split-K", "splits > K/64"); }
+    { TileArgs b = ta; expect(check_tile_reduce_args(TG_F32, b, (const float*)P, 4), nullptr, "reduce F32"); }
+    { TileArgs b = ta; b.scale = (const half_t*)P; b.x = (half_t*)P; b.ss = (float*)P;
+      expect(check_tile_reduce_args(TG_RESID, b, (const float*)P, 4), nullptr, "reduce RESID"); }
+    { TileArgs b = ta; expect(check_tile_reduce_args(TG_RESID, b, (const float*)P, 4), "RESID", "reduce RESID args"); }
+    { TileArgs b = ta; b.N = 4000; expect(check_tile_reduce_args(TG_F32, b, (const float*)P, 4), "multiple of 64", "reduce N"); }
+    { TileArgs b = ta; expect(check_tile_reduce_args(TG_SWIGLU, b, (const float*)P, 4), "F32 and RESID", "reduce epi"); }
   }
   if (fails == 0) std::printf("ok\n");
   return fails ? 1 : 0;
