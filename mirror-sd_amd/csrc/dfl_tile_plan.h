@@ -53,20 +53,21 @@ constexpr int tile_stages(int wt, int mtw, int rbw, int wn, int kc) {
 
 // Estimated cycles of one k-block (32 k) of a workgroup: the larger of the MFMA time of a
 // SIMD (32 cycles per 32x32x16 MFMA, wn waves per SIMD) and the copy time of the block's X
-// and weight bytes at the copy rate measured for global -> LDS traffic (about 24 B per
-// cycle and CU, 14 TB/s over the chip).
+// and weight bytes at the global -> LDS rate measured over every shape at M = 256 (15.5-19
+// B per cycle and CU: 16).
 inline double tile_kblock_cycles(const TileShape& s) {
   const double mfma = 32.0 * 2 * s.mtw * s.rbw * s.wn;
   const double bytes = TG_WM * s.mtw * 2048.0 + s.rbw * s.wn * 1024.0 * (s.wt == WT_INT8 ? 1 : 2);
-  return std::max(mfma, bytes / 24.0);
+  return std::max(mfma, bytes / 16.0);
 }
 
 // The instantiated shape (and split-K factor) with the least estimated time, in cycles of
 // 2.4 GHz: rounds of one workgroup per CU x k-blocks x cycles per k-block.  A split-K
 // (allowed with split) runs fewer k-blocks per workgroup on larger tiles, so less X per
-// flop, but each workgroup writes its fp32 tile (at about 21 B per cycle) and a reduction
-// launch reads every plane (at about 2 KB per cycle over the chip, plus 3 us).  pairs:
-// each wave must hold gate|up row-block pairs (SWIGLU), i.e. an even rbw.
+// flop, but each workgroup writes its fp32 tile (about 21 B per cycle) and a reduction
+// launch reads every plane (about 1.3 KB per cycle over the chip, plus 12000 cycles of
+// launch and tail); fitted to the measured split-K times of the 8B-class products.
+// pairs: each wave must hold gate|up row-block pairs (SWIGLU), i.e. an even rbw.
 inline TilePlan tile_plan(int M, int N, int K, int wt, int n_cu, bool pairs = false,
                           bool split = false) {
   TilePlan best{};
@@ -81,7 +82,7 @@ inline TilePlan tile_plan(int M, int N, int K, int wt, int n_cu, bool pairs = fa
       const long long rounds = (tiles * sp + n_cu - 1) / n_cu;
       double t = (double)rounds * ((double)K / 32 / sp) * tile_kblock_cycles(s);
       if (sp > 1)
-        t += (double)bm * bn * 4 / 21.0 + (double)(sp + 1) * M * N * 4 / 2083.0 + 7200.0;
+        t += (double)bm * bn * 4 / 21.0 + (double)(sp + 1) * M * N * 4 / 1300.0 + 12000.0;
       if (t < best_t * 0.999) {
         best_t = t;
         best.mtw = s.mtw;
