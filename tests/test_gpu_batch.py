@@ -87,6 +87,35 @@ def test_batch_small_matches_oracle_and_single_sequence(seq_ctx, B):
     m.close()
 
 
+@pytest.mark.parametrize("seq_ctx,B", [((40, 130, 75), 29),      # 87 rows: partial m-tile
+                                       ((33, 100, 64, 9), 32)])  # 128 rows
+def test_batch_split_k_matches_oracle(seq_ctx, B):
+    """H1024 / 8:2 heads / FFN 4096 at 87 and 128 stacked rows: the tile GEMM splits o and
+    down over k (fp32 planes summed in order by the reduce kernel with the RESID epilogue),
+    against the oracle per sequence."""
+    from mirror_sd_amd.config import _draft_cfg
+    from mirror_sd_amd.dflash import DFlashDraftModel
+    cfg = _draft_cfg(1024, 8, 2, 4096, 2, vocab=4096, block=B)
+    t = synth.make_weights_numpy(cfg, seed=4)
+    inps = synth.make_batch_inputs_numpy(cfg, B, seq_ctx, seed=4)
+    W = O.OracleWeights(cfg, t)
+    m = DFlashDraftModel(cfg, max_ctx=max(seq_ctx), max_block=B, max_seqs=len(seq_ctx))
+    m.load_weights(torch_tensors(t, "cuda"))
+    for i, inp in enumerate(inps):
+        m.ingest_seq(i, torch.from_numpy(inp["target_hidden"]))
+    ids_b = np.stack([inp["ids"] for inp in inps])
+    ids, logits, h = m.draft_batch(ids=torch.from_numpy(ids_b), return_logits=True,
+                                   return_hidden=True)
+    torch.cuda.synchronize()
+    ids, logits, h = ids.cpu().numpy(), logits.cpu().numpy(), h.float().cpu().numpy()
+    for i, inp in enumerate(inps):
+        h_ref, ids_ref, ids64, ti, tv = _oracle_both(W, inp)
+        assert_close_fp16(h[i], h_ref, what=f"split-K batch {seq_ctx} sequence {i} hidden")
+        check_argmax(ids[i], logits[i], ids_ref, ids64, f"split-K batch {seq_ctx} sequence {i}",
+                     ti, tv, LOGIT_TOL)
+    m.close()
+
+
 def test_batch_full_matches_golden():
     from mirror_sd_amd.dflash import DFlashDraftModel
     name = "llama8b_batch"
