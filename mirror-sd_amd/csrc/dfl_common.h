@@ -49,13 +49,13 @@ DFL_DEV u32x4 load_stream(const void* p) {
 DFL_DEV u32x4 load_vec(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 DFL_DEV half8_t as_half8(u32x4 v) { return __builtin_bit_cast(half8_t, v); }
 
-// Exact int8 -> fp16 conversion of 16 packed bytes (bytes 0..7 -> lo, 8..15 -> hi).
-// For q in [-127, 127]: u = q ^ 0x80 = q + 128 in [1, 255]; the fp16 bit pattern
-// 0x6400 | u encodes 1024 + u exactly, so (0x6400 | u) - 1152 = q exactly.
+// Exact int8 -> fp16 conversion of 16 packed bytes (bytes 0..7 -> lo, 8..15 -> hi).  The
+// packers store each weight q in [-127, 127] biased, as the byte u = q ^ 0x80 = q + 128 in
+// [1, 255]; the fp16 bit pattern 0x6400 | u encodes 1024 + u exactly, so
+// (0x6400 | u) - 1152 = q exactly: 16 VALU instructions per 16 weights.
 DFL_DEV void dequant_i8x16(u32x4 w, half8_t& lo, half8_t& hi) {
   const uint32_t k64 = 0x64646464u;
-  const u32x4 x = w ^ 0x80808080u;
-  uint32_t d[4] = {x.x, x.y, x.z, x.w};
+  uint32_t d[4] = {w.x, w.y, w.z, w.w};
   uint32_t o[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {

@@ -3,7 +3,7 @@
 // Weight layout in HBM (written once at load by the pack kernels): blocks of 32 rows x
 // KBK k-values (KBK = 32 for int8, 16 for fp16), 1 KiB each, ordered [row-block][k-block];
 // inside a block lane l's 16 bytes are
-//   int8: W[rb*32 + l%32][kb*32 + 16*(l/32) + 0..15]
+//   int8: W[rb*32 + l%32][kb*32 + 16*(l/32) + 0..15], each stored as q ^ 0x80 (= q + 128)
 //   fp16: W[rb*32 + l%32][kb*16 +  8*(l/32) + 0..7]
 // so one wave-wide 128-bit load reads 1 KiB contiguous and hands every lane its
 // v_mfma_f32_32x32x16_f16 A-fragment directly (int8: two MFMAs per load, after the exact
@@ -55,7 +55,12 @@ __global__ __launch_bounds__(64) void pack_i8_kernel(const int8_t* __restrict__ 
   const int KB = K / 32;
   const int drb = rb0 + rb * rb_step;
   const int8_t* src = q + (size_t)(rb * 32 + (l & 31)) * K + (size_t)kb * 32 + 16 * (l >> 5);
-  dst[((size_t)drb * KB + kb) * 64 + l] = *reinterpret_cast<const uint4*>(src);
+  uint4 v = *reinterpret_cast<const uint4*>(src);
+  v.x ^= 0x80808080u;   // biased bytes q + 128 (dequant_i8x16)
+  v.y ^= 0x80808080u;
+  v.z ^= 0x80808080u;
+  v.w ^= 0x80808080u;
+  dst[((size_t)drb * KB + kb) * 64 + l] = v;
   if (kb == 0 && l < 32) dscale[(size_t)drb * 32 + l] = s[(size_t)rb * 32 + l];
 }
 

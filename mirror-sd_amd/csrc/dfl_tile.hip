@@ -132,6 +132,39 @@ DFL_DEV void tg_read_frags(TgFrag<WT, MTW, RBW>& f, const unsigned char* xs, int
   }
 }
 
+// int8 weights with two m-tiles per wave, dequantised one row-block ahead: the 2 * MTW
+// MFMAs of row-block r issue between the 16 VALU instructions that dequantise row-block
+// r + 1 (row-block 0 of the next k-block, w_next, after the last), so the matrix unit runs
+// while the wave's VALU work issues (one compute wave per SIMD: nothing else hides it).
+// d holds row-block 0 of this k-block on entry and that of the next k-block on exit.
+template <int MTW, int RBW, int NACC>
+DFL_DEV void tg_mfma_i8(const TgFrag<WT_INT8, MTW, RBW>& f, half8_t (&d)[2], const u32x4& w_next,
+                        floatx16 (&acc)[RBW][MTW][NACC]) {
+  __builtin_amdgcn_sched_barrier(0);
+  half8_t lo = d[0], hi = d[1];
+  static_for<0, RBW>([&](auto r) {
+    half8_t nlo, nhi;
+    if constexpr (r + 1 < RBW) dequant_i8x16(f.w[0][r + 1], nlo, nhi);
+    else dequant_i8x16(w_next, nlo, nhi);
+    static_for<0, MTW>([&](auto t) {
+      acc[r][t][0] = mfma32x32x16(f.x[0][t][0], lo, acc[r][t][0]);
+      acc[r][t][NACC - 1] = mfma32x32x16(f.x[0][t][1], hi, acc[r][t][NACC - 1]);
+    });
+    lo = nlo;
+    hi = nhi;
+  });
+  // keeps the next k-block's dequantisation here rather than sunk to its first use
+  asm volatile("" : "+v"(lo), "+v"(hi));
+  d[0] = lo;
+  d[1] = hi;
+  constexpr int PER = (16 + 2 * MTW - 1) / (2 * MTW);
+  static_for<0, RBW * 2 * MTW>([&](auto) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+    __builtin_amdgcn_sched_group_barrier(0x002, PER, 0);  // PER VALU
+  });
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 template <int WT, int MTW, int RBW, int NACC>
 DFL_DEV void tg_mfma(const TgFrag<WT, MTW, RBW>& f, floatx16 (&acc)[RBW][MTW][NACC]) {
   if constexpr (WT == WT_INT8) {
@@ -266,11 +299,24 @@ __global__ __launch_bounds__(64 * (TG_WM * WN + (tile_loader(WN) ? 1 : 0))) void
     }
     tg_read_frags<S>(f, tg_lds + (sv % S::STAGES) * S::STAGE, v % S::KBS, wm, wn, lane);
   };
-  for (int u = 0; u < nkb; u += 2) {   // nkb is even (whole 64-k steps)
-    next(u, f1);
-    tg_mfma<WT, MTW, RBW, S::NACC>(f0, acc);
-    if (u + 2 < nkb) next(u + 1, f0);
-    tg_mfma<WT, MTW, RBW, S::NACC>(f1, acc);
+  if constexpr (WT == WT_INT8 && MTW >= 2) {
+    // (with one m-tile the dequantisation outweighs the MFMAs; nothing to hide it under)
+    half8_t d[2];
+    dequant_i8x16(f0.w[0][0], d[0], d[1]);
+    for (int u = 0; u < nkb; u += 2) {   // nkb is even (whole 64-k steps)
+      next(u, f1);
+      tg_mfma_i8<MTW, RBW, S::NACC>(f0, d, f1.w[0][0], acc);
+      if (u + 2 < nkb) next(u + 1, f0);
+      // after the last k-block this dequantises stale registers, never used
+      tg_mfma_i8<MTW, RBW, S::NACC>(f1, d, f0.w[0][0], acc);
+    }
+  } else {
+    for (int u = 0; u < nkb; u += 2) {   // nkb is even (whole 64-k steps)
+      next(u, f1);
+      tg_mfma<WT, MTW, RBW, S::NACC>(f0, acc);
+      if (u + 2 < nkb) next(u + 1, f0);
+      tg_mfma<WT, MTW, RBW, S::NACC>(f1, acc);
+    }
   }
 
   // epilogue, rows m < M only.  Lane l holds, in register i of block (r, t), row
