@@ -11,15 +11,17 @@
 //
 // At M = 256 an int8 weight byte feeds 512 flop, above the MI355X ridge (~312 flop/B), so
 // these shapes are MFMA-bound rather than HBM-bound; what bounds them in practice is the
-// global -> LDS copy rate (about 14 TB/s over the chip), so the larger the workgroup tile,
-// the fewer bytes per flop.  A workgroup of 4 * WN waves (WN = 1 or 2 wave columns)
-// computes a BM x BN output tile: BM = 128 * MTW rows (wave row wm owns m-tiles
+// global -> LDS copy rate (12.5-20.5 B per cycle and CU, 8-13 TB/s over the chip, set by
+// how fast the issuing waves issue copies), so the larger the workgroup tile, the fewer
+// bytes per flop.  A workgroup of 4 * WN compute waves (WN = 1 or 2 wave columns; plus
+// four loader waves that issue every copy when WN = 1) computes a BM x BN output tile:
+// BM = 128 * MTW rows (wave row wm owns m-tiles
 // [wm*MTW, (wm+1)*MTW)), BN = 32 * RBW * WN columns (wave column wn owns row-blocks
 // [wn*RBW, (wn+1)*RBW)).  K is walked in stages of KC (32 or 64): each stage's X records
 // (BM/32 tiles x KC/16 KiB, contiguous per tile) and weight blocks (contiguous per
 // row-block) are copied global -> LDS with global_load_lds (1 KiB per wave instruction,
-// no VGPR staging), the copies spread over the waves, into a ring of 3 to 8 stage buffers
-// (as many as 160 KiB holds), all but three in flight.  The compute waves work per k-block
+// no VGPR staging), the copies spread over the issuing waves, into a ring of 3 to 8 stage
+// buffers (as many as 160 KiB holds), all but three in flight.  The compute waves work per k-block
 // of 32: the next block's fragments are read from LDS (lane-linear 16-byte reads,
 // conflict-free) while the current block is multiplied; int8 blocks are dequantised
 // exactly in registers (dequant_i8x16).
@@ -42,11 +44,11 @@ namespace {
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-
 template <int WT, int MTW, int RBW, int WN, int KC>
 struct TgShape {
   static constexpr int NW = TG_WM * WN;                      // compute waves
-  static constexpr bool LOADER = tile_loader(WN);            // + a loader wave
+  static constexpr bool LOADER = tile_loader(WN);            // + loader waves
+  static constexpr int NLOAD = tile_loaders(WN);
   static constexpr int MT = TG_WM * MTW;                     // m-tiles per workgroup
   static constexpr int RB = RBW * WN;                        // row-blocks per workgroup
   static constexpr int KBS = KC / 32;                        // k-blocks of 32 per stage
@@ -56,12 +58,13 @@ struct TgShape {
   static constexpr int W_BLOCKS = RB * WBLK;
   static constexpr int STAGE = X_BYTES + W_BLOCKS * 1024;
   static constexpr int IPS = STAGE / 1024;                   // copies per stage
-  // copies per issuing wave (at least): all of them for the loader
-  static constexpr int PER_WAVE_MIN = LOADER ? IPS : IPS / NW;
+  // copies per issuing wave (at least)
+  static constexpr int PER_WAVE_MIN = LOADER ? IPS / NLOAD : IPS / NW;
   static constexpr int STAGES = tile_stages(WT, MTW, RBW, WN, KC);
   static constexpr int LDS = STAGES * STAGE;
   static_assert(STAGE == tile_stage_bytes(WT, MTW, RBW, WN, KC), "stage size");
-  static_assert((STAGES - 3) * (LOADER ? IPS : (IPS + NW - 1) / NW) < 64 && STAGES >= 3,
+  static_assert((STAGES - 3) * (LOADER ? (IPS + NLOAD - 1) / NLOAD : (IPS + NW - 1) / NW) < 64 &&
+                    STAGES >= 3,
                 "vmcnt range");
   static_assert(LDS <= TG_LDS_BUDGET, "LDS budget");
   static constexpr int NACC = MTW * RBW >= 4 ? 1 : 2;        // independent MFMA chains
@@ -194,7 +197,7 @@ DFL_DEV void tg_mfma(const TgFrag<WT, MTW, RBW>& f, floatx16 (&acc)[RBW][MTW][NA
 // issued right after B(t).  B(-1) precedes the first read.  Every wave passes B(-1) ..
 // B(nst - 2).
 template <int WT, int EPI, int MTW, int RBW, int WN, int KC>
-__global__ __launch_bounds__(64 * (TG_WM * WN + (tile_loader(WN) ? 1 : 0))) void tile_gemm_kernel(
+__global__ __launch_bounds__(64 * (TG_WM * WN + tile_loaders(WN))) void tile_gemm_kernel(
     TileArgs a) {
   using S = TgShape<WT, MTW, RBW, WN, KC>;
   extern __shared__ __attribute__((aligned(1024))) unsigned char tg_lds[];
@@ -226,11 +229,11 @@ __global__ __launch_bounds__(64 * (TG_WM * WN + (tile_loader(WN) ? 1 : 0))) void
   const int MTt = (a.M + 31) >> 5;             // m-tiles present in X
   const int KBW = WT == WT_INT8 ? K / 32 : K / 16;   // weight blocks per row-block
 
-  // copy i of a stage (X records first, then weight blocks) is issued by the loader, or by
-  // compute wave i % NW
-  constexpr int ISSUERS = S::LOADER ? 1 : S::NW;
-  const int iw = S::LOADER ? 0 : wv;
-  auto issue_stage = [&](int ls) __attribute__((always_inline)) {
+  // copy i of a stage (X records first, then weight blocks) is issued by loader wave
+  // i % NLOAD, or by compute wave i % NW
+  constexpr int ISSUERS = S::LOADER ? S::NLOAD : S::NW;
+  // iw: the issuing wave's index among the ISSUERS (a constant in each loader branch)
+  auto issue_stage = [&](int ls, int iw) __attribute__((always_inline)) {
     unsigned char* buf = tg_lds + (ls % S::STAGES) * S::STAGE;
     const int s = st0 + ls;   // stage of K
 #pragma unroll
@@ -265,22 +268,28 @@ __global__ __launch_bounds__(64 * (TG_WM * WN + (tile_loader(WN) ? 1 : 0))) void
   });
 
   if constexpr (S::LOADER) {
-    if (wv == S::NW) {
-      // ---- loader wave: the copies and the waits; the compute waves only pass barriers ----
-      for (int t = 0; t < S::STAGES - 2 && t < nst; ++t) issue_stage(t);
-      for (int t = -1; t <= nst - 2; ++t) {
-        wait_stage(t);
-        tg_barrier();   // B(t)
-        if (t + S::STAGES - 1 < nst) issue_stage(t + S::STAGES - 1);
-      }
+    if (wv >= S::NW) {
+      // ---- loader waves: the copies and the waits; the compute waves only pass barriers ----
+      auto load = [&](int iw) __attribute__((always_inline)) {
+        for (int t = 0; t < S::STAGES - 2 && t < nst; ++t) issue_stage(t, iw);
+        for (int t = -1; t <= nst - 2; ++t) {
+          wait_stage(t);
+          tg_barrier();   // B(t)
+          if (t + S::STAGES - 1 < nst) issue_stage(t + S::STAGES - 1, iw);
+        }
+      };
+      // one branch per loader, so each one's copy indexes are constants
+      static_for<0, S::NLOAD>([&](auto j) {
+        if (wv == S::NW + (int)j) load(j);
+      });
       return;
     }
     tg_barrier();   // B(-1)
   } else {
-    for (int t = 0; t < S::STAGES - 2 && t < nst; ++t) issue_stage(t);
+    for (int t = 0; t < S::STAGES - 2 && t < nst; ++t) issue_stage(t, wv);
     wait_stage(-1);
     tg_barrier();   // B(-1)
-    if (S::STAGES - 2 < nst) issue_stage(S::STAGES - 2);
+    if (S::STAGES - 2 < nst) issue_stage(S::STAGES - 2, wv);
   }
 
   // k-blocks u = 0 .. nkb-1 of this split (local stage u / KBS); f0 / f1 alternate
@@ -295,7 +304,7 @@ __global__ __launch_bounds__(64 * (TG_WM * WN + (tile_loader(WN) ? 1 : 0))) void
       if constexpr (!S::LOADER) wait_stage(sv - 1);
       tg_barrier();   // B(sv - 1)
       if constexpr (!S::LOADER)
-        if (sv - 1 + S::STAGES - 1 < nst) issue_stage(sv - 1 + S::STAGES - 1);
+        if (sv - 1 + S::STAGES - 1 < nst) issue_stage(sv - 1 + S::STAGES - 1, wv);
     }
     tg_read_frags<S>(f, tg_lds + (sv % S::STAGES) * S::STAGE, v % S::KBS, wm, wn, lane);
   };
@@ -438,7 +447,7 @@ __global__ __launch_bounds__(64 * (TG_WM * WN + (tile_loader(WN) ? 1 : 0))) void
 template <int WT, int EPI, int MTW, int RBW, int WN, int KC>
 void launch_tile(const TileArgs& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   using S = TgShape<WT, MTW, RBW, WN, KC>;
-  const dim3 grid(a.tiles_m * a.tiles_n * a.splits), block(64 * (S::NW + (S::LOADER ? 1 : 0)));
+  const dim3 grid(a.tiles_m * a.tiles_n * a.splits), block(64 * (S::NW + S::NLOAD));
   if (e0 || e1)
     hipExtLaunchKernelGGL((tile_gemm_kernel<WT, EPI, MTW, RBW, WN, KC>), grid, block, S::LDS, st,
                           e0, e1, 0, a);

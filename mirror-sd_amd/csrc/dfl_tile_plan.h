@@ -29,10 +29,13 @@ constexpr TileShape kTileShapes[] = {
 };
 
 constexpr int tile_waves(int wn) { return TG_WM * wn; }
-// The 4-wave shapes (wn == 1) add a loader wave that issues every global -> LDS copy (the
-// compute waves never stall on a full memory queue); the 8-wave shapes have no room for a
-// ninth wave's registers, so their compute waves issue the copies themselves.
-constexpr bool tile_loader(int wn) { return wn == 1; }
+// The 4-wave shapes (wn == 1) add four loader waves that issue every global -> LDS copy
+// (the compute waves never stall on a full memory queue, and four issuing waves copy
+// 20-28 % faster than one: the copy rate is bounded by how fast copies are issued); the
+// 8-wave shapes have no room for more waves' registers, so their compute waves issue the
+// copies themselves.
+constexpr int tile_loaders(int wn) { return wn == 1 ? 4 : 0; }
+constexpr bool tile_loader(int wn) { return tile_loaders(wn) > 0; }
 // Bytes of one stage: the X records of the workgroup's m-tiles (2 KiB per tile and k-block
 // of 32) and its weight blocks (1 KiB per row-block and 32 (int8) or 16 (fp16) k).
 constexpr int tile_stage_bytes(int wt, int mtw, int rbw, int wn, int kc) {
@@ -44,7 +47,8 @@ constexpr int tile_stage_bytes(int wt, int mtw, int rbw, int wn, int kc) {
 constexpr int tile_stages(int wt, int mtw, int rbw, int wn, int kc) {
   const int sb = tile_stage_bytes(wt, mtw, rbw, wn, kc);
   const int per_wave =
-      tile_loader(wn) ? sb / 1024 : (sb / 1024 + tile_waves(wn) - 1) / tile_waves(wn);
+      tile_loader(wn) ? (sb / 1024 + tile_loaders(wn) - 1) / tile_loaders(wn)
+                      : (sb / 1024 + tile_waves(wn) - 1) / tile_waves(wn);
   const int by_lds = TG_LDS_BUDGET / sb;
   const int by_cnt = 3 + 63 / (per_wave > 0 ? per_wave : 1);
   const int s = by_lds < by_cnt ? by_lds : by_cnt;
@@ -53,20 +57,25 @@ constexpr int tile_stages(int wt, int mtw, int rbw, int wn, int kc) {
 
 // Estimated cycles of one k-block (32 k) of a workgroup: the larger of the MFMA time of a
 // SIMD (32 cycles per 32x32x16 MFMA, wn waves per SIMD) and the copy time of the block's X
-// and weight bytes at the global -> LDS rate measured over every shape at M = 256 (15.5-19
-// B per cycle and CU: 16).
+// and weight bytes at the global -> LDS rate measured for the shape at M = 128-4096 (B per
+// cycle and CU: 20.5 with loader waves and 64-k stages, 18.5 with 32-k stages (one barrier
+// per k-block), 12.5 when the 8 compute waves issue the copies).
 inline double tile_kblock_cycles(const TileShape& s) {
   const double mfma = 32.0 * 2 * s.mtw * s.rbw * s.wn;
   const double bytes = TG_WM * s.mtw * 2048.0 + s.rbw * s.wn * 1024.0 * (s.wt == WT_INT8 ? 1 : 2);
-  return std::max(mfma, bytes / 16.0);
+  const double rate = tile_loader(s.wn) ? (s.kc == 64 ? 20.5 : 18.5) : 12.5;
+  return std::max(mfma, bytes / rate);
 }
 
 // The instantiated shape (and split-K factor) with the least estimated time, in cycles of
-// 2.4 GHz: rounds of one workgroup per CU x k-blocks x cycles per k-block.  A split-K
-// (allowed with split) runs fewer k-blocks per workgroup on larger tiles, so less X per
-// flop, but each workgroup writes its fp32 tile (about 21 B per cycle) and a reduction
-// launch reads every plane (about 1.3 KB per cycle over the chip, plus 12000 cycles of
-// launch and tail); fitted to the measured split-K times of the 8B-class products.
+// 2.4 GHz: rounds of one workgroup per CU x k-blocks x cycles per k-block, where a last
+// partial round after full ones counts 0.75-1 of a round (its few workgroups copy faster:
+// 0.75 measured at 16 of 256).  A split-K (allowed with split) runs fewer k-blocks per
+// workgroup on larger tiles, so less X per flop, but each workgroup writes its fp32 tile
+// (about 21 B per cycle) and a reduction launch reads every plane (about 1.3 KB per cycle
+// over the chip, plus 12000 cycles of launch and tail).  Fitted to the measured times of
+// the 8B- and 27B-class stacked products, the prompt-sized K|V ingest and the fp16
+// lm_head (each picks its measured-fastest plan).
 // pairs: each wave must hold gate|up row-block pairs (SWIGLU), i.e. an even rbw.
 inline TilePlan tile_plan(int M, int N, int K, int wt, int n_cu, bool pairs = false,
                           bool split = false) {
@@ -79,8 +88,10 @@ inline TilePlan tile_plan(int M, int N, int K, int wt, int n_cu, bool pairs = fa
     const long long tiles = (long long)((M + bm - 1) / bm) * (N / bn);
     for (int sp = 1; sp <= (split ? 16 : 1) && sp <= K / 64; sp *= 2) {
       if (sp > 1 && tiles * sp > n_cu) break;
-      const long long rounds = (tiles * sp + n_cu - 1) / n_cu;
-      double t = (double)rounds * ((double)K / 32 / sp) * tile_kblock_cycles(s);
+      const long long full = tiles * sp / n_cu, part = tiles * sp % n_cu;
+      const double rounds =
+          (double)full + (part == 0 ? 0.0 : full > 0 ? 0.75 + 0.25 * part / n_cu : 1.0);
+      double t = rounds * ((double)K / 32 / sp) * tile_kblock_cycles(s);
       if (sp > 1)
         t += (double)bm * bn * 4 / 21.0 + (double)(sp + 1) * M * N * 4 / 1300.0 + 12000.0;
       if (t < best_t * 0.999) {
