@@ -31,8 +31,10 @@ GROUPS = [
     ("gate|up (SWIGLU, norm-on-load)", r"gsk_gemm_kernel<0, 1, true, 4>"),
     ("lm_head (fp16, ARGMAX, norm-on-load)", r"gsk_(gemm|dyn)_kernel<1, 2, true, 4>"),
     ("M-split stream-K (stacked rows up to 64)", r"gsk_gemm_m_kernel"),
-    ("tile GEMM int8, fp32 rows (stacked qkv; prompt-sized ingest K|V)", r"tile_gemm_kernel<0, 0,"),
-    ("tile GEMM int8, RESID (stacked o, down)", r"tile_gemm_kernel<0, 1,"),
+    ("tile GEMM int8, fp32 rows (stacked qkv; split-K planes of o, down; prompt-sized ingest K|V)",
+     r"tile_gemm_kernel<0, 0,"),
+    ("tile GEMM int8, RESID (stacked o, down without split-K)", r"tile_gemm_kernel<0, 1,"),
+    ("split-K plane sum + epilogue (stacked o, down: RESID)", r"tile_reduce_kernel"),
     ("tile GEMM int8, SWIGLU (stacked gate|up)", r"tile_gemm_kernel<0, 2,"),
     ("tile GEMM fp16, ARGMAX (stacked lm_head)", r"tile_gemm_kernel<1, 3,"),
     ("argmax of the partial keys (stacked lm_head)", r"argmax_parts_kernel"),
