@@ -9,7 +9,6 @@
 #include <string>
 #include <vector>
 
-#include <rocblas/rocblas.h>
 
 #include "dflash_hip.h"
 #include "dfl_kernels.h"
@@ -37,7 +36,8 @@ constexpr int ING_MAX = 4096;      // context rows per ingest pass (at most)
 // Ingest calls of at most SMALL_ING rows (the per-step context of a decode loop: acceptance
 // + 1 rows) run on the stream-K kernels, which stream each weight once at HBM rate; larger
 // (prompt) ingests are compute-bound: their K|V rows run on the tile GEMM (MFMA) over the
-// packed int8 qkv matrix, the fc on rocBLAS over the fp16 fc weight.
+// packed int8 qkv matrix, the fc on the tile GEMM over the packed fp16 fc weight, reading
+// the context rows (or the tapped layers' rows) where they lie.
 constexpr int SMALL_ING = 64;
 constexpr int MAX_CHUNKS = 64;     // attention key splits
 constexpr int MT_MAX = 8;          // 32-row m-tiles per M-split GEMM launch
@@ -121,7 +121,6 @@ struct dfl_ctx {
   half_t* kc(const Layer& L, int seq) const { return L.Kc + (size_t)seq * kv_seq; }
   half_t* vt(const Layer& L, int seq) const { return L.Vt + (size_t)seq * kv_seq; }
   std::vector<Layer> layers;
-  half_t* w_fc = nullptr;    // [H][n_target_feat * H] fc weight, row-major fp16
   half_t* hidden_norm = nullptr;
   bool fc_loaded = false;
   half_t* final_norm = nullptr;
@@ -150,10 +149,10 @@ struct dfl_ctx {
   int* dyn_next = nullptr;       // [2] work counters of the balanced lm_head (self-resetting)
   float* sk_ss = nullptr;        // [m-tiles][H/64 or H/32][32] row sums of squares of x (RESID)
   SKPlan sk_qkv, sk_o, sk_gu, sk_down, sk_lm;
-  // context ingest: `ing` rows per pass (compute-bound: fc on rocBLAS, K|V on the tile GEMM)
+  // context ingest: `ing` rows per pass (compute-bound: fc and K|V on the tile GEMM)
   int ing = 0;
-  rocblas_handle blas = nullptr;
   float* fc32 = nullptr;      // [ing][H] fc GEMM rows (fp32)
+  half_t* xf = nullptr;       // [ing][n_target_feat * H] fc input rows, fragment layout
   half_t* xn = nullptr;       // [ing/32][32][H] hidden_norm(fc) (or fused) rows, fragment layout
   float* kv32 = nullptr;      // [ing][2*NKV*128] K|V GEMM rows (fp32)
   // per-step ingest of up to SMALL_ING rows on the stream-K kernels (no library GEMM): the
@@ -175,7 +174,6 @@ struct dfl_ctx {
   std::vector<ProfRec> recs;
 
   ~dfl_ctx() {
-    if (blas) (void)rocblas_destroy_handle(blas);
     for (auto& r : recs) {
       (void)hipEventDestroy(r.a);
       (void)hipEventDestroy(r.b);
@@ -244,30 +242,7 @@ static int check_launch(const char* what) {
   return DFL_OK;
 }
 
-// Y (row-major [n][m], fp32, row stride ldy) = beta * Y + B A^T for row-major fp16 A [m][k]
-// (row stride lda) and B [n][k] (row stride ldb): in rocBLAS's column-major terms
-// Y^T = A^T(op transpose) * B^T, fp32 accumulation.
-static int blas_gemm(dfl_ctx* ctx, int m, int n, int k, const half_t* A, int lda, const half_t* B,
-                     int ldb, float beta, float* Y, int ldy, hipStream_t st) {
-  rocblas_status s = rocblas_set_stream(ctx->blas, st);
-  if (s == rocblas_status_success) {
-    const float one = 1.0f;
-    s = rocblas_gemm_ex(ctx->blas, rocblas_operation_transpose, rocblas_operation_none, m, n, k,
-                        &one, A, rocblas_datatype_f16_r, lda, B, rocblas_datatype_f16_r, ldb,
-                        &beta, Y, rocblas_datatype_f32_r, ldy, Y, rocblas_datatype_f32_r, ldy,
-                        rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-  }
-  if (s == rocblas_status_success) return DFL_OK;
-  return fail(DFL_EHIP, std::string("rocblas_gemm_ex (") + std::to_string(m) + "x" +
-                            std::to_string(n) + "x" + std::to_string(k) +
-                            "): " + rocblas_status_to_string(s));
-}
-
-// Ingest buffers and the rocBLAS handle.  The handle works in a fixed workspace owned by
-// the context (a GEMM that wanted more fails with an error instead of allocating), so no
-// later call allocates device memory.
-constexpr size_t BLAS_WS_BYTES = 128ull << 20;
-
+// Ingest buffers, allocated here so that no later call allocates device memory.
 static int setup_ingest(dfl_ctx* x) {
   const int H = x->H, Nkv = 2 * x->NKV * 128;
   x->ing = std::max(32, std::min(ING_MAX, ((x->cfg.max_ctx + 31) / 32) * 32));
@@ -281,13 +256,9 @@ static int setup_ingest(dfl_ctx* x) {
       (r = x->alloc(&x->s_kv_all, (size_t)x->NL * Nkv)))
     return r;
   if ((r = x->alloc(&x->xn, (size_t)x->ing * H))) return r;
-  if (x->NF > 0 && (r = x->alloc(&x->fc32, (size_t)x->ing * H))) return r;
-  if (rocblas_create_handle(&x->blas) != rocblas_status_success)
-    return fail(DFL_EHIP, "dfl_create: rocblas_create_handle failed");
-  unsigned char* ws = nullptr;
-  if ((r = x->alloc(&ws, BLAS_WS_BYTES))) return r;
-  if (rocblas_set_workspace(x->blas, ws, BLAS_WS_BYTES) != rocblas_status_success)
-    return fail(DFL_EHIP, "dfl_create: rocblas_set_workspace failed");
+  if (x->NF > 0 && ((r = x->alloc(&x->fc32, (size_t)x->ing * H)) ||
+                    (r = x->alloc(&x->xf, (size_t)x->ing * x->NF * H))))
+    return r;
   return DFL_OK;
 }
 
@@ -504,14 +475,13 @@ int dfl_load_fc(dfl_ctx* ctx, const uint16_t* fc_weight, const uint16_t* hidden_
   if (ctx->NF <= 0) return fail(DFL_ESTATE, "dfl_load_fc: context created with n_target_feat = 0");
   hipStream_t st = (hipStream_t)stream;
   const int K = ctx->NF * ctx->H;
-  if (!ctx->w_fc) {
-    DFL_TRY(ctx->alloc(&ctx->w_fc, (size_t)ctx->H * K));
+  if (!ctx->w_fc_pk) {
     DFL_TRY(ctx->alloc(&ctx->hidden_norm, (size_t)ctx->H));
+    DFL_TRY(ctx->alloc(&ctx->w_fc_pk, (size_t)ctx->H * K / 8));
   }
-  DFL_HIP(hipMemcpyAsync(ctx->w_fc, fc_weight, (size_t)ctx->H * K * 2, hipMemcpyDeviceToDevice, st));
   DFL_HIP(hipMemcpyAsync(ctx->hidden_norm, hidden_norm, ctx->H * 2, hipMemcpyDeviceToDevice, st));
-  // the same weight in the stream-K fp16 block layout, for per-step ingests
-  if (!ctx->w_fc_pk) DFL_TRY(ctx->alloc(&ctx->w_fc_pk, (size_t)ctx->H * K / 8));
+  // the fc weight in the packed fp16 block layout, read by the stream-K (per-step) and
+  // tile (prompt-sized) GEMMs
   launch_pack_f16(reinterpret_cast<const half_t*>(fc_weight), ctx->H, K, ctx->w_fc_pk, st);
   DFL_TRY(check_launch("pack fc"));
   ctx->fc_loaded = true;
@@ -822,14 +792,9 @@ static int ingest(dfl_ctx* ctx, const uint16_t* src, int C, bool fused, void* st
   const int K = ctx->NF * H;
   const half_t* in = reinterpret_cast<const half_t*>(src);
   ctx->sq().last_block = 0;
-  // per-step context rows: stream-K kernels (16-byte aligned rows; else the library path)
-  bool aligned = true;
-  if (feats) {
-    for (int j = 0; j < feats->n; ++j) aligned &= !(reinterpret_cast<uintptr_t>(feats->p[j]) & 15);
-  } else {
-    aligned = !(reinterpret_cast<uintptr_t>(in) & 15);
-  }
-  if (C > 0 && C <= SMALL_ING && aligned && (fused || ctx->w_fc_pk)) {
+  // per-step context rows: stream-K kernels (any alignment: the rows are gathered into
+  // fragment layout first)
+  if (C > 0 && C <= SMALL_ING && (fused || ctx->w_fc_pk)) {
     DFL_TRY(ingest_small(ctx, in, C, fused, feats, st));
     DFL_TRY(check_launch("ingest"));
     ctx->sq().offset += C;
@@ -849,18 +814,26 @@ static int ingest(dfl_ctx* ctx, const uint16_t* src, int C, bool fused, void* st
       DFL_TRY(ingest_kv_rows(ctx, ctx->xn, rows, r0, st));
     } else {
       // hidden_norm(fc(target_hidden)): fc output rounded to fp16 (Linear), then RMSNorm.
-      // Tapped-layer features: fc(concat(f_j)) = sum_j f_j W_fc[:, jH:(j+1)H]^T.
+      // The rows (or the tapped layers' rows: feature j gives columns [jH, (j+1)H)) are
+      // gathered into fragment layout (any alignment), then the tile GEMM over the packed
+      // fp16 fc weight.
+      FeatPtrs f{};
+      if (feats) {
+        f = *feats;
+        for (int j = 0; j < f.n; ++j) f.p[j] += (size_t)r0 * f.ld;
+      } else {
+        f.n = ctx->NF;
+        f.ld = K;
+        for (int j = 0; j < f.n; ++j) f.p[j] = in + (size_t)r0 * K + (size_t)j * H;
+      }
       {
         ProfScope ps(ctx, P_INGEST_FC, 0, st);
-        if (feats) {
-          for (int j = 0; j < feats->n; ++j)
-            DFL_TRY(blas_gemm(ctx, H, rows, H, ctx->w_fc + (size_t)j * H, K,
-                              feats->p[j] + (size_t)r0 * feats->ld, (int)feats->ld,
-                              j ? 1.f : 0.f, ctx->fc32, H, st));
-        } else {
-          DFL_TRY(blas_gemm(ctx, H, rows, K, ctx->w_fc, K, in + (size_t)r0 * K, K, 0.f,
-                            ctx->fc32, H, st));
-        }
+        launch_feats_to_afl(f, rows, H, ctx->xf, st);
+      }
+      DFL_TRY(tgemm(ctx, P_INGEST_FC, WT_F16, TG_F32, ctx->w_fc_pk, H, K, ctx->xf, rows,
+                    tile_f32(ctx->fc32, H), st));
+      {
+        ProfScope ps(ctx, P_INGEST_FC, 0, st);
         launch_fc_norm_rows(ctx->fc32, rows, H, ctx->hidden_norm, ctx->cfg.rms_eps, ctx->xn, st);
       }
       DFL_TRY(ingest_kv_rows(ctx, ctx->xn, rows, r0, st));

@@ -737,7 +737,8 @@ def _feature_ptrs(feats, H: int, device):
     ld = rows[0].stride(0)
     ok = all(t.stride(1) == 1 and t.stride(0) == ld and t.data_ptr() % 16 == 0 for t in rows)
     if not ok or ld % 8 or ld < H:
-        rows = [t.contiguous() for t in rows]
+        # fresh storage is 16-byte aligned (a contiguous view at an odd offset stays unaligned)
+        rows = [t.clone(memory_format=torch.contiguous_format) for t in rows]
         ld = H
     arr = (ctypes.c_void_p * len(rows))(*[t.data_ptr() for t in rows])
     return arr, len(rows), ld, C, rows

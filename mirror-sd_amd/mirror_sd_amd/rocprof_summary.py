@@ -38,7 +38,6 @@ GROUPS = [
     ("tile GEMM int8, SWIGLU (stacked gate|up)", r"tile_gemm_kernel<0, 2,"),
     ("tile GEMM fp16, ARGMAX (stacked lm_head)", r"tile_gemm_kernel<1, 3,"),
     ("argmax of the partial keys (stacked lm_head)", r"argmax_parts_kernel"),
-    ("library GEMM (rocBLAS: prompt-sized ingest fc)", r"Cijk_"),
     ("fc rows: fp16 rounding + hidden_norm (prompt-sized ingest)", r"fc_norm_rows_kernel"),
     ("RMSNorm rows (stacked blocks)", r"afl_rows_kernel"),
     ("block attention", r"block_attn_kernel"),

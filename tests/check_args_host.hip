@@ -20,7 +20,7 @@ static void expect(const char* got, const char* needle, const char* what) {
 }
 
 int main() {
-  static char dummy[64];
+  alignas(16) static char dummy[64];
   void* P = dummy;
   StreamArgs a{};
   a.W = (const uint4*)P; a.scale = (const half_t*)P; a.N = 5120; a.KB = 160;
