@@ -399,9 +399,12 @@ DFL_DEV EpiIn epi_prefetch(const StreamArgs& a, int lane, int t) {
 // global inputs from epi_prefetch (EPI_STORE, EPI_RESID, EPI_SWIGLU).
 // Row n of the packed matrix in accumulator r of block tt: n = (2t+tt)*32 + 8*(r/4)
 // + 4*g + (r%4), activation row m = lane % 32.
+// ARGMAX with key_acc: the row's best key so far is kept in *key_acc (lanes 0..31, one row
+// each) instead of an atomicMax per tile; the caller publishes it once at its end.
 template <int EPI>
 DFL_DEV void tile_epilogue(const StreamArgs& a, int lane, int t, const floatx16& acc0,
-                           const floatx16& acc1, const EpiIn& in) {
+                           const floatx16& acc1, const EpiIn& in,
+                           unsigned long long* key_acc = nullptr) {
   const int m = lane & 31, g = lane >> 5;
   const bool row_ok = m < a.M;
   const int nb = (2 * t) * 32 + 4 * g;
@@ -510,7 +513,8 @@ DFL_DEV void tile_epilogue(const StreamArgs& a, int lane, int t, const floatx16&
       if (g == 0 && row_ok && bn != 0x7fffffff) {
         const unsigned long long key =
             ((unsigned long long)float_order_key(best) << 32) | (0xFFFFFFFFu - (uint32_t)bn);
-        atomicMax(a.keys + m, key);
+        if (key_acc) *key_acc = key > *key_acc ? key : *key_acc;
+        else atomicMax(a.keys + m, key);
       }
     }
   }
@@ -569,12 +573,12 @@ DFL_DEV void sum_wave_partials(int lane, float (*red)[WG_WAVES][2048], int* arri
 template <int EPI>
 DFL_DEV void reduce_segment(const StreamArgs& a, int lane, float (*red)[WG_WAVES][2048],
                             int* arrived, int* reduced, int si, int t, int slot, int count,
-                            const int* abort = nullptr) {
+                            const int* abort = nullptr, unsigned long long* key_acc = nullptr) {
   const EpiIn in = epi_prefetch<EPI>(a, lane, t);   // in flight while the partials arrive
   floatx16 acc0, acc1;
   sum_wave_partials(lane, red, arrived, reduced, si, acc0, acc1, abort);
   const bool complete = count == 1 || finish_split_tile(a, lane, t, slot, count, acc0, acc1);
-  if (complete) tile_epilogue<EPI>(a, lane, t, acc0, acc1, in);
+  if (complete) tile_epilogue<EPI>(a, lane, t, acc0, acc1, in, key_acc);
 }
 
 // Q or K head h of the fused qkv projection, complete: lo = d 0..63 (tile 2h), hi = d
@@ -858,6 +862,9 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_gemm_kernel(StreamArg
 
   // ---- reducer wave ----
   if constexpr (NORM) reducer_norm_prologue<WT>(a, lane, gsh, ss_s, rn_s, &ready);
+  // ARGMAX: each row's best key over the tiles this wave completes, one atomicMax at the end
+  unsigned long long kacc = 0;
+  unsigned long long* ka = EPI == EPI_ARGMAX ? &kacc : nullptr;
   int si = 0;
   for (long long u = u0; u < u1; ++si) {
     const int t = (int)(u / a.KB);
@@ -881,11 +888,14 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_gemm_kernel(StreamArg
       first = worker_of(tu0, U, G);
       count = worker_of(tu0 + a.KB - 1, U, G) - first + 1;
     }
-    reduce_segment<EPI>(a, lane, red, arrived, &reduced, si, t, b - first, count);
+    reduce_segment<EPI>(a, lane, red, arrived, &reduced, si, t, b - first, count, nullptr, ka);
     u += kbe - kbs;
   }
   for (long long u = v0; u < v1; u += a.KB, ++si)   // whole tiles: local epilogues
-    reduce_segment<EPI>(a, lane, red, arrived, &reduced, si, (int)(u / a.KB), 0, 1);
+    reduce_segment<EPI>(a, lane, red, arrived, &reduced, si, (int)(u / a.KB), 0, 1, nullptr,
+                        ka);
+  if constexpr (EPI == EPI_ARGMAX)
+    if (a.keys && lane < 32 && lane < a.M && kacc) atomicMax(a.keys + lane, kacc);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -991,17 +1001,24 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_dyn_kernel(StreamArgs
     ++n_pub;
   };
   int si = 0;
+  // ARGMAX: the best key of each row over this workgroup's tiles, one atomicMax per row at
+  // the end (one per row and tile contended on the same 32 keys: 8.5 us of the lm_head)
+  unsigned long long kacc = 0;
+  unsigned long long* ka = EPI == EPI_ARGMAX ? &kacc : nullptr;
   for (int i = 0; i < S; ++i, ++si) {
     if (i == S - 1) publish_next();   // entry 0 before the last static segment's wait
-    reduce_segment<EPI>(a, lane, red, arrived, &reduced, si, b * S + i, 0, 1, &abort);
+    reduce_segment<EPI>(a, lane, red, arrived, &reduced, si, b * S + i, 0, 1, &abort, ka);
   }
   if (S == 0) publish_next();
   for (int k = 0;; ++k, ++si) {
     const int c = __shfl(q_chunk[k & 3], 0, 64);   // entry k, published by this wave
     if (c < 0) break;
     publish_next();                   // entry k + 1 before waiting for chunk k
-    reduce_segment<EPI>(a, lane, red, arrived, &reduced, si, T0 + (c >> 1), c & 1, 2, &abort);
+    reduce_segment<EPI>(a, lane, red, arrived, &reduced, si, T0 + (c >> 1), c & 1, 2, &abort,
+                        ka);
   }
+  if constexpr (EPI == EPI_ARGMAX)
+    if (a.keys && lane < 32 && lane < a.M && kacc) atomicMax(a.keys + lane, kacc);
   // this workgroup's epilogue atomics and stores are performed before it counts itself
   // finished, so the last one to finish sees every tile's argmax key
   __builtin_amdgcn_s_waitcnt(0);
