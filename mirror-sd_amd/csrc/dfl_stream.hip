@@ -1187,10 +1187,12 @@ SKPlan streamk_plan_balanced(int N, int KB, int n_cu) {
   const long long nt = N / 64;
   if (nt < 2LL * n_cu || (KB & 1)) return p;
   p.workers = n_cu;
-  // about 86 % of the tiles statically: below the share that the slowest XCD finishes in
-  // the balanced time when the XCDs' rates differ by up to a quarter
-  // (clamped so that the static tiles never pass the last tile)
-  p.dyn_static = (int)std::min(nt / n_cu, (nt * 86 + 50LL * n_cu) / (100LL * n_cu));
+  // whole rounds of tiles statically, the remainder (less than one tile per workgroup) as
+  // balanced half tiles: with one argmax atomic per row and workgroup the XCDs stream at
+  // the same rate (242 us at 27B against 251 with 86 % static and 254 with 72 %; the
+  // spread of up to a quarter between XCDs measured earlier came with an atomicMax per
+  // tile on the same 32 keys)
+  p.dyn_static = (int)(nt / n_cu);
   p.seg_cap = std::max(p.seg_cap, 2);
   return p;
 }
