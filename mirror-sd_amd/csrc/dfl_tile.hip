@@ -43,6 +43,7 @@ namespace dfl {
 namespace {
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+constexpr int TG_GROUP_M = 4;   // m-tile rows per group of the tile order
 
 template <int WT, int MTW, int RBW, int WN, int KC>
 struct TgShape {
@@ -206,7 +207,7 @@ __global__ __launch_bounds__(64 * (TG_WM * WN + tile_loaders(WN))) void tile_gem
   const int wm = wv % TG_WM, wn = wv / TG_WM;
 
   // XCD-aware tile order: consecutive workgroups go to different XCDs, so tile t is run by
-  // workgroup b with t = (b % 8) * (G / 8) + b / 8; the tiles of one m-tile row (sharing X)
+  // workgroup b with t = (b % 8) * (G / 8) + b / 8; neighbouring tiles (sharing X or W)
   // then run on one XCD and share its L2.
   const int G = gridDim.x;
   const int b = blockIdx.x;
@@ -217,8 +218,17 @@ __global__ __launch_bounds__(64 * (TG_WM * WN + tile_loaders(WN))) void tile_gem
   const int tiles = a.tiles_m * a.tiles_n;
   const int sp = gt / tiles;
   const int tile = gt - sp * tiles;
-  const int tm = tile / a.tiles_n;
-  const int tn = tile - tm * a.tiles_n;
+  // tile order in groups of TG_GROUP_M m-tile rows: consecutive tiles walk down a group's
+  // rows, then across its columns, so the 32 tiles an XCD runs at once cover a 4 x 8
+  // block (X of 4 row tiles, W of 8 column tiles) instead of 1 x 32 (W of 32): at large M
+  // (the prompt-sized fc: 16 x 40 tiles, X 210 MB, W 262 MB) each XCD re-reads a quarter
+  // of the weights per round instead of most of them.  One row tile: plain order.
+  const int gsz = TG_GROUP_M * a.tiles_n;
+  const int grp = tile / gsz, first_m = grp * TG_GROUP_M;
+  const int gm = min(a.tiles_m - first_m, TG_GROUP_M);
+  const int tig = tile - grp * gsz;
+  const int tm = first_m + tig % gm;
+  const int tn = tig / gm;
   const int mt0 = tm * S::MT;                  // first m-tile of this workgroup
   const int nb0 = tn * S::RB;                  // first weight row-block
   const int K = a.K;

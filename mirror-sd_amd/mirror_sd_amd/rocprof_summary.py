@@ -37,6 +37,8 @@ GROUPS = [
     ("split-K plane sum + epilogue (stacked o, down: RESID)", r"tile_reduce_kernel"),
     ("tile GEMM int8, SWIGLU (stacked gate|up)", r"tile_gemm_kernel<0, 2,"),
     ("tile GEMM fp16, ARGMAX (stacked lm_head)", r"tile_gemm_kernel<1, 3,"),
+    ("tile GEMM fp16, fp32 rows (prompt-sized ingest fc)", r"tile_gemm_kernel<1, 0,"),
+    ("rows into fragment layout (ingest input, fused-rows ingest)", r"feats_to_afl_kernel"),
     ("argmax of the partial keys (stacked lm_head)", r"argmax_parts_kernel"),
     ("fc rows: fp16 rounding + hidden_norm (prompt-sized ingest)", r"fc_norm_rows_kernel"),
     ("RMSNorm rows (stacked blocks)", r"afl_rows_kernel"),
