@@ -204,7 +204,7 @@ def run_workload(wl, args, sweep, want_cpu):
     out_ids = torch.empty((n_seq * wl.block,), dtype=torch.int32, device="cuda")
 
     # context ingest (fc fusion + per-layer K/V), timed as its own phase after one untimed
-    # ingest (the first GEMM calls load the BLAS library's kernels)
+    # ingest (the first launches load the kernels' code objects)
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     def ingest_all():
         for i, t in enumerate(ths):
