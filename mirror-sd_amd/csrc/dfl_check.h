@@ -49,6 +49,11 @@ inline const char* check_stream_args(int wt, int epi, bool norm, const StreamArg
       if (m_split || a.M > 32 || !norm) return "QKROPE is the single-tile normed qkv kernel";
       if (a.N != (r.NH + 2 * r.NKV) * 128 || r.NH < 1 || r.NKV < 1)
         return "QKROPE rows are not the q|k|v heads";
+      if (a.N > QK_N_MAX) return "QKROPE: more q|k|v rows than the scales' LDS copy holds";
+      if (!a.scale || (reinterpret_cast<uintptr_t>(a.scale) & 15) ||
+          (reinterpret_cast<uintptr_t>(r.cs) & 15) || (reinterpret_cast<uintptr_t>(r.q_norm) & 15) ||
+          (reinterpret_cast<uintptr_t>(r.k_norm) & 15))
+        return "QKROPE tables must be 16-byte aligned";
       if (!r.Q || !r.cs || !r.q_norm || !r.k_norm || !r.sq.Kc || !r.sq.Vt || r.cap < 1)
         return "QKROPE outputs or tables missing";
       break;

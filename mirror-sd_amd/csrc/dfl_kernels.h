@@ -22,6 +22,7 @@ struct RopeSeq {
 
 // EPI_QKROPE outputs: Q [NH][M][128], the K cache rows and the Vt cache columns of the
 // sequence's rows (positions sq.pos0 + m, cache rows through cache_slot).
+constexpr int QK_N_MAX = 16384;   // QKROPE: most q|k|v rows (the scales' LDS copy)
 struct RopeEpi {
   half_t* Q;
   const float* cs;          // [M][64] (cos, sin) of position pos0 + m, frequency j (embed_norm)

@@ -586,11 +586,20 @@ DFL_DEV void reduce_segment(const StreamArgs& a, int lane, float (*red)[WG_WAVES
 // neox pair (d, d + 64) at the same register.  Per head and row: fp16 Linear output, RMSNorm
 // over the 128 d (q_norm / k_norm), split-half RoPE with the block's angle table ([m][j]
 // cos, sin, j = d mod 64), then Q[h][m] or the K cache row (qk_rope_kernel's arithmetic;
-// dflash.py:251-252, 263-275).
+// dflash.py:251-252, 263-275).  Its tables are LDS copies made by the reducer wave at the
+// start of the launch (QkTables), so none of its reads waits on global memory.
+struct QkTables {
+  const half_t* scale;   // [N] per-row scales of the q|k|v matrix
+  const float* cs;       // [M][64] (cos, sin) of the block's positions
+  const half_t* gn;      // [2][128] q_norm, k_norm
+};
 DFL_DEV void qk_head_epilogue(const StreamArgs& a, int lane, int h, const floatx16& lo0,
-                              const floatx16& lo1, const floatx16& hi0, const floatx16& hi1) {
+                              const floatx16& lo1, const floatx16& hi0, const floatx16& hi1,
+                              const QkTables& tb) {
   const RopeEpi& r = a.rope;
   const int m = lane & 31, g = lane >> 5;
+  __builtin_amdgcn_s_waitcnt(0);   // the reducer's table copies (issued at its start) landed
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   const int nlo = 128 * h + 4 * g;   // packed row of d = 4g (+ 32 tt + 8 q + c)
   float vl[32], vh[32];
   float ss = 0.f;
@@ -598,8 +607,8 @@ DFL_DEV void qk_head_epilogue(const StreamArgs& a, int lane, int h, const floatx
   for (int i = 0; i < 32; ++i) {   // i = 16 tt + 4 q + c: d = 32 tt + 8 q + 4 g + c
     const int f = 32 * (i >> 4) + 8 * ((i >> 2) & 3) + (i & 3);
     const float al = i < 16 ? lo0[i] : lo1[i - 16], ah = i < 16 ? hi0[i] : hi1[i - 16];
-    vl[i] = h2f(f2h(al * h2f(a.scale[nlo + f])));
-    vh[i] = h2f(f2h(ah * h2f(a.scale[nlo + 64 + f])));
+    vl[i] = h2f(f2h(al * h2f(tb.scale[nlo + f])));
+    vh[i] = h2f(f2h(ah * h2f(tb.scale[nlo + 64 + f])));
     ss += vl[i] * vl[i] + vh[i] * vh[i];
   }
   ss += __shfl_xor(ss, 32, 64);
@@ -613,12 +622,12 @@ DFL_DEV void qk_head_epilogue(const StreamArgs& a, int lane, int h, const floatx
     if (crow < 0) return;
     dst = r.sq.Kc + ((size_t)(h - r.NH) * r.cap + crow) * 128;
   }
-  const half_t* gn = is_q ? r.q_norm : r.k_norm;
+  const half_t* gn = tb.gn + (is_q ? 0 : 128);
   const float rr = 1.0f / sqrtf(ss * (1.0f / 128.0f) + r.eps);
 #pragma unroll
   for (int q8 = 0; q8 < 8; ++q8) {   // 4 consecutive d per (tt, q)
     const int f0 = 32 * (q8 >> 2) + 8 * (q8 & 3) + 4 * g;
-    const floatx4* csp = reinterpret_cast<const floatx4*>(r.cs + 2 * (m * 64 + f0));
+    const floatx4* csp = reinterpret_cast<const floatx4*>(tb.cs + 2 * (m * 64 + f0));
     const floatx4 cs01 = csp[0], cs23 = csp[1];   // (cos, sin) of f0 .. f0 + 3
     half4_t ol, oh;
 #pragma unroll
@@ -643,7 +652,7 @@ DFL_DEV void qk_head_epilogue(const StreamArgs& a, int lane, int h, const floatx
 // as a per-tile completion) and runs qk_head_epilogue.
 DFL_DEV void reduce_head(const StreamArgs& a, int lane, float (*red)[WG_WAVES][2048],
                          int* arrived, int* reduced, int si, int t, int slot, int c_lo,
-                         int c_hi) {
+                         int c_hi, const QkTables& tb) {
   floatx16 acc0, acc1;
   sum_wave_partials(lane, red, arrived, reduced, si, acc0, acc1);
   const int t0 = t & ~1;
@@ -652,7 +661,7 @@ DFL_DEV void reduce_head(const StreamArgs& a, int lane, float (*red)[WG_WAVES][2
   add_slots(a, lane, t0, c_lo, lo0, lo1);
   add_slots(a, lane, t0 + 1, c_hi, hi0, hi1);
   if (lane == 0) a.tile_cnt[t0] = 0;   // next use is a later launch
-  qk_head_epilogue(a, lane, t0 >> 1, lo0, lo1, hi0, hi1);
+  qk_head_epilogue(a, lane, t0 >> 1, lo0, lo1, hi0, hi1, tb);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -832,6 +841,10 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_gemm_kernel(StreamArg
   // only after its previous segment was reduced); reduced: segments summed so far;
   // ready: norm prologue state (PRO_ISSUED, PRO_DONE)
   __shared__ int arrived[2], reduced, ready;
+  // QKROPE: the head epilogue's tables (scales, angles, Q/K norm gains), copied to LDS
+  __shared__ __attribute__((aligned(16))) half_t qk_sc[EPI == EPI_QKROPE ? QK_N_MAX : 8];
+  __shared__ __attribute__((aligned(16))) float qk_cs[EPI == EPI_QKROPE ? 32 * 128 : 4];
+  __shared__ __attribute__((aligned(16))) half_t qk_gn[EPI == EPI_QKROPE ? 256 : 8];
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -862,6 +875,13 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_gemm_kernel(StreamArg
 
   // ---- reducer wave ----
   if constexpr (NORM) reducer_norm_prologue<WT>(a, lane, gsh, ss_s, rn_s, &ready);
+  [[maybe_unused]] const QkTables qkt{qk_sc, qk_cs, qk_gn};
+  if constexpr (EPI == EPI_QKROPE) {   // needed by the first head's epilogue, not before
+    copy_to_lds(a.scale, qk_sc, a.N * 2, lane);
+    copy_to_lds(a.rope.cs, qk_cs, a.M * 64 * 8, lane);
+    copy_to_lds(a.rope.q_norm, qk_gn, 256, lane);
+    copy_to_lds(a.rope.k_norm, qk_gn + 128, 256, lane);
+  }
   // ARGMAX: each row's best key over the tiles this wave completes, one atomicMax at the end
   unsigned long long kacc = 0;
   unsigned long long* ka = EPI == EPI_ARGMAX ? &kacc : nullptr;
@@ -877,7 +897,7 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_gemm_kernel(StreamArg
         const int c_lo = worker_of(h0 + a.KB - 1, U, G) - f_lo + 1;
         const int c_hi = worker_of(h0 + 2 * a.KB - 1, U, G) - f_hi + 1;
         reduce_head(a, lane, red, arrived, &reduced, si, t, b - ((t & 1) ? f_hi : f_lo), c_lo,
-                    c_hi);
+                    c_hi, qkt);
         u += kbe - kbs;
         continue;
       }
