@@ -17,7 +17,11 @@ After the headline, the same run times the block step at resident contexts 64, 2
 8 sequences x 32 rows, ragged contexts: ``batched``); both are extra keys, never ``value``.
 
 Prints ONE JSON line.  ``value`` is the mean draft-block latency in microseconds over
-the timed steps (inputs resident in HBM).  ``roofline`` describes the W8A16 projection
+the timed steps (inputs resident in HBM), after ``--warmup`` untimed blocks (default 200,
+about 0.2 s): the GPU reaches its sustained clocks only after ~0.1 s of continuous work
+(blocks run ~3 % slower before, and again after a second of idle), and a drafting loop
+runs continuously.  The context sweep and the decode-loop steps run after the headline
+(the GPU already warm) with a 5-block warmup each.  ``roofline`` describes the W8A16 projection
 GEMM kernel, timed live with HIP events on the library's stream in a separate pass of
 ``--profile-steps`` blocks.  ``cpu_baseline`` times the CPU oracle (numpy fp32,
 dequantised weights) on a bounded number of the same blocks on this host.
@@ -183,7 +187,9 @@ def run_workload(wl, args, sweep, want_cpu):
     t_setup = time.perf_counter()
     n_seq = len(wl.seq_ctx) if batched else 1
     # room for the swept contexts and for the rows the decode-loop steps append
-    steady_rows = 0 if batched or not args.steady else (args.warmup + args.steps) * 32
+    # sweep and decode-loop steps come after the headline's warmup and timed blocks
+    warm_after = min(args.warmup, 5)
+    steady_rows = 0 if batched or not args.steady else (warm_after + args.steps) * 32
     model, host = build_model(wl, args.seed, keep_host=want_cpu,
                               max_ctx=max([wl.ctx + steady_rows] + sweep), max_seqs=n_seq)
     if batched:
@@ -345,7 +351,7 @@ def run_workload(wl, args, sweep, want_cpu):
             def ingest_only():
                 ingest_k()
                 _lib.check(L.dfl_cache_trim(ctx, k), "dfl_cache_trim")
-            for _ in range(args.warmup):
+            for _ in range(warm_after):
                 ingest_only()
             torch.cuda.synchronize()
             ev0.record(stream)
@@ -355,7 +361,7 @@ def run_workload(wl, args, sweep, want_cpu):
             torch.cuda.synchronize()
             ing_us = ev0.elapsed_time(ev1) * 1e3 / args.steps
             n_app = 0
-            for _ in range(args.warmup):
+            for _ in range(warm_after):
                 ingest_k()
                 step()
                 n_app += k
@@ -390,7 +396,7 @@ def run_workload(wl, args, sweep, want_cpu):
             torch.cuda.synchronize()
             ing = ev0.elapsed_time(ev1)
             del sw
-            for _ in range(args.warmup):
+            for _ in range(warm_after):
                 step()
             ms_c, _, _ = timed(args.steps, False)
             nb = algorithmic_bytes(cfg, wl.block, C)["total"]
@@ -428,7 +434,9 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=200,
+                    help="untimed blocks before the timed ones (the GPU's clocks ramp up "
+                         "over the first ~0.1 s of continuous work)")
     ap.add_argument("--workload", default="dflash_27b")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--profile-steps", type=int, default=5)

@@ -1,7 +1,11 @@
 """Condense rocprofv3 output of a bench run into the short text kept under profiles/.
 
 Inputs (csv output of rocprofv3):
-  --stats   <dir>/<name>_kernel_stats.csv from ``--kernel-trace --stats``
+  --stats   <dir>/<name>_kernel_stats.csv from ``--kernel-trace --stats``, or
+  --trace   <dir>/<name>_kernel_trace.csv from ``--kernel-trace`` with ``--skip-blocks N``:
+            the durations of every dispatch except those of the first N draft blocks (the
+            bench's warmup, run while the GPU's clocks ramp up), so that the averages cover
+            the same blocks as the bench's timed region
   --fetch   <dir>/<name>_counter_collection.csv from ``--pmc FETCH_SIZE``
   --write   <dir>/<name>_counter_collection.csv from ``--pmc WRITE_SIZE``
 Both counter runs include a plain elementwise copy of known size (bench.py
@@ -59,6 +63,26 @@ def read_stats(path):
     return rows
 
 
+def read_trace(path, skip_blocks, block_rx):
+    """(calls, total ns) per kernel name from a kernel trace, leaving out the dispatches
+    from the first draft block's start (a dispatch matching block_rx) to the start of
+    block skip_blocks + 1; dispatches before the first block (context ingest) are kept."""
+    with open(path) as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    starts = [i for i, r in enumerate(rows) if re.search(block_rx, r["Kernel_Name"])]
+    lo = hi = 0
+    if skip_blocks > 0 and starts:
+        lo = starts[0]
+        hi = starts[skip_blocks] if skip_blocks < len(starts) else len(rows)
+    stats = {}
+    for i, r in enumerate(rows):
+        if lo <= i < hi:
+            continue
+        c, t = stats.get(r["Kernel_Name"], (0, 0.0))
+        stats[r["Kernel_Name"]] = (c + 1, t + int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    return stats
+
+
 def read_counter(path):
     per = collections.defaultdict(list)
     with open(path) as f:
@@ -73,7 +97,11 @@ def match(names, rx):
 
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    ap.add_argument("--stats", required=True)
+    ap.add_argument("--stats")
+    ap.add_argument("--trace")
+    ap.add_argument("--skip-blocks", type=int, default=0)
+    ap.add_argument("--block-start", default=r"embed_norm_kernel",
+                    help="regex of the first kernel of a draft block (trace mode)")
     ap.add_argument("--fetch")
     ap.add_argument("--write")
     ap.add_argument("--copy-mib", type=int, default=1024)
@@ -84,13 +112,18 @@ def main(argv=None):
     ap.add_argument("--json")
     a = ap.parse_args(argv)
 
-    stats = read_stats(a.stats)
+    if bool(a.stats) == bool(a.trace):
+        print("pass exactly one of --stats / --trace", file=sys.stderr)
+        return 2
+    stats = read_stats(a.stats) if a.stats else read_trace(a.trace, a.skip_blocks, a.block_start)
     out = [f"# rocprofv3 summary: {a.workload} draft block", ""]
     if a.note:
         out += [a.note, ""]
     if a.commands:
         out += ["Commands:", "", "```", a.commands.strip(), "```", ""]
-    out += ["## Kernel durations (--kernel-trace --stats)", "",
+    head = ("## Kernel durations (--kernel-trace --stats)" if a.stats else
+            f"## Kernel durations (--kernel-trace; the {a.skip_blocks} warmup blocks left out)")
+    out += [head, "",
             "| group | calls | avg us | total ms |", "|---|---:|---:|---:|"]
     for label, rx in GROUPS:
         ns = match(stats, rx)

@@ -183,3 +183,23 @@ def test_model_refuses_scaled_rope():
     cfg = DFlashConfig.from_dict({"hidden_size": 256, "rope_scaling": {"rope_type": "default"}})
     from mirror_sd_amd.config import require_unscaled_rope
     require_unscaled_rope(cfg)   # the default type is plain RoPE
+
+
+def test_rocprof_summary_trace_skips_warmup_blocks(tmp_path):
+    """Trace mode of the profile summariser: the dispatches of the first N blocks (from
+    the first block-start kernel to the start of block N + 1) are left out; dispatches
+    before the first block (context ingest) and after the warmup are averaged."""
+    from mirror_sd_amd import rocprof_summary as rs
+    seq = [("ingest_k", 100)] + [(k, d) for b in range(4)
+                                 for k, d in (("embed_norm_kernel", 10 + b), ("gemm_k", 50 + b))]
+    path = tmp_path / "t_kernel_trace.csv"
+    t, lines = 0, ["Kernel_Name,Start_Timestamp,End_Timestamp"]
+    for name, dur in seq:
+        lines.append(f"{name},{t},{t + dur}")
+        t += dur + 5
+    path.write_text("\n".join(lines) + "\n")
+    st = rs.read_trace(str(path), 2, r"embed_norm")
+    assert st == {"ingest_k": (1, 100.0), "embed_norm_kernel": (2, 12.0 + 13.0),
+                  "gemm_k": (2, 52.0 + 53.0)}
+    assert rs.read_trace(str(path), 0, r"embed_norm")["gemm_k"] == (4, 50.0 + 51 + 52 + 53)
+    assert rs.read_trace(str(path), 9, r"embed_norm") == {"ingest_k": (1, 100.0)}
