@@ -160,8 +160,7 @@ struct dfl_ctx {
   // fp16 fc and K|V rows
   uint4* w_fc_pk = nullptr;   // packed fc [H][NF*H] (KB = NF*H/16)
   half_t* si_in = nullptr;    // [SMALL_ING/32][32][max(NF,1)*H] fragment-layout input rows
-  half_t* si_fc = nullptr;    // [SMALL_ING][H] fc rows (fp16)
-  half_t* si_xn = nullptr;    // [SMALL_ING/32][32][H] fragment-layout hidden_norm rows
+  half_t* si_xn = nullptr;    // [SMALL_ING/32][32][H] fragment-layout fc rows (fp16)
   half_t* si_kv = nullptr;    // [SMALL_ING][NL*2*NKV*128] K|V rows of every layer (fp16, scaled)
   // the K|V rows of every layer side by side ([NL*2*NKV*128][H] packed int8 + scales), so
   // that one launch projects a per-step ingest's rows for all layers (a copy of 2*NKV*128
@@ -249,7 +248,6 @@ static int setup_ingest(dfl_ctx* x) {
   int r = DFL_OK;
   if ((r = x->alloc(&x->kv32, (size_t)x->ing * Nkv))) return r;
   if ((r = x->alloc(&x->si_in, (size_t)SMALL_ING * std::max(x->NF, 1) * H, true)) ||
-      (r = x->alloc(&x->si_fc, (size_t)SMALL_ING * H)) ||
       (r = x->alloc(&x->si_xn, (size_t)SMALL_ING * H, true)) ||
       (r = x->alloc(&x->si_kv, (size_t)SMALL_ING * x->NL * Nkv)) ||
       (r = x->alloc(&x->w_kv_all, (size_t)x->NL * Nkv * H / 16)) ||
@@ -518,7 +516,7 @@ static int skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const SKPlan& p,
                    int M, const half_t* gnorm, bool rn_from_ss, half_t* out, int ldo,
                    half_t* xres, float* logits, unsigned long long* keys, hipStream_t st,
                    int32_t* ids = nullptr, bool* ids_done = nullptr,
-                   const RopeEpi* rope = nullptr) {
+                   const RopeEpi* rope = nullptr, bool x_zero = false) {
   const long long wbytes = (wt == WT_INT8) ? (long long)N * KB * 32 + 2LL * N
                                            : (long long)N * KB * 16 * 2;
   const int ss_stride = (ctx->H / 64) * 32;
@@ -553,6 +551,7 @@ static int skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const SKPlan& p,
     a.out = out ? out + (size_t)m0 * ldo : nullptr;
     a.ldo = ldo;
     a.x = xres ? xres + (size_t)m0 * ldo : nullptr;
+    a.x_zero = x_zero;
     a.ss_part = ctx->sk_ss + (size_t)g0 * ss_stride;
     a.eps = ctx->cfg.rms_eps;
     a.logits = logits ? logits + (size_t)m0 * N : nullptr;
@@ -709,10 +708,13 @@ static int ingest_kv_rows(dfl_ctx* ctx, const half_t* xa, int rows, int r0, hipS
 }
 
 // Per-step ingest of C <= SMALL_ING context rows on the stream-K kernels: the rows (or the
-// tapped layers' features) into fragment layout; unless already fused, fc as an fp16 STORE
-// GEMM (each fc weight byte read once) and hidden_norm; then per layer the K|V rows of the
-// packed W8A16 qkv matrix as an int8 STORE GEMM (the Linear's scale and fp16 rounding in
-// its epilogue) and k_norm + RoPE into the cache.  Same arithmetic as the library path.
+// tapped layers' features) into fragment layout; unless already fused, fc as an fp16 GEMM
+// (each fc weight byte read once) whose RESID epilogue, with the residual taken as zero,
+// writes the fp16 Linear output in fragment layout and its per-tile row sums of squares;
+// then the K|V rows of every active layer as one int8 STORE GEMM that applies hidden_norm
+// as it loads those rows (norm-on-load, 1/rms from the fc's row sums; the Linear's scale
+// and fp16 rounding in its epilogue) and k_norm + RoPE into the cache.  The arithmetic of
+// the prompt-sized path (fp32 accumulation, the same rounding points).
 static int ingest_small(dfl_ctx* ctx, const half_t* in, int C, bool fused, const FeatPtrs* feats,
                         hipStream_t st) {
   const int H = ctx->H, NH = ctx->NH, NKV = ctx->NKV, Nkv = 2 * NKV * 128;
@@ -729,22 +731,22 @@ static int ingest_small(dfl_ctx* ctx, const half_t* in, int C, bool fused, const
     ProfScope ps(ctx, P_INGEST_FC, 0, st);
     launch_feats_to_afl(f, C, H, ctx->si_in, st);
   }
-  if (!fused) {
+  if (!fused) {   // fc rows (fp16, fragment layout) and their per-tile sums of squares
     const int K = ctx->NF * H;
-    DFL_TRY(skgemm(ctx, P_INGEST_FC, WT_F16, EPI_STORE, ctx->sk_fc, ctx->w_fc_pk, nullptr, H,
-                   K / 16, ctx->si_in, K, C, nullptr, false, ctx->si_fc, H, nullptr, nullptr,
-                   nullptr, st));
-    ProfScope ps(ctx, P_INGEST_FC, 0, st);
-    launch_rows_norm_afl(ctx->si_fc, H, C, H, ctx->hidden_norm, ctx->cfg.rms_eps, ctx->si_xn, st);
+    DFL_TRY(skgemm(ctx, P_INGEST_FC, WT_F16, EPI_RESID, ctx->sk_fc, ctx->w_fc_pk, nullptr, H,
+                   K / 16, ctx->si_in, K, C, nullptr, false, nullptr, H, ctx->si_xn, nullptr,
+                   nullptr, st, nullptr, nullptr, nullptr, /*x_zero=*/true));
     xsrc = ctx->si_xn;
   }
-  // the K|V rows of all active layers in one GEMM (the all-layer matrix), then k_norm + RoPE
-  // and the cache writes for up to SEQ_MAX layers per launch
+  // the K|V rows of all active layers in one GEMM (the all-layer matrix; hidden_norm on
+  // load unless the rows came fused), then k_norm + RoPE and the cache writes for up to
+  // SEQ_MAX layers per launch
   const int KB = H / 32;
   const int Nall = ctx->active * Nkv;
   DFL_TRY(skgemm(ctx, P_INGEST_KV, WT_INT8, EPI_STORE, streamk_plan(Nall, KB, ctx->n_cu),
-                 ctx->w_kv_all, ctx->s_kv_all, Nall, KB, xsrc, H, C, nullptr, false, ctx->si_kv,
-                 Nall, nullptr, nullptr, nullptr, st));
+                 ctx->w_kv_all, ctx->s_kv_all, Nall, KB, xsrc, H, C,
+                 fused ? nullptr : ctx->hidden_norm, !fused, ctx->si_kv, Nall, nullptr, nullptr,
+                 nullptr, st));
   for (int l0 = 0; l0 < ctx->active; l0 += SEQ_MAX) {
     const int nl = std::min(SEQ_MAX, ctx->active - l0);
     QKRopeArgs q{};

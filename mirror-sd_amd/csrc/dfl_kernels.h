@@ -54,6 +54,8 @@ struct StreamArgs {
   half_t* out;              // STORE: row-major [M][ldo] fp16; SWIGLU: fragment-layout tile [32][N/2]
   int ldo;
   half_t* x;                // RESID: residual stream, fragment-layout tile [32][N], updated in place
+  int x_zero;               // RESID: x is taken as zero and not read (x = fp16(y * s): a Linear
+                            // output in fragment layout with its per-tile row sums of squares)
   float* ss_part;           // RESID: [N/64][32] per-tile row sums of squares of the updated x
   float eps;
   float* logits;            // ARGMAX: optional [M][ldl] fp32
@@ -177,11 +179,8 @@ void launch_concat_feats(const FeatPtrs& f, int rows, int H, half_t* out, hipStr
 void launch_fc_norm_rows(const float* fc32, int rows, int H, const half_t* g, float eps,
                          half_t* xn, hipStream_t st);
 // Stream-K ingest inputs: concat_j(f_j) rows (f.n features of H columns, H % 8 == 0) into
-// activation fragment layout tiles [ceil(rows/32)][32][f.n*H], padding rows zero; and
-// hidden_norm of fp16 rows x [rows][H] (row stride ld) into tiles [ceil(rows/32)][32][H].
+// activation fragment layout tiles [ceil(rows/32)][32][f.n*H], padding rows zero.
 void launch_feats_to_afl(const FeatPtrs& f, int rows, int H, half_t* afl, hipStream_t st);
-void launch_rows_norm_afl(const half_t* x, int ld, int rows, int H, const half_t* g, float eps,
-                          half_t* afl, hipStream_t st);
 void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* noise, int B,
                        int H, int V, const half_t* g, float eps, half_t* x, half_t* h,
                        float* rnorm, int* err, hipStream_t st,

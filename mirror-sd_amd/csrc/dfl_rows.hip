@@ -169,46 +169,6 @@ void launch_feats_to_afl(const FeatPtrs& f, int rows, int H, half_t* afl, hipStr
                      0, st, f, H, rows, afl);
 }
 
-// hidden_norm of fp16 rows (the ingest's fc output): x [rows][H] (row stride ld) ->
-// fp16(fp16(x * r) * g) into activation fragment layout tiles [tiles][32][H]; rows in
-// [rows, 32 * tiles) are zero.
-__global__ __launch_bounds__(ROW_THREADS) void rows_norm_afl_kernel(
-    const half_t* __restrict__ x, int ld, int rows, int H, const half_t* __restrict__ g,
-    float eps, half_t* __restrict__ afl) {
-  __shared__ float red[16];
-  const int r = blockIdx.x;
-  if (r >= rows) {   // padding row: zero
-    for (int k = threadIdx.x; k < H; k += ROW_THREADS) afl[afl_index(r, k, H)] = (half_t)0.0f;
-    return;
-  }
-  float v[ROW_MAXV];
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < ROW_MAXV; ++i) {
-    const int k = threadIdx.x + i * ROW_THREADS;
-    v[i] = 0.f;
-    if (k < H) {
-      v[i] = h2f(x[(size_t)r * ld + k]);
-      ss += v[i] * v[i];
-    }
-  }
-  ss = block_sum(ss, red);
-  const float rr = 1.0f / sqrtf(ss / (float)H + eps);
-#pragma unroll
-  for (int i = 0; i < ROW_MAXV; ++i) {
-    const int k = threadIdx.x + i * ROW_THREADS;
-    if (k < H) afl[afl_index(r, k, H)] = rms_out(v[i], rr, g[k]);
-  }
-}
-
-void launch_rows_norm_afl(const half_t* x, int ld, int rows, int H, const half_t* g, float eps,
-                          half_t* afl, hipStream_t st) {
-  const int tiles = (rows + 31) / 32;
-  if (tiles == 0) return;
-  hipLaunchKernelGGL(rows_norm_afl_kernel, dim3(32 * tiles), dim3(ROW_THREADS), 0, st, x, ld, rows,
-                     H, g, eps, afl);
-}
-
 // hidden_norm(fc(.)) for the ingest: fc32 [rows][H] fp32 GEMM rows, rounded to fp16 (the
 // Linear output), then RMSNorm (fp16(fp16(x * r) * g)) into fragment-layout tiles xn
 // [ceil(rows/32)][32][H] (the K|V tile GEMM's input).

@@ -390,7 +390,8 @@ DFL_DEV EpiIn epi_prefetch(const StreamArgs& a, int lane, int t) {
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        in.xv[tt][q] = *reinterpret_cast<const half4_t*>(a.x + afl_offset(m, nb + 32 * tt + 8 * q));
+        in.xv[tt][q] = a.x_zero ? (half4_t){0, 0, 0, 0}
+                                : *reinterpret_cast<const half4_t*>(a.x + afl_offset(m, nb + 32 * tt + 8 * q));
   }
   return in;
 }
@@ -1274,6 +1275,10 @@ bool launch_streamk_gemm_m(int wt, int epi, bool norm, const StreamArgs& a, cons
   DFL_SKM_CASE(WT_F16, EPI_ARGMAX)
   DFL_SKM_CASE(WT_F16, EPI_STORE)
 #undef DFL_SKM_CASE
+  if (wt == WT_F16 && epi == EPI_RESID && !norm) {   // the per-step ingest's fc (x_zero)
+    launch_m_t<WT_F16, EPI_RESID, false>(a, p, st, ev_start, ev_stop);
+    return true;
+  }
   return false;
 }
 
@@ -1297,6 +1302,10 @@ bool launch_streamk_gemm(int wt, int epi, bool norm, const StreamArgs& a, const 
   DFL_SK_CASE(WT_INT8, EPI_SWIGLU)
   DFL_SK_CASE(WT_F16, EPI_ARGMAX)
   DFL_SK_CASE(WT_F16, EPI_STORE)
+  if (wt == WT_F16 && epi == EPI_RESID && !norm) {   // the per-step ingest's fc (x_zero)
+    launch_t<WT_F16, EPI_RESID, false>(a, p, st, ev_start, ev_stop);
+    return true;
+  }
   if (wt == WT_INT8 && epi == EPI_QKROPE && norm && a.M <= 32) {   // one sequence, one m-tile
     launch_t<WT_INT8, EPI_QKROPE, true>(a, p, st, ev_start, ev_stop);
     return true;
