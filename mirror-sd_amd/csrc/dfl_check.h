@@ -61,6 +61,7 @@ inline const char* check_stream_args(int wt, int epi, bool norm, const StreamArg
     default:
       return "unknown epilogue";
   }
+  if (a.x_zero && epi != EPI_RESID) return "a zero residual (x_zero) is a RESID option";
   if (p.dyn_static > 0 && (!a.dyn_next || !a.err || (a.KB & 1) || epi != EPI_ARGMAX))
     return "balanced plan needs work counters, an error word and an even k-block count";
   if (a.dp > 0 && ((long long)a.dp * p.workers > a.N / 64 || m_split))

@@ -48,6 +48,8 @@ int main() {
   { StreamArgs b = a; b.dp = 2; expect(check_stream_args(WT_INT8, EPI_RESID, false, b, p, false), "hybrid", "dp"); }
   { StreamArgs b = a; SKPlan q = p; q.dyn_static = 2; expect(check_stream_args(WT_F16, EPI_STORE, false, b, q, false), "balanced", "dyn"); }
   { StreamArgs b = a; b.ws = nullptr; expect(check_stream_args(WT_INT8, EPI_RESID, false, b, p, false), "workspace", "ws"); }
+  { StreamArgs b = a; b.x_zero = 1; expect(check_stream_args(WT_F16, EPI_RESID, false, b, p, false), nullptr, "x_zero RESID"); }
+  { StreamArgs b = a; b.x_zero = 1; expect(check_stream_args(WT_INT8, EPI_STORE, false, b, p, false), "x_zero", "x_zero STORE"); }
   { StreamArgs b = a; expect(check_stream_args(7, EPI_RESID, false, b, p, false), "weight type", "wt"); }
   { StreamArgs b = a; expect(check_stream_args(WT_INT8, 42, false, b, p, false), "epilogue", "epi"); }
 
