@@ -38,6 +38,14 @@ exactly (``q`` has 8 significant bits and ``s`` 11, so the product is exact in
 fp32 and fp64); ``y = (x @ q.T) * s`` is algebraically identical.  Logits are
 never rounded to fp16 before the argmax (ties broken by lowest index).
 
+Summation order: every dot product over the Linear input (``linear_w8``,
+``linear_dense``, ``lm_head_logits``) and over the keys (``sdpa_gqa``'s P.V) is one
+matmul by default.  Inside ``accumulation_split(n)`` each is summed over n contiguous
+ranges of its reduction axis, added in order -- the way a GPU GEMM splits k across
+workgroups.  In fp32 this changes only the rounding; the fixtures record the argmax of
+such runs so that a row whose argmax depends on the summation order (the oracle itself
+cannot decide it) is known.
+
 Parity status of each function is recorded in the tests that pin it
 (tests/test_oracle.py): all functions above are pinned by closed forms,
 invariants, brute force or library routines; the MLX-internal rounding inside
@@ -52,6 +60,42 @@ from typing import Dict, List, Optional, Tuple
 import numpy as np
 
 F64 = np.float64
+
+
+# ---------------------------------------------------------------------------
+# Summation order of the reduction matmuls
+# ---------------------------------------------------------------------------
+
+_SPLIT = [1]
+
+
+class accumulation_split:
+    """Context manager: sum each reduction matmul over n contiguous ranges (see above)."""
+
+    def __init__(self, n: int):
+        self.n = int(n)
+
+    def __enter__(self):
+        self.prev = _SPLIT[0]
+        _SPLIT[0] = self.n
+        return self
+
+    def __exit__(self, *exc):
+        _SPLIT[0] = self.prev
+        return False
+
+
+def _mm(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """a @ b, the reduction axis (a's last, b's first) summed in _SPLIT[0] ordered ranges."""
+    n = _SPLIT[0]
+    K = a.shape[-1]
+    if n <= 1 or K < n:
+        return a @ b
+    y = a[..., :K // n] @ b[:K // n]
+    for i in range(1, n):
+        lo, hi = K * i // n, K * (i + 1) // n
+        y = y + a[..., lo:hi] @ b[lo:hi]
+    return y
 
 
 # ---------------------------------------------------------------------------
@@ -153,7 +197,7 @@ def sdpa_gqa(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, fp16: bo
         s = s - s.max(axis=-1, keepdims=True)
         p = np.exp(s)
         p /= p.sum(axis=-1, keepdims=True)
-        out[h] = p @ v[g].astype(dtype)
+        out[h] = _mm(p, v[g].astype(dtype))
     return _r(out, fp16, dtype)
 
 
@@ -163,15 +207,15 @@ def linear_w8(x: np.ndarray, qs, fp16: bool, dtype=F64) -> np.ndarray:
     ``qs`` is (q, s) or a pre-dequantised dense [oc, ic] matrix.
     """
     if isinstance(qs, np.ndarray):
-        y = x.astype(dtype, copy=False) @ qs.T
+        y = _mm(x.astype(dtype, copy=False), qs.T)
     else:
         q, s = qs
-        y = (x.astype(dtype, copy=False) @ q.astype(dtype).T) * s.astype(dtype)[None, :]
+        y = _mm(x.astype(dtype, copy=False), q.astype(dtype).T) * s.astype(dtype)[None, :]
     return _r(y, fp16, dtype)
 
 
 def linear_dense(x: np.ndarray, w: np.ndarray, fp16: bool, dtype=F64) -> np.ndarray:
-    y = x.astype(dtype, copy=False) @ w.astype(dtype, copy=False).T
+    y = _mm(x.astype(dtype, copy=False), w.astype(dtype, copy=False).T)
     return _r(y, fp16, dtype)
 
 
@@ -376,7 +420,7 @@ def lm_head_logits(h: np.ndarray, w_lm: np.ndarray, dtype=F64, chunk: int = 1638
     h = h.astype(dtype)
     out = np.empty((h.shape[0], w_lm.shape[0]), dtype=dtype)
     for i in range(0, w_lm.shape[0], chunk):
-        out[:, i:i + chunk] = h @ w_lm[i:i + chunk].astype(dtype, copy=False).T
+        out[:, i:i + chunk] = _mm(h, w_lm[i:i + chunk].astype(dtype, copy=False).T)
     return out
 
 

@@ -29,10 +29,13 @@ The oracle runs in its fp16-boundary mode (the MLX rounding points) with fp32
 accumulation for the two full models, fp64 for the single layer.
 
 Every fixture with argmax ids also holds ``ids_f64`` / ``top2_val_f64``: the same forward
-with fp64 accumulation (same fp16 rounding points).  A row whose argmax differs between
-the two runs is decided by accumulation rounding alone; those rows are the only ones the
-GPU parity tests may exempt from exact argmax agreement.  ``--add-f64`` adds these arrays
-to existing fixtures without touching the rest.
+with fp64 accumulation (same fp16 rounding points), and ``ids_ksplit`` [len(KSPLITS), rows]:
+the fp32 forward with every reduction matmul summed over 2, 4 and 8 ordered ranges of its
+reduction axis (``dflash_oracle.accumulation_split``: how a GPU GEMM splits k, as rounding
+alone).  A row whose argmax differs between these runs is decided by accumulation
+rounding alone; those rows are the only ones the GPU parity tests may exempt from exact
+argmax agreement.  ``--add-f64`` / ``--add-ksplit`` add these arrays to existing fixtures
+without touching the rest.
 """
 
 from __future__ import annotations
@@ -87,6 +90,20 @@ def case_layer(name="qwen3_4b_layer", seed=0):
         input_digests(t, inp)
 
 
+KSPLITS = (2, 4, 8)
+
+
+def ksplit_ids(W, inp):
+    """[len(KSPLITS), rows] argmax ids of the fp32 forward in the other summation orders."""
+    out = []
+    for n in KSPLITS:
+        with O.accumulation_split(n):
+            _, _, ids = O.draft_block(W, inp["ids"], inp["target_hidden"], fp16=True,
+                                      dtype=np.float32)
+        out.append(ids.astype(np.int32))
+    return np.stack(out)
+
+
 def f64_outputs(W, inp):
     """ids and top-2 logits of the fp64-accumulation run (fp16 rounding points kept)."""
     _, logits, ids = O.draft_block(W, inp["ids"], inp["target_hidden"], fp16=True,
@@ -103,6 +120,8 @@ def case_full(name, seed=0, f64_only=False):
     dig = input_digests(t, inp)
     W = O.OracleWeights(cfg, t)
     del t
+    if f64_only == "ksplit":
+        return dict(ids_ksplit=ksplit_ids(W, inp)), dig
     ids64, tv64 = f64_outputs(W, inp)
     if f64_only:
         return dict(ids_f64=ids64, top2_val_f64=tv64), dig
@@ -110,7 +129,7 @@ def case_full(name, seed=0, f64_only=False):
                                    dtype=np.float32)
     ti, tv = top2(logits)
     return dict(hidden=h.astype(np.float16), ids=ids.astype(np.int32), top2_idx=ti,
-                top2_val=tv, ids_f64=ids64, top2_val_f64=tv64), dig
+                top2_val=tv, ids_f64=ids64, top2_val_f64=tv64, ids_ksplit=ksplit_ids(W, inp)), dig
 
 
 STEADY_BASE, STEADY_STEPS = 4096, (1, 16, 32)
@@ -133,6 +152,11 @@ def case_steady(name="dflash_27b_steady", seed=0, f64_only=False):
     for i, k in enumerate(STEADY_STEPS):
         n += k
         sub = {"ids": inp["ids"], "target_hidden": inp["target_hidden"][:n]}
+        if f64_only == "ksplit":
+            out[f"s{i}_ids_ksplit"] = ksplit_ids(W, sub)
+            print(f"{name}: step {i} ({n} context rows) done", flush=True)
+            continue
+        out[f"s{i}_ids_ksplit"] = ksplit_ids(W, sub)
         ids64, tv64 = f64_outputs(W, sub)
         out[f"s{i}_ids_f64"], out[f"s{i}_top2_val_f64"] = ids64, tv64
         if f64_only:
@@ -154,8 +178,11 @@ def case_batch(name="llama8b_batch", seed=0, f64_only=False):
     dig = input_digests(t, {f"{k}.s{i}": v for i, inp in enumerate(inps) for k, v in inp.items()})
     W = O.OracleWeights(cfg, t)
     del t
-    hs, idss, tis, tvs, i64s, v64s = [], [], [], [], [], []
+    hs, idss, tis, tvs, i64s, v64s, kss = [], [], [], [], [], [], []
     for inp in inps:
+        kss.append(ksplit_ids(W, inp))
+        if f64_only == "ksplit":
+            continue
         ids64, tv64 = f64_outputs(W, inp)
         i64s.append(ids64)
         v64s.append(tv64)
@@ -168,11 +195,14 @@ def case_batch(name="llama8b_batch", seed=0, f64_only=False):
         idss.append(ids.astype(np.int32))
         tis.append(ti)
         tvs.append(tv)
+    ks = dict(ids_ksplit=np.concatenate(kss, axis=1))
+    if f64_only == "ksplit":
+        return ks, dig
     f64 = dict(ids_f64=np.concatenate(i64s), top2_val_f64=np.concatenate(v64s))
     if f64_only:
         return f64, dig
     return dict(hidden=np.concatenate(hs), ids=np.concatenate(idss), top2_idx=np.concatenate(tis),
-                top2_val=np.concatenate(tvs), **f64), dig
+                top2_val=np.concatenate(tvs), **f64, **ks), dig
 
 
 CASES = {
@@ -189,15 +219,15 @@ ARGMAX_CASES = [n for n in CASES if n != "qwen3_4b_layer"]
 
 
 def main(argv):
-    add_f64 = "--add-f64" in argv
+    add = "ksplit" if "--add-ksplit" in argv else ("--add-f64" in argv)
     names = [a for a in argv if not a.startswith("--")] or \
-        (ARGMAX_CASES if add_f64 else list(CASES))
+        (ARGMAX_CASES if add else list(CASES))
     for n in names:
         t0 = time.time()
         path = os.path.join(HERE, f"{n}.npz")
-        out, dig = CASES[n](f64_only=add_f64)
+        out, dig = CASES[n](f64_only=add)
         keys = sorted(dig)
-        if add_f64:   # keep the stored outputs; the inputs must be the ones they came from
+        if add:   # keep the stored outputs; the inputs must be the ones they came from
             with np.load(path) as old:
                 kept = {k: old[k] for k in old.files}
             assert dict(zip(kept["digest_names"].tolist(),

@@ -5,7 +5,7 @@ sequence through the single-sequence forward.  Checked against the oracle per se
 (small shapes, oracle at test time) and, at the 8 x 32-row LLaMA-8B-class shape with
 contexts [4146, 4443, 6312, 7812, 779, 1619, 6833, 7798], against the committed fixture.
 Tolerances as for the single-sequence draft: hidden cosine >= 0.9995 and max-abs <= 2e-2,
-argmax identical except where the oracle's fp32- and fp64-accumulation runs disagree
+argmax identical except where the oracle's accumulation runs disagree
 (parity_util.check_argmax).
 """
 
@@ -18,7 +18,7 @@ from golden.make_golden import input_digests
 from mirror_sd_amd import synth
 from mirror_sd_amd.config import workload
 from oracle import dflash_oracle as O
-from parity_util import assert_close_fp16, check_argmax, torch_tensors
+from parity_util import assert_close_fp16, check_argmax, oracle_alt_runs, torch_tensors
 
 pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
@@ -142,5 +142,5 @@ def test_batch_full_matches_golden():
     M = ids_b.size
     assert_close_fp16(h.float().cpu().numpy().reshape(M, -1), g["hidden"], what=f"{name} hidden")
     check_argmax(ids.cpu().numpy().reshape(M), logits.cpu().numpy().reshape(M, -1), g["ids"],
-                 g["ids_f64"], name, g["top2_idx"], g["top2_val"], LOGIT_TOL)
+                 oracle_alt_runs(g), name, g["top2_idx"], g["top2_val"], LOGIT_TOL, noise_rule=True)
     m.close()

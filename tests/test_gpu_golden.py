@@ -5,9 +5,12 @@ The fixtures hold the oracle's outputs for the seeded synthetic inputs of
 block 16, context 2048) and the 27B-class headline draft (5 layers, H5120, block 32,
 context 4096), so the HIP path is checked at full size without running the oracle on
 the GPU host.  Tolerances: final hidden cosine >= 0.9995 and max-abs <= 2e-2 (fp16);
-argmax identical on every row except where the oracle itself is undecided (its fp32- and
-fp64-accumulation runs disagree, or its top-2 gap lies within 4 x the measured logit noise;
-parity_util.check_argmax states the rule and prints the counts); GPU logits at the
+argmax identical on every row except where the oracle itself is undecided: its runs that
+differ in accumulation only (fp32, fp64, and fp32 with every reduction summed over 2, 4 or
+8 ordered k-ranges, all stored in the fixture) do not all agree, and the GPU picked one of
+their ids; or, failing that, where the GPU picked the oracle's runner-up and the top-2 gap
+lies within 4 x the measured logit noise (parity_util.check_argmax states the rule and
+prints the counts of each kind); GPU logits at the
 oracle's top-2 indices within LOGIT_TOL of the oracle's values.
 """
 
@@ -19,7 +22,8 @@ import pytest
 from golden.make_golden import input_digests
 from mirror_sd_amd import synth
 from mirror_sd_amd.config import workload
-from parity_util import assert_close_fp16, check_argmax, device_errors, torch_tensors
+from parity_util import (assert_close_fp16, check_argmax, device_errors, oracle_alt_runs,
+                         torch_tensors)
 
 pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
@@ -71,7 +75,8 @@ def test_full_draft_matches_golden(name):
     assert_close_fp16(h.float().cpu().numpy(), g["hidden"], what=f"{name} final hidden")
     lg = logits.cpu().numpy()
     ids = ids.cpu().numpy()
-    check_argmax(ids, lg, g["ids"], g["ids_f64"], name, g["top2_idx"], g["top2_val"], LOGIT_TOL)
+    check_argmax(ids, lg, g["ids"], oracle_alt_runs(g), name, g["top2_idx"], g["top2_val"], LOGIT_TOL,
+                 noise_rule=True)
     # the lm_head hands half tiles out at run time from self-resetting counters: later
     # launches on the same inputs give the same bits, and no queue wait gave up
     for rep in range(2):
@@ -112,8 +117,8 @@ def sweep_model():
 
 def _check_against(g, name, ids, logits, h):
     assert_close_fp16(h.float().cpu().numpy(), g["hidden"], what=f"{name} final hidden")
-    check_argmax(ids.cpu().numpy(), logits.cpu().numpy(), g["ids"], g["ids_f64"], name,
-                 g["top2_idx"], g["top2_val"], LOGIT_TOL)
+    check_argmax(ids.cpu().numpy(), logits.cpu().numpy(), g["ids"], oracle_alt_runs(g), name,
+                 g["top2_idx"], g["top2_val"], LOGIT_TOL, noise_rule=True)
 
 
 @pytest.mark.parametrize("ctx", SWEEP)
@@ -180,8 +185,8 @@ def test_decode_loop_matches_golden():
         h, _, lg, idg = m._draft(ids=ids, want_logits=True, want_ids=True)
         torch.cuda.synchronize()
         assert_close_fp16(h.float().cpu().numpy(), g[f"s{i}_hidden"], what=f"{name} step {i} hidden")
-        check_argmax(idg.cpu().numpy(), lg.cpu().numpy(), g[f"s{i}_ids"], g[f"s{i}_ids_f64"],
+        check_argmax(idg.cpu().numpy(), lg.cpu().numpy(), g[f"s{i}_ids"], oracle_alt_runs(g, f"s{i}_"),
                      f"{name} step {i} ({n} context rows)", g[f"s{i}_top2_idx"],
-                     g[f"s{i}_top2_val"], LOGIT_TOL)
+                     g[f"s{i}_top2_val"], LOGIT_TOL, noise_rule=True)
     assert device_errors(m) == 0
     m.close()

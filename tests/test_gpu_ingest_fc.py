@@ -3,8 +3,8 @@ of the concatenated target_hidden, of the tapped layers or of strided slices of 
 buffers (any alignment) are gathered into fragment layout and the fc fusion projection
 runs on the tile GEMM over the packed fp16 fc weight.  Every variant matches the oracle
 within the draft tolerance, its argmax ids pass the suite's agreement rule (check_argmax:
-a row may differ only where the oracle's fp32 and fp64 runs disagree or the oracle's top-2
-gap is within the measured logit noise), and the variants agree with each other within
+a row may differ only where the oracle's fp32 and fp64 runs disagree), and the variants
+agree with each other within
 SAME_TOL."""
 
 import numpy as np

@@ -208,6 +208,35 @@ def test_linear_w8_exact_integer_and_onehot():
                                   q[:, 7].astype(np.float64) * s.astype(np.float64))
 
 
+def test_accumulation_split_orders():
+    """accumulation_split(n) sums a reduction over n ordered contiguous ranges: exact
+    integer sums are unchanged at every n, the fp32 result is the ordered sum of the range
+    products computed by hand, the default (and the state after the context) is one plain
+    matmul, and a ragged n (K not a multiple of n) still covers every k once."""
+    rng = np.random.default_rng(12)
+    w = (rng.standard_normal((12, 23)) * 0.02).astype(np.float32)
+    q, s = O.quantize_w8(w)
+    x = rng.integers(-3, 4, size=(3, 23)).astype(np.float64)
+    base = O.linear_w8(x, (q, s), False)
+    for n in (2, 3, 4, 8):
+        with O.accumulation_split(n):
+            np.testing.assert_array_equal(O.linear_w8(x, (q, s), False), base)
+    a = rng.standard_normal((5, 23)).astype(np.float32)
+    b = rng.standard_normal((23, 7)).astype(np.float32)
+    with O.accumulation_split(3):
+        got = O._mm(a, b)
+    want = ((a[:, 0:7] @ b[0:7]) + (a[:, 7:15] @ b[7:15])) + (a[:, 15:23] @ b[15:23])
+    np.testing.assert_array_equal(got, want)
+    np.testing.assert_allclose(got, a.astype(np.float64) @ b.astype(np.float64), rtol=1e-5,
+                               atol=1e-5)
+    np.testing.assert_array_equal(O._mm(a, b), a @ b)
+    with O.accumulation_split(4):
+        with O.accumulation_split(2):
+            assert O._SPLIT[0] == 2
+        assert O._SPLIT[0] == 4
+    assert O._SPLIT[0] == 1
+
+
 def test_mlp_zero_and_bruteforce():
     cfg = small_cfg()
     rng = np.random.default_rng(11)
