@@ -55,8 +55,11 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 // PIPE (one sequence, chunks of several stages, one workgroup of <= 5 waves per CU): two
 // stage buffers (160 KiB), the next stage's loads in flight while this one computes.
-template <bool PIPE>
-__global__ __launch_bounds__(PIPE ? 320 : 768) void block_attn_kernel(AttnArgs a) {
+// MAXW: the most waves a launch of the instantiation has.  Up to 5 waves (one per query
+// tile of the production shapes) the compiler has 2 waves' registers per SIMD and spills
+// nothing; the 12-wave instantiation (key-lane waves of small shapes) is held to 168.
+template <bool PIPE, int MAXW>
+__global__ __launch_bounds__(64 * MAXW) void block_attn_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
   const int g = blockIdx.y;
   const int lane = threadIdx.x & 63;
@@ -140,11 +143,30 @@ __global__ __launch_bounds__(PIPE ? 320 : 768) void block_attn_kernel(AttnArgs a
       const unsigned char* kb_lds = buf + j * AT_KBLK + koff * 256;
       const unsigned char* vb_lds = buf + AT_STAGE_BLOCKS * AT_KBLK + j * AT_VBLK;
       floatx16 s = {};
-      static_for<0, 8>([&](auto st) {
-        const u32x4 kf =
-            *reinterpret_cast<const u32x4*>(kb_lds + (((8 * gg + st) ^ kxor) << 4));
-        s = mfma32x32x16(as_half8(kf), qf[st], s);
-      });
+      u32x4 vf[4][2];
+      if constexpr (PIPE) {
+        // all eight K fragment reads in flight before the first product, and the V
+        // fragments read while the softmax runs (the two-buffer kernel has the registers)
+        u32x4 kf[8];
+        static_for<0, 8>([&](auto st) {
+          kf[st] = *reinterpret_cast<const u32x4*>(kb_lds + (((8 * gg + st) ^ kxor) << 4));
+        });
+        __builtin_amdgcn_sched_barrier(0);
+        static_for<0, 8>([&](auto st) { s = mfma32x32x16(as_half8(kf[st]), qf[st], s); });
+        static_for<0, 4>([&](auto dt) {
+          const unsigned char* vr = vb_lds + (dt * 32 + vrow) * 64;
+          const int vx = vswz(dt * 32 + vrow);
+          vf[dt][0] = *reinterpret_cast<const u32x4*>(vr + ((gg ^ vx) << 4));
+          vf[dt][1] = *reinterpret_cast<const u32x4*>(vr + (((gg + 2) ^ vx) << 4));
+        });
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+        static_for<0, 8>([&](auto st) {
+          const u32x4 kf =
+              *reinterpret_cast<const u32x4*>(kb_lds + (((8 * gg + st) ^ kxor) << 4));
+          s = mfma32x32x16(as_half8(kf), qf[st], s);
+        });
+      }
       // Accumulator r holds key kbase + (r < 8 ? 8*gg + r : 16 + 8*gg + r - 8).
       const int kbase = k0 + 32 * j;
       float psum = 0.f;
@@ -216,10 +238,16 @@ __global__ __launch_bounds__(PIPE ? 320 : 768) void block_attn_kernel(AttnArgs a
       }
       lrun += psum + __shfl_xor(psum, 32, 64);
       static_for<0, 4>([&](auto dt) {
-        const unsigned char* vr = vb_lds + (dt * 32 + vrow) * 64;
-        const int vx = vswz(dt * 32 + vrow);
-        const u32x4 v1 = *reinterpret_cast<const u32x4*>(vr + ((gg ^ vx) << 4));
-        const u32x4 v2 = *reinterpret_cast<const u32x4*>(vr + (((gg + 2) ^ vx) << 4));
+        u32x4 v1, v2;
+        if constexpr (PIPE) {
+          v1 = vf[dt][0];
+          v2 = vf[dt][1];
+        } else {
+          const unsigned char* vr = vb_lds + (dt * 32 + vrow) * 64;
+          const int vx = vswz(dt * 32 + vrow);
+          v1 = *reinterpret_cast<const u32x4*>(vr + ((gg ^ vx) << 4));
+          v2 = *reinterpret_cast<const u32x4*>(vr + (((gg + 2) ^ vx) << 4));
+        }
         o[dt] = mfma32x32x16(as_half8(v1), p1, o[dt]);
         o[dt] = mfma32x32x16(as_half8(v2), p2, o[dt]);
       });
@@ -348,12 +376,13 @@ bool launch_block_attention(const AttnArgs& a_in, hipStream_t st) {
   const bool pipe = a.n_seq == 1 && a.sq[0].chunk > 32 * AT_STAGE_BLOCKS && a.kw == 1 &&
                     a.q_per_group <= 5 && (long long)a.chunk0[1] * a.NKV * groups <= a.n_cu &&
                     a.lds_max >= 2 * AT_STAGE_BYTES;
+  const dim3 grid(a.chunk0[a.n_seq], a.NKV, groups), block(64 * a.q_per_group * a.kw);
   if (pipe)
-    hipLaunchKernelGGL(block_attn_kernel<true>, dim3(a.chunk0[a.n_seq], a.NKV, groups),
-                       dim3(64 * a.q_per_group), 2 * AT_STAGE_BYTES, st, a);
+    hipLaunchKernelGGL((block_attn_kernel<true, 5>), grid, block, 2 * AT_STAGE_BYTES, st, a);
+  else if (a.q_per_group * a.kw <= 5)
+    hipLaunchKernelGGL((block_attn_kernel<false, 5>), grid, block, lds_bytes, st, a);
   else
-    hipLaunchKernelGGL(block_attn_kernel<false>, dim3(a.chunk0[a.n_seq], a.NKV, groups),
-                       dim3(64 * a.q_per_group * a.kw), lds_bytes, st, a);
+    hipLaunchKernelGGL((block_attn_kernel<false, 12>), grid, block, lds_bytes, st, a);
   hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_seq * a.NH * a.B), dim3(128), 0, st, a);
   return true;
 }
