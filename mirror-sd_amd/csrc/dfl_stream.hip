@@ -361,6 +361,11 @@ DFL_DEV bool finish_split_tile(const StreamArgs& a, int lane, int t, int slot, i
   return true;
 }
 
+// 64 fp16 ones: the "scales" of a tile's epilogue over fp16 weights.
+__device__ __attribute__((aligned(16))) const half_t kOnes64[64] = {
+    1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1,
+    1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1};
+
 // Global inputs of a tile's epilogue, loaded ahead of it (before the reducer waits for
 // the streaming waves' partials) so that completing the launch's last tiles costs no load
 // latency: the per-row scales of the lane's 32 rows and, for RESID, its residual values.
@@ -374,15 +379,13 @@ DFL_DEV EpiIn epi_prefetch(const StreamArgs& a, int lane, int t) {
   EpiIn in;
   const int m = lane & 31, g = lane >> 5;
   const int nb = (2 * t) * 32 + 4 * g;
-  if (a.scale) {
+  // the scales, or ones for fp16 weights: one pointer, no branch (a branch here made the
+  // compiler keep the values in a scratch array on the tile's completion path)
+  const half_t* sp = a.scale ? a.scale + nb : kOnes64 + 4 * g;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      in.s0[q] = *reinterpret_cast<const half4_t*>(a.scale + nb + 8 * q);
-      in.s1[q] = *reinterpret_cast<const half4_t*>(a.scale + nb + 32 + 8 * q);
-    }
-  } else {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) in.s0[q] = in.s1[q] = (half4_t){1, 1, 1, 1};
+  for (int q = 0; q < 4; ++q) {
+    in.s0[q] = *reinterpret_cast<const half4_t*>(sp + 8 * q);
+    in.s1[q] = *reinterpret_cast<const half4_t*>(sp + 32 + 8 * q);
   }
   if constexpr (EPI == EPI_RESID) {
     // x is an AFL tile [32][N] (32 rows always allocated)
