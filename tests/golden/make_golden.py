@@ -112,7 +112,7 @@ def f64_outputs(W, inp):
     return ids.astype(np.int32), tv
 
 
-def case_full(name, seed=0, f64_only=False):
+def case_full(name, seed=0, only=None):
     wl = workload(name)
     cfg = wl.cfg
     t = synth.make_weights_numpy(cfg, seed=seed)
@@ -120,10 +120,10 @@ def case_full(name, seed=0, f64_only=False):
     dig = input_digests(t, inp)
     W = O.OracleWeights(cfg, t)
     del t
-    if f64_only == "ksplit":
+    if only == "ksplit":
         return dict(ids_ksplit=ksplit_ids(W, inp)), dig
     ids64, tv64 = f64_outputs(W, inp)
-    if f64_only:
+    if only == "f64":
         return dict(ids_f64=ids64, top2_val_f64=tv64), dig
     h, logits, ids = O.draft_block(W, inp["ids"], inp["target_hidden"], fp16=True,
                                    dtype=np.float32)
@@ -135,7 +135,7 @@ def case_full(name, seed=0, f64_only=False):
 STEADY_BASE, STEADY_STEPS = 4096, (1, 16, 32)
 
 
-def case_steady(name="dflash_27b_steady", seed=0, f64_only=False):
+def case_steady(name="dflash_27b_steady", seed=0, only=None):
     """The decode-loop protocol: the context grows by STEADY_STEPS rows after a 4096-row
     prefix; a draft after each step equals a single pass over the prefix (context K/V
     depend only on the fused context rows and their positions)."""
@@ -152,14 +152,14 @@ def case_steady(name="dflash_27b_steady", seed=0, f64_only=False):
     for i, k in enumerate(STEADY_STEPS):
         n += k
         sub = {"ids": inp["ids"], "target_hidden": inp["target_hidden"][:n]}
-        if f64_only == "ksplit":
+        if only != "f64":
             out[f"s{i}_ids_ksplit"] = ksplit_ids(W, sub)
+        if only == "ksplit":
             print(f"{name}: step {i} ({n} context rows) done", flush=True)
             continue
-        out[f"s{i}_ids_ksplit"] = ksplit_ids(W, sub)
         ids64, tv64 = f64_outputs(W, sub)
         out[f"s{i}_ids_f64"], out[f"s{i}_top2_val_f64"] = ids64, tv64
-        if f64_only:
+        if only == "f64":
             continue
         h, logits, ids = O.draft_block(W, sub["ids"], sub["target_hidden"], fp16=True,
                                        dtype=np.float32)
@@ -170,7 +170,7 @@ def case_steady(name="dflash_27b_steady", seed=0, f64_only=False):
     return out, dig
 
 
-def case_batch(name="llama8b_batch", seed=0, f64_only=False):
+def case_batch(name="llama8b_batch", seed=0, only=None):
     wl = workload(name)
     cfg = wl.cfg
     t = synth.make_weights_numpy(cfg, seed=seed)
@@ -180,13 +180,14 @@ def case_batch(name="llama8b_batch", seed=0, f64_only=False):
     del t
     hs, idss, tis, tvs, i64s, v64s, kss = [], [], [], [], [], [], []
     for inp in inps:
-        kss.append(ksplit_ids(W, inp))
-        if f64_only == "ksplit":
+        if only != "f64":
+            kss.append(ksplit_ids(W, inp))
+        if only == "ksplit":
             continue
         ids64, tv64 = f64_outputs(W, inp)
         i64s.append(ids64)
         v64s.append(tv64)
-        if f64_only:
+        if only == "f64":
             continue
         h, logits, ids = O.draft_block(W, inp["ids"], inp["target_hidden"], fp16=True,
                                        dtype=np.float32)
@@ -195,37 +196,38 @@ def case_batch(name="llama8b_batch", seed=0, f64_only=False):
         idss.append(ids.astype(np.int32))
         tis.append(ti)
         tvs.append(tv)
-    ks = dict(ids_ksplit=np.concatenate(kss, axis=1))
-    if f64_only == "ksplit":
-        return ks, dig
-    f64 = dict(ids_f64=np.concatenate(i64s), top2_val_f64=np.concatenate(v64s))
-    if f64_only:
+    f64 = dict(ids_f64=np.concatenate(i64s), top2_val_f64=np.concatenate(v64s)) if i64s else {}
+    if only == "f64":
         return f64, dig
+    ks = dict(ids_ksplit=np.concatenate(kss, axis=1))
+    if only == "ksplit":
+        return ks, dig
     return dict(hidden=np.concatenate(hs), ids=np.concatenate(idss), top2_idx=np.concatenate(tis),
                 top2_val=np.concatenate(tvs), **f64, **ks), dig
 
 
 CASES = {
-    "qwen3_4b_layer": lambda f64_only=False: case_layer("qwen3_4b_layer"),
-    "qwen3_8b_draft": lambda f64_only=False: case_full("qwen3_8b_draft", f64_only=f64_only),
-    "dflash_27b": lambda f64_only=False: case_full("dflash_27b", f64_only=f64_only),
-    **{f"dflash_27b_ctx{c}": (lambda f64_only=False, c=c:
-                              case_full(f"dflash_27b_ctx{c}", f64_only=f64_only))
+    "qwen3_4b_layer": lambda only=None: case_layer("qwen3_4b_layer"),
+    "qwen3_8b_draft": lambda only=None: case_full("qwen3_8b_draft", only=only),
+    "dflash_27b": lambda only=None: case_full("dflash_27b", only=only),
+    **{f"dflash_27b_ctx{c}": (lambda only=None, c=c:
+                              case_full(f"dflash_27b_ctx{c}", only=only))
        for c in (64, 2048, 16384, 32768)},
-    "llama8b_batch": lambda f64_only=False: case_batch("llama8b_batch", f64_only=f64_only),
-    "dflash_27b_steady": lambda f64_only=False: case_steady(f64_only=f64_only),
+    "llama8b_batch": lambda only=None: case_batch("llama8b_batch", only=only),
+    "dflash_27b_steady": lambda only=None: case_steady(only=only),
 }
 ARGMAX_CASES = [n for n in CASES if n != "qwen3_4b_layer"]
 
 
 def main(argv):
-    add = "ksplit" if "--add-ksplit" in argv else ("--add-f64" in argv)
+    # None: write whole fixtures; "f64" / "ksplit": add those runs' arrays to existing ones
+    add = "ksplit" if "--add-ksplit" in argv else ("f64" if "--add-f64" in argv else None)
     names = [a for a in argv if not a.startswith("--")] or \
         (ARGMAX_CASES if add else list(CASES))
     for n in names:
         t0 = time.time()
         path = os.path.join(HERE, f"{n}.npz")
-        out, dig = CASES[n](f64_only=add)
+        out, dig = CASES[n](only=add)
         keys = sorted(dig)
         if add:   # keep the stored outputs; the inputs must be the ones they came from
             with np.load(path) as old:
