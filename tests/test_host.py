@@ -203,3 +203,53 @@ def test_rocprof_summary_trace_skips_warmup_blocks(tmp_path):
                   "gemm_k": (2, 52.0 + 53.0)}
     assert rs.read_trace(str(path), 0, r"embed_norm")["gemm_k"] == (4, 50.0 + 51 + 52 + 53)
     assert rs.read_trace(str(path), 9, r"embed_norm") == {"ingest_k": (1, 100.0)}
+
+
+def test_argmax_agreement_rule():
+    """parity_util.check_argmax: a GPU id that differs from the oracle's fp32 run passes only
+    if another accumulation run of the oracle picked it (any row of alt_ids), or, with
+    noise_rule=True, if it is the oracle's runner-up and the top-2 gap is inside the
+    measured noise band; anything else raises.  The exact ids must be the logits' argmax."""
+    import copy
+    import parity_util as P
+    saved = copy.deepcopy(P.ARGMAX_TOTALS)   # synthetic rows stay out of the session totals
+    try:
+        _argmax_rule_cases(P)
+    finally:
+        P.ARGMAX_TOTALS.clear()
+        P.ARGMAX_TOTALS.update(saved)
+
+
+def _argmax_rule_cases(P):
+    rows, V = 6, 16
+    ref = np.arange(rows) % V
+    lg = np.zeros((rows, V))
+    lg[np.arange(rows), ref] = 1.0
+    ti = np.stack([ref, (ref + 1) % V], 1)
+    tv = np.take_along_axis(lg, ti, 1).copy()
+    tv[:, 1] = 0.5
+    ids = ref.copy()
+    # row 2: the GPU picks id 9, which the oracle's second alternative run also picked
+    ids[2] = 9
+    lg[2] = 0.0
+    lg[2, 9] = 1.0
+    alts = np.stack([ref, ref.copy()])
+    alts[1, 2] = 9
+    assert P.check_argmax(ids, lg, ref, alts, "alt run", ti, tv, 5.0) == (5, 6, 1)
+    with pytest.raises(AssertionError):
+        P.check_argmax(ids, lg, ref, alts[:1], "no run picked it", ti, tv, 5.0)
+    # row 4: the runner-up with a gap far inside the noise band: exempt only with the rule
+    ids2 = ref.copy()
+    ids2[4] = ti[4, 1]
+    lg2 = lg.copy()
+    lg2[2] = 0.0
+    lg2[2, ref[2]] = 1.0
+    lg2[4] = 0.0
+    lg2[4, ti[4, 1]] = 1.0
+    tv2 = tv.copy()
+    tv2[4] = [1.0, 1.0 - 1e-9]
+    with pytest.raises(AssertionError):
+        P.check_argmax(ids2, lg2, ref, ref, "strict", ti, tv2, 5.0)
+    assert P.check_argmax(ids2, lg2, ref, ref, "noise", ti, tv2, 5.0, noise_rule=True)[2] == 1
+    with pytest.raises(AssertionError):   # ids must be the argmax of the logits
+        P.check_argmax(ids, lg2, ref, alts, "not argmax", ti, tv, 5.0)
