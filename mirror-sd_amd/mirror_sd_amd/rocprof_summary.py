@@ -28,13 +28,17 @@ import sys
 
 # kernel groups: (label, regex on the kernel name)
 GROUPS = [
-    ("proj_gemm_w8a16", r"gsk_gemm_kernel<0, [0-9], (true|false), 4>"),
+    ("proj_gemm_w8a16", r"gsk_gemm_kernel<0, [145], (true|false), 4>"),
     ("qkv (norm-on-load; Q/K norm + RoPE + cache scatter in the epilogue)",
-     r"gsk_gemm_kernel<0, [35], true, 4>"),
+     r"gsk_gemm_kernel<0, 5, true, 4>"),
     ("o / down (RESID)", r"gsk_gemm_kernel<0, 4, false, 4>"),
     ("gate|up (SWIGLU, norm-on-load)", r"gsk_gemm_kernel<0, 1, true, 4>"),
     ("lm_head (fp16, ARGMAX, norm-on-load)", r"gsk_(gemm|dyn)_kernel<1, 2, true, 4>"),
     ("M-split stream-K (stacked rows up to 64)", r"gsk_gemm_m_kernel"),
+    ("per-step ingest fc (fp16, zero-residual RESID: rows + row sums)",
+     r"gsk_gemm_kernel<1, 4, false, 4>"),
+    ("per-step ingest K|V, all layers (int8 STORE, hidden_norm on load)",
+     r"gsk_gemm_kernel<0, 3, true, 4>"),
     ("tile GEMM int8, fp32 rows (stacked qkv; split-K planes of o, down; prompt-sized ingest K|V)",
      r"tile_gemm_kernel<0, 0,"),
     ("tile GEMM int8, RESID (stacked o, down without split-K)", r"tile_gemm_kernel<0, 1,"),
@@ -63,12 +67,17 @@ def read_stats(path):
     return rows
 
 
-def read_trace(path, skip_blocks, block_rx):
+def read_trace(path, skip_blocks, block_rx, from_rx=None, from_index=0):
     """(calls, total ns) per kernel name from a kernel trace, leaving out the dispatches
     from the first draft block's start (a dispatch matching block_rx) to the start of
-    block skip_blocks + 1; dispatches before the first block (context ingest) are kept."""
+    block skip_blocks + 1; dispatches before the first block (context ingest) are kept.
+    With from_rx, every dispatch before the from_index-th (0-based) one matching from_rx
+    is left out first."""
     with open(path) as f:
         rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    if from_rx:
+        hits = [i for i, r in enumerate(rows) if re.search(from_rx, r["Kernel_Name"])]
+        rows = rows[hits[from_index]:] if from_index < len(hits) else []
     starts = [i for i, r in enumerate(rows) if re.search(block_rx, r["Kernel_Name"])]
     lo = hi = 0
     if skip_blocks > 0 and starts:
@@ -102,6 +111,10 @@ def main(argv=None):
     ap.add_argument("--skip-blocks", type=int, default=0)
     ap.add_argument("--block-start", default=r"embed_norm_kernel",
                     help="regex of the first kernel of a draft block (trace mode)")
+    ap.add_argument("--from-kernel", default=None,
+                    help="trace mode: drop every dispatch before the --from-index-th one "
+                         "whose name matches this regex")
+    ap.add_argument("--from-index", type=int, default=0)
     ap.add_argument("--fetch")
     ap.add_argument("--write")
     ap.add_argument("--copy-mib", type=int, default=1024)
@@ -115,14 +128,18 @@ def main(argv=None):
     if bool(a.stats) == bool(a.trace):
         print("pass exactly one of --stats / --trace", file=sys.stderr)
         return 2
-    stats = read_stats(a.stats) if a.stats else read_trace(a.trace, a.skip_blocks, a.block_start)
+    stats = read_stats(a.stats) if a.stats else read_trace(a.trace, a.skip_blocks, a.block_start,
+                                                             a.from_kernel, a.from_index)
     out = [f"# rocprofv3 summary: {a.workload} draft block", ""]
     if a.note:
         out += [a.note, ""]
     if a.commands:
         out += ["Commands:", "", "```", a.commands.strip(), "```", ""]
     head = ("## Kernel durations (--kernel-trace --stats)" if a.stats else
-            f"## Kernel durations (--kernel-trace; the {a.skip_blocks} warmup blocks left out)")
+            f"## Kernel durations (--kernel-trace; the {a.skip_blocks} warmup blocks left out)"
+            if not a.from_kernel else
+            f"## Kernel durations (--kernel-trace; from dispatch {a.from_index} of "
+            f"{a.from_kernel} on)")
     out += [head, "",
             "| group | calls | avg us | total ms |", "|---|---:|---:|---:|"]
     for label, rx in GROUPS:

@@ -203,6 +203,9 @@ def test_rocprof_summary_trace_skips_warmup_blocks(tmp_path):
                   "gemm_k": (2, 52.0 + 53.0)}
     assert rs.read_trace(str(path), 0, r"embed_norm")["gemm_k"] == (4, 50.0 + 51 + 52 + 53)
     assert rs.read_trace(str(path), 9, r"embed_norm") == {"ingest_k": (1, 100.0)}
+    # from the 3rd gemm_k dispatch on (blocks 2 and 3), nothing else skipped
+    assert rs.read_trace(str(path), 0, r"embed_norm", r"gemm_k", 2) == {
+        "embed_norm_kernel": (1, 13.0), "gemm_k": (2, 52.0 + 53.0)}
 
 
 def test_argmax_agreement_rule():
