@@ -57,15 +57,22 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // stage buffers (160 KiB), the next stage's loads in flight while this one computes.
 // MAXW: the most waves a launch of the instantiation has.  Up to 5 waves (one per query
 // tile of the production shapes) the compiler has 2 waves' registers per SIMD and spills
-// nothing; the 12-wave instantiation (key-lane waves of small shapes) is held to 168.
+// nothing; the 12-wave instantiation (key-lane waves of small shapes) is held to 168.  The
+// two-buffer kernel with 5 query tiles runs on 8 waves (SPLIT below: 32K keys 1034 vs
+// 1050-1056 us per block).
 template <bool PIPE, int MAXW>
 __global__ __launch_bounds__(64 * MAXW) void block_attn_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
   const int g = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  const int KW = a.kw;
-  const int qtl = wv / KW, kwi = wv - qtl * KW;        // query tile in group, key lane
+  // SPLIT: the two-buffer kernel with 5 query tiles on 8 waves -- waves 0-3 take tiles 0-3
+  // whole, waves 4-7 the key blocks of tile 4 round-robin (at most 7 of a stage's 25
+  // tile-blocks per SIMD instead of 10); tile 4's four states merge in LDS at the end
+  constexpr bool SPLIT = PIPE && MAXW == 8;
+  const int KW = SPLIT ? (wv < 4 ? 1 : 4) : a.kw;
+  const int qtl = SPLIT ? (wv < 4 ? wv : 4) : wv / KW;   // query tile in group
+  const int kwi = SPLIT ? (wv < 4 ? 0 : wv - 4) : wv - qtl * KW;   // key lane
   const int ratio = a.NH / a.NKV;
   const int R = ratio * a.B;
   int sidx = 0;                                          // sequence of chunk blockIdx.x
@@ -265,8 +272,9 @@ __global__ __launch_bounds__(64 * MAXW) void block_attn_kernel(AttnArgs a) {
   __syncthreads();   // the stage buffers are reused by the merge
 
   // Merge the KW key lanes of each query tile (fixed order), then store the partial.
-  if (KW > 1) {
-    float* part = reinterpret_cast<float*>(lds) + (size_t)(qtl * (KW - 1)) * (AT_PART_BYTES / 4);
+  if (SPLIT || a.kw > 1) {   // (uniform over the workgroup: every wave reaches the barrier)
+    float* part = reinterpret_cast<float*>(lds) +
+                  (SPLIT ? 0 : (size_t)(qtl * (KW - 1)) * (AT_PART_BYTES / 4));
     if (kwi > 0) {
       float* my = part + (size_t)(kwi - 1) * (AT_PART_BYTES / 4);
       static_for<0, 4>([&](auto dt) {
@@ -377,7 +385,9 @@ bool launch_block_attention(const AttnArgs& a_in, hipStream_t st) {
                     a.q_per_group <= 5 && (long long)a.chunk0[1] * a.NKV * groups <= a.n_cu &&
                     a.lds_max >= 2 * AT_STAGE_BYTES;
   const dim3 grid(a.chunk0[a.n_seq], a.NKV, groups), block(64 * a.q_per_group * a.kw);
-  if (pipe)
+  if (pipe && a.q_per_group == 5)
+    hipLaunchKernelGGL((block_attn_kernel<true, 8>), grid, dim3(512), 2 * AT_STAGE_BYTES, st, a);
+  else if (pipe)
     hipLaunchKernelGGL((block_attn_kernel<true, 5>), grid, block, 2 * AT_STAGE_BYTES, st, a);
   else if (a.q_per_group * a.kw <= 5)
     hipLaunchKernelGGL((block_attn_kernel<false, 5>), grid, block, lds_bytes, st, a);
