@@ -139,34 +139,49 @@ void launch_concat_feats(const FeatPtrs& f, int rows, int H, half_t* out, hipStr
 // Context rows into activation fragment layout tiles for the stream-K ingest GEMMs: row r,
 // column k of concat_j(f_j) (feature j gives columns [j*H, (j+1)*H), read through its row
 // stride) goes to afl_index(r, k, K), K = f.n * H; rows in [rows, 32 * tiles) are zero.
-// One thread per 8 consecutive columns (16 bytes, contiguous in both layouts).
+// One workgroup per 32-row tile and 64-column slab, through LDS so that both sides are
+// contiguous: each row's 128 bytes are read by 8 lanes, and the slab's 4 fragment records
+// (4 KiB, consecutive in the layout) are written by one 16-byte store per lane.
+constexpr int AFL_SLAB = 64;
 __global__ __launch_bounds__(256) void feats_to_afl_kernel(FeatPtrs f, int H, int rows,
                                                            half_t* __restrict__ afl) {
-  const int r = blockIdx.y;
+  __shared__ __attribute__((aligned(16))) half_t tile[32][AFL_SLAB + 8];
   const int K = f.n * H;
-  const int k = (blockIdx.x * 256 + threadIdx.x) * 8;
-  if (k >= K) return;
-  u32x4 v = {0u, 0u, 0u, 0u};
-  if (r < rows) {
-    const int j = k / H;
-    const half_t* src = f.p[j] + (size_t)r * f.ld + (k - j * H);
-    if (!(reinterpret_cast<uintptr_t>(src) & 15)) {
-      v = *reinterpret_cast<const u32x4*>(src);
-    } else {   // a caller's buffer without 16-byte alignment: 2-byte loads
-      half8_t h;
+  const int t = blockIdx.y, k0 = blockIdx.x * AFL_SLAB, p = threadIdx.x;
+  {   // read: lane p takes row p / 8, columns k0 + 8 * (p % 8) .. + 7
+    const int m = p >> 3, c = 8 * (p & 7), k = k0 + c, r = t * 32 + m;
+    if (k < K) {
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (r < rows) {
+        const int j = k / H;
+        const half_t* src = f.p[j] + (size_t)r * f.ld + (k - j * H);
+        if (!(reinterpret_cast<uintptr_t>(src) & 15)) {
+          v = *reinterpret_cast<const u32x4*>(src);
+        } else {   // a caller's buffer without 16-byte alignment: 2-byte loads
+          half8_t h;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) h[i] = src[i];
-      v = __builtin_bit_cast(u32x4, h);
+          for (int i = 0; i < 8; ++i) h[i] = src[i];
+          v = __builtin_bit_cast(u32x4, h);
+        }
+      }
+      *reinterpret_cast<u32x4*>(&tile[m][c]) = v;
     }
   }
-  *reinterpret_cast<u32x4*>(afl + afl_index(r, k, K)) = v;
+  __syncthreads();
+  {   // write: lane p stores record p / 64 of the slab, lane slot p % 64
+    const int R = p >> 6, l = p & 63, m = l & 31;
+    const int c = 32 * (R >> 1) + 16 * (l >> 5) + 8 * (R & 1), k = k0 + c;
+    if (k < K)
+      *reinterpret_cast<u32x4*>(afl + afl_index(t * 32 + m, k, K)) =
+          *reinterpret_cast<const u32x4*>(&tile[m][c]);
+  }
 }
 
 void launch_feats_to_afl(const FeatPtrs& f, int rows, int H, half_t* afl, hipStream_t st) {
   const int tiles = (rows + 31) / 32;
   if (tiles == 0) return;
-  hipLaunchKernelGGL(feats_to_afl_kernel, dim3((f.n * H / 8 + 255) / 256, 32 * tiles), dim3(256),
-                     0, st, f, H, rows, afl);
+  hipLaunchKernelGGL(feats_to_afl_kernel, dim3((f.n * H + AFL_SLAB - 1) / AFL_SLAB, tiles),
+                     dim3(256), 0, st, f, H, rows, afl);
 }
 
 // hidden_norm(fc(.)) for the ingest: fc32 [rows][H] fp32 GEMM rows, rounded to fp16 (the
