@@ -204,6 +204,12 @@ int dfl_embed_block_noalloc(const int32_t* ids, int32_t B, const uint16_t* embed
                             int32_t V, int32_t top_k, uint16_t* out_noise, int32_t* err_flags,
                             void* stream);
 
+/* Test hook, no counterpart in the reference: on != 0 makes every work-queue wait of the
+ * balanced lm_head give up after a few hundred rounds (its bounded-wait path: every wave
+ * still ends, the ids of those calls are invalid and device error bit 2 is set); 0 restores
+ * normal operation.  Off when a context is created. */
+int dfl_test_queue_timeout(dfl_ctx* ctx, int32_t on);
+
 /* Sticky device-side error flags (bit 0: a token id outside [0, vocab); bit 1: soft-anchor
  * logits without a single number; bit 2: a work-queue wait of the lm_head gave up, its
  * results are invalid); reading clears. */

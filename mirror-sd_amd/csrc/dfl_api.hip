@@ -13,6 +13,7 @@
 #include "dflash_hip.h"
 #include "dfl_kernels.h"
 #include "dfl_check.h"
+#include "dfl_sk_plan.h"
 #include "dfl_tile_plan.h"
 
 using namespace dfl;
@@ -170,6 +171,7 @@ struct dfl_ctx {
   SKPlan sk_fc;
   std::vector<void*> allocs;
   int prof = 0;   // 0 off, 1 every kernel group, 2 stream-K GEMM launches only
+  int test_queue_timeout = 0;   // dfl_test_queue_timeout: balanced lm_head waits give up
   std::vector<ProfRec> recs;
 
   ~dfl_ctx() {
@@ -542,10 +544,12 @@ static int skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const SKPlan& p,
     a.gnorm = gnorm;
     a.ws = ctx->sk_ws;
     // one m-tile: the hybrid plan when it has whole tiles per workgroup; the M-split kernel
-    // keeps the contiguous partition
-    a.dp = mt_n == 1 ? p.dp : 0;
-    // test hook of the balanced kernel's bounded work-queue wait (its give-up path)
-    a.dyn_test_timeout = p.dyn_static > 0 && std::getenv("DFL_TEST_QUEUE_TIMEOUT") != nullptr;
+    // and the fused qkv kernel (a Q/K head's two tiles complete together) keep the
+    // contiguous partition
+    a.dp = streamk_launch_dp(p, epi, mt_n > 1);
+    // test hook of the balanced kernel's bounded work-queue wait (its give-up path), set
+    // only through dfl_test_queue_timeout
+    a.dyn_test_timeout = p.dyn_static > 0 && ctx->test_queue_timeout;
     a.seg_cap = a.dp > 0 ? p.sk_seg_cap : p.seg_cap;
     a.tile_cnt = ctx->sk_tile_cnt;
     a.out = out ? out + (size_t)m0 * ldo : nullptr;
@@ -1396,6 +1400,12 @@ int dfl_embed_block_noalloc(const int32_t* ids, int32_t B, const uint16_t* embed
                      logits_dtype, V, top_k, cand, reinterpret_cast<half_t*>(out_noise),
                      reinterpret_cast<int*>(err_flags), (hipStream_t)stream);
   return check_launch("dfl_embed_block_noalloc");
+}
+
+int dfl_test_queue_timeout(dfl_ctx* ctx, int32_t on) {
+  if (!ctx) return fail(DFL_EINVAL, "dfl_test_queue_timeout: null context");
+  ctx->test_queue_timeout = on != 0;
+  return DFL_OK;
 }
 
 int dfl_device_errors(dfl_ctx* ctx, int32_t* flags, void* stream) {

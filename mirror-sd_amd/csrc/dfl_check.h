@@ -66,6 +66,9 @@ inline const char* check_stream_args(int wt, int epi, bool norm, const StreamArg
     return "balanced plan needs work counters, an error word and an even k-block count";
   if (a.dp > 0 && ((long long)a.dp * p.workers > a.N / 64 || m_split))
     return "hybrid plan with more whole tiles than the matrix has";
+  // the fused qkv kernel completes a Q/K head's two tiles together over the contiguous
+  // stream-K partition only (its whole-tile loop runs the V-head epilogue)
+  if (a.dp > 0 && epi == EPI_QKROPE) return "QKROPE takes the contiguous partition (dp = 0)";
   return nullptr;
 }
 

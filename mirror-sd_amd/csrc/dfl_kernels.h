@@ -82,11 +82,8 @@ struct SKPlan {
                             // units of the first N/64 - dp * workers tiles
   int sk_seg_cap = 0;       // hybrid plan: workspace slots per split tile
 };
-SKPlan streamk_plan(int N, int KB, int n_cu);
-// Balanced plan for a long matrix (the lm_head): most tiles statically, whole, and the
-// rest in half tiles handed out at run time, so that CUs that stream faster take more.
-// Falls back to streamk_plan when the matrix has fewer than 2 tiles per CU.
-SKPlan streamk_plan_balanced(int N, int KB, int n_cu);
+// streamk_plan / streamk_plan_balanced (the partition of a matrix over the CUs) are in
+// dfl_sk_plan.h.
 // M-split variant for 2 <= MT <= 8 m-tiles (M <= 256 rows): every weight block is read
 // once for all m-tiles.  X, out, x, ss_*, rnorm, logits, keys point at m-tile 0; m-tile mt
 // is 32*mt rows further (ss blocks ss_mstride floats further).  ws holds

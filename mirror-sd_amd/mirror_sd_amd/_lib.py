@@ -78,6 +78,7 @@ SIGNATURES = {
                                           c_int32, c_int32, c_int32, c_void_p, c_void_p,
                                           c_void_p]),
     "dfl_device_errors": (c_int32, [c_void_p, ctypes.POINTER(c_int32), c_void_p]),
+    "dfl_test_queue_timeout": (c_int32, [c_void_p, c_int32]),
 }
 
 _lib = None

@@ -5,6 +5,7 @@
 #include <cstring>
 
 #include "dfl_check.h"
+#include "dfl_sk_plan.h"
 #include "dfl_tile_plan.h"
 
 using namespace dfl;
@@ -52,6 +53,35 @@ int main() {
   { StreamArgs b = a; b.x_zero = 1; expect(check_stream_args(WT_INT8, EPI_STORE, false, b, p, false), "x_zero", "x_zero STORE"); }
   { StreamArgs b = a; expect(check_stream_args(7, EPI_RESID, false, b, p, false), "weight type", "wt"); }
   { StreamArgs b = a; expect(check_stream_args(WT_INT8, 42, false, b, p, false), "epilogue", "epi"); }
+
+  {   // the fused qkv launch (QKROPE) keeps the contiguous partition at every CU count,
+      // also where the plan has whole tiles per workgroup (dp > 0): 27B qkv (112 tiles) on
+      // <= 112 CUs, or 128 q|k|v heads (256 tiles) on 256 CUs
+    StreamArgs r = a;
+    r.N = 7168; r.KB = 160; r.scale = (const half_t*)P;
+    r.rope.NH = 40; r.rope.NKV = 8; r.rope.Q = (half_t*)P; r.rope.cs = (const float*)P;
+    r.rope.q_norm = (const half_t*)P; r.rope.k_norm = (const half_t*)P;
+    r.rope.sq.Kc = (half_t*)P; r.rope.sq.Vt = (half_t*)P; r.rope.cap = 4128;
+    const int heads[][2] = {{40, 8}, {32, 8}, {96, 16}};
+    const int cus[] = {32, 64, 80, 104, 112, 200, 256, 304};
+    for (const auto& hk : heads)
+      for (int ncu : cus) {
+        StreamArgs b = r;
+        b.rope.NH = hk[0]; b.rope.NKV = hk[1]; b.N = (hk[0] + 2 * hk[1]) * 128;
+        const SKPlan sp = streamk_plan(b.N, b.KB, ncu);
+        b.dp = streamk_launch_dp(sp, EPI_QKROPE, false);
+        b.seg_cap = b.dp > 0 ? sp.sk_seg_cap : sp.seg_cap;
+        char what[96];
+        std::snprintf(what, sizeof what, "QKROPE launch %d/%d heads on %d CUs", hk[0], hk[1], ncu);
+        if (b.dp != 0) expect("dp > 0", nullptr, what);
+        expect(check_stream_args(WT_INT8, EPI_QKROPE, true, b, sp, false), nullptr, what);
+        // the other epilogues take the hybrid plan whenever it has whole tiles
+        if (streamk_launch_dp(sp, EPI_STORE, false) != sp.dp) expect("store dp", nullptr, what);
+        if (streamk_launch_dp(sp, EPI_STORE, true) != 0) expect("m-split dp", nullptr, what);
+      }
+    { StreamArgs b = r; b.dp = 1; SKPlan sp = streamk_plan(7168, 160, 64); b.seg_cap = sp.sk_seg_cap;
+      expect(check_stream_args(WT_INT8, EPI_QKROPE, true, b, sp, false), "QKROPE", "QKROPE with dp > 0"); }
+  }
 
   QKRopeArgs q{};
   q.qkv16 = (const half_t*)P; q.M = 32; q.N = 7168; q.n_seq = 1; q.col_slot0 = 0; q.slot0 = 0;

@@ -356,11 +356,12 @@ def test_capacity_boundaries():
                           what=f"layer {layer} values")
 
 
-def test_lm_head_queue_give_up_reports_error_and_recovers(monkeypatch):
+def test_lm_head_queue_give_up_reports_error_and_recovers():
     """The balanced lm_head's bounded work-queue wait: forced to give up from the host
-    (DFL_TEST_QUEUE_TIMEOUT makes its wait condition unsatisfiable for a few hundred
-    rounds), every wave still ends, device error bit 2 is set, and the next call -- its
-    self-resetting counters re-armed -- gives the same results as before."""
+    (the dfl_test_queue_timeout hook makes its wait condition unsatisfiable for a few
+    hundred rounds), every wave still ends, device error bit 2 is set, and the next call --
+    its self-resetting counters re-armed -- gives the same results as before."""
+    from mirror_sd_amd import _lib
     from parity_util import device_errors
     cfg = DFlashConfig(hidden_size=256, num_hidden_layers=1, intermediate_size=512,
                        num_attention_heads=4, num_key_value_heads=2, head_dim=128,
@@ -374,11 +375,14 @@ def test_lm_head_queue_give_up_reports_error_and_recovers(monkeypatch):
     torch.cuda.synchronize()
     assert device_errors(m) == 0
     ids, lg = ids.cpu().numpy(), lg.cpu().numpy()
-    monkeypatch.setenv("DFL_TEST_QUEUE_TIMEOUT", "1")
-    m.draft(torch.from_numpy(inp["ids"]), torch.from_numpy(inp["target_hidden"]))
-    torch.cuda.synchronize()
+    L = _lib.load()
+    _lib.check(L.dfl_test_queue_timeout(m._ctx, 1), "dfl_test_queue_timeout")
+    try:
+        m.draft(torch.from_numpy(inp["ids"]), torch.from_numpy(inp["target_hidden"]))
+        torch.cuda.synchronize()
+    finally:
+        _lib.check(L.dfl_test_queue_timeout(m._ctx, 0), "dfl_test_queue_timeout")
     assert device_errors(m) & 4
-    monkeypatch.delenv("DFL_TEST_QUEUE_TIMEOUT")
     for _ in range(2):
         ids2, lg2 = m.draft(torch.from_numpy(inp["ids"]), torch.from_numpy(inp["target_hidden"]),
                             return_logits=True)
@@ -389,11 +393,12 @@ def test_lm_head_queue_give_up_reports_error_and_recovers(monkeypatch):
     m.close()
 
 
-@pytest.mark.parametrize("n_heads", [24, 32])
+@pytest.mark.parametrize("n_heads", [24, 32, 40])
 def test_two_stage_attention_with_sink_window_matches_oracle(n_heads):
     """Long single-sequence contexts run the attention with two LDS stage buffers (chunks of
-    more than 160 keys, one workgroup per CU): here with 3 and 4 query tiles per KV head
-    (24 / 32 query heads over 8 KV heads, block 32) and a sink + window ring whose chunks
+    more than 160 keys, one workgroup per CU): here with 3, 4 and 5 query tiles per KV head
+    (24 / 32 / 40 query heads over 8 KV heads, block 32; 5 tiles is the 27B-class shape,
+    whose last query tile runs over 4 waves merged in LDS) and a sink + window ring whose chunks
     span several stages, against the oracle's windowed cache over two steps (the second
     evicts middle rows; 64 + 6400 keys are live)."""
     cfg = DFlashConfig(hidden_size=256, num_hidden_layers=1, intermediate_size=512,
