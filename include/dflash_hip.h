@@ -155,6 +155,16 @@ int dfl_cache_set_window(dfl_ctx* ctx, int32_t sink, int32_t window);
 /* Set the absolute position of the next context row without touching cached rows
  * (the ANE caller assigns cache.offset directly, generate.py:1409-1417). */
 int dfl_cache_set_offset(dfl_ctx* ctx, int64_t offset);
+/* Assign one layer's cache (c_new.keys = c_old.keys / .values in generate.py:917-941;
+ * DFlashKVCache.keys / .values, dflash.py:161-162): keys and values are [NKV][L][128] fp16
+ * device rows in the reference's order (post-RoPE keys, values), either may be NULL (then
+ * that half is left as it is).  The sequence's cache then holds these L rows -- with a sink +
+ * window, L > sink + window keeps the first sink and the newest window rows, as the
+ * reference's next update_and_fetch does.  The offset is not changed (set it with
+ * dfl_cache_set_offset).  The cached row count is shared by all layers of the sequence:
+ * assign every layer with the same L. */
+int dfl_cache_assign(dfl_ctx* ctx, int32_t layer, const uint16_t* keys, const uint16_t* values,
+                     int32_t L, void* stream);
 /* Current cached rows and absolute position offset. */
 int dfl_cache_state(const dfl_ctx* ctx, int32_t* len, int64_t* offset);
 /* Device pointers of layer `layer`'s cache: K [NKV][cap][128], Vt [NKV][128][cap]. */
@@ -203,6 +213,18 @@ int dfl_embed_block_noalloc(const int32_t* ids, int32_t B, const uint16_t* embed
                             int32_t H, const void* correction_logits, int32_t logits_dtype,
                             int32_t V, int32_t top_k, uint16_t* out_noise, int32_t* err_flags,
                             void* stream);
+
+/* Scaled RoPE (the scaling_config of mlx_lm's initialize_rope, called by
+ * Qwen3DFlashAttention, dflash.py:254-261): type DFL_ROPE_DEFAULT (unscaled, the state after
+ * dfl_create), DFL_ROPE_LINEAR (positions divided by factor) or DFL_ROPE_LLAMA3 (Llama 3.1:
+ * frequencies of wavelength above original_max_position_embeddings / low_freq_factor divided
+ * by factor, below original / high_freq_factor kept, smooth in between).  The other
+ * arguments are unused for the default type. */
+#define DFL_ROPE_DEFAULT 0
+#define DFL_ROPE_LINEAR 1
+#define DFL_ROPE_LLAMA3 2
+int dfl_set_rope_scaling(dfl_ctx* ctx, int32_t type, double factor, double low_freq_factor,
+                         double high_freq_factor, int32_t original_max_position_embeddings);
 
 /* Test hook, no counterpart in the reference: on != 0 makes every work-queue wait of the
  * balanced lm_head give up after a few hundred rounds (its bounded-wait path: every wave

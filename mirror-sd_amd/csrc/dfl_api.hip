@@ -145,6 +145,11 @@ struct dfl_ctx {
   half_t* qkvbuf = nullptr;      // [RM][NQKV] fp16 projections
   float* rnorm = nullptr;        // [RM] 1/rms of the residual rows
   float* rope_cs = nullptr;      // [32][64][2] RoPE cos, sin of a block's rows (one sequence)
+  // scaled RoPE (dfl_set_rope_scaling): the 64 frequencies, fp64; unscaled RoPE computes
+  // theta^(-j/64) in the kernels
+  double* rope_inv = nullptr;
+  bool rope_scaled = false;
+  const double* rope_freqs() const { return rope_scaled ? rope_inv : nullptr; }
   float* sk_ws = nullptr;        // split-tile partials
   int* sk_tile_cnt = nullptr;    // [max tiles]
   int* dyn_next = nullptr;       // [2] work counters of the balanced lm_head (self-resetting)
@@ -364,6 +369,7 @@ int dfl_create(const dfl_config* cfg, dfl_ctx** out) {
     if ((r = x->alloc(&x->qkvbuf, Bm * x->NQKV)) || (r = x->alloc(&x->rnorm, bm32)) ||
         (r = x->alloc(&x->sk_ws, wsn)) || (r = x->alloc(&x->sk_tile_cnt, tiles, true)) ||
         (r = x->alloc(&x->dyn_next, 2, true)) || (r = x->alloc(&x->rope_cs, 32 * 64 * 2)) ||
+        (r = x->alloc(&x->rope_inv, 64)) ||
         (r = x->alloc(&x->sk_ss, (bm32 / 32) * (size_t)(x->H / 32) * 32))) {
       delete x;
       return r;
@@ -702,6 +708,7 @@ static int ingest_kv_rows(dfl_ctx* ctx, const half_t* xa, int rows, int r0, hipS
     q.k_norm = L.k_norm;
     q.eps = ctx->cfg.rms_eps;
     q.log2_theta = std::log2(ctx->cfg.rope_theta);
+    q.inv_freq = ctx->rope_freqs();
     q.Q = nullptr;
     q.cap = ctx->cap;
     rope_seq(ctx, ctx->cur, L, ctx->sq().offset + r0, rows, q.sq[0]);
@@ -768,6 +775,7 @@ static int ingest_small(dfl_ctx* ctx, const half_t* in, int C, bool fused, const
     q.k_norm = ctx->layers[l0].k_norm;
     q.eps = ctx->cfg.rms_eps;
     q.log2_theta = std::log2(ctx->cfg.rope_theta);
+    q.inv_freq = ctx->rope_freqs();
     q.Q = nullptr;
     q.cap = ctx->cap;
     for (int i = 0; i < nl; ++i) {
@@ -938,7 +946,7 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
     launch_embed_norm(ids, ctx->embed, reinterpret_cast<const half_t*>(noise_emb), M, H, ctx->V,
                       ctx->layers[0].in_norm, eps, ctx->x, nullptr, ctx->rnorm, ctx->err, st,
                       fuse_rope ? ctx->rope_cs : nullptr, ctx->seqs[seq0].offset,
-                      std::log2(ctx->cfg.rope_theta));
+                      std::log2(ctx->cfg.rope_theta), ctx->rope_freqs());
   }
 
   // Attention key split.  One sequence: about one workgroup per CU ((chunks x KV heads) ~
@@ -1025,6 +1033,8 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
       q.k_norm = Ly.k_norm;
       q.eps = eps;
       q.log2_theta = std::log2(ctx->cfg.rope_theta);
+      q.inv_freq = ctx->rope_freqs();
+    q.inv_freq = ctx->rope_freqs();
       q.Q = ctx->Q + (size_t)g0 * NH * B * 128;
       q.cap = ctx->cap;
       AttnArgs at{};
@@ -1400,6 +1410,82 @@ int dfl_embed_block_noalloc(const int32_t* ids, int32_t B, const uint16_t* embed
                      logits_dtype, V, top_k, cand, reinterpret_cast<half_t*>(out_noise),
                      reinterpret_cast<int*>(err_flags), (hipStream_t)stream);
   return check_launch("dfl_embed_block_noalloc");
+}
+
+int dfl_set_rope_scaling(dfl_ctx* ctx, int32_t type, double factor, double low_freq_factor,
+                         double high_freq_factor, int32_t original_max_position_embeddings) {
+  if (!ctx) return fail(DFL_EINVAL, "dfl_set_rope_scaling: null context");
+  if (type == DFL_ROPE_DEFAULT) {
+    ctx->rope_scaled = false;
+    return DFL_OK;
+  }
+  if (type != DFL_ROPE_LINEAR && type != DFL_ROPE_LLAMA3)
+    return fail(DFL_EINVAL, "dfl_set_rope_scaling: unknown RoPE type " + std::to_string(type));
+  if (!(factor > 0.0)) return fail(DFL_EINVAL, "dfl_set_rope_scaling: factor must be positive");
+  if (type == DFL_ROPE_LLAMA3 &&
+      (!(high_freq_factor > low_freq_factor) || !(low_freq_factor > 0.0) ||
+       original_max_position_embeddings <= 0))
+    return fail(DFL_EINVAL, "dfl_set_rope_scaling: llama3 needs 0 < low_freq_factor < "
+                            "high_freq_factor and a positive original context length");
+  const double theta = ctx->cfg.rope_theta;
+  const double pi = 3.14159265358979323846;
+  double f[64];
+  for (int j = 0; j < 64; ++j) {
+    // the unscaled frequency of pair j, theta^(-2j/128), as the kernels compute it
+    const double base = std::exp2(-(double)j * (1.0 / 64.0) * std::log2(theta));
+    if (type == DFL_ROPE_LINEAR) {   // positions scaled by 1 / factor
+      f[j] = base / factor;
+      continue;
+    }
+    // llama3 (Llama 3.1): wavelengths above original / low_freq_factor are stretched by
+    // factor, those below original / high_freq_factor kept, and the band between
+    // interpolated smoothly in the frequency
+    const double old_len = (double)original_max_position_embeddings;
+    const double low_wavelen = old_len / low_freq_factor, high_wavelen = old_len / high_freq_factor;
+    const double wavelen = 2.0 * pi / base;
+    if (wavelen > low_wavelen) {
+      f[j] = base / factor;
+    } else if (wavelen > high_wavelen && wavelen < low_wavelen) {
+      const double s = (old_len / wavelen - low_freq_factor) / (high_freq_factor - low_freq_factor);
+      f[j] = base * ((1.0 - s) / factor + s);
+    } else {
+      f[j] = base;
+    }
+  }
+  DFL_HIP(hipMemcpy(ctx->rope_inv, f, sizeof f, hipMemcpyHostToDevice));
+  ctx->rope_scaled = true;
+  return DFL_OK;
+}
+
+int dfl_cache_assign(dfl_ctx* ctx, int32_t layer, const uint16_t* keys, const uint16_t* values,
+                     int32_t L, void* stream) {
+  if (!ctx) return fail(DFL_EINVAL, "dfl_cache_assign: null context");
+  if (layer < 0 || layer >= ctx->NL) return fail(DFL_ERANGE, "dfl_cache_assign: layer out of range");
+  if (L < 0) return fail(DFL_EINVAL, "dfl_cache_assign: negative row count");
+  if (L > 0 && !keys && !values) return fail(DFL_EINVAL, "dfl_cache_assign: no keys or values");
+  SeqState& q = ctx->sq();
+  // a sink + window cache keeps its first sink rows and newest window rows (the reference's
+  // next update_and_fetch applies the same window before any attention reads the rows)
+  int keep_head = L, keep_tail = 0;
+  if (q.window && L > q.sink + q.window) {
+    keep_head = q.sink;
+    keep_tail = q.window;
+  }
+  const int kept = keep_head + keep_tail;
+  if (kept > ctx->cfg.max_ctx)
+    return fail(DFL_ERANGE, "dfl_cache_assign: " + std::to_string(kept) +
+                                " rows exceed the cache capacity max_ctx " +
+                                std::to_string(ctx->cfg.max_ctx));
+  const Layer& Ly = ctx->layers[layer];
+  launch_cache_assign(reinterpret_cast<const half_t*>(keys), reinterpret_cast<const half_t*>(values),
+                      ctx->NKV, L, keep_head, keep_tail, ctx->kc(Ly, ctx->cur), ctx->vt(Ly, ctx->cur),
+                      ctx->cap, (hipStream_t)stream);
+  DFL_TRY(check_launch("dfl_cache_assign"));
+  // rows in order: the sink rows, then the window rows from ring slot 0
+  q.len = kept;
+  q.ring_j = q.window ? std::max(0, kept - q.sink) : 0;
+  q.last_block = 0;
+  return DFL_OK;
 }
 
 int dfl_test_queue_timeout(dfl_ctx* ctx, int32_t on) {

@@ -181,7 +181,16 @@ void launch_feats_to_afl(const FeatPtrs& f, int rows, int H, half_t* afl, hipStr
 void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* noise, int B,
                        int H, int V, const half_t* g, float eps, half_t* x, half_t* h,
                        float* rnorm, int* err, hipStream_t st,
-                       float* rope_cs = nullptr, long long pos0 = 0, double log2_theta = 0.0);
+                       float* rope_cs = nullptr, long long pos0 = 0, double log2_theta = 0.0,
+                       const double* inv_freq = nullptr);
+// A layer's cache set to L rows in the reference's row order: k and v are [NKV][L][128] fp16
+// (DFlashKVCache.keys / .values of one sequence, [1, NKV, L, D]); row r of the source goes to
+// cache row dst_row(r) = r for r < keep_head, else r - (L - keep_tail) + keep_head for the
+// last keep_tail rows (the rows between are dropped: a sink + window cache keeps its first
+// keep_head = sink rows and its newest keep_tail = window rows); k -> Kc rows, v -> Vt
+// columns.  Either of k / v may be null.
+void launch_cache_assign(const half_t* k, const half_t* v, int NKV, int L, int keep_head,
+                         int keep_tail, half_t* Kc, half_t* Vt, int cap, hipStream_t st);
 // x in the activation fragment layout (afl_index) [M][N] -> h [M][N], row-major or (h_afl)
 // fragment layout: h = fp16(fp16(x * r[m]) * g[n])  (apply_norm), or a plain row-major copy
 // (afl_to_rows).  r[m] = 1/rms of row m from ss [M/32 m-tiles][ss_tiles][32] (row sums of
@@ -215,6 +224,8 @@ struct QKRopeArgs {
   int NH, NKV;
   const half_t* q_norm; const half_t* k_norm; float eps;
   double log2_theta;
+  const double* inv_freq;                    // [64] scaled RoPE frequencies, or nullptr:
+                                             // theta^(-j/64) from log2_theta
   half_t* Q;
   int cap;
   RopeSeq sq[SEQ_MAX];

@@ -17,7 +17,8 @@ __global__ __launch_bounds__(ROW_THREADS) void embed_norm_kernel(
     const int32_t* __restrict__ ids, const half_t* __restrict__ embed,
     const half_t* __restrict__ noise, int H, int V, const half_t* __restrict__ g, float eps,
     half_t* __restrict__ x, half_t* __restrict__ h, float* __restrict__ rnorm,
-    int* __restrict__ err, float* __restrict__ rope_cs, long long pos0, double log2_theta) {
+    int* __restrict__ err, float* __restrict__ rope_cs, long long pos0, double log2_theta,
+    const double* __restrict__ inv_freq_tab) {
   __shared__ float sm[16];
   const int b = blockIdx.x;
   const half_t* src = noise + (size_t)b * H;
@@ -37,9 +38,10 @@ __global__ __launch_bounds__(ROW_THREADS) void embed_norm_kernel(
   if (rope_cs && threadIdx.x < 64) {
     // RoPE angles of row b for the fused qkv epilogue (while the row's loads are in
     // flight), in fp64 as qk_rope_kernel computes them: position pos0 + b times
-    // theta^(-j/64)
+    // theta^(-j/64), or the scaled frequency table
     const int j = threadIdx.x;
-    const double inv_freq = exp2(-(double)j * (1.0 / 64.0) * log2_theta);
+    const double inv_freq =
+        inv_freq_tab ? inv_freq_tab[j] : exp2(-(double)j * (1.0 / 64.0) * log2_theta);
     double sd, cd;
     sincos((double)(pos0 + b) * inv_freq, &sd, &cd);
     rope_cs[2 * (b * 64 + j)] = (float)cd;
@@ -71,9 +73,46 @@ __global__ __launch_bounds__(ROW_THREADS) void embed_norm_kernel(
 void launch_embed_norm(const int32_t* ids, const half_t* embed, const half_t* noise, int B,
                        int H, int V, const half_t* g, float eps, half_t* x, half_t* h,
                        float* rnorm, int* err, hipStream_t st, float* rope_cs, long long pos0,
-                       double log2_theta) {
+                       double log2_theta, const double* inv_freq) {
   hipLaunchKernelGGL(embed_norm_kernel, dim3(B), dim3(ROW_THREADS), 0, st, ids, embed, noise, H,
-                     V, g, eps, x, h, rnorm, err, B <= 32 ? rope_cs : nullptr, pos0, log2_theta);
+                     V, g, eps, x, h, rnorm, err, B <= 32 ? rope_cs : nullptr, pos0, log2_theta,
+                     inv_freq);
+}
+
+// One wave per (KV head, source row): the row's 128 K values to its cache row, the 128 V
+// values down its Vt column.
+__global__ __launch_bounds__(256) void cache_assign_kernel(const half_t* __restrict__ k,
+                                                           const half_t* __restrict__ v, int NKV,
+                                                           int L, int keep_head, int keep_tail,
+                                                           half_t* __restrict__ Kc,
+                                                           half_t* __restrict__ Vt, int cap) {
+  const long long wid = ((long long)blockIdx.x * 256 + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (wid >= (long long)NKV * L) return;
+  const int g = (int)(wid / L), r = (int)(wid - (long long)g * L);
+  int dst;
+  if (r < keep_head) dst = r;
+  else if (r >= L - keep_tail) dst = r - (L - keep_tail) + keep_head;
+  else return;   // an evicted middle row
+  const size_t src = ((size_t)g * L + r) * 128;
+  if (k) {
+    half_t* kd = Kc + ((size_t)g * cap + dst) * 128;
+    kd[lane] = k[src + lane];
+    kd[lane + 64] = k[src + lane + 64];
+  }
+  if (v) {
+    half_t* vd = Vt + (size_t)g * 128 * cap + dst;
+    vd[(size_t)lane * cap] = v[src + lane];
+    vd[(size_t)(lane + 64) * cap] = v[src + lane + 64];
+  }
+}
+
+void launch_cache_assign(const half_t* k, const half_t* v, int NKV, int L, int keep_head,
+                         int keep_tail, half_t* Kc, half_t* Vt, int cap, hipStream_t st) {
+  const long long waves = (long long)NKV * L;
+  if (waves == 0) return;
+  hipLaunchKernelGGL(cache_assign_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, k, v,
+                     NKV, L, keep_head, keep_tail, Kc, Vt, cap);
 }
 
 // x (activation fragment layout, [M][N]) -> h, row-major or (h_afl) in the fragment layout;
@@ -268,7 +307,8 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(QKRopeArgs a) {
   const float r = 1.0f / sqrtf(ss * (1.0f / 128.0f) + a.eps);
   const float y0 = h2f(rms_out(v0, r, gn[lane]));
   const float y1 = h2f(rms_out(v1, r, gn[lane + 64]));
-  const double inv_freq = exp2(-(double)lane * (1.0 / 64.0) * a.log2_theta);
+  const double inv_freq =
+      a.inv_freq ? a.inv_freq[lane] : exp2(-(double)lane * (1.0 / 64.0) * a.log2_theta);
   const double ang = (double)(sq.pos0 + m) * inv_freq;
   double sd, cd;
   sincos(ang, &sd, &cd);

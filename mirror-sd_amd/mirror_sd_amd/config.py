@@ -205,10 +205,38 @@ def workload(name: str) -> Workload:
     raise KeyError(name)
 
 
-def require_unscaled_rope(cfg) -> None:
-    """Raise NotImplementedError for a rope_scaling other than the default: the reference
-    scales RoPE through mlx_lm's initialize_rope (mirror_sd/dflash.py:254-262); only
-    unscaled neox RoPE is implemented here."""
+ROPE_DEFAULT, ROPE_LINEAR, ROPE_LLAMA3 = 0, 1, 2   # dfl_set_rope_scaling types
+
+
+def rope_scaling_args(cfg) -> tuple:
+    """The RoPE variant of ``cfg.rope_scaling`` as the library's dfl_set_rope_scaling
+    arguments (type, factor, low_freq_factor, high_freq_factor,
+    original_max_position_embeddings).
+
+    The reference builds its RoPE with mlx_lm's ``initialize_rope(head_dim, base=rope_theta,
+    traditional=False, scaling_config=rope_scaling, max_position_embeddings=...)``
+    (mirror_sd/dflash.py:254-261; mlx-lm >= 0.23, pyproject.toml:7).  Its rope types:
+    "default" (and no scaling) -> plain RoPE; "linear" -> positions scaled by 1 / factor;
+    "llama3" -> Llama 3.1 frequency scaling with low_freq_factor 1, high_freq_factor 4 and
+    original_max_position_embeddings 8192 when absent.  Other types (yarn, longrope) raise
+    NotImplementedError.  The type is read from "type", then "rope_type", as mlx_lm does.
+    """
     rs = getattr(cfg, "rope_scaling", None)
-    if rs is not None and (rs.get("rope_type", rs.get("type")) not in (None, "default")):
-        raise NotImplementedError(f"rope_scaling {rs!r}: only unscaled RoPE is implemented")
+    if rs is None:
+        return (ROPE_DEFAULT, 1.0, 1.0, 4.0, 8192)
+    rope_type = rs.get("type") or rs.get("rope_type", "default")
+    if rope_type == "default":
+        return (ROPE_DEFAULT, 1.0, 1.0, 4.0, 8192)
+    if rope_type == "linear":
+        return (ROPE_LINEAR, float(rs["factor"]), 1.0, 4.0, 8192)
+    if rope_type == "llama3":
+        return (ROPE_LLAMA3, float(rs["factor"]), float(rs.get("low_freq_factor", 1.0)),
+                float(rs.get("high_freq_factor", 4.0)),
+                int(rs.get("original_max_position_embeddings", 8192)))
+    raise NotImplementedError(f"rope_scaling {rs!r}: RoPE types default, linear and llama3 "
+                              "are implemented")
+
+
+def require_supported_rope(cfg) -> None:
+    """Raise NotImplementedError for a rope_scaling this library does not implement."""
+    rope_scaling_args(cfg)

@@ -25,7 +25,7 @@ import ctypes
 from typing import Dict, List, Optional
 
 from . import _lib
-from .config import DFlashConfig, require_unscaled_rope
+from .config import DFlashConfig, rope_scaling_args
 from .synth import PROJ_NAMES, proj_key
 
 __all__ = ["DFlashDraftModel", "DFlashKVCache", "sample"]
@@ -46,10 +46,15 @@ class DFlashKVCache:
 
     ``offset`` counts absolute positions, ``trim(n)`` drops the last n rows exactly as
     the reference does; the device cache is reconciled with these handles at the next
-    forward call.  ``keys`` / ``values`` are ``[1, NKV, L, 128]`` (keys after k_norm and
-    RoPE, as the reference stores them), in the reference's row order: with a sink +
-    window the device keeps the window as a ring, and the rows are gathered in order
-    (sink rows, then the window oldest first).
+    forward call.  ``keys`` / ``values`` are ``[B_, NKV, L, 128]`` (keys after k_norm and
+    RoPE, as the reference stores them; B_ = the batch of the last forward, 1 by default),
+    in the reference's row order: with a sink + window the device keeps the window as a
+    ring, and the rows are gathered in order (sink rows, then the window oldest first).
+
+    ``keys`` / ``values`` are assignable (``c_new.keys = c_old.keys``, generate.py:917-941)
+    and ``update_and_fetch(keys, values)`` appends rows as dflash.py:168-177 does: such a
+    handle then holds its rows as its own tensors until the next forward writes every
+    layer's rows back into the device cache (dfl_cache_assign).
     """
 
     def __init__(self, model: "DFlashDraftModel", layer: int, generation: int,
@@ -62,11 +67,16 @@ class DFlashKVCache:
         self.offset = 0
         self._len = 0
         self._has_keys = False
+        self._k = None   # rows held by the handle (assigned / appended), [B_, NKV, L, D]
+        self._v = None
 
     def trim(self, n: int):
         if self._has_keys and n > 0:
             self._len = max(self._len - n, 0)
             self.offset -= n
+            if self._k is not None:
+                self._k = self._k[:, :, :self._len]
+                self._v = self._v[:, :, :self._len] if self._v is not None else None
 
     def _appended(self, n: int):
         """Book n appended rows: a sink + window cache holds at most sink + window
@@ -77,27 +87,78 @@ class DFlashKVCache:
             self._len = min(self._len, self.sink_size + self.window_size)
         self._has_keys = True
 
-    def _rows(self):
-        return self._model._cache_rows()
+    def _device(self, which: int):
+        """The device cache's rows of this layer for every sequence of the last forward
+        (the device first takes the length the handles book: a forward leaves its block
+        rows uncommitted until the next call, the reference's cache holds them until trim)."""
+        import torch
+        m = self._model
+        if not m._rows_dirty and m._handles:
+            m._sync_cache(m._handles, n_seq=m._batch)
+        out = []
+        for seq in range(m._batch):
+            m.select_seq(seq)
+            try:
+                rows = m._cache_rows()[:self._len]
+                k, vt = m._make_cache_views()[self.layer] if seq else m._cache_tensors[self.layer]
+                out.append(k[:, rows] if which == 0 else vt[:, :, rows].transpose(1, 2))
+            finally:
+                m.select_seq(0)
+        return torch.stack(out, 0)
 
     @property
     def keys(self):
         if not self._has_keys:
             return None
-        k, vt = self._model._cache_tensors[self.layer]
-        return k[:, self._rows()].unsqueeze(0)
+        return self._k if self._k is not None else self._device(0)
 
     @property
     def values(self):
         if not self._has_keys:
             return None
-        k, vt = self._model._cache_tensors[self.layer]
-        return vt[:, :, self._rows()].transpose(1, 2).unsqueeze(0)
+        return self._v if self._v is not None else self._device(1)
+
+    def _hold(self):
+        """Take this layer's current rows as the handle's own tensors (all live handles of
+        the model do the same, so that no handle reads rows another one rewrote)."""
+        self._model._hold_rows()
+
+    @keys.setter
+    def keys(self, value):
+        self._hold()
+        self._k = None if value is None else self._model._as_rows(value)
+        self._settle()
+
+    @values.setter
+    def values(self, value):
+        self._hold()
+        self._v = None if value is None else self._model._as_rows(value)
+        self._settle()
+
+    def _settle(self):
+        self._model._rows_dirty = True
+        if self._k is None:
+            self._len, self._has_keys, self._v = 0, False, None
+        else:
+            self._len, self._has_keys = int(self._k.shape[2]), True
 
     def update_and_fetch(self, keys, values):
-        raise NotImplementedError(
-            "the device cache is filled by DFlashDraftModel.__call__; update_and_fetch is "
-            "not callable directly")
+        """dflash.py:168-177: append [B_, NKV, n, D] keys / values (post-RoPE), advance the
+        offset by n, keep sink + window rows when windowed; returns the cached rows."""
+        import torch
+        self._hold()
+        k, v = self._model._as_rows(keys), self._model._as_rows(values)
+        if self._k is not None and self._has_keys:
+            k = torch.cat([self._k, k], dim=2)
+            v = torch.cat([self._v, v], dim=2)
+        self.offset += int(keys.shape[2])
+        L, S, Wn = k.shape[2], self.sink_size, self.window_size
+        if S > 0 and Wn > 0 and L > S + Wn:   # _apply_window, dflash.py:179-193
+            k = torch.cat([k[:, :, :S], k[:, :, L - Wn:]], dim=2)
+            v = torch.cat([v[:, :, :S], v[:, :, L - Wn:]], dim=2)
+        self._k, self._v = k, v
+        self._settle()
+        return self._k, self._v
 
     def state(self):
         if not self._has_keys:
@@ -111,7 +172,7 @@ class DFlashDraftModel:
     def __init__(self, config: DFlashConfig, max_ctx: int = 8192, max_block: Optional[int] = None,
                  device=None, n_target_feat: Optional[int] = None, max_seqs: int = 1):
         import torch
-        require_unscaled_rope(config)
+        rope = rope_scaling_args(config)   # raises for a RoPE variant not implemented
         self.config = config
         self.block_size = config.block_size
         self.mask_token_id = config.mask_token_id
@@ -133,7 +194,12 @@ class DFlashDraftModel:
         with torch.cuda.device(self.device):
             _lib.check(self._L.dfl_create(ctypes.byref(cfg), ctypes.byref(h)), "dfl_create")
         self._ctx = h
+        if rope[0] != 0:
+            _lib.check(self._L.dfl_set_rope_scaling(self._ctx, *rope), "dfl_set_rope_scaling")
         self._keep: Dict[str, object] = {}   # caller-owned buffers the library points at
+        self._batch = 1                      # sequences of the last forward (cache handles)
+        self._handles: List["DFlashKVCache"] = []   # handles of the live cache
+        self._rows_dirty = False             # handles hold rows not yet in the device cache
         self._gen = 0
         self._cache_tensors = self._make_cache_views()
         self._layers_loaded = [False] * config.num_hidden_layers
@@ -299,10 +365,64 @@ class DFlashDraftModel:
         the device cache keeps the first sink_size rows and the newest window_size rows
         (dflash.py:179-193)."""
         self._gen += 1
-        _lib.check(self._L.dfl_cache_set_window(self._ctx, int(sink_size), int(window_size)),
-                   "dfl_cache_set_window")
-        return [DFlashKVCache(self, i, self._gen, sink_size, window_size)
-                for i in range(self.num_draft_layers)]
+        for seq in range(self.max_seqs):
+            self.select_seq(seq)
+            try:
+                _lib.check(self._L.dfl_cache_set_window(self._ctx, int(sink_size),
+                                                        int(window_size)), "dfl_cache_set_window")
+            finally:
+                self.select_seq(0)
+        self._rows_dirty = False
+        self._handles = [DFlashKVCache(self, i, self._gen, sink_size, window_size)
+                         for i in range(self.num_draft_layers)]
+        return list(self._handles)
+
+    def _as_rows(self, t):
+        """[B_, NKV, L, D] (or [NKV, L, D]) fp16 rows on this device, from torch or numpy."""
+        import numpy as np
+        import torch
+        if isinstance(t, np.ndarray):
+            t = torch.from_numpy(t)
+        t = t.to(self.device, torch.float16)
+        if t.dim() == 3:
+            t = t.unsqueeze(0)
+        NKV, D = self.config.num_key_value_heads, self.config.head_dim
+        if t.dim() != 4 or t.shape[1] != NKV or t.shape[3] != D:
+            raise ValueError(f"cache rows must be [B_, {NKV}, L, {D}], got {tuple(t.shape)}")
+        return t.contiguous()
+
+    def _hold_rows(self):
+        """Every live handle takes its layer's device rows as its own tensors (once)."""
+        for c in self._handles:
+            if c._has_keys and c._k is None:
+                c._k = c._device(0).contiguous()
+                c._v = c._device(1).contiguous()
+
+    def _write_back(self, cache, n_seq: int):
+        """Write the rows the handles hold into the device cache (every layer, every
+        sequence), then the handles read the device again."""
+        for c in cache:
+            B_ = c._k.shape[0] if c._k is not None else n_seq
+            if c._has_keys and (c._v is None or c._v.shape != c._k.shape):
+                raise ValueError(f"layer {c.layer}: keys and values of different shapes")
+            if B_ != n_seq:
+                raise ValueError(f"layer {c.layer}: rows for {B_} sequences, the forward has {n_seq}")
+        st = self._stream()
+        for seq in range(n_seq):
+            self.select_seq(seq)
+            try:
+                for c in cache:
+                    k = c._k[seq] if c._has_keys else None
+                    v = c._v[seq] if c._has_keys else None
+                    L = int(k.shape[1]) if k is not None else 0
+                    _lib.check(self._L.dfl_cache_assign(self._ctx, c.layer, _lib.ptr(k),
+                                                        _lib.ptr(v), L, st), "dfl_cache_assign")
+            finally:
+                self.select_seq(0)
+        self._keep["cache_rows"] = [(c._k, c._v) for c in cache]
+        for c in cache:
+            c._k = c._v = None
+        self._rows_dirty = False
 
     def _cache_rows(self):
         """Cache rows of the cached rows in the reference's order (a device index tensor)."""
@@ -321,8 +441,9 @@ class DFlashDraftModel:
                    "dfl_cache_state")
         return n.value, off.value
 
-    def _sync_cache(self, cache: List[DFlashKVCache], check_only: bool = False):
-        """Bring the device cache to the state the per-layer handles describe."""
+    def _sync_cache(self, cache: List[DFlashKVCache], check_only: bool = False, n_seq: int = 1):
+        """Bring the device cache (sequences 0 .. n_seq-1, in lockstep) to the state the
+        per-layer handles describe."""
         if any(c._gen != self._gen or c._model is not self for c in cache):
             raise ValueError("stale cache: create caches with this model's make_cache()")
         lens = {c._len for c in cache}
@@ -332,12 +453,24 @@ class DFlashDraftModel:
         want_len, want_off = lens.pop(), offs.pop()
         if check_only:
             return
-        dev_len, dev_off = self._device_state()
-        if want_len > dev_len:
-            _lib.check(self._L.dfl_cache_commit(self._ctx, want_len - dev_len), "dfl_cache_commit")
-        elif want_len < dev_len:
-            _lib.check(self._L.dfl_cache_trim(self._ctx, dev_len - want_len), "dfl_cache_trim")
-        _lib.check(self._L.dfl_cache_set_offset(self._ctx, want_off), "dfl_cache_set_offset")
+        if self._rows_dirty:
+            self._write_back(cache, n_seq)
+        for seq in range(n_seq):
+            if seq:
+                self.select_seq(seq)
+            try:
+                dev_len, dev_off = self._device_state()
+                if want_len > dev_len:
+                    _lib.check(self._L.dfl_cache_commit(self._ctx, want_len - dev_len),
+                               "dfl_cache_commit")
+                elif want_len < dev_len:
+                    _lib.check(self._L.dfl_cache_trim(self._ctx, dev_len - want_len),
+                               "dfl_cache_trim")
+                _lib.check(self._L.dfl_cache_set_offset(self._ctx, want_off),
+                           "dfl_cache_set_offset")
+            finally:
+                if seq:
+                    self.select_seq(0)
 
     # ------------------------------------------------------------------ forward
     def _apply_num_layers(self):
@@ -401,10 +534,7 @@ class DFlashDraftModel:
             if noise.shape[1] != H:
                 raise ValueError(f"noise_embedding must be [B, {H}]")
         else:
-            ids = torch.as_tensor(ids, dtype=torch.int32).reshape(-1)
-            if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= V):
-                raise ValueError(f"token id outside [0, {V})")
-            ids = ids.to(self.device).contiguous()
+            ids = _check_ids(ids, V).to(self.device).contiguous()
             B = ids.numel()
         if not all(self._layers_loaded[:self.num_draft_layers]) or not self._has_head:
             raise RuntimeError("weights not loaded")
@@ -419,29 +549,76 @@ class DFlashDraftModel:
         return out_h, out_p, out_l, out_i
 
     def __call__(self, noise_embedding, target_hidden, mask=None, cache=None, **kwargs):
-        """dflash.py:384-403.  noise_embedding [1, q, H], target_hidden [1, C, nf*H] (or
-        the list of the nf tapped layer outputs [1, C, H], read without concatenating);
-        returns final-normed hidden [1, q, H] (fp16).  With ``cache`` the context rows
-        are appended to the cache and the block rows are left in it (offset += C + q)
-        until the caller's ``trim(q)``, exactly as update_and_fetch + trim behave."""
+        """dflash.py:384-403.  noise_embedding [B_, q, H], target_hidden [B_, C, nf*H] (or,
+        for B_ = 1, the list of the nf tapped layer outputs [1, C, H], read without
+        concatenating); returns final-normed hidden [B_, q, H] (fp16).  With ``cache`` the
+        context rows are appended to the cache and the block rows are left in it (offset
+        += C + q) until the caller's ``trim(q)``, exactly as update_and_fetch + trim
+        behave.  B_ > 1 runs sequences 0 .. B_-1 of the model (max_seqs >= B_) in lockstep,
+        their projections stacked in one pass (dfl_draft_batch)."""
         if mask is not None:
             raise ValueError("DFlash drafting is non-causal; mask must be None (dflash.py:215-233)")
         self._apply_num_layers()
         q = noise_embedding.shape[-2]
+        B_ = noise_embedding.shape[0] if noise_embedding.dim() == 3 else 1
+        if isinstance(target_hidden, (list, tuple)):
+            if B_ != 1:
+                raise ValueError("a list of tapped layer outputs is a batch of one")
+        elif (target_hidden.shape[0] if target_hidden.dim() == 3 else 1) != B_:
+            raise ValueError("noise_embedding and target_hidden differ in batch size")
+        if B_ > self.max_seqs:
+            raise ValueError(f"batch of {B_} sequences, the model was created with "
+                             f"max_seqs={self.max_seqs}")
+        if cache is not None:
+            cache = list(cache)[:self.num_draft_layers]
+            self._sync_cache(cache, n_seq=B_)
+        self._batch = B_
+        C = 0
+        for b in range(B_):
+            if b:
+                self.select_seq(b)
+            try:
+                if cache is None:
+                    _lib.check(self._L.dfl_cache_reset(self._ctx), "dfl_cache_reset")
+                th = target_hidden if B_ == 1 else target_hidden[b]
+                C = self._ingest(th)
+            finally:
+                if b:
+                    self.select_seq(0)
         if cache is None:
-            _lib.check(self._L.dfl_cache_reset(self._ctx), "dfl_cache_reset")
             self._gen += 1
-            self._ingest(target_hidden)
+        if B_ == 1:
             out_h, _, _, _ = self._draft(noise=noise_embedding)
-            _lib.check(self._L.dfl_cache_reset(self._ctx), "dfl_cache_reset")
-            return out_h.unsqueeze(0)
-        cache = list(cache)[:self.num_draft_layers]
-        self._sync_cache(cache)
-        C = self._ingest(target_hidden)
-        out_h, _, _, _ = self._draft(noise=noise_embedding)
+            out_h = out_h.unsqueeze(0)
+        else:
+            out_h = self._draft_seqs(noise_embedding)
+        if cache is None:
+            for b in range(B_):
+                self.select_seq(b)
+                _lib.check(self._L.dfl_cache_reset(self._ctx), "dfl_cache_reset")
+            self.select_seq(0)
+            self._batch = 1
+            return out_h
         for c in cache:       # context + block rows, as update_and_fetch leaves them
             c._appended(C + q)
-        return out_h.unsqueeze(0)
+        return out_h
+
+    def _draft_seqs(self, noise):
+        """Final-normed hidden [n_seq, B, H] of one block per sequence (dfl_draft_batch)."""
+        import torch
+        H = self.config.hidden_size
+        noise = noise.to(self.device, torch.float16).contiguous()
+        n_seq, B = noise.shape[0], noise.shape[1]
+        if noise.shape[2] != H:
+            raise ValueError(f"noise_embedding must be [B_, q, {H}]")
+        if not all(self._layers_loaded[:self.num_draft_layers]) or not self._has_head:
+            raise RuntimeError("weights not loaded")
+        out_h = torch.empty((n_seq * B, H), dtype=torch.float16, device=self.device)
+        _lib.check(self._L.dfl_draft_batch(self._ctx, n_seq, noise.data_ptr(), None, B,
+                                           out_h.data_ptr(), None, None, None, self._stream()),
+                   "dfl_draft_batch")
+        self._keep["draft_src"] = (noise, None)
+        return out_h.reshape(n_seq, B, H)
 
     def draft(self, ids, target_hidden=None, cache=None, return_logits=False,
               return_hidden=False, fused_context=False):
@@ -513,12 +690,10 @@ class DFlashDraftModel:
                 raise ValueError(f"noise must be [n_seq, B, {H}]")
             src_n, src_i = noise, None
         else:
-            ids = torch.as_tensor(ids, dtype=torch.int32)
+            ids = _check_ids(ids, V, flat=False)
             if ids.dim() != 2:
                 raise ValueError("ids must be [n_seq, B]")
             n_seq, B = ids.shape
-            if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= V):
-                raise ValueError(f"token id outside [0, {V})")
             src_n, src_i = None, ids.to(self.device).contiguous()
         if not all(self._layers_loaded[:self.num_draft_layers]) or not self._has_lm:
             raise RuntimeError("weights (with lm_head) not loaded")
@@ -599,12 +774,10 @@ class DFlashDraftModel:
         import torch
         if not self._has_embed:
             raise RuntimeError("embedding not loaded")
-        ids = torch.as_tensor(block_ids, dtype=torch.int32).reshape(-1)
         V_emb = self.config.vocab_size
+        ids = _check_ids(block_ids, V_emb)
         if ids.numel() == 0:
             raise ValueError("block_ids is empty")
-        if int(ids.min()) < 0 or int(ids.max()) >= V_emb:
-            raise ValueError(f"token id outside [0, {V_emb})")
         ids = ids.to(self.device).contiguous()
         B, H = ids.numel(), self.config.hidden_size
         out = torch.empty((B, H), dtype=torch.float16, device=self.device)
@@ -712,6 +885,22 @@ class DFlashDraftModel:
     def run_prepared(self):
         self.run_kernels()
         return self.read_output()
+
+
+def _check_ids(ids, V: int, flat: bool = True):
+    """Token ids as an int32 tensor.  Host ids outside [0, V) raise ValueError here; ids
+    already on the device are not read back (that would synchronise the host with the
+    stream on every call): the kernels flag them in the device error word (bit 0, read with
+    dfl_device_errors) and use a zero row."""
+    import torch
+    t = torch.as_tensor(ids)
+    if t.dtype != torch.int32:
+        t = t.to(torch.int32)
+    if flat:
+        t = t.reshape(-1)
+    if not t.is_cuda and t.numel() and (int(t.min()) < 0 or int(t.max()) >= V):
+        raise ValueError(f"token id outside [0, {V})")
+    return t
 
 
 def _feature_ptrs(feats, H: int, device):

@@ -32,7 +32,7 @@ import json
 from pathlib import Path
 from typing import Dict, Iterable, List, Optional, Tuple
 
-from .config import DFlashConfig, require_unscaled_rope
+from .config import DFlashConfig, require_supported_rope
 from .synth import PROJ_NAMES, proj_key
 
 __all__ = ["load_dflash_model", "load_config", "load_safetensors", "expected_names",
@@ -51,7 +51,7 @@ def load_config(model_path, overrides: Optional[Dict] = None) -> DFlashConfig:
     if overrides:
         d.update(overrides)
     cfg = DFlashConfig.from_dict(d)
-    require_unscaled_rope(cfg)
+    require_supported_rope(cfg)
     return cfg
 
 

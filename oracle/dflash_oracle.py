@@ -156,14 +156,43 @@ def head_rms_norm(x: np.ndarray, g: np.ndarray, eps: float, fp16: bool, dtype=F6
     return rms_norm(x, g, eps, fp16, dtype)
 
 
-def rope_inv_freq(head_dim: int, theta: float) -> np.ndarray:
-    """inv_freq_j = theta^(-2j/head_dim), j in [0, head_dim/2) (float64)."""
+def rope_inv_freq(head_dim: int, theta: float, scaling: Optional[dict] = None) -> np.ndarray:
+    """inv_freq_j = theta^(-2j/head_dim), j in [0, head_dim/2) (float64), with the rope_scaling
+    of the reference's ``initialize_rope(head_dim, base=theta, traditional=False,
+    scaling_config=scaling)`` (dflash.py:254-261; mlx-lm >= 0.23, not vendored):
+
+    * "linear": nn.RoPE(scale = 1 / factor), i.e. every frequency divided by factor;
+    * "llama3" (mlx_lm Llama3RoPE, the Llama 3.1 scheme): with L0 =
+      original_max_position_embeddings (8192), lf = low_freq_factor (1), hf =
+      high_freq_factor (4) and wavelength w = 2 pi / inv_freq, frequencies with w > L0 / lf
+      are divided by factor, w < L0 / hf are kept, and in between
+      inv_freq * ((1 - s) / factor + s) with s = (L0 / w - lf) / (hf - lf).
+    """
     j = np.arange(head_dim // 2, dtype=F64)
-    return 1.0 / (float(theta) ** (2.0 * j / head_dim))
+    inv = 1.0 / (float(theta) ** (2.0 * j / head_dim))
+    if scaling is None:
+        return inv
+    kind = scaling.get("type") or scaling.get("rope_type", "default")
+    if kind == "default":
+        return inv
+    factor = float(scaling["factor"])
+    if kind == "linear":
+        return inv / factor
+    if kind != "llama3":
+        raise NotImplementedError(f"rope_scaling type {kind!r}")
+    L0 = float(scaling.get("original_max_position_embeddings", 8192))
+    lf = float(scaling.get("low_freq_factor", 1.0))
+    hf = float(scaling.get("high_freq_factor", 4.0))
+    wavelen = 2.0 * np.pi / inv
+    s = (L0 / wavelen - lf) / (hf - lf)
+    smooth = inv * ((1.0 - s) / factor + s)
+    out = np.where(wavelen > L0 / lf, inv / factor, inv)
+    mid = (wavelen > L0 / hf) & (wavelen < L0 / lf)
+    return np.where(mid, smooth, out)
 
 
 def rope_neox(x: np.ndarray, positions: np.ndarray, theta: float, fp16: bool,
-              dtype=F64) -> np.ndarray:
+              dtype=F64, scaling: Optional[dict] = None) -> np.ndarray:
     """Split-half (neox) rotary embedding of x [rows, heads, D] at ``positions`` [rows].
 
     out[..., :D/2] = x1*cos - x2*sin ; out[..., D/2:] = x2*cos + x1*sin with
@@ -171,7 +200,7 @@ def rope_neox(x: np.ndarray, positions: np.ndarray, theta: float, fp16: bool,
     """
     D = x.shape[-1]
     half = D // 2
-    ang = positions.astype(F64)[:, None] * rope_inv_freq(D, theta)[None, :]
+    ang = positions.astype(F64)[:, None] * rope_inv_freq(D, theta, scaling)[None, :]
     c = np.cos(ang).astype(dtype)[:, None, :]
     s = np.sin(ang).astype(dtype)[:, None, :]
     x = x.astype(dtype, copy=False)
@@ -323,8 +352,9 @@ def attention(h, ctx, lw, cfg, cache: Optional[OracleKVCache], fp16: bool, dtype
     v = linear_w8(kv_in, lw["v_proj"], fp16, dtype).reshape(C + q_len, NKV, D)
     k = head_rms_norm(k, lw["k_norm"], eps, fp16, dtype)
     off = cache.offset if cache is not None else 0
-    q = rope_neox(q, off + C + np.arange(q_len), theta, fp16, dtype)
-    k = rope_neox(k, off + np.arange(C + q_len), theta, fp16, dtype)
+    rs = getattr(cfg, "rope_scaling", None)
+    q = rope_neox(q, off + C + np.arange(q_len), theta, fp16, dtype, rs)
+    k = rope_neox(k, off + np.arange(C + q_len), theta, fp16, dtype, rs)
     q, k, v = q.transpose(1, 0, 2), k.transpose(1, 0, 2), v.transpose(1, 0, 2)
     if cache is not None:
         k, v = cache.update_and_fetch(k, v)

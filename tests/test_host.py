@@ -172,17 +172,42 @@ def test_bench_compiles_and_refuses_several_gpus():
     assert "one GPU" in r.stderr
 
 
-def test_model_refuses_scaled_rope():
-    """A config carrying a non-default rope_scaling is refused by the model itself, not only
-    by the loader (the reference applies the scaling in initialize_rope, dflash.py:254-262)."""
+def test_model_refuses_unimplemented_rope_scaling():
+    """A rope_scaling type the library does not implement (yarn) is refused by the model
+    itself, not only by the loader; default, linear and llama3 map to the library's RoPE
+    types with mlx_lm's defaults for absent llama3 keys (initialize_rope, called at
+    dflash.py:254-261)."""
     from mirror_sd_amd.dflash import DFlashDraftModel
+    from mirror_sd_amd.config import rope_scaling_args, ROPE_DEFAULT, ROPE_LINEAR, ROPE_LLAMA3
     cfg = DFlashConfig.from_dict({"hidden_size": 256, "num_hidden_layers": 1,
                                   "rope_scaling": {"rope_type": "yarn", "factor": 4.0}})
     with pytest.raises(NotImplementedError):
         DFlashDraftModel(cfg, max_ctx=16)
-    cfg = DFlashConfig.from_dict({"hidden_size": 256, "rope_scaling": {"rope_type": "default"}})
-    from mirror_sd_amd.config import require_unscaled_rope
-    require_unscaled_rope(cfg)   # the default type is plain RoPE
+    for rs, want in [(None, ROPE_DEFAULT), ({"rope_type": "default"}, ROPE_DEFAULT),
+                     ({"type": "linear", "factor": 2.0}, ROPE_LINEAR)]:
+        cfg = DFlashConfig.from_dict({"hidden_size": 256, **({"rope_scaling": rs} if rs else {})})
+        assert rope_scaling_args(cfg)[0] == want
+    cfg = DFlashConfig.from_dict({"rope_scaling": {"rope_type": "llama3", "factor": 8.0}})
+    assert rope_scaling_args(cfg) == (ROPE_LLAMA3, 8.0, 1.0, 4.0, 8192)
+    # "type" is read before "rope_type", as mlx_lm does
+    cfg = DFlashConfig.from_dict({"rope_scaling": {"type": "llama3", "rope_type": "yarn",
+                                                   "factor": 32.0, "low_freq_factor": 2.0,
+                                                   "high_freq_factor": 8.0,
+                                                   "original_max_position_embeddings": 4096}})
+    assert rope_scaling_args(cfg) == (ROPE_LLAMA3, 32.0, 2.0, 8.0, 4096)
+
+
+def test_host_ids_checked_device_ids_not_read_back():
+    """Host token ids outside [0, V) raise at the call; the check never reads device ids back
+    (the kernels flag those in the device error word instead)."""
+    import torch
+    from mirror_sd_amd.dflash import _check_ids
+    with pytest.raises(ValueError):
+        _check_ids([0, 5, 7], 7)
+    with pytest.raises(ValueError):
+        _check_ids(torch.tensor([-1, 2]), 7)
+    t = _check_ids(np.array([[1, 2], [3, 4]], dtype=np.int64), 7, flat=False)
+    assert t.dtype == torch.int32 and t.shape == (2, 2)
 
 
 def test_rocprof_summary_trace_skips_warmup_blocks(tmp_path):

@@ -42,10 +42,14 @@ def test_config_defaults_follow_from_dict(tmp_path):
     assert cfg.target_layer_ids == build_target_layer_ids(36, 5) == [1, 9, 17, 25, 33]
 
 
-def test_config_rejects_rope_scaling(tmp_path):
-    _write_cfg(tmp_path, rope_scaling={"rope_type": "llama3", "factor": 8.0})
+def test_config_rope_scaling(tmp_path):
+    """llama3 (LLaMA-3.1 checkpoints) and linear scaling load; a type the library does not
+    implement is refused at load."""
+    _write_cfg(tmp_path, rope_scaling={"rope_type": "yarn", "factor": 4.0})
     with pytest.raises(NotImplementedError):
         loader.load_config(tmp_path)
+    _write_cfg(tmp_path, rope_scaling={"rope_type": "llama3", "factor": 8.0})
+    assert loader.load_config(tmp_path).rope_scaling["rope_type"] == "llama3"
     _write_cfg(tmp_path, rope_scaling={"rope_type": "default"})
     assert loader.load_config(tmp_path).rope_scaling == {"rope_type": "default"}
     with pytest.raises(FileNotFoundError):

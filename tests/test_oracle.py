@@ -134,6 +134,41 @@ def test_rope_complex_form_and_hand_example():
     np.testing.assert_allclose(y4, exp, rtol=1e-14)
 
 
+def test_rope_llama3_frequency_bands():
+    """Llama 3.1 frequency scaling (mlx_lm Llama3RoPE, the reference's initialize_rope with
+    rope_type llama3): frequencies whose wavelength 2 pi / f is below L0 / hf are unchanged,
+    above L0 / lf divided by the factor, and the band between interpolated; the interpolation
+    meets both neighbours at the band edges (s = 0 -> f / factor, s = 1 -> f), stays
+    between them and falls monotonically with j; linear scaling divides every frequency."""
+    D, theta, fac, L0, lf, hf = 128, 5e5, 8.0, 8192, 1.0, 4.0
+    rs = {"rope_type": "llama3", "factor": fac, "low_freq_factor": lf, "high_freq_factor": hf,
+          "original_max_position_embeddings": L0}
+    base = O.rope_inv_freq(D, theta)
+    got = O.rope_inv_freq(D, theta, rs)
+    wl = 2 * np.pi / base
+    hi, lo = wl < L0 / hf, wl > L0 / lf
+    mid = ~hi & ~lo
+    assert hi.sum() > 10 and lo.sum() > 10 and mid.sum() >= 3   # all three bands occur
+    np.testing.assert_array_equal(got[hi], base[hi])
+    np.testing.assert_allclose(got[lo], base[lo] / fac, rtol=1e-15)
+    assert np.all(got[mid] < base[mid]) and np.all(got[mid] > base[mid] / fac)
+    assert np.all(np.diff(got) < 0)
+    # band edges: a frequency at wavelength exactly L0 / hf (s = 1) keeps its value, at L0 / lf
+    # (s = 0) the interpolation gives f / factor
+    for w_edge, want in [(L0 / hf, 1.0), (L0 / lf, 1.0 / fac)]:
+        f = 2 * np.pi / w_edge
+        s = (L0 / w_edge - lf) / (hf - lf)
+        assert abs(((1 - s) / fac + s) - want) < 1e-15
+    # hand value: the first frequency of the band, computed from the scheme's definition
+    j = int(np.argmax(mid))
+    s = (L0 * base[j] / (2 * np.pi) - lf) / (hf - lf)
+    assert abs(got[j] - base[j] * ((1 - s) / fac + s)) < 1e-18
+    np.testing.assert_allclose(O.rope_inv_freq(D, theta, {"type": "linear", "factor": 4.0}),
+                               base / 4.0, rtol=1e-15)
+    with pytest.raises(NotImplementedError):
+        O.rope_inv_freq(D, theta, {"rope_type": "yarn", "factor": 4.0})
+
+
 def test_rope_relative_position():
     rng = np.random.default_rng(6)
     q = rng.standard_normal((1, 1, 32))
