@@ -226,6 +226,16 @@ int dfl_embed_block_noalloc(const int32_t* ids, int32_t B, const uint16_t* embed
 int dfl_set_rope_scaling(dfl_ctx* ctx, int32_t type, double factor, double low_freq_factor,
                          double high_freq_factor, int32_t original_max_position_embeddings);
 
+/* Draft tokens as samples (sample(logits, temperature), dflash.py:133-136, called at
+ * generate.py:605): with temperature >= 1e-5 the out_ids of later dfl_draft_block /
+ * dfl_draft_batch calls are categorical draws from softmax(logits / temperature) per row,
+ * taken by the Gumbel-max rule inside the lm_head (argmax of logits / T + Gumbel noise; the
+ * optional fp32 logits stay the plain logits); below 1e-5 (the state after dfl_create) they
+ * are the argmax.  The noise of each call is a function of seed and the number of sampling
+ * calls since this one (deterministic for a given seed; the reference draws from MLX's
+ * global generator, so individual draws cannot match it). */
+int dfl_set_sampling(dfl_ctx* ctx, float temperature, uint64_t seed);
+
 /* Test hook, no counterpart in the reference: on != 0 makes every work-queue wait of the
  * balanced lm_head give up after a few hundred rounds (its bounded-wait path: every wave
  * still ends, the ids of those calls are invalid and device error bit 2 is set); 0 restores

@@ -177,6 +177,12 @@ struct dfl_ctx {
   std::vector<void*> allocs;
   int prof = 0;   // 0 off, 1 every kernel group, 2 stream-K GEMM launches only
   int test_queue_timeout = 0;   // dfl_test_queue_timeout: balanced lm_head waits give up
+  // dfl_set_sampling: draft ids as categorical samples at temperature 1 / samp_invT (0:
+  // argmax); each sampling call draws its noise from seed + its call count
+  float samp_invT = 0.f;
+  unsigned long long samp_seed = 0, samp_calls = 0;
+  float call_invT = 0.f;        // the current call's (set by draft_rows before its lm_head)
+  uint32_t call_seed = 0;
   std::vector<ProfRec> recs;
 
   ~dfl_ctx() {
@@ -570,6 +576,11 @@ static int skgemm(dfl_ctx* ctx, int cat, int wt, int epi, const SKPlan& p,
     a.dyn_static = p.dyn_static;
     a.dyn_next = ctx->dyn_next;
     a.err = ctx->err;
+    if (epi == EPI_ARGMAX) {
+      a.samp_invT = ctx->call_invT;
+      a.samp_seed = ctx->call_seed;
+      a.samp_row0 = m0;
+    }
     // the balanced kernel (one m-tile) finalises the argmax ids itself
     const bool fin = ids && keys && p.dyn_static > 0 && n_mt == 1;
     a.ids = fin ? ids : nullptr;
@@ -619,6 +630,10 @@ static int tgemm(dfl_ctx* ctx, int cat, int wt, int epi, const uint4* W, int N, 
   a.K = K;
   a.X = X;
   a.M = M;
+  if (epi == TG_ARGMAX) {
+    a.samp_invT = ctx->call_invT;
+    a.samp_seed = ctx->call_seed;
+  }
   TileArgs g = a;   // the GEMM's own arguments: F32 planes when split
   if (p.splits > 1) {
     g = TileArgs{};
@@ -1120,6 +1135,14 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
   }
   // row sums of squares of x: per 64 columns (stream-K RESID) or 32 (tile RESID)
   const int ss_tiles = stacked ? H / 32 : H / 64;
+  // a sampling call: its own noise seed (splitmix64 of the seed and the call count)
+  ctx->call_invT = out_ids ? ctx->samp_invT : 0.f;
+  if (ctx->call_invT > 0.f) {
+    unsigned long long z = ctx->samp_seed + 0x9E3779B97F4A7C15ull * (++ctx->samp_calls);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    ctx->call_seed = (uint32_t)(z ^ (z >> 31));
+  }
   if ((out_logits || out_ids) && stacked) {
     // stacked blocks: final norm into fragment-layout rows, then the lm_head tile GEMM with
     // the argmax keys (and the fp32 logits if asked for)
@@ -1485,6 +1508,17 @@ int dfl_cache_assign(dfl_ctx* ctx, int32_t layer, const uint16_t* keys, const ui
   q.len = kept;
   q.ring_j = q.window ? std::max(0, kept - q.sink) : 0;
   q.last_block = 0;
+  return DFL_OK;
+}
+
+int dfl_set_sampling(dfl_ctx* ctx, float temperature, uint64_t seed) {
+  if (!ctx) return fail(DFL_EINVAL, "dfl_set_sampling: null context");
+  if (!(temperature >= 0.f) || std::isinf(temperature))
+    return fail(DFL_EINVAL, "dfl_set_sampling: temperature must be a finite value >= 0");
+  // greedy below 1e-5, as sample() does (dflash.py:133-136)
+  ctx->samp_invT = temperature < 1e-5f ? 0.f : 1.0f / temperature;
+  ctx->samp_seed = seed;
+  ctx->samp_calls = 0;
   return DFL_OK;
 }
 

@@ -114,6 +114,28 @@ DFL_DEV float block_sum(float v, float* smem /* >= 16 floats */) {
   return t;
 }
 
+// Gumbel-max sampling: argmax_n (l_n / T + G_n) over independent standard Gumbel G_n is a
+// draw from softmax(l / T) (the categorical of dflash.py:133-136).  The noise of (row,
+// column) comes from a 32-bit integer hash (C. Wellons' "lowbias32" finaliser) of the column
+// mixed with the row's salt, itself a hash of the call's seed and the row; U = (24 hash bits
+// + 1/2) 2^-24 lies in (0, 1) and G = -ln(-ln U), so G never exceeds 17.3.
+DFL_DEV uint32_t hash32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return x;
+}
+DFL_DEV uint32_t gumbel_row_salt(uint32_t seed, int row) {
+  return hash32(seed ^ hash32((uint32_t)row * 0x9E3779B9u + 0x85ebca6bu));
+}
+DFL_DEV float gumbel_noise(uint32_t salt, int col) {
+  const uint32_t h = hash32(salt ^ ((uint32_t)col * 0xc2b2ae35u));
+  const float u = ((float)(h >> 8) + 0.5f) * (1.0f / 16777216.0f);
+  return -__logf(-__logf(u));
+}
+
 // Monotone map of a float onto uint32 so that unsigned comparison orders floats.
 DFL_DEV uint32_t float_order_key(float f) {
   uint32_t b = __float_as_uint(f);

@@ -73,6 +73,11 @@ struct StreamArgs {
   int dp;                   // hybrid plan (SKPlan::dp): whole tiles per workgroup
   int dyn_test_timeout;     // balanced mode: force the work-queue wait to give up (test hook)
   RopeEpi rope;             // EPI_QKROPE
+  // ARGMAX as a categorical sample (Gumbel-max, gumbel_noise): samp_invT = 1 / temperature
+  // (0: plain argmax), samp_seed the call's seed, samp_row0 the first row's index for the noise
+  float samp_invT;
+  uint32_t samp_seed;
+  int samp_row0;
 };
 struct SKPlan {
   int workers = 1;          // workgroups (one per CU)
@@ -121,6 +126,8 @@ struct TileArgs {
                             // launch_argmax_parts
   int tiles_m, tiles_n;     // set by the launcher from the plan
   int splits;               // split-K: F32 sums of split s into plane s of Y ([splits][M][ldy])
+  float samp_invT;          // ARGMAX: categorical sample at temperature 1 / samp_invT (0: argmax)
+  uint32_t samp_seed;
 };
 struct TilePlan {
   int mtw = 0;              // m-tiles per wave: 1 (128-row workgroup tile) or 2 (256 rows)

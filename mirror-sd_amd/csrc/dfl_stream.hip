@@ -498,18 +498,24 @@ DFL_DEV void tile_epilogue(const StreamArgs& a, int lane, int t, const floatx16&
       }
     }
     if (a.keys) {
-      // scan in increasing n so that strict '>' keeps the lowest index on ties
+      // scan in increasing n so that strict '>' keeps the lowest index on ties; a sampling
+      // call ranks l / T + Gumbel noise instead of l
+      const bool samp = a.samp_invT > 0.f;
+      const uint32_t salt = samp ? gumbel_row_salt(a.samp_seed, a.samp_row0 + m) : 0u;
+      auto rank = [&](float l, int n) { return samp ? l * a.samp_invT + gumbel_noise(salt, n) : l; };
       float best = -INFINITY;
       int bn = 0x7fffffff;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int n = nb + 8 * (r >> 2) + (r & 3);
-        if (acc0[r] > best) { best = acc0[r]; bn = n; }
+        const float v = rank(acc0[r], n);
+        if (v > best) { best = v; bn = n; }
       }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int n = nb + 32 + 8 * (r >> 2) + (r & 3);
-        if (acc1[r] > best) { best = acc1[r]; bn = n; }
+        const float v = rank(acc1[r], n);
+        if (v > best) { best = v; bn = n; }
       }
       const float ob = __shfl_xor(best, 32, 64);
       const int on = __shfl_xor(bn, 32, 64);
@@ -827,6 +833,7 @@ DFL_DEV StreamArgs mtile_view(const StreamArgs& a, int mt) {
   if (a.ss_part) v.ss_part = a.ss_part + (size_t)mt * a.ss_mstride;
   if (a.logits) v.logits = a.logits + rows * a.ldl;
   if (a.keys) v.keys = a.keys + rows;
+  v.samp_row0 = a.samp_row0 + (int)rows;
   return v;
 }
 

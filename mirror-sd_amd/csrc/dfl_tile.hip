@@ -427,16 +427,21 @@ __global__ __launch_bounds__(64 * (TG_WM * WN + tile_loaders(WN))) void tile_gem
     // never chosen), then the best of the 32 lanes as (order-preserving value << 32 |
     // ~index), stored in the wave column's own slot (no atomics: each row key would
     // otherwise take one atomic from every column tile)
+    // (a sampling call ranks l / T + Gumbel noise instead of l)
     unsigned long long* part = a.keys + (size_t)(nb0 / RBW + wn) * a.M;
+    const bool samp = a.samp_invT > 0.f;
     static_for<0, MTW>([&](auto t) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         float best = -INFINITY;
         int bn = -1;
+        const uint32_t salt = samp ? gumbel_row_salt(a.samp_seed, row_of(t, i)) : 0u;
         static_for<0, RBW>([&](auto r) {
-          if (v[r][t][i] > best) {
-            best = v[r][t][i];
-            bn = n_lane + 32 * r;
+          const int n = n_lane + 32 * r;
+          const float val = samp ? v[r][t][i] * a.samp_invT + gumbel_noise(salt, n) : v[r][t][i];
+          if (val > best) {
+            best = val;
+            bn = n;
           }
         });
         unsigned long long key =

@@ -79,6 +79,7 @@ SIGNATURES = {
                                           c_void_p]),
     "dfl_device_errors": (c_int32, [c_void_p, ctypes.POINTER(c_int32), c_void_p]),
     "dfl_test_queue_timeout": (c_int32, [c_void_p, c_int32]),
+    "dfl_set_sampling": (c_int32, [c_void_p, ctypes.c_float, ctypes.c_uint64]),
     "dfl_cache_assign": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p, c_int32, c_void_p]),
     "dfl_set_rope_scaling": (c_int32, [c_void_p, c_int32, ctypes.c_double, ctypes.c_double,
                                        ctypes.c_double, c_int32]),

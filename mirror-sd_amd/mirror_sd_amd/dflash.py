@@ -32,7 +32,8 @@ __all__ = ["DFlashDraftModel", "DFlashKVCache", "sample"]
 
 
 def sample(logits, temperature: float = 0.0):
-    """dflash.py:133-136: greedy argmax below 1e-5, else categorical."""
+    """dflash.py:133-136 on host-visible logits: greedy argmax below 1e-5, else categorical.
+    (The draft's own lm_head samples on the GPU: DFlashDraftModel.set_sampling.)"""
     import torch
     if temperature < 1e-5:
         return torch.argmax(logits, dim=-1)
@@ -620,15 +621,30 @@ class DFlashDraftModel:
         self._keep["draft_src"] = (noise, None)
         return out_h.reshape(n_seq, B, H)
 
-    def draft(self, ids, target_hidden=None, cache=None, return_logits=False,
-              return_hidden=False, fused_context=False):
-        """Fused entry point: block token ids [B] (+ new target_hidden rows) in,
-        per-position argmax ids [B] (and fp32 logits [B, V]) out.
+    def set_sampling(self, temperature: float = 0.0, seed: Optional[int] = None):
+        """Draft ids of later calls (draft, draft_batch, run_kernels) are samples from
+        softmax(logits / temperature) -- sample(), dflash.py:133-136 -- drawn on the GPU by
+        the Gumbel-max rule in the lm_head; greedy (argmax) below 1e-5.  ``seed`` fixes the
+        noise (None: a fresh random seed); successive calls draw fresh noise."""
+        import random
+        if seed is None:
+            seed = random.getrandbits(64)
+        _lib.check(self._L.dfl_set_sampling(self._ctx, float(temperature), int(seed) & (2**64 - 1)),
+                   "dfl_set_sampling")
 
-        Equivalent to the serial caller's embed -> draft -> lm_head -> argmax ->
+    def draft(self, ids, target_hidden=None, cache=None, return_logits=False,
+              return_hidden=False, fused_context=False, temperature: Optional[float] = None,
+              seed: Optional[int] = None):
+        """Fused entry point: block token ids [B] (+ new target_hidden rows) in,
+        per-position draft ids [B] (and fp32 logits [B, V]) out.
+
+        Equivalent to the serial caller's embed -> draft -> lm_head -> sample ->
         trim sequence (generate.py:594-609) for all B positions; position 0 (the
-        anchor) is included, callers use 1..B-1.
+        anchor) is included, callers use 1..B-1.  The ids are the argmax, or with
+        ``temperature`` (set_sampling) samples at that temperature.
         """
+        if temperature is not None:
+            self.set_sampling(temperature, seed)
         self._apply_num_layers()
         if cache is None:
             _lib.check(self._L.dfl_cache_reset(self._ctx), "dfl_cache_reset")
@@ -675,12 +691,16 @@ class DFlashDraftModel:
         finally:
             self.select_seq(0)
 
-    def draft_batch(self, ids=None, noise=None, return_logits=False, return_hidden=False):
+    def draft_batch(self, ids=None, noise=None, return_logits=False, return_hidden=False,
+                    temperature: Optional[float] = None, seed: Optional[int] = None):
         """One block for each of sequences 0 .. n_seq-1 at once: ``ids`` [n_seq, B] (or
         ``noise`` [n_seq, B, H]) -> argmax ids [n_seq, B] (+ fp32 logits [n_seq, B, V],
         final-normed hidden [n_seq, B, H]).  Each sequence attends to its own cached
-        context plus its block (the block rows stay uncommitted, as after draft())."""
+        context plus its block (the block rows stay uncommitted, as after draft()).  With
+        ``temperature`` the ids are samples (set_sampling)."""
         import torch
+        if temperature is not None:
+            self.set_sampling(temperature, seed)
         self._apply_num_layers()
         H, V = self.config.hidden_size, self.config.vocab_size
         if noise is not None:

@@ -250,3 +250,61 @@ def test_device_ids_out_of_range_flag_without_host_sync():
     with pytest.raises(ValueError):
         m.draft(bad.cpu(), torch.from_numpy(inp["target_hidden"]))
     m.close()
+
+
+def _chi2_pvalue(counts, probs):
+    """Pearson chi-square goodness of fit of counts against probs, categories with an
+    expected count below 5 lumped together; returns the p-value."""
+    from scipy.stats import chi2
+    n = counts.sum()
+    exp = probs * n
+    big = exp >= 5
+    obs = np.append(counts[big], counts[~big].sum())
+    e = np.append(exp[big], exp[~big].sum())
+    keep = e > 0
+    stat = float(((obs[keep] - e[keep]) ** 2 / e[keep]).sum())
+    return float(chi2.sf(stat, keep.sum() - 1))
+
+
+@pytest.mark.parametrize("V,n_seq,B", [(1024, 1, 8), (32768, 1, 8), (1024, 3, 32)])
+def test_sampling_matches_softmax(V, n_seq, B):
+    """set_sampling(T): the draft ids are draws from softmax(logits / T) per row -- the
+    categorical of sample() (dflash.py:133-136).  Over 600 seeds, each row's counts fit
+    softmax(logits / T) of the same call's returned logits (chi-square, Bonferroni over
+    rows); a fixed seed repeats its draws; T below 1e-5 gives the argmax.  Shapes: the plain
+    stream-K lm_head (V 1024), the balanced one (V 32768), the stacked tile GEMM (3 x 32
+    rows)."""
+    cfg = _cfg(None, layers=1, vocab=V)
+    cfg.block_size = B
+    t = synth.make_weights_numpy(cfg, seed=26)
+    m = _model(cfg, max_ctx=64, max_seqs=n_seq)
+    m.load_weights(torch_tensors(t, "cuda"))
+    rng = np.random.default_rng(27)
+    ids = torch.from_numpy(rng.integers(0, V, (n_seq, B)).astype(np.int32)).cuda()
+    for s in range(n_seq):
+        m.ingest_seq(s, torch.from_numpy(synth.np_normal(28 + s, "th", (16, 5 * 256), 1.0,
+                                                         np.float16)))
+
+    def call(T, seed, logits=False):
+        r = m.draft_batch(ids=ids, return_logits=logits, temperature=T, seed=seed)
+        return r
+
+    g, lg = call(0.0, 0, logits=True)
+    lg = lg.reshape(n_seq * B, V).double().cpu().numpy()
+    np.testing.assert_array_equal(g.reshape(-1).cpu().numpy(), np.argmax(lg, axis=1))
+    np.testing.assert_array_equal(call(1e-6, 5).cpu().numpy(), g.cpu().numpy())
+    T = float(np.median(lg.std(axis=1))) / 3.0   # logits / T spread ~ 3: a few dozen likely ids
+    a1, a2 = call(T, 123).cpu().numpy(), call(T, 123).cpu().numpy()
+    np.testing.assert_array_equal(a1, a2)
+    N = 600
+    draws = np.stack([call(T, 1000 + i).reshape(-1).cpu().numpy() for i in range(N)])
+    rows = n_seq * B
+    p_min = 1.0
+    for r in range(rows):
+        p = np.exp((lg[r] - lg[r].max()) / T)
+        p /= p.sum()
+        counts = np.bincount(draws[:, r], minlength=V).astype(np.float64)
+        p_min = min(p_min, _chi2_pvalue(counts, p))
+    assert p_min * rows > 1e-3, f"a row's draws do not fit softmax(logits / T): p = {p_min}"
+    assert len(np.unique(draws[:, 0])) > 3   # the samples are not the argmax
+    m.close()
