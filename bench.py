@@ -174,6 +174,48 @@ def cpu_baseline(wl, model, host, ids, max_seconds=12.0, max_blocks=8):
                       f"dequantised W8A16 weights, context K/V precomputed)"}
 
 
+def python_path_steps(model, wl, args, ids, k=16):
+    """The decode-loop step through the Python drop-in interface, as the serial caller
+    makes it (generate.py:591-609): ``draft_model(noise_embedding, target_hidden, cache)``
+    with k new context rows, the host waiting for the result, then ``c.trim(block)`` on
+    every layer's cache; and the fused ``draft(ids, target_hidden, cache)`` (ids instead of
+    hidden states) the same way.  Wall-clock per step, host overhead included."""
+    import torch
+    from mirror_sd_amd import synth
+    cfg = wl.cfg
+    full = synth.make_inputs_torch(cfg, wl.block, wl.ctx, seed=args.seed, device="cuda")
+    rows = synth.make_inputs_torch(cfg, wl.block, k, seed=args.seed + 7,
+                                   device="cuda")["target_hidden"][None]
+    noise = model.embed_block(ids)
+    cache = model.make_cache(0, 0)
+    model(noise, full["target_hidden"][None], cache=cache)   # the resident context
+    for c in cache:
+        c.trim(wl.block)
+    del full
+    res = {}
+    for name, call in (("call", lambda: model(noise, rows, cache=cache)),
+                       ("draft", lambda: model.draft(ids, rows, cache=cache))):
+        n = 0
+        for it in range(5 + args.steps):
+            if it == 5:
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+            out = call()
+            torch.cuda.synchronize()   # the caller reads the result (mx.eval, generate.py:606)
+            for c in cache:
+                c.trim(wl.block)
+            n += 1
+        res[f"{name}_step_us"] = round((time.perf_counter() - t0) * 1e6 / args.steps, 2)
+    res["what"] = (f"wall-clock per decode-loop step through the Python interface: {k} new "
+                   f"context rows + the block ({wl.ctx}-row resident context), host waits for "
+                   f"the result, then trim(block) on every layer: call_step_us = "
+                   f"draft_model(noise, target_hidden, cache) (hidden states out), "
+                   f"draft_step_us = draft(ids, target_hidden, cache) (ids out)")
+    print(f"python path, {k} new rows: __call__ {res['call_step_us']:.1f} us, draft() "
+          f"{res['draft_step_us']:.1f} us per step", file=sys.stderr, flush=True)
+    return res
+
+
 def run_workload(wl, args, sweep, want_cpu):
     """Build the model of workload ``wl``, ingest its context(s), time ``args.steps`` draft
     blocks (after ``args.warmup``), profile the kernels and optionally sweep the resident
@@ -406,6 +448,10 @@ def run_workload(wl, args, sweep, want_cpu):
             print(f"context {C}: block {ms_c * 1e3:.1f} us, ingest {ing:.2f} ms",
                   file=sys.stderr, flush=True)
 
+    python_path = None
+    if not batched and args.steady:
+        python_path = python_path_steps(model, wl, args, ids)
+
     cpu = None
     if want_cpu:
         try:
@@ -420,7 +466,7 @@ def run_workload(wl, args, sweep, want_cpu):
             "nbytes": nbytes, "roofline": roofline, "kernels": kernels, "cpu": cpu,
             "ingest_ms": ingest_ms, "first_ingest_s": first_ingest_s, "setup_s": setup_s,
             "ms_events": ms_events, "context_sweep": context_sweep, "steady": steady,
-            "first_ids": first_ids,
+            "python_path": python_path, "first_ids": first_ids,
             "n_seq": n_seq, "batched": batched}
 
 
@@ -528,6 +574,7 @@ def main():
                    "wall_ms_per_step": round(r["wall_s"] * 1e3 / args.steps, 4)},
         "kernels": r["kernels"],
         "steady_step": r["steady"],
+        "python_path": r["python_path"],
         "context_sweep": r["context_sweep"],
         "batched": extra,
         "draft_ids_head": r["first_ids"][:4],
