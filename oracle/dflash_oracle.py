@@ -85,6 +85,27 @@ class accumulation_split:
         return False
 
 
+_PV16 = [False]
+
+
+class attention_fp16_p:
+    """Context manager: the attention's probabilities go into P.V rounded to fp16, and the
+    softmax denominator is the sum of those fp16 values -- the rounding points of a
+    flash-attention kernel that feeds fp16 P to its P.V product (p = exp(s - max) unnormalised,
+    O = sum fp16(p) v / sum fp16(p)).  MLX's fused SDPA does not state its own rounding
+    points, so this is another run whose argmax differences mark rows the oracle cannot
+    decide."""
+
+    def __enter__(self):
+        self.prev = _PV16[0]
+        _PV16[0] = True
+        return self
+
+    def __exit__(self, *exc):
+        _PV16[0] = self.prev
+        return False
+
+
 def _mm(a: np.ndarray, b: np.ndarray) -> np.ndarray:
     """a @ b, the reduction axis (a's last, b's first) summed in _SPLIT[0] ordered ranges."""
     n = _SPLIT[0]
@@ -225,6 +246,10 @@ def sdpa_gqa(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, fp16: bo
         s = (q[h].astype(dtype) @ k[g].astype(dtype).T) * dtype(scale)
         s = s - s.max(axis=-1, keepdims=True)
         p = np.exp(s)
+        if _PV16[0]:
+            p = p.astype(np.float16).astype(dtype)
+            out[h] = _mm(p, v[g].astype(dtype)) / p.sum(axis=-1, keepdims=True)
+            continue
         p /= p.sum(axis=-1, keepdims=True)
         out[h] = _mm(p, v[g].astype(dtype))
     return _r(out, fp16, dtype)

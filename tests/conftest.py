@@ -36,9 +36,9 @@ def pytest_terminal_summary(terminalreporter):
         terminalreporter.write_line(
             f"argmax agreement over {len(ARGMAX_TOTALS['cases'])} checks: {a}/{n} = {a / n:.4f} "
             f"(exempt: {ARGMAX_TOTALS['undecided']} oracle-undecided, {ARGMAX_TOTALS['noise']} "
-            f"within the logit noise)")
+            f"listed unbacked)")
         for what, n_agree, rows, n_und, n_noise in ARGMAX_TOTALS["cases"]:
             if n_agree < rows:
                 terminalreporter.write_line(
                     f"  {what}: {n_agree}/{rows} (exempt {n_und} oracle-undecided, "
-                    f"{n_noise} within the logit noise)")
+                    f"{n_noise} listed unbacked)")

@@ -8,10 +8,10 @@ the GPU host.  Tolerances: final hidden cosine >= 0.9995 and max-abs <= 2e-2 (fp
 argmax identical on every row except where the oracle itself is undecided: its runs that
 differ in accumulation only (fp32, fp64, and fp32 with every reduction summed over 2, 4 or
 8 ordered k-ranges, all stored in the fixture) do not all agree, and the GPU picked one of
-their ids; or, failing that, where the GPU picked the oracle's runner-up and the top-2 gap
-lies within 4 x the measured logit noise (parity_util.check_argmax states the rule and
-prints the counts of each kind); GPU logits at the
-oracle's top-2 indices within LOGIT_TOL of the oracle's values.
+their ids -- at most the committed number of such rows per fixture -- or the row is the one
+listed with its id in parity_util.KNOWN_UNBACKED (check_argmax states the rule and prints
+the counts); GPU logits at the oracle's top-2 indices within LOGIT_TOL of the oracle's
+values.
 """
 
 import os
@@ -75,8 +75,7 @@ def test_full_draft_matches_golden(name):
     assert_close_fp16(h.float().cpu().numpy(), g["hidden"], what=f"{name} final hidden")
     lg = logits.cpu().numpy()
     ids = ids.cpu().numpy()
-    check_argmax(ids, lg, g["ids"], oracle_alt_runs(g), name, g["top2_idx"], g["top2_val"], LOGIT_TOL,
-                 noise_rule=True)
+    check_argmax(ids, lg, g["ids"], oracle_alt_runs(g), name, g["top2_idx"], g["top2_val"], LOGIT_TOL)
     # the lm_head hands half tiles out at run time from self-resetting counters: later
     # launches on the same inputs give the same bits, and no queue wait gave up
     for rep in range(2):
@@ -118,7 +117,7 @@ def sweep_model():
 def _check_against(g, name, ids, logits, h):
     assert_close_fp16(h.float().cpu().numpy(), g["hidden"], what=f"{name} final hidden")
     check_argmax(ids.cpu().numpy(), logits.cpu().numpy(), g["ids"], oracle_alt_runs(g), name,
-                 g["top2_idx"], g["top2_val"], LOGIT_TOL, noise_rule=True)
+                 g["top2_idx"], g["top2_val"], LOGIT_TOL)
 
 
 @pytest.mark.parametrize("ctx", SWEEP)
@@ -187,6 +186,6 @@ def test_decode_loop_matches_golden():
         assert_close_fp16(h.float().cpu().numpy(), g[f"s{i}_hidden"], what=f"{name} step {i} hidden")
         check_argmax(idg.cpu().numpy(), lg.cpu().numpy(), g[f"s{i}_ids"], oracle_alt_runs(g, f"s{i}_"),
                      f"{name} step {i} ({n} context rows)", g[f"s{i}_top2_idx"],
-                     g[f"s{i}_top2_val"], LOGIT_TOL, noise_rule=True)
+                     g[f"s{i}_top2_val"], LOGIT_TOL)
     assert device_errors(m) == 0
     m.close()

@@ -235,17 +235,26 @@ def test_rocprof_summary_trace_skips_warmup_blocks(tmp_path):
 
 def test_argmax_agreement_rule():
     """parity_util.check_argmax: a GPU id that differs from the oracle's fp32 run passes only
-    if another accumulation run of the oracle picked it (any row of alt_ids), or, with
-    noise_rule=True, if it is the oracle's runner-up and the top-2 gap is inside the
-    measured noise band; anything else raises.  The exact ids must be the logits' argmax."""
+    if another accumulation run of the oracle picked it (any row of alt_ids) and the check's
+    committed budget of such rows is not exceeded, or if the row is listed with that id in
+    KNOWN_UNBACKED; a runner-up inside any gap, however small, raises otherwise.  The exact
+    ids must be the logits' argmax."""
     import copy
     import parity_util as P
     saved = copy.deepcopy(P.ARGMAX_TOTALS)   # synthetic rows stay out of the session totals
+    budgets, known = dict(P.EXEMPT_BUDGET), dict(P.KNOWN_UNBACKED)
     try:
+        P.EXEMPT_BUDGET["alt run"] = 1
+        P.EXEMPT_BUDGET["alt run, two rows"] = 1
+        P.KNOWN_UNBACKED[("listed", 4)] = 1 + 4 % 16
         _argmax_rule_cases(P)
     finally:
         P.ARGMAX_TOTALS.clear()
         P.ARGMAX_TOTALS.update(saved)
+        P.EXEMPT_BUDGET.clear()
+        P.EXEMPT_BUDGET.update(budgets)
+        P.KNOWN_UNBACKED.clear()
+        P.KNOWN_UNBACKED.update(known)
 
 
 def _argmax_rule_cases(P):
@@ -264,9 +273,19 @@ def _argmax_rule_cases(P):
     alts = np.stack([ref, ref.copy()])
     alts[1, 2] = 9
     assert P.check_argmax(ids, lg, ref, alts, "alt run", ti, tv, 5.0) == (5, 6, 1)
+    with pytest.raises(AssertionError):   # no other run picked it
+        P.check_argmax(ids, lg, ref, alts[:1], "alt run", ti, tv, 5.0)
+    with pytest.raises(AssertionError):   # an unlisted check has no budget
+        P.check_argmax(ids, lg, ref, alts, "no budget", ti, tv, 5.0)
+    # two backed rows against a budget of one
+    ids3, lg3, alts3 = ids.copy(), lg.copy(), alts.copy()
+    ids3[3] = 11
+    lg3[3] = 0.0
+    lg3[3, 11] = 1.0
+    alts3[0, 3] = 11
     with pytest.raises(AssertionError):
-        P.check_argmax(ids, lg, ref, alts[:1], "no run picked it", ti, tv, 5.0)
-    # row 4: the runner-up with a gap far inside the noise band: exempt only with the rule
+        P.check_argmax(ids3, lg3, ref, alts3, "alt run, two rows", ti, tv, 5.0)
+    # row 4: the runner-up with a gap of 1e-9, backed by no run: fails unless listed
     ids2 = ref.copy()
     ids2[4] = ti[4, 1]
     lg2 = lg.copy()
@@ -278,6 +297,12 @@ def _argmax_rule_cases(P):
     tv2[4] = [1.0, 1.0 - 1e-9]
     with pytest.raises(AssertionError):
         P.check_argmax(ids2, lg2, ref, ref, "strict", ti, tv2, 5.0)
-    assert P.check_argmax(ids2, lg2, ref, ref, "noise", ti, tv2, 5.0, noise_rule=True)[2] == 1
+    assert P.check_argmax(ids2, lg2, ref, ref, "listed", ti, tv2, 5.0)[2] == 1
+    ids4, lg4 = ids2.copy(), lg2.copy()   # a listed row with another id fails
+    ids4[4] = 7
+    lg4[4] = 0.0
+    lg4[4, 7] = 1.0
+    with pytest.raises(AssertionError):
+        P.check_argmax(ids4, lg4, ref, ref, "listed", ti, tv2, 5.0)
     with pytest.raises(AssertionError):   # ids must be the argmax of the logits
         P.check_argmax(ids, lg2, ref, alts, "not argmax", ti, tv, 5.0)

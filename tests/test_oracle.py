@@ -200,6 +200,29 @@ def test_sdpa_single_key_and_identical_keys():
         np.testing.assert_allclose(o[h], np.broadcast_to(vv[h // 2].mean(0), (3, 8)), rtol=1e-12)
 
 
+def test_sdpa_fp16_p_closed_forms():
+    """attention_fp16_p (fp16 P into P.V, the denominator the sum of those fp16 values): one
+    key gives its value row; identical keys give the mean of V (every p = 1 exactly); against
+    the default softmax the output moves only by P's fp16 rounding (relative 2^-11)."""
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal((4, 3, 128))
+    k = rng.standard_normal((2, 1, 128))
+    v = rng.standard_normal((2, 1, 128))
+    with O.attention_fp16_p():
+        out = O.sdpa_gqa(q, k, v, 128 ** -0.5, False)
+    np.testing.assert_allclose(out, np.repeat(v, 2, axis=0).repeat(3, axis=1), rtol=1e-15)
+    k2 = np.repeat(rng.standard_normal((2, 1, 128)), 7, axis=1)
+    v2 = rng.standard_normal((2, 7, 128))
+    with O.attention_fp16_p():
+        out2 = O.sdpa_gqa(q, k2, v2, 128 ** -0.5, False)
+    np.testing.assert_allclose(out2[0, 0], v2[0].mean(axis=0), rtol=1e-13)
+    k3, v3 = rng.standard_normal((2, 50, 128)), rng.standard_normal((2, 50, 128))
+    ref = O.sdpa_gqa(q, k3, v3, 128 ** -0.5, False)
+    with O.attention_fp16_p():
+        got = O.sdpa_gqa(q, k3, v3, 128 ** -0.5, False)
+    assert 0 < np.abs(got - ref).max() < 2e-3
+
+
 def test_sdpa_gqa_mapping_onehot():
     # V of kv head g is the constant g: output of query head h must be h // rep.
     NH, NKV, L, D = 8, 2, 5, 4
