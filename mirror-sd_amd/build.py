@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import argparse
 import glob
+import json
 import os
 import shutil
 import subprocess
@@ -23,6 +24,10 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "mirror_sd_amd", "libdflash_hip.so")
+# Per-kernel register, scratch, LDS and occupancy figures of the last build (the compiler's
+# kernel-resource-usage remarks), one record per kernel symbol.
+RESOURCES = os.path.join(BUILD, "kernel_resources.json")
+_USAGE_FLAG = "-Rpass-analysis=kernel-resource-usage"
 ARCH = os.environ.get("DFL_OFFLOAD_ARCH", "gfx950")
 
 
@@ -50,27 +55,63 @@ _HOST_FEATURE_NOTE = "'-packed-fp32-ops' is not a recognized feature for this ta
 
 
 def compiler_messages(text: str) -> str:
-    return "\n".join(l for l in text.splitlines()
-                     if l.strip() and _HOST_FEATURE_NOTE not in l and "--hip-link" not in l)
+    """Compiler output minus the host feature note and the resource-usage remarks (with the
+    source-snippet lines printed under each remark)."""
+    keep, in_remark = [], False
+    for l in text.splitlines():
+        if _USAGE_FLAG in l:
+            in_remark = True
+            continue
+        gutter, bar, _ = l.partition("|")
+        if in_remark and bar and (not gutter.strip() or gutter.strip().isdigit()):
+            continue   # "  23 | source" and "     | ^" under the remark
+        in_remark = False
+        if l.strip() and _HOST_FEATURE_NOTE not in l and "--hip-link" not in l:
+            keep.append(l)
+    return "\n".join(keep)
 
 
-def compile_one(src: str, debug: bool) -> str:
+def resource_usage(text: str) -> dict:
+    """Parse the kernel-resource-usage remarks ("Function Name: f" followed by "Key: value"
+    lines) into {kernel: {key: value}}; numeric values become ints."""
+    out, cur = {}, None
+    for line in text.splitlines():
+        if _USAGE_FLAG not in line or "remark:" not in line:
+            continue
+        body = line.split("remark:", 1)[1].split("[" + _USAGE_FLAG, 1)[0].strip()
+        key, _, val = body.partition(":")
+        val = val.strip()
+        if key == "Function Name":
+            cur = out.setdefault(val, {})
+        elif cur is not None:
+            cur[key.strip()] = int(val) if val.lstrip("-").isdigit() else val
+    return out
+
+
+def compile_one(src: str, debug: bool):
     obj = os.path.join(BUILD, os.path.basename(src).replace(".hip", ".o"))
-    cmd = [hipcc(), *common_flags(debug), "-c", src, "-o", obj]
+    cmd = [hipcc(), *common_flags(debug), _USAGE_FLAG, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     msgs = compiler_messages(r.stdout + "\n" + r.stderr)
     if msgs:
         print(f"{os.path.basename(src)}:\n{msgs}", file=sys.stderr)
-    return obj
+    return obj, resource_usage(r.stdout + "\n" + r.stderr)
 
 
 def build(jobs: int = 8, debug: bool = False, verbose: bool = True) -> str:
     os.makedirs(BUILD, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
-        objs = list(ex.map(lambda s: compile_one(s, debug), srcs))
+        done = list(ex.map(lambda s: compile_one(s, debug), srcs))
+    objs = [o for o, _ in done]
+    usage = {k: v for _, u in done for k, v in u.items()}
+    with open(RESOURCES, "w") as f:
+        json.dump(usage, f, indent=1, sort_keys=True)
+    spills = sorted(k for k, v in usage.items() if v.get("ScratchSize [bytes/lane]", 0))
+    if spills and not debug:
+        print(f"warning: kernels using scratch (register spills): {spills}", file=sys.stderr)
     tmp = OUT + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -607,7 +607,8 @@ static int qk_rope(const QKRopeArgs& q, hipStream_t st) {
 static int block_attention(const AttnArgs& at, hipStream_t st) {
   if (const char* why = check_attn_args(at))
     return fail(DFL_EINVAL, std::string("attention launch refused: ") + why);
-  launch_block_attention(at, st);
+  if (!launch_block_attention(at, st))
+    return fail(DFL_EINVAL, "attention launch refused: more than 8 waves per workgroup");
   return DFL_OK;
 }
 

@@ -55,11 +55,12 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 // PIPE (one sequence, chunks of several stages, one workgroup of <= 5 waves per CU): two
 // stage buffers (160 KiB), the next stage's loads in flight while this one computes.
-// MAXW: the most waves a launch of the instantiation has.  Up to 5 waves (one per query
-// tile of the production shapes) the compiler has 2 waves' registers per SIMD and spills
-// nothing; the 12-wave instantiation (key-lane waves of small shapes) is held to 168.  The
-// two-buffer kernel with 5 query tiles runs on 8 waves (SPLIT below: 32K keys 1034 vs
-// 1050-1056 us per block).
+// MAXW: the most waves a launch of the instantiation has.  The kernel needs about 190
+// VGPRs, so a CU holds 8 of its waves (2 per SIMD): MAXW <= 8 gives every instantiation
+// that budget (a 12-wave bound held it to 168 and spilled 21 VGPRs), and the launcher keeps
+// a workgroup's waves within 8, or 4 where two workgroups share a CU.  The two-buffer kernel
+// with 5 query tiles runs on 8 waves (SPLIT below: 32K keys 1034 vs 1050-1056 us per
+// block).
 template <bool PIPE, int MAXW>
 __global__ __launch_bounds__(64 * MAXW) void block_attn_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
@@ -372,10 +373,15 @@ bool launch_block_attention(const AttnArgs& a_in, hipStream_t st) {
   const int n_qt = (R + 31) / 32;
   a.q_per_group = std::min(n_qt, 8);
   // Extra waves per query tile only where the tiles alone leave the CU short of waves;
-  // each takes at least one key block of the chunk.
+  // each takes at least one key block of the chunk.  At most 8 waves per CU (the kernel's
+  // registers allow 2 per SIMD): 8 per workgroup for one sequence (one workgroup per CU),
+  // 4 for several (two per CU).
   int cblocks = 1 << 30;
   for (int i = 0; i < a.n_seq; ++i) cblocks = std::min(cblocks, a.sq[i].chunk / 32);
-  a.kw = a.q_per_group >= 3 ? 1 : std::max(1, std::min(std::min(4, cblocks), 12 / a.q_per_group));
+  const int wg_waves = a.n_seq == 1 ? 8 : 4;
+  a.kw = a.q_per_group >= 3 ? 1
+                            : std::max(1, std::min(std::min(4, cblocks), wg_waves / a.q_per_group));
+  if (a.q_per_group * a.kw > 8) return false;   // beyond every instantiation's bound
   const int groups = (n_qt + a.q_per_group - 1) / a.q_per_group;
   const int merge_bytes = a.q_per_group * (a.kw - 1) * AT_PART_BYTES;
   const int lds_bytes = std::max(AT_STAGE_BYTES, merge_bytes);
@@ -392,7 +398,7 @@ bool launch_block_attention(const AttnArgs& a_in, hipStream_t st) {
   else if (a.q_per_group * a.kw <= 5)
     hipLaunchKernelGGL((block_attn_kernel<false, 5>), grid, block, lds_bytes, st, a);
   else
-    hipLaunchKernelGGL((block_attn_kernel<false, 12>), grid, block, lds_bytes, st, a);
+    hipLaunchKernelGGL((block_attn_kernel<false, 8>), grid, block, lds_bytes, st, a);
   hipLaunchKernelGGL(attn_merge_kernel, dim3(a.n_seq * a.NH * a.B), dim3(128), 0, st, a);
   return true;
 }

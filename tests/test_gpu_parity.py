@@ -430,3 +430,26 @@ def test_two_stage_attention_with_sink_window_matches_oracle(n_heads):
             c.trim(B)
         ocache[0].trim(B)
     assert ocache[0].keys.shape[1] == sink + window - B   # eviction happened
+
+
+@pytest.mark.parametrize("B,C", [(16, 3500), (16, 2048), (8, 3500)])
+def test_key_lane_attention_waves_match_oracle(B, C):
+    """Blocks of one or two 32-row query tiles per KV head (32 query heads over 8 KV heads,
+    block 8 or 16) take extra key-lane waves per tile, merged in LDS: 16 rows at 3500 / 2048
+    context rows run 4 / 3 key lanes (8 / 6 waves per workgroup), 8 rows at 3500 run 4 (4
+    waves).  Against the oracle forward."""
+    cfg = DFlashConfig(hidden_size=256, num_hidden_layers=1, intermediate_size=512,
+                       num_attention_heads=32, num_key_value_heads=8, head_dim=128,
+                       vocab_size=1024, block_size=B, mask_token_id=1023)
+    t = synth.make_weights_numpy(cfg, seed=12)
+    W = O.OracleWeights(cfg, t)
+    ids = np.array([5] + [1023] * (B - 1), dtype=np.int32)
+    noise = O.embed(W, ids).astype(np.float16)
+    th = synth.np_normal(12, f"keylane.{B}.{C}", (C, 5 * cfg.hidden_size), 1.0, np.float16)
+    print(f"key-lane attention: block {B}, {C} context rows", flush=True)
+    m = _model(cfg, max_ctx=C + B)
+    m.load_weights(torch_tensors(t, "cuda"))
+    ref = O.draft_forward(W, noise, th, fp16=True)
+    out = m(torch.from_numpy(noise)[None], torch.from_numpy(th)[None])
+    torch.cuda.synchronize()
+    assert_close_fp16(out[0].float().cpu().numpy(), ref, what=f"block {B}, ctx {C}")

@@ -33,6 +33,20 @@ def test_header_symbols_exported():
     assert set(_lib.SIGNATURES) == set(syms)
 
 
+def test_no_kernel_spills():
+    """Every kernel of the last build fits in its registers: no scratch memory (register
+    spills) and no dynamic stack, from the compiler's resource-usage record of the build."""
+    import json
+    path = os.path.join(ROOT, "mirror-sd_amd", "_build", "kernel_resources.json")
+    if not os.path.exists(path):
+        pytest.skip("no resource record: the library was not built by mirror-sd_amd/build.py here")
+    usage = json.load(open(path))
+    assert sum("block_attn_kernel" in k for k in usage) >= 4 and len(usage) >= 50
+    spills = {k: v["ScratchSize [bytes/lane]"] for k, v in usage.items()
+              if v["ScratchSize [bytes/lane]"] or v["VGPRs Spill"] or v["Dynamic Stack"] != "False"}
+    assert not spills, f"kernels using scratch (bytes per lane): {spills}"
+
+
 def _cfg(**over):
     c = dict(hidden=256, n_heads=4, n_kv_heads=2, head_dim=128, intermediate=512, n_layers=2,
              n_target_feat=5, vocab=1024, max_block=16, max_ctx=64, rms_eps=1e-6,
