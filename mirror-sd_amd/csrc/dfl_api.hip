@@ -1050,7 +1050,6 @@ static int draft_rows(dfl_ctx* ctx, const char* who, int seq0, int n_seq,
       q.eps = eps;
       q.log2_theta = std::log2(ctx->cfg.rope_theta);
       q.inv_freq = ctx->rope_freqs();
-    q.inv_freq = ctx->rope_freqs();
       q.Q = ctx->Q + (size_t)g0 * NH * B * 128;
       q.cap = ctx->cap;
       AttnArgs at{};
