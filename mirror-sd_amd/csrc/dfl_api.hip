@@ -621,9 +621,12 @@ static int tgemm(dfl_ctx* ctx, int cat, int wt, int epi, const uint4* W, int N, 
                  const half_t* X, int M, const TileArgs& e, hipStream_t st,
                  int* n_parts = nullptr) {
   const bool split_ok = (epi == TG_F32 || epi == TG_RESID) && ctx->tile_ws && M <= ctx->RM;
-  TilePlan p = tile_plan(M, N, K, wt, ctx->n_cu, epi == TG_SWIGLU, split_ok);
-  if (p.splits > 1 && (size_t)p.splits * M * N > ctx->tile_ws_floats)
-    p = tile_plan(M, N, K, wt, ctx->n_cu, epi == TG_SWIGLU);   // planes do not fit: no split
+  // re-tiled last rounds for the epilogues whose outputs do not depend on the tile shape
+  // (the ARGMAX keys are per wave column)
+  const bool retile = epi != TG_ARGMAX;
+  TilePlan p = tile_plan(M, N, K, wt, ctx->n_cu, epi == TG_SWIGLU, split_ok, retile);
+  if (p.splits > 1 && (size_t)p.splits * M * N > ctx->tile_ws_floats)   // planes do not fit
+    p = tile_plan(M, N, K, wt, ctx->n_cu, epi == TG_SWIGLU, false, retile);
   if (n_parts) *n_parts = N / (32 * p.rbw);
   TileArgs a = e;
   a.W = W;

@@ -5,6 +5,7 @@
 #pragma once
 
 #include "dfl_kernels.h"
+#include "dfl_tile_plan.h"
 
 namespace dfl {
 
@@ -146,6 +147,15 @@ inline const char* check_tile_args(int wt, int epi, const TileArgs& a, const Til
     return "tile counts do not cover the product";
   if (p.splits < 1 || p.splits > a.K / 64) return "split-K factor outside [1, K/64]";
   if (p.splits > 1 && epi != TG_F32) return "split-K writes F32 planes only";
+  if (p.tail_shape >= 0) {
+    if (p.tail_shape >= kNumTileShapes || p.splits != 1) return "re-tiled tail: unknown shape";
+    const TileShape& u = kTileShapes[p.tail_shape];
+    if (u.wt != wt || a.K % u.kc || (128 * p.mtw) % (128 * u.mtw) ||
+        (32 * p.rbw * p.wn) % (32 * u.rbw * u.wn) || (epi == TG_SWIGLU && u.rbw % 2))
+      return "re-tiled tail: the shape does not divide the plan's tiles";
+    if (p.head_tiles < 1 || p.head_tiles >= p.tiles_m * p.tiles_n)
+      return "re-tiled tail: needs head tiles and a tail";
+  }
   if ((long long)p.tiles_m * p.tiles_n * p.splits > 0x7fffffffLL) return "too many tiles";
   return nullptr;
 }

@@ -126,6 +126,11 @@ struct TileArgs {
                             // launch_argmax_parts
   int tiles_m, tiles_n;     // set by the launcher from the plan
   int splits;               // split-K: F32 sums of split s into plane s of Y ([splits][M][ldy])
+  // Tile range of the launch: tiles [tile0, tile0 + ntiles) of the plan's order (ntiles ==
+  // 0: every tile).  With pmt > 0 the launch re-tiles them: each of those (parent) tiles of
+  // pmt m-tiles x prb row-blocks is covered by workgroups of the launch's smaller shape.
+  int tile0, ntiles;
+  int pmt, prb;
   float samp_invT;          // ARGMAX: categorical sample at temperature 1 / samp_invT (0: argmax)
   uint32_t samp_seed;
 };
@@ -136,6 +141,11 @@ struct TilePlan {
   int kc = 0;               // k per LDS stage: 32 or 64
   int tiles_m = 0, tiles_n = 0;
   int splits = 1;           // split-K factor (F32 planes, then launch_tile_reduce)
+  // tail re-tiling: the first head_tiles tiles run in full rounds of the CUs; the rest (a
+  // partial last round) run on the smaller shape tail_shape (an index of kTileShapes),
+  // several workgroups per tile, each over the whole K, so the sums are unchanged
+  int head_tiles = 0;
+  int tail_shape = -1;
 };
 // (tile_plan / tile_lds_bytes: dfl_tile_plan.h)
 // The split-K planes parts [splits][M][N] summed in plane order, with epilogue TG_F32 (into

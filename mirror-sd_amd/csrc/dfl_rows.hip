@@ -266,41 +266,95 @@ void launch_afl_to_rows(const half_t* x, int M, int N, half_t* h, hipStream_t st
 }
 
 
-// One wave per (sequence, row m, head slot); lane j holds head elements j and j + 64, which are
-// exactly the neox RoPE pair (dflash.py:263-275, split-half rotation), so the
-// rotation is lane-local.  Angles are computed in fp64 (pos * theta^(-j/64)).
+// Head slots [slot0, slot0 + n_slots) in q|k|v numbering: Q heads, then K heads, then V
+// heads (slot >= NH + NKV).  The launch's blocks come in two parts: the first handles the
+// Q/K slots, one wave per (sequence, row m, slot); the rest the V slots, one workgroup per
+// (sequence, V slot, 64 rows).
+struct QkRopeGrid {
+  int qk0, nqk, v0, nv;      // first Q/K slot and count, first V slot and count
+  long long qk_blocks;       // blocks of the Q/K part (4 waves each)
+  int v_tiles;               // 64-row tiles per sequence
+};
+__host__ __device__ inline QkRopeGrid qk_rope_grid(const QKRopeArgs& a) {
+  QkRopeGrid gr;
+  const int kvs = a.NH + a.NKV, end = a.slot0 + a.n_slots;
+  gr.qk0 = a.slot0;
+  gr.nqk = (end < kvs ? end : kvs) - a.slot0;
+  if (gr.nqk < 0) gr.nqk = 0;
+  gr.v0 = a.slot0 > kvs ? a.slot0 : kvs;
+  gr.nv = end - gr.v0;
+  if (gr.nv < 0) gr.nv = 0;
+  gr.qk_blocks = ((long long)a.M * gr.nqk * a.n_seq + 3) / 4;
+  gr.v_tiles = (a.M + 63) / 64;
+  return gr;
+}
+
+// Column of slot `slot`, element 0, and the row index of row m in the projection rows.
+DFL_DEV void qk_rope_src(const QKRopeArgs& a, int sidx, int m, int slot, size_t& row, int& c0) {
+  row = a.layer_cols ? (size_t)m : (size_t)sidx * a.M + m;
+  c0 = (a.layer_cols ? sidx * a.layer_cols : 0) + (slot - a.col_slot0) * 128;
+}
+
+// Projection value (fp16 Linear output, as float) of row `row`, column c: rounded by the GEMM
+// epilogue (qkv16), or here from the fp32 GEMM rows and the per-column scales (qkv32).
+DFL_DEV float qk_rope_value(const QKRopeArgs& a, size_t row, int c) {
+  return a.qkv32 ? h2f(f2h(a.qkv32[row * a.N + c] * h2f(a.oscale[c]))) : h2f(a.qkv16[row * a.N + c]);
+}
+
+// Q/K part: lane j holds head elements j and j + 64, which are exactly the neox RoPE pair
+// (dflash.py:263-275, split-half rotation), so the rotation is lane-local.  Angles are
+// computed in fp64 (pos * theta^(-j/64), or the scaled frequency table).
+// V part: the workgroup reads its 64 rows x 128 values row by row (coalesced), transposes
+// them through LDS and writes each Vt row d as 64 consecutive cache columns, so the
+// transposed cache layout costs no scattered 2-byte stores.
 __global__ __launch_bounds__(256) void qk_rope_kernel(QKRopeArgs a) {
+  __shared__ half_t vt_s[128][66];   // [d][row], rows padded against bank conflicts
+  const QkRopeGrid gr = qk_rope_grid(a);
+  if ((long long)blockIdx.x >= gr.qk_blocks) {
+    const long long vb = (long long)blockIdx.x - gr.qk_blocks;
+    const int tile = (int)(vb % gr.v_tiles);
+    const long long sv = vb / gr.v_tiles;
+    const int sidx = (int)(sv / gr.nv), slot = gr.v0 + (int)(sv % gr.nv);
+    const RopeSeq& sq = a.sq[sidx];
+    const int m0 = tile * 64;
+    for (int i = threadIdx.x; i < 64 * 128; i += 256) {
+      const int r = i >> 7, d = i & 127;
+      half_t v = (half_t)0.0f;
+      if (m0 + r < a.M) {
+        size_t row;
+        int c0;
+        qk_rope_src(a, sidx, m0 + r, slot, row, c0);
+        v = f2h(qk_rope_value(a, row, c0 + d));
+      }
+      vt_s[d][r] = v;
+    }
+    __syncthreads();
+    const int gk = slot - (a.NH + a.NKV);
+    half_t* vt = sq.Vt + (size_t)gk * 128 * a.cap;
+    for (int i = threadIdx.x; i < 64 * 128; i += 256) {
+      const int d = i >> 6, r = i & 63;
+      if (m0 + r >= a.M) continue;
+      const int crow = cache_slot(sq, a.M, m0 + r);
+      if (crow >= 0) vt[(size_t)d * a.cap + crow] = vt_s[d][r];
+    }
+    return;
+  }
   const int lane = threadIdx.x & 63;
   const long long p = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const long long per_seq = (long long)a.M * a.n_slots;
+  const long long per_seq = (long long)a.M * gr.nqk;
   if (p >= per_seq * a.n_seq) return;
   const int sidx = (int)(p / per_seq);
   const long long pr = p - (long long)sidx * per_seq;
-  const int m = (int)(pr / a.n_slots);
-  const int slot = a.slot0 + (int)(pr - (long long)m * a.n_slots);
+  const int m = (int)(pr / gr.nqk);
+  const int slot = gr.qk0 + (int)(pr - (long long)m * gr.nqk);
   const RopeSeq& sq = a.sq[sidx];
-  const size_t row = a.layer_cols ? (size_t)m : (size_t)sidx * a.M + m;
-  const int c0 = (a.layer_cols ? sidx * a.layer_cols : 0) + (slot - a.col_slot0) * 128 + lane;
   const int crow = slot >= a.NH ? cache_slot(sq, a.M, m) : 0;
   if (crow < 0) return;   // whole wave: one (row, head slot) per wave
-  // projections scaled and rounded to fp16 (Linear output): by the GEMM epilogue (qkv16),
-  // or here from the fp32 GEMM rows and the per-row scales (qkv32, oscale)
-  float v0, v1;
-  if (a.qkv32) {
-    v0 = h2f(f2h(a.qkv32[row * a.N + c0] * h2f(a.oscale[c0])));
-    v1 = h2f(f2h(a.qkv32[row * a.N + c0 + 64] * h2f(a.oscale[c0 + 64])));
-  } else {
-    v0 = h2f(a.qkv16[row * a.N + c0]);
-    v1 = h2f(a.qkv16[row * a.N + c0 + 64]);
-  }
-  const int kv_slot0 = a.NH + a.NKV;
-  if (slot >= kv_slot0) {   // V head: no norm, no rotation
-    const int gk = slot - kv_slot0;
-    half_t* vt = sq.Vt + (size_t)gk * 128 * a.cap + crow;
-    vt[(size_t)lane * a.cap] = f2h(v0);
-    vt[(size_t)(lane + 64) * a.cap] = f2h(v1);
-    return;
-  }
+  size_t row;
+  int c0;
+  qk_rope_src(a, sidx, m, slot, row, c0);
+  const float v0 = qk_rope_value(a, row, c0 + lane);
+  const float v1 = qk_rope_value(a, row, c0 + lane + 64);
   const bool is_q = slot < a.NH;
   const half_t* gn = is_q ? a.q_norm : (a.layer_cols ? a.k_norm_s[sidx] : a.k_norm);
   const float ss = wave_sum(v0 * v0 + v1 * v1);
@@ -328,8 +382,9 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(QKRopeArgs a) {
 
 bool launch_qk_rope(const QKRopeArgs& a, hipStream_t st) {
   if (check_qk_rope_args(a)) return false;
-  const long long waves = (long long)a.M * a.n_slots * a.n_seq;
-  hipLaunchKernelGGL(qk_rope_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, a);
+  const QkRopeGrid gr = qk_rope_grid(a);
+  const long long blocks = gr.qk_blocks + (long long)a.n_seq * gr.nv * gr.v_tiles;
+  hipLaunchKernelGGL(qk_rope_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
   return true;
 }
 

@@ -45,6 +45,16 @@ namespace {
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 constexpr int TG_GROUP_M = 4;   // m-tile rows per group of the tile order
 
+// Tile `tile` of the group order (see tile_gemm_kernel) -> its m-tile row tm and column tn.
+DFL_DEV void tile_coords(const TileArgs& a, int tile, int& tm, int& tn) {
+  const int gsz = TG_GROUP_M * a.tiles_n;
+  const int grp = tile / gsz, first_m = grp * TG_GROUP_M;
+  const int gm = min(a.tiles_m - first_m, TG_GROUP_M);
+  const int tig = tile - grp * gsz;
+  tm = first_m + tig % gm;
+  tn = tig / gm;
+}
+
 template <int WT, int MTW, int RBW, int WN, int KC>
 struct TgShape {
   static constexpr int NW = TG_WM * WN;                      // compute waves
@@ -215,22 +225,29 @@ __global__ __launch_bounds__(64 * (TG_WM * WN + tile_loaders(WN))) void tile_gem
   // split-K (a.splits > 1): workgroup gt takes k-split gt / tiles of tile gt % tiles (the
   // workgroups of one split, which read the same X k-slice, neighbour each other) and writes
   // its fp32 sums into plane split of Y (reduced by tile_reduce_kernel)
-  const int tiles = a.tiles_m * a.tiles_n;
+  // re-tiling (a.pmt > 0): workgroup gt covers sub-tile gt % nsub of parent tile
+  // tile0 + gt / nsub, whose m-tiles and row-blocks it splits in this shape's units
+  const int sub_n = a.pmt ? a.prb / S::RB : 1;
+  const int nsub = a.pmt ? (a.pmt / S::MT) * sub_n : 1;
+  const int tiles = a.ntiles ? a.ntiles * nsub : a.tiles_m * a.tiles_n;   // of this launch
   const int sp = gt / tiles;
-  const int tile = gt - sp * tiles;
+  const int job = gt - sp * tiles;
   // tile order in groups of TG_GROUP_M m-tile rows: consecutive tiles walk down a group's
   // rows, then across its columns, so the 32 tiles an XCD runs at once cover a 4 x 8
   // block (X of 4 row tiles, W of 8 column tiles) instead of 1 x 32 (W of 32): at large M
   // (the prompt-sized fc: 16 x 40 tiles, X 210 MB, W 262 MB) each XCD re-reads a quarter
   // of the weights per round instead of most of them.  One row tile: plain order.
-  const int gsz = TG_GROUP_M * a.tiles_n;
-  const int grp = tile / gsz, first_m = grp * TG_GROUP_M;
-  const int gm = min(a.tiles_m - first_m, TG_GROUP_M);
-  const int tig = tile - grp * gsz;
-  const int tm = first_m + tig % gm;
-  const int tn = tig / gm;
-  const int mt0 = tm * S::MT;                  // first m-tile of this workgroup
-  const int nb0 = tn * S::RB;                  // first weight row-block
+  int tm, tn, mt0, nb0;   // first m-tile and weight row-block of this workgroup
+  if (a.pmt) {
+    const int su = job % nsub;
+    tile_coords(a, a.tile0 + job / nsub, tm, tn);
+    mt0 = tm * a.pmt + (su / sub_n) * S::MT;
+    nb0 = tn * a.prb + (su % sub_n) * S::RB;
+  } else {
+    tile_coords(a, a.tile0 + job, tm, tn);
+    mt0 = tm * S::MT;
+    nb0 = tn * S::RB;
+  }
   const int K = a.K;
   // this split's stages [st0, st0 + nst), in whole 64-k steps (an even number of k-blocks)
   const int npair = K / 64;
@@ -462,7 +479,9 @@ __global__ __launch_bounds__(64 * (TG_WM * WN + tile_loaders(WN))) void tile_gem
 template <int WT, int EPI, int MTW, int RBW, int WN, int KC>
 void launch_tile(const TileArgs& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   using S = TgShape<WT, MTW, RBW, WN, KC>;
-  const dim3 grid(a.tiles_m * a.tiles_n * a.splits), block(64 * (S::NW + S::NLOAD));
+  const int nsub = a.pmt ? (a.pmt / S::MT) * (a.prb / S::RB) : 1;
+  const dim3 grid((a.ntiles ? a.ntiles * nsub : a.tiles_m * a.tiles_n) * a.splits),
+      block(64 * (S::NW + S::NLOAD));
   if (e0 || e1)
     hipExtLaunchKernelGGL((tile_gemm_kernel<WT, EPI, MTW, RBW, WN, KC>), grid, block, S::LDS, st,
                           e0, e1, 0, a);
@@ -471,13 +490,15 @@ void launch_tile(const TileArgs& a, hipStream_t st, hipEvent_t e0, hipEvent_t e1
 }
 
 // The epilogues each weight type has: int8 F32 / RESID / SWIGLU (gate|up pairs), fp16 F32 /
-// ARGMAX.
+// ARGMAX.  Shape I runs when `shape` is I, or (shape < 0) when it is the plan's.
 template <int I>
 bool launch_shape_i(int wt, int epi, const TileArgs& a, const TilePlan& p, hipStream_t st,
-                    hipEvent_t e0, hipEvent_t e1) {
-  if constexpr (I < (int)(sizeof(kTileShapes) / sizeof(kTileShapes[0]))) {
+                    hipEvent_t e0, hipEvent_t e1, int shape = -1) {
+  if constexpr (I < kNumTileShapes) {
     constexpr TileShape s = kTileShapes[I];
-    if (wt == s.wt && p.mtw == s.mtw && p.rbw == s.rbw && p.wn == s.wn && p.kc == s.kc) {
+    if (wt == s.wt && (shape >= 0 ? shape == I
+                                  : (!s.tail && p.mtw == s.mtw && p.rbw == s.rbw &&
+                                     p.wn == s.wn && p.kc == s.kc))) {
       if (epi == TG_F32) {
         launch_tile<s.wt, TG_F32, s.mtw, s.rbw, s.wn, s.kc>(a, st, e0, e1);
         return true;
@@ -500,7 +521,7 @@ bool launch_shape_i(int wt, int epi, const TileArgs& a, const TilePlan& p, hipSt
       }
       return false;
     }
-    return launch_shape_i<I + 1>(wt, epi, a, p, st, e0, e1);
+    return launch_shape_i<I + 1>(wt, epi, a, p, st, e0, e1, shape);
   }
   return false;
 }
@@ -559,7 +580,16 @@ bool launch_tile_gemm(int wt, int epi, const TileArgs& a0, const TilePlan& p, hi
   a.tiles_m = p.tiles_m;
   a.tiles_n = p.tiles_n;
   a.splits = p.splits;
-  return launch_shape_i<0>(wt, epi, a, p, st, ev_start, ev_stop);
+  a.tile0 = a.ntiles = a.pmt = a.prb = 0;
+  if (p.tail_shape < 0) return launch_shape_i<0>(wt, epi, a, p, st, ev_start, ev_stop);
+  // the head tiles in whole rounds, then the tail tiles re-tiled on the smaller shape
+  a.ntiles = p.head_tiles;
+  if (!launch_shape_i<0>(wt, epi, a, p, st, ev_start, nullptr)) return false;
+  a.tile0 = p.head_tiles;
+  a.ntiles = p.tiles_m * p.tiles_n - p.head_tiles;
+  a.pmt = TG_WM * p.mtw;
+  a.prb = p.rbw * p.wn;
+  return launch_shape_i<0>(wt, epi, a, p, st, nullptr, ev_stop, p.tail_shape);
 }
 
 }  // namespace dfl

@@ -15,18 +15,22 @@ constexpr int TG_LDS_BUDGET = 160 * 1024;  // one workgroup per CU
 
 // The tile shapes the library instantiates: mtw m-tiles (32 rows) and rbw weight
 // row-blocks (32 columns) per wave, wn wave columns (4 * wn waves), kc k per LDS stage.
+// tail: used only to re-tile the partial last round of a larger shape's plan.
 struct TileShape {
   int wt, mtw, rbw, wn, kc;
+  bool tail;
 };
 constexpr TileShape kTileShapes[] = {
-    {WT_INT8, 1, 1, 1, 64},   // 128 x 32
-    {WT_INT8, 1, 2, 1, 64},   // 128 x 64
-    {WT_INT8, 2, 4, 1, 64},   // 256 x 128
-    {WT_INT8, 2, 4, 2, 32},   // 256 x 256
-    {WT_F16, 2, 2, 1, 64},    // 256 x 64
-    {WT_F16, 2, 4, 1, 32},    // 256 x 128
-    {WT_F16, 2, 4, 2, 32},    // 256 x 256
+    {WT_INT8, 1, 1, 1, 64, false},   // 128 x 32
+    {WT_INT8, 1, 2, 1, 64, false},   // 128 x 64
+    {WT_INT8, 2, 4, 1, 64, false},   // 256 x 128
+    {WT_INT8, 2, 4, 2, 32, false},   // 256 x 256
+    {WT_F16, 2, 2, 1, 64, false},    // 256 x 64
+    {WT_F16, 2, 4, 1, 32, false},    // 256 x 128
+    {WT_F16, 2, 4, 2, 32, false},    // 256 x 256
+    {WT_F16, 1, 4, 1, 64, true},     // 128 x 128
 };
+constexpr int kNumTileShapes = (int)(sizeof(kTileShapes) / sizeof(kTileShapes[0]));
 
 constexpr int tile_waves(int wn) { return TG_WM * wn; }
 // The 4-wave shapes (wn == 1) add four loader waves that issue every global -> LDS copy
@@ -76,13 +80,17 @@ inline double tile_kblock_cycles(const TileShape& s) {
 // over the chip, plus 12000 cycles of launch and tail).  Fitted to the measured times of
 // the 8B- and 27B-class stacked products, the prompt-sized K|V ingest and the fp16
 // lm_head (each picks its measured-fastest plan).
+// Re-tiling (allowed with retile, no split-K): a plan of more tiles than CUs whose last
+// round is partial may run that round's tiles on a smaller shape whose tiles divide them,
+// several workgroups per tile over the whole K (the same sums), so that the last round
+// finishes sooner; it costs one more launch (about 12000 cycles).
 // pairs: each wave must hold gate|up row-block pairs (SWIGLU), i.e. an even rbw.
 inline TilePlan tile_plan(int M, int N, int K, int wt, int n_cu, bool pairs = false,
-                          bool split = false) {
+                          bool split = false, bool retile = false) {
   TilePlan best{};
   double best_t = 1e300;
   for (const TileShape& s : kTileShapes) {
-    if (s.wt != wt || K % s.kc || (pairs && s.rbw % 2)) continue;
+    if (s.tail || s.wt != wt || K % s.kc || (pairs && s.rbw % 2)) continue;
     const int bm = 32 * TG_WM * s.mtw, bn = 32 * s.rbw * s.wn;
     if (N % bn) continue;
     const long long tiles = (long long)((M + bm - 1) / bm) * (N / bn);
@@ -103,6 +111,33 @@ inline TilePlan tile_plan(int M, int N, int K, int wt, int n_cu, bool pairs = fa
         best.tiles_m = (M + bm - 1) / bm;
         best.tiles_n = N / bn;
         best.splits = sp;
+        best.head_tiles = 0;
+        best.tail_shape = -1;
+      }
+    }
+    const long long full = tiles / n_cu, part = tiles % n_cu;
+    if (!retile || full < 1 || part == 0) continue;
+    for (int i = 0; i < kNumTileShapes; ++i) {
+      const TileShape& u = kTileShapes[i];
+      const int um = 32 * TG_WM * u.mtw, un = 32 * u.rbw * u.wn;
+      if (u.wt != wt || K % u.kc || (pairs && u.rbw % 2) || bm % um || bn % un ||
+          (um == bm && un == bn))
+        continue;
+      const long long sub = (long long)(bm / um) * (bn / un);
+      const long long ur = (part * sub + n_cu - 1) / n_cu;   // rounds of the sub-tiles
+      const double t = ((double)full * tile_kblock_cycles(s) + ur * tile_kblock_cycles(u)) *
+                           ((double)K / 32) + 12000.0;
+      if (t < best_t * 0.999) {
+        best_t = t;
+        best.mtw = s.mtw;
+        best.rbw = s.rbw;
+        best.wn = s.wn;
+        best.kc = s.kc;
+        best.tiles_m = (M + bm - 1) / bm;
+        best.tiles_n = N / bn;
+        best.splits = 1;
+        best.head_tiles = (int)(full * n_cu);
+        best.tail_shape = i;
       }
     }
   }

@@ -177,6 +177,35 @@ int main() {
     { TileArgs b = ta; expect(check_tile_reduce_args(TG_RESID, b, (const float*)P, 4), "RESID", "reduce RESID args"); }
     { TileArgs b = ta; b.N = 4000; expect(check_tile_reduce_args(TG_F32, b, (const float*)P, 4), "multiple of 64", "reduce N"); }
     { TileArgs b = ta; expect(check_tile_reduce_args(TG_SWIGLU, b, (const float*)P, 4), "F32 and RESID", "reduce epi"); }
+    // re-tiled tail: the prompt-sized fc (4096 rows, 5120 x 25600 fp16) has a partial last
+    // round on 256 CUs; the plan runs the full rounds whole and the rest on a smaller shape
+    // whose tiles divide the plan's
+    const TilePlan rt = tile_plan(4096, 5120, 25600, WT_F16, 256, false, false, true);
+    const long long rt_tiles = (long long)rt.tiles_m * rt.tiles_n;
+    if (rt.tail_shape < 0) expect("no re-tiled tail", nullptr, "fc re-tiled tail");
+    if (rt.head_tiles % 256 || rt.head_tiles < 256 || rt.head_tiles >= rt_tiles)
+      expect("head not whole rounds", nullptr, "fc head tiles");
+    { TileArgs b = ta; b.M = 4096; b.N = 5120; b.K = 25600; b.ldy = 5120;
+      expect(check_tile_args(WT_F16, TG_F32, b, rt), nullptr, "re-tiled plan");
+      TilePlan q = rt; q.tail_shape = 0;   // an int8 shape
+      expect(check_tile_args(WT_F16, TG_F32, b, q), "divide", "re-tiled wrong type");
+      q = rt; q.head_tiles = 0;
+      expect(check_tile_args(WT_F16, TG_F32, b, q), "head", "re-tiled no head");
+      q = rt; q.tail_shape = kNumTileShapes;
+      expect(check_tile_args(WT_F16, TG_F32, b, q), "unknown", "re-tiled shape index"); }
+    // none without permission, nor when the tiles fill whole rounds (K|V ingest: 16 x 16
+    // tiles of 256 x 128), nor in the plain plan's shape list
+    if (tile_plan(4096, 5120, 25600, WT_F16, 256).tail_shape != -1) expect("tail", nullptr, "fc no re-tile");
+    if (tile_plan(4096, 2048, 5120, WT_INT8, 256, false, false, true).tail_shape != -1)
+      expect("tail", nullptr, "K|V whole rounds");
+    for (int M : {256, 1024, 4096})
+      for (int N : {5120, 28672, 128256}) {
+        const TilePlan q = tile_plan(M, N, 5120, WT_F16, 256);
+        for (const TileShape& u : kTileShapes)
+          if (u.tail && u.wt == WT_F16 && q.mtw == u.mtw && q.rbw == u.rbw && q.wn == u.wn &&
+              q.kc == u.kc)
+            expect("tail-only shape planned", nullptr, "plain plan shapes");
+      }
   }
   if (fails == 0) std::printf("ok\n");
   return fails ? 1 : 0;
