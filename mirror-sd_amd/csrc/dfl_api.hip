@@ -158,6 +158,7 @@ struct dfl_ctx {
   // context ingest: `ing` rows per pass (compute-bound: fc and K|V on the tile GEMM)
   int ing = 0;
   float* fc32 = nullptr;      // [ing][H] fc GEMM rows (fp32)
+  float* ing_cs = nullptr;    // [ing][64][2] RoPE (cos, sin) of a prompt-sized pass's rows
   half_t* xf = nullptr;       // [ing][n_target_feat * H] fc input rows, fragment layout
   half_t* xn = nullptr;       // [ing/32][32][H] hidden_norm(fc) (or fused) rows, fragment layout
   float* kv32 = nullptr;      // [ing][2*NKV*128] K|V GEMM rows (fp32)
@@ -266,7 +267,9 @@ static int setup_ingest(dfl_ctx* x) {
       (r = x->alloc(&x->w_kv_all, (size_t)x->NL * Nkv * H / 16)) ||
       (r = x->alloc(&x->s_kv_all, (size_t)x->NL * Nkv)))
     return r;
-  if ((r = x->alloc(&x->xn, (size_t)x->ing * H))) return r;
+  if ((r = x->alloc(&x->xn, (size_t)x->ing * H)) ||
+      (r = x->alloc(&x->ing_cs, (size_t)x->ing * 128)))
+    return r;
   if (x->NF > 0 && ((r = x->alloc(&x->fc32, (size_t)x->ing * H)) ||
                     (r = x->alloc(&x->xf, (size_t)x->ing * x->NF * H))))
     return r;
@@ -706,6 +709,11 @@ static void rope_seq(dfl_ctx* ctx, int seq, const Layer& L, long long pos0, int 
 static int ingest_kv_rows(dfl_ctx* ctx, const half_t* xa, int rows, int r0, hipStream_t st) {
   const int H = ctx->H, NH = ctx->NH, NKV = ctx->NKV;
   const int Nkv = 2 * NKV * 128;
+  {   // the rows' RoPE angles, once for every layer
+    ProfScope ps(ctx, P_INGEST_KV, 0, st);
+    launch_rope_table(rows, ctx->sq().offset + r0, std::log2(ctx->cfg.rope_theta),
+                      ctx->rope_freqs(), ctx->ing_cs, st);
+  }
   for (int l = 0; l < ctx->active; ++l) {
     Layer& L = ctx->layers[l];
     // the K|V rows start at packed row-block NH*128/32 of the qkv matrix
@@ -728,6 +736,7 @@ static int ingest_kv_rows(dfl_ctx* ctx, const half_t* xa, int rows, int r0, hipS
     q.eps = ctx->cfg.rms_eps;
     q.log2_theta = std::log2(ctx->cfg.rope_theta);
     q.inv_freq = ctx->rope_freqs();
+    q.cs = ctx->ing_cs;
     q.Q = nullptr;
     q.cap = ctx->cap;
     rope_seq(ctx, ctx->cur, L, ctx->sq().offset + r0, rows, q.sq[0]);
@@ -795,8 +804,8 @@ static int ingest_small(dfl_ctx* ctx, const half_t* in, int C, bool fused, const
     q.eps = ctx->cfg.rms_eps;
     q.log2_theta = std::log2(ctx->cfg.rope_theta);
     q.inv_freq = ctx->rope_freqs();
-    q.Q = nullptr;
-    q.cap = ctx->cap;
+    q.Q = nullptr;   // (a per-step call's few rows compute their angles in place: an angle
+    q.cap = ctx->cap;   // table would cost one more launch than it saves)
     for (int i = 0; i < nl; ++i) {
       const Layer& L = ctx->layers[l0 + i];
       q.k_norm_s[i] = L.k_norm;

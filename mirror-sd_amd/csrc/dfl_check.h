@@ -91,6 +91,9 @@ inline const char* check_qk_rope_args(const QKRopeArgs& a) {
     return "slots past the row width";
   }
   if (a.slot0 < a.NH && !a.Q) return "Q slots without a Q output";
+  if (a.cs && !a.layer_cols)
+    for (int s = 1; s < a.n_seq; ++s)
+      if (a.sq[s].pos0 != a.sq[0].pos0) return "one angle table for sequences at other positions";
   if (!a.q_norm || !a.k_norm || a.cap < 1) return "missing norms or cache capacity";
   if (a.slot0 + a.n_slots > a.NH)
     for (int s = 0; s < a.n_seq; ++s)

@@ -243,6 +243,9 @@ struct QKRopeArgs {
   double log2_theta;
   const double* inv_freq;                    // [64] scaled RoPE frequencies, or nullptr:
                                              // theta^(-j/64) from log2_theta
+  const float* cs;                           // [M][64] (cos, sin) of row m's position, made by
+                                             // launch_rope_table (entries sharing positions),
+                                             // or nullptr: computed per row and head
   half_t* Q;
   int cap;
   RopeSeq sq[SEQ_MAX];
@@ -261,6 +264,10 @@ DFL_DEV int cache_slot(const RopeSeq& q, int M, int m) {
 }
 // Returns false (and launches nothing) when the struct fails check_qk_rope_args.
 bool launch_qk_rope(const QKRopeArgs& a, hipStream_t st);
+// cs[m][j] = (cos, sin) of (pos0 + m) * inv_freq[j] (fp64 angle, as qk_rope_kernel computes
+// it), for m < M, j < 64; inv_freq nullptr: theta^(-j/64) from log2_theta.
+void launch_rope_table(int M, long long pos0, double log2_theta, const double* inv_freq,
+                       float* cs, hipStream_t st);
 // ids[m] = ~low32(keys[m]); keys[m] = 0.
 void launch_argmax_finalize(unsigned long long* keys, int M, int32_t* ids, hipStream_t st);
 // ids[m] from the largest of parts[p][m], p < P (the tile GEMM's ARGMAX keys); -1 if none.

@@ -361,14 +361,23 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(QKRopeArgs a) {
   const float r = 1.0f / sqrtf(ss * (1.0f / 128.0f) + a.eps);
   const float y0 = h2f(rms_out(v0, r, gn[lane]));
   const float y1 = h2f(rms_out(v1, r, gn[lane + 64]));
-  const double inv_freq =
-      a.inv_freq ? a.inv_freq[lane] : exp2(-(double)lane * (1.0 / 64.0) * a.log2_theta);
-  const double ang = (double)(sq.pos0 + m) * inv_freq;
-  double sd, cd;
-  sincos(ang, &sd, &cd);
-  const float c = (float)cd, sn = (float)sd;
-  const half_t o0 = f2h(y0 * c - y1 * sn);
-  const half_t o1 = f2h(y1 * c + y0 * sn);
+  float c, sn;
+  if (a.cs) {
+    c = a.cs[2 * (m * 64 + lane)];
+    sn = a.cs[2 * (m * 64 + lane) + 1];
+  } else {
+    const double inv_freq =
+        a.inv_freq ? a.inv_freq[lane] : exp2(-(double)lane * (1.0 / 64.0) * a.log2_theta);
+    const double ang = (double)(sq.pos0 + m) * inv_freq;
+    double sd, cd;
+    sincos(ang, &sd, &cd);
+    c = (float)cd;
+    sn = (float)sd;
+  }
+  // the rotation's contraction written out (the y * c products fused, the y * sn products
+  // rounded), so that the result does not depend on the compiler's choice of fma
+  const half_t o0 = f2h(__builtin_fmaf(y0, c, -(y1 * sn)));
+  const half_t o1 = f2h(__builtin_fmaf(y1, c, y0 * sn));
   half_t* dst;
   if (is_q) {
     dst = a.Q + (((size_t)sidx * a.NH + slot) * a.M + m) * 128;
@@ -378,6 +387,26 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(QKRopeArgs a) {
   }
   dst[lane] = o0;
   dst[lane + 64] = o1;
+}
+
+__global__ __launch_bounds__(256) void rope_table_kernel(int M, long long pos0, double log2_theta,
+                                                         const double* __restrict__ inv_freq,
+                                                         float* __restrict__ cs) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= M * 64) return;
+  const int m = i >> 6, j = i & 63;
+  const double f = inv_freq ? inv_freq[j] : exp2(-(double)j * (1.0 / 64.0) * log2_theta);
+  double sd, cd;
+  sincos((double)(pos0 + m) * f, &sd, &cd);
+  cs[2 * i] = (float)cd;
+  cs[2 * i + 1] = (float)sd;
+}
+
+void launch_rope_table(int M, long long pos0, double log2_theta, const double* inv_freq,
+                       float* cs, hipStream_t st) {
+  if (M <= 0) return;
+  hipLaunchKernelGGL(rope_table_kernel, dim3((M * 64 + 255) / 256), dim3(256), 0, st, M, pos0,
+                     log2_theta, inv_freq, cs);
 }
 
 bool launch_qk_rope(const QKRopeArgs& a, hipStream_t st) {

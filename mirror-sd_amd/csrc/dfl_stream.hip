@@ -647,8 +647,10 @@ DFL_DEV void qk_head_epilogue(const StreamArgs& a, int lane, int h, const floatx
       const float y1 = h2f(rms_out(vh[i], rr, gn[f + 64]));
       const floatx4& cp = c < 2 ? cs01 : cs23;
       const float cc = cp[2 * (c & 1)], sn = cp[2 * (c & 1) + 1];
-      ol[c] = f2h(y0 * cc - y1 * sn);
-      oh[c] = f2h(y1 * cc + y0 * sn);
+      // the contraction written out (the y0 products fused, the y1 products rounded), so
+      // that the result does not depend on the compiler's choice of fma
+      ol[c] = f2h(__builtin_fmaf(cc, y0, -(sn * y1)));
+      oh[c] = f2h(__builtin_fmaf(sn, y0, cc * y1));
     }
     *reinterpret_cast<half4_t*>(dst + f0) = ol;
     *reinterpret_cast<half4_t*>(dst + 64 + f0) = oh;

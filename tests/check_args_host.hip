@@ -106,6 +106,14 @@ int main() {
     { QKRopeArgs c = b; c.k_norm_s[3] = nullptr; expect(check_qk_rope_args(c), "k_norm", "layer mode norm"); }
     { QKRopeArgs c = b; c.slot0 = 0; c.col_slot0 = 0; c.n_slots = 56; c.Q = (half_t*)P;
       expect(check_qk_rope_args(c), "K|V rows only", "layer mode Q"); }
+    { QKRopeArgs c = b; c.cs = (const float*)P; c.sq[2].pos0 = 99;   // layers share the rows
+      expect(check_qk_rope_args(c), nullptr, "layer mode angle table"); }
+  }
+  {   // one angle table only for sequences at the same positions
+    QKRopeArgs b = q; b.n_seq = 2; b.sq[1] = b.sq[0]; b.cs = (const float*)P;
+    expect(check_qk_rope_args(b), nullptr, "angle table, same positions");
+    b.sq[1].pos0 += 32;
+    expect(check_qk_rope_args(b), "angle table", "angle table, other positions");
   }
 
   AttnArgs t{};
