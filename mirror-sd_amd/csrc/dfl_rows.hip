@@ -269,7 +269,9 @@ void launch_afl_to_rows(const half_t* x, int M, int N, half_t* h, hipStream_t st
 // Head slots [slot0, slot0 + n_slots) in q|k|v numbering: Q heads, then K heads, then V
 // heads (slot >= NH + NKV).  The launch's blocks come in two parts: the first handles the
 // Q/K slots, one wave per (sequence, row m, slot); the rest the V slots, one workgroup per
-// (sequence, V slot, 64 rows).
+// (sequence, V slot, 64 rows).  Below QKR_V_TILE_MIN rows (a decode step's few context rows)
+// the 64-row V workgroups would mostly idle: there the per-row waves take the V slots too.
+constexpr int QKR_V_TILE_MIN = 64;
 struct QkRopeGrid {
   int qk0, nqk, v0, nv;      // first Q/K slot and count, first V slot and count
   long long qk_blocks;       // blocks of the Q/K part (4 waves each)
@@ -279,11 +281,17 @@ __host__ __device__ inline QkRopeGrid qk_rope_grid(const QKRopeArgs& a) {
   QkRopeGrid gr;
   const int kvs = a.NH + a.NKV, end = a.slot0 + a.n_slots;
   gr.qk0 = a.slot0;
-  gr.nqk = (end < kvs ? end : kvs) - a.slot0;
-  if (gr.nqk < 0) gr.nqk = 0;
-  gr.v0 = a.slot0 > kvs ? a.slot0 : kvs;
-  gr.nv = end - gr.v0;
-  if (gr.nv < 0) gr.nv = 0;
+  if (a.M < QKR_V_TILE_MIN) {   // few rows: the V slots by the per-row waves too
+    gr.nqk = a.n_slots;
+    gr.v0 = end;
+    gr.nv = 0;
+  } else {
+    gr.nqk = (end < kvs ? end : kvs) - a.slot0;
+    if (gr.nqk < 0) gr.nqk = 0;
+    gr.v0 = a.slot0 > kvs ? a.slot0 : kvs;
+    gr.nv = end - gr.v0;
+    if (gr.nv < 0) gr.nv = 0;
+  }
   gr.qk_blocks = ((long long)a.M * gr.nqk * a.n_seq + 3) / 4;
   gr.v_tiles = (a.M + 63) / 64;
   return gr;
@@ -355,6 +363,12 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(QKRopeArgs a) {
   qk_rope_src(a, sidx, m, slot, row, c0);
   const float v0 = qk_rope_value(a, row, c0 + lane);
   const float v1 = qk_rope_value(a, row, c0 + lane + 64);
+  if (slot >= a.NH + a.NKV) {   // V head (few rows): down its Vt column, no norm or rotation
+    half_t* vt = sq.Vt + (size_t)(slot - a.NH - a.NKV) * 128 * a.cap + crow;
+    vt[(size_t)lane * a.cap] = f2h(v0);
+    vt[(size_t)(lane + 64) * a.cap] = f2h(v1);
+    return;
+  }
   const bool is_q = slot < a.NH;
   const half_t* gn = is_q ? a.q_norm : (a.layer_cols ? a.k_norm_s[sidx] : a.k_norm);
   const float ss = wave_sum(v0 * v0 + v1 * v1);

@@ -8,6 +8,10 @@ Inputs (csv output of rocprofv3):
             the same blocks as the bench's timed region
   --fetch   <dir>/<name>_counter_collection.csv from ``--pmc FETCH_SIZE``
   --write   <dir>/<name>_counter_collection.csv from ``--pmc WRITE_SIZE``
+  --mfma    <dir>/<name>_counter_collection.csv from ``--pmc MfmaUtil MfmaFlopsF16``: per
+            group, the matrix cores' busy share (MfmaUtil: MFMA-busy cycles over the active
+            cycles of every SIMD) and the fp16 MFMA rate (MfmaFlopsF16 over the dispatch's
+            own duration in that run; counters are collected with the dispatches serialised)
 Both counter runs include a plain elementwise copy of known size (bench.py
 ``--copy-probe-mib``); its readings give the factor that turns each counter into bytes
 (FETCH_SIZE / WRITE_SIZE are reported in KiB, but what one KiB of reading means depends
@@ -45,7 +49,8 @@ GROUPS = [
     ("split-K plane sum + epilogue (stacked o, down: RESID)", r"tile_reduce_kernel"),
     ("tile GEMM int8, SWIGLU (stacked gate|up)", r"tile_gemm_kernel<0, 2,"),
     ("tile GEMM fp16, ARGMAX (stacked lm_head)", r"tile_gemm_kernel<1, 3,"),
-    ("tile GEMM fp16, fp32 rows (prompt-sized ingest fc)", r"tile_gemm_kernel<1, 0,"),
+    ("tile GEMM fp16, fp32 rows (prompt-sized ingest fc)", r"tile_gemm_kernel<1, 0, 2,"),
+    ("tile GEMM fp16 128x128 (the fc's last round, re-tiled)", r"tile_gemm_kernel<1, 0, 1,"),
     ("rows into fragment layout (ingest input, fused-rows ingest)", r"feats_to_afl_kernel"),
     ("argmax of the partial keys (stacked lm_head)", r"argmax_parts_kernel"),
     ("fc rows: fp16 rounding + hidden_norm (prompt-sized ingest)", r"fc_norm_rows_kernel"),
@@ -53,6 +58,7 @@ GROUPS = [
     ("block attention", r"block_attn_kernel"),
     ("attention merge", r"attn_merge_kernel"),
     ("qk norm + rope (context ingest, stacked blocks)", r"qk_rope_kernel"),
+    ("RoPE angle table (prompt-sized ingest)", r"rope_table_kernel"),
     ("embed + norm", r"embed_norm_kernel"),
     ("argmax finalize", r"argmax_finalize_kernel"),
 ]
@@ -100,6 +106,20 @@ def read_counter(path):
     return per
 
 
+def read_counters(path):
+    """{kernel: [ {counter: value, "_ns": duration} per dispatch ]}"""
+    disp = collections.defaultdict(dict)
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            d = disp[(r["Kernel_Name"], r["Dispatch_Id"])]
+            d[r["Counter_Name"]] = float(r["Counter_Value"])
+            d["_ns"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+    per = collections.defaultdict(list)
+    for (k, _), d in disp.items():
+        per[k].append(d)
+    return per
+
+
 def match(names, rx):
     return [n for n in names if re.search(rx, n)]
 
@@ -117,6 +137,7 @@ def main(argv=None):
     ap.add_argument("--from-index", type=int, default=0)
     ap.add_argument("--fetch")
     ap.add_argument("--write")
+    ap.add_argument("--mfma")
     ap.add_argument("--copy-mib", type=int, default=1024)
     ap.add_argument("--workload", required=True)
     ap.add_argument("--commands", default="", help="text of the commands that made the inputs")
@@ -178,6 +199,23 @@ def main(argv=None):
             out.append(f"| {label} | {len(fv)} | {rd / 1e6:.2f} | {wr / 1e6:.2f} | "
                        f"{(rd + wr) / 1e6:.2f} |")
             traffic[label] = {"read_bytes": rd, "write_bytes": wr, "bytes_per_launch": rd + wr}
+        out.append("")
+    if a.mfma:
+        mf = read_counters(a.mfma)
+        out += ["## Matrix cores (--pmc MfmaUtil MfmaFlopsF16)", "",
+                "MfmaUtil: MFMA-busy cycles over the active cycles of every SIMD of the GPU, in "
+                "percent (rocprofv3's derived metric). fp16 MFMA TFLOP/s: MfmaFlopsF16 (fp16 MFMA "
+                "operations of the dispatch) over its duration in the counter run; dense fp16 "
+                "peak 2500 TFLOP/s.", "",
+                "| group | dispatches | MfmaUtil % | fp16 MFMA TFLOP/s | % of peak |",
+                "|---|---:|---:|---:|---:|"]
+        for label, rx in GROUPS:
+            ds = [d for n in match(mf, rx) for d in mf[n] if "MfmaUtil" in d]
+            if not ds:
+                continue
+            util = sum(d["MfmaUtil"] for d in ds) / len(ds)
+            tf = sum(d.get("MfmaFlopsF16", 0.0) / max(d["_ns"], 1) / 1e3 for d in ds) / len(ds)
+            out.append(f"| {label} | {len(ds)} | {util:.1f} | {tf:.1f} | {tf / 2500 * 100:.1f} |")
         out.append("")
     with open(a.md, "w") as f:
         f.write("\n".join(out) + "\n")
