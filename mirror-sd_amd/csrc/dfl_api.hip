@@ -161,7 +161,7 @@ struct dfl_ctx {
   float* ing_cs = nullptr;    // [ing][64][2] RoPE (cos, sin) of a prompt-sized pass's rows
   half_t* xf = nullptr;       // [ing][n_target_feat * H] fc input rows, fragment layout
   half_t* xn = nullptr;       // [ing/32][32][H] hidden_norm(fc) (or fused) rows, fragment layout
-  float* kv32 = nullptr;      // [ing][2*NKV*128] K|V GEMM rows (fp32)
+  float* kv32 = nullptr;      // [ing][NL*2*NKV*128] K|V GEMM rows of every layer (fp32)
   // per-step ingest of up to SMALL_ING rows on the stream-K kernels (no library GEMM): the
   // fc weight packed in fp16 blocks, input / normed rows in activation fragment layout,
   // fp16 fc and K|V rows
@@ -260,7 +260,7 @@ static int setup_ingest(dfl_ctx* x) {
   const int H = x->H, Nkv = 2 * x->NKV * 128;
   x->ing = std::max(32, std::min(ING_MAX, ((x->cfg.max_ctx + 31) / 32) * 32));
   int r = DFL_OK;
-  if ((r = x->alloc(&x->kv32, (size_t)x->ing * Nkv))) return r;
+  if ((r = x->alloc(&x->kv32, (size_t)x->ing * x->NL * Nkv))) return r;
   if ((r = x->alloc(&x->si_in, (size_t)SMALL_ING * std::max(x->NF, 1) * H, true)) ||
       (r = x->alloc(&x->si_xn, (size_t)SMALL_ING * H, true)) ||
       (r = x->alloc(&x->si_kv, (size_t)SMALL_ING * x->NL * Nkv)) ||
@@ -620,14 +620,21 @@ static int block_attention(const AttnArgs& at, hipStream_t st) {
 // Split-K (F32 and RESID epilogues of stacked blocks, when the plan finds it faster): the
 // GEMM writes fp32 planes into tile_ws and launch_tile_reduce applies the epilogue.
 // n_parts (ARGMAX): receives the number of partial key rows written (one per wave column).
+// like_n (optional): plan with the tile shape the product of like_n columns would have, so
+// that a product stacked over several such (the all-layer K|V ingest) sums every element
+// exactly as the single one does.
 static int tgemm(dfl_ctx* ctx, int cat, int wt, int epi, const uint4* W, int N, int K,
                  const half_t* X, int M, const TileArgs& e, hipStream_t st,
-                 int* n_parts = nullptr) {
-  const bool split_ok = (epi == TG_F32 || epi == TG_RESID) && ctx->tile_ws && M <= ctx->RM;
+                 int* n_parts = nullptr, int like_n = 0) {
+  const bool split_ok = (epi == TG_F32 || epi == TG_RESID) && ctx->tile_ws && M <= ctx->RM &&
+                        !like_n;
   // re-tiled last rounds for the epilogues whose outputs do not depend on the tile shape
   // (the ARGMAX keys are per wave column)
   const bool retile = epi != TG_ARGMAX;
-  TilePlan p = tile_plan(M, N, K, wt, ctx->n_cu, epi == TG_SWIGLU, split_ok, retile);
+  TilePlan like{};
+  if (like_n) like = tile_plan(M, like_n, K, wt, ctx->n_cu, epi == TG_SWIGLU);
+  TilePlan p = tile_plan(M, N, K, wt, ctx->n_cu, epi == TG_SWIGLU, split_ok, retile,
+                         like_n ? &like : nullptr);
   if (p.splits > 1 && (size_t)p.splits * M * N > ctx->tile_ws_floats)   // planes do not fit
     p = tile_plan(M, N, K, wt, ctx->n_cu, epi == TG_SWIGLU, false, retile);
   if (n_parts) *n_parts = N / (32 * p.rbw);
@@ -702,44 +709,48 @@ static void rope_seq(dfl_ctx* ctx, int seq, const Layer& L, long long pos0, int 
   r.ring_W = q.window;
 }
 
-// Per-layer K/V of `rows` fused context rows (fragment-layout tiles xa): the K|V rows of the
-// packed W8A16 qkv matrix on the tile GEMM (fp32 integer-weight sums), then per-row scale +
-// fp16 rounding, k_norm + RoPE on K, appended at cache row len + r0 with absolute position
-// offset + r0.
+// K/V of `rows` fused context rows (fragment-layout tiles xa) for every active layer: the
+// all-layer packed K|V matrix on the tile GEMM (one product: fp32 integer-weight sums, the
+// same sums per element as a product per layer), then per-row scale + fp16 rounding,
+// k_norm + RoPE on K (angles from one table for all layers), appended at cache row
+// len + r0 with absolute position offset + r0, for up to SEQ_MAX layers per qk_rope launch.
 static int ingest_kv_rows(dfl_ctx* ctx, const half_t* xa, int rows, int r0, hipStream_t st) {
   const int H = ctx->H, NH = ctx->NH, NKV = ctx->NKV;
-  const int Nkv = 2 * NKV * 128;
+  const int Nkv = 2 * NKV * 128, Nall = ctx->active * Nkv;
   {   // the rows' RoPE angles, once for every layer
     ProfScope ps(ctx, P_INGEST_KV, 0, st);
     launch_rope_table(rows, ctx->sq().offset + r0, std::log2(ctx->cfg.rope_theta),
                       ctx->rope_freqs(), ctx->ing_cs, st);
   }
-  for (int l = 0; l < ctx->active; ++l) {
-    Layer& L = ctx->layers[l];
-    // the K|V rows start at packed row-block NH*128/32 of the qkv matrix
-    const uint4* w_kv = L.w_qkv + (size_t)(NH * 128 / 32) * (H / 32) * 64;
-    DFL_TRY(tgemm(ctx, P_INGEST_KV, WT_INT8, TG_F32, w_kv, Nkv, H, xa, rows, tile_f32(ctx->kv32, Nkv),
-                  st));
+  DFL_TRY(tgemm(ctx, P_INGEST_KV, WT_INT8, TG_F32, ctx->w_kv_all, Nall, H, xa, rows,
+                tile_f32(ctx->kv32, Nall), st, nullptr, /*like_n=*/Nkv));
+  for (int l0 = 0; l0 < ctx->active; l0 += SEQ_MAX) {
+    const int nl = std::min(SEQ_MAX, ctx->active - l0);
     QKRopeArgs q{};
-    q.qkv32 = ctx->kv32;
-    q.oscale = L.s_qkv + NH * 128;   // scales of the k|v rows, in row order
+    q.qkv32 = ctx->kv32 + (size_t)l0 * Nkv;
+    q.oscale = ctx->s_kv_all + (size_t)l0 * Nkv;   // scales of the k|v rows, in row order
     q.M = rows;
-    q.N = Nkv;
-    q.n_seq = 1;
+    q.N = Nall;
+    q.n_seq = nl;
+    q.layer_cols = Nkv;
     q.col_slot0 = NH;
     q.slot0 = NH;
     q.n_slots = 2 * NKV;
     q.NH = NH;
     q.NKV = NKV;
-    q.q_norm = L.q_norm;
-    q.k_norm = L.k_norm;
+    q.q_norm = ctx->layers[l0].q_norm;
+    q.k_norm = ctx->layers[l0].k_norm;
     q.eps = ctx->cfg.rms_eps;
     q.log2_theta = std::log2(ctx->cfg.rope_theta);
     q.inv_freq = ctx->rope_freqs();
     q.cs = ctx->ing_cs;
     q.Q = nullptr;
     q.cap = ctx->cap;
-    rope_seq(ctx, ctx->cur, L, ctx->sq().offset + r0, rows, q.sq[0]);
+    for (int i = 0; i < nl; ++i) {
+      const Layer& L = ctx->layers[l0 + i];
+      q.k_norm_s[i] = L.k_norm;
+      rope_seq(ctx, ctx->cur, L, ctx->sq().offset + r0, rows, q.sq[i]);
+    }
     ProfScope ps(ctx, P_INGEST_KV, 0, st);
     DFL_TRY(qk_rope(q, st));
   }

@@ -81,7 +81,7 @@ inline const char* check_qk_rope_args(const QKRopeArgs& a) {
       a.slot0 + a.n_slots > a.NH + 2 * a.NKV)
     return "head slots outside the q|k|v heads";
   if (a.layer_cols) {
-    if (a.qkv32 || a.slot0 < a.NH) return "layer mode takes fp16 K|V rows only";
+    if (a.slot0 < a.NH) return "layer mode takes K|V rows only";
     if ((long long)(a.slot0 + a.n_slots - a.col_slot0) * 128 > a.layer_cols ||
         (long long)a.n_seq * a.layer_cols > a.N)
       return "slots past the row width";
@@ -154,7 +154,8 @@ inline const char* check_tile_args(int wt, int epi, const TileArgs& a, const Til
     if (p.tail_shape >= kNumTileShapes || p.splits != 1) return "re-tiled tail: unknown shape";
     const TileShape& u = kTileShapes[p.tail_shape];
     if (u.wt != wt || a.K % u.kc || (128 * p.mtw) % (128 * u.mtw) ||
-        (32 * p.rbw * p.wn) % (32 * u.rbw * u.wn) || (epi == TG_SWIGLU && u.rbw % 2))
+        (32 * p.rbw * p.wn) % (32 * u.rbw * u.wn) || (epi == TG_SWIGLU && u.rbw % 2) ||
+        tile_nacc(u.mtw, u.rbw) != tile_nacc(p.mtw, p.rbw))
       return "re-tiled tail: the shape does not divide the plan's tiles";
     if (p.head_tiles < 1 || p.head_tiles >= p.tiles_m * p.tiles_n)
       return "re-tiled tail: needs head tiles and a tail";

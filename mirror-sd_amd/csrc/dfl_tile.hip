@@ -78,7 +78,7 @@ struct TgShape {
                     STAGES >= 3,
                 "vmcnt range");
   static_assert(LDS <= TG_LDS_BUDGET, "LDS budget");
-  static constexpr int NACC = MTW * RBW >= 4 ? 1 : 2;        // independent MFMA chains
+  static constexpr int NACC = tile_nacc(MTW, RBW);           // independent MFMA chains
 };
 
 // s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt

@@ -31,6 +31,10 @@ constexpr TileShape kTileShapes[] = {
     {WT_F16, 1, 4, 1, 64, true},     // 128 x 128
 };
 constexpr int kNumTileShapes = (int)(sizeof(kTileShapes) / sizeof(kTileShapes[0]));
+// Independent MFMA accumulation chains of a shape's waves (TgShape::NACC): with two, the
+// k-blocks alternate between them and the chains are added at the end, so the sums are
+// rounded differently from a shape with one.
+constexpr int tile_nacc(int mtw, int rbw) { return mtw * rbw >= 4 ? 1 : 2; }
 
 constexpr int tile_waves(int wn) { return TG_WM * wn; }
 // The 4-wave shapes (wn == 1) add four loader waves that issue every global -> LDS copy
@@ -84,13 +88,20 @@ inline double tile_kblock_cycles(const TileShape& s) {
 // round is partial may run that round's tiles on a smaller shape whose tiles divide them,
 // several workgroups per tile over the whole K (the same sums), so that the last round
 // finishes sooner; it costs one more launch (about 12000 cycles).
+// Only the sub-shapes with the parent's accumulation chains qualify, so a tile's sums do
+// not depend on which round it ran in.
 // pairs: each wave must hold gate|up row-block pairs (SWIGLU), i.e. an even rbw.
+// like (optional): only that shape (mtw, rbw, wn, kc), so that a product runs with the
+// accumulation of another plan's (e.g. one layer's product stacked over several layers).
 inline TilePlan tile_plan(int M, int N, int K, int wt, int n_cu, bool pairs = false,
-                          bool split = false, bool retile = false) {
+                          bool split = false, bool retile = false,
+                          const TilePlan* like = nullptr) {
   TilePlan best{};
   double best_t = 1e300;
   for (const TileShape& s : kTileShapes) {
     if (s.tail || s.wt != wt || K % s.kc || (pairs && s.rbw % 2)) continue;
+    if (like && (s.mtw != like->mtw || s.rbw != like->rbw || s.wn != like->wn || s.kc != like->kc))
+      continue;
     const int bm = 32 * TG_WM * s.mtw, bn = 32 * s.rbw * s.wn;
     if (N % bn) continue;
     const long long tiles = (long long)((M + bm - 1) / bm) * (N / bn);
@@ -121,7 +132,7 @@ inline TilePlan tile_plan(int M, int N, int K, int wt, int n_cu, bool pairs = fa
       const TileShape& u = kTileShapes[i];
       const int um = 32 * TG_WM * u.mtw, un = 32 * u.rbw * u.wn;
       if (u.wt != wt || K % u.kc || (pairs && u.rbw % 2) || bm % um || bn % un ||
-          (um == bm && un == bn))
+          (um == bm && un == bn) || tile_nacc(u.mtw, u.rbw) != tile_nacc(s.mtw, s.rbw))
         continue;
       const long long sub = (long long)(bm / um) * (bn / un);
       const long long ur = (part * sub + n_cu - 1) / n_cu;   // rounds of the sub-tiles
