@@ -121,6 +121,29 @@ def test_launch_argument_checks(tmp_path):
     assert r.returncode == 0 and r.stdout.strip() == "ok", r.stdout + r.stderr
 
 
+def test_launch_argument_checks_sanitized(tmp_path):
+    """The same host program built with AddressSanitizer and UndefinedBehaviorSanitizer on its
+    host code (the launch checks and the tile planner are host code): no out-of-bounds
+    access, leak or undefined behaviour in any of the checks."""
+    import shutil
+    import subprocess
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(hipcc):
+        pytest.skip("hipcc not available")
+    exe = str(tmp_path / "check_args_host_san")
+    csrc = os.path.join(ROOT, "mirror-sd_amd", "csrc")
+    r = subprocess.run([hipcc, "--offload-arch=gfx950", "-std=c++17", "-O1", "-g",
+                        "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+                        "-Xarch_host", "-fno-sanitize-recover=undefined",
+                        "-Xarch_host", "-fno-omit-frame-pointer", "-I", csrc,
+                        os.path.join(ROOT, "tests", "check_args_host.hip"), "-o", exe],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:halt_on_error=1")
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120, env=env)
+    assert r.returncode == 0 and r.stdout.strip() == "ok", r.stdout + r.stderr
+
+
 def test_build_target_layer_ids():
     assert build_target_layer_ids(36, 5) == [1, 9, 17, 25, 33]
     assert build_target_layer_ids(36, 1) == [18]
