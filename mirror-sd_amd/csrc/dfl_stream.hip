@@ -335,17 +335,38 @@ DFL_DEV int publish_partial(const StreamArgs& a, int lane, int t, int slot, int*
   return prev;
 }
 
-// acc += slots 0 .. count-1 of tile t, in slot order (deterministic sums).
+// acc += slots 0 .. count-1 of tile t, in slot order (deterministic sums).  The loads of up to
+// three slots are issued together: a device-coherent round trip costs 1-2 us at a launch's
+// end (several under a full weight stream), and the last worker of a split tile would
+// otherwise wait one per slot.
+// Slot j at slot0 + j * stride floats.
+DFL_DEV void add_slots_at(const float* slot0, size_t stride, int lane, int count,
+                          floatx16& acc0, floatx16& acc1) {
+  constexpr int C = 3;
+  for (int j0 = 0; j0 < count; j0 += C) {
+    float v0[C][16], v1[C][16];
+#pragma unroll
+    for (int jj = 0; jj < C; ++jj) {
+      const float* src = slot0 + (size_t)min(j0 + jj, count - 1) * stride;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        v0[jj][r] = load_agent(src + r * 64 + lane);
+        v1[jj][r] = load_agent(src + 1024 + r * 64 + lane);
+      }
+    }
+#pragma unroll
+    for (int jj = 0; jj < C; ++jj)
+      if (j0 + jj < count)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          acc0[r] += v0[jj][r];
+          acc1[r] += v1[jj][r];
+        }
+  }
+}
 DFL_DEV void add_slots(const StreamArgs& a, int lane, int t, int count, floatx16& acc0,
                        floatx16& acc1) {
-  for (int j = 0; j < count; ++j) {
-    const float* src = ws_slot(a, t, j);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      acc0[r] += load_agent(src + r * 64 + lane);
-      acc1[r] += load_agent(src + 1024 + r * 64 + lane);
-    }
-  }
+  add_slots_at(ws_slot(a, t, 0), 2048, lane, count, acc0, acc1);
 }
 
 // Cross-worker completion of tile t.  `slot` is this worker's index among the `count`
@@ -670,8 +691,35 @@ DFL_DEV void reduce_head(const StreamArgs& a, int lane, float (*red)[WG_WAVES][2
   const int t0 = t & ~1;
   if (publish_partial(a, lane, t, slot, a.tile_cnt + t0, acc0, acc1) != c_lo + c_hi - 1) return;
   floatx16 lo0 = (floatx16){}, lo1 = (floatx16){}, hi0 = (floatx16){}, hi1 = (floatx16){};
-  add_slots(a, lane, t0, c_lo, lo0, lo1);
-  add_slots(a, lane, t0 + 1, c_hi, hi0, hi1);
+  if (c_lo <= 2 && c_hi <= 2) {   // both tiles' slots in one round trip
+    float v[4][32];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int tt = jj >> 1, j = jj & 1, c = tt ? c_hi : c_lo;
+      const float* src = ws_slot(a, t0 + tt, min(j, c - 1));
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        v[jj][r] = load_agent(src + r * 64 + lane);
+        v[jj][16 + r] = load_agent(src + 1024 + r * 64 + lane);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        if (j < c_lo) {
+          lo0[r] += v[j][r];
+          lo1[r] += v[j][16 + r];
+        }
+        if (j < c_hi) {
+          hi0[r] += v[2 + j][r];
+          hi1[r] += v[2 + j][16 + r];
+        }
+      }
+  } else {
+    add_slots(a, lane, t0, c_lo, lo0, lo1);
+    add_slots(a, lane, t0 + 1, c_hi, hi0, hi1);
+  }
   if (lane == 0) a.tile_cnt[t0] = 0;   // next use is a later launch
   qk_head_epilogue(a, lane, t0 >> 1, lo0, lo1, hi0, hi1, tb);
 }
@@ -1168,14 +1216,8 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_gemm_m_kernel(StreamA
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         for (int mt = 0; mt < a.MT; ++mt) {
           floatx16 acc0 = (floatx16){}, acc1 = (floatx16){};
-          for (int j = 0; j < count; ++j) {
-            const float* src = a.ws + (((size_t)t * a.seg_cap + j) * a.MT + mt) * 2048;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              acc0[r] += load_agent(src + r * 64 + lane);
-              acc1[r] += load_agent(src + 1024 + r * 64 + lane);
-            }
-          }
+          add_slots_at(a.ws + ((size_t)t * a.seg_cap * a.MT + mt) * 2048, (size_t)a.MT * 2048,
+                       lane, count, acc0, acc1);
           tile_epilogue<EPI>(mtile_view(a, mt), lane, t, acc0, acc1);
         }
         if (lane == 0) a.tile_cnt[t] = 0;   // next use is a later launch
