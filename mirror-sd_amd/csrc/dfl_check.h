@@ -95,6 +95,13 @@ inline const char* check_qk_rope_args(const QKRopeArgs& a) {
     for (int s = 1; s < a.n_seq; ++s)
       if (a.sq[s].pos0 != a.sq[0].pos0) return "one angle table for sequences at other positions";
   if (!a.q_norm || !a.k_norm || a.cap < 1) return "missing norms or cache capacity";
+  // 4-element vector loads and stores: rows, scales, gains, angles and outputs aligned
+  auto mis = [](const void* q, uintptr_t m) { return (reinterpret_cast<uintptr_t>(q) & m) != 0; };
+  if (a.N % 4 || mis(a.qkv32, 15) || mis(a.oscale, 7) || mis(a.qkv16, 7) || mis(a.q_norm, 7) ||
+      mis(a.k_norm, 7) || mis(a.cs, 15) || mis(a.Q, 7))
+    return "QK rope rows, scales, gains, angle table or Q not aligned for 4-element access";
+  for (int s = 0; s < a.n_seq; ++s)
+    if (mis(a.k_norm_s[s], 7) || mis(a.sq[s].Kc, 7)) return "k_norm or K cache not 8-byte aligned";
   if (a.slot0 + a.n_slots > a.NH)
     for (int s = 0; s < a.n_seq; ++s)
       if (!a.sq[s].Kc || !a.sq[s].Vt) return "K/V slots without cache pointers";

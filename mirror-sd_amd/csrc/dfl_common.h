@@ -88,6 +88,28 @@ DFL_DEV float h2f(half_t h) { return (float)h; }
 DFL_DEV half_t f2h(float f) { return (half_t)f; }   // round-to-nearest-even
 // RMSNorm output expression: fp16(fp16(x * r) * g)  (nn.RMSNorm, dflash.py:338-339).
 DFL_DEV half_t rms_out(float x, float r, half_t g) { return f2h(h2f(f2h(x * r)) * h2f(g)); }
+// rms_out with fp16(x * r) rounded once from the exact product (v_fma_mix, +0 addend).  The
+// compiler turns f2h(x * r) into either that or an fp32 product and a conversion (two
+// roundings, now and then a different fp16) depending on the surrounding code; a kernel
+// whose results must not depend on that choice uses this form.
+DFL_DEV half_t rms_out_once(float x, float r, half_t g) {
+  uint32_t d = 0;
+  asm("v_fma_mixlo_f16 %0, %1, %2, 0" : "+v"(d) : "v"(x), "v"(r));
+  return f2h(h2f(__builtin_bit_cast(half_t, (uint16_t)d)) * h2f(g));
+}
+// fp16(a * b + c) rounded once from the exact fma (the same choice for fp16(fmaf(a, b, c))).
+DFL_DEV half_t fma_f16_once(float a, float b, float c) {
+  uint32_t d = 0;
+  asm("v_fma_mixlo_f16 %0, %1, %2, %3" : "+v"(d) : "v"(a), "v"(b), "v"(c));
+  return __builtin_bit_cast(half_t, (uint16_t)d);
+}
+// fp16(x * s) for an fp16 scale s, rounded once from the exact product (the same choice).
+DFL_DEV half_t mul_f16_once(float x, half_t s) {
+  uint32_t d = 0;
+  const uint32_t sv = __builtin_bit_cast(uint16_t, s);
+  asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "+v"(d) : "v"(x), "v"(sv));
+  return __builtin_bit_cast(half_t, (uint16_t)d);
+}
 
 // Wave64 reductions via cross-lane shuffles.
 DFL_DEV float wave_sum(float v) {

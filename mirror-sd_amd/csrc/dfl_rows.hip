@@ -268,13 +268,16 @@ void launch_afl_to_rows(const half_t* x, int M, int N, half_t* h, hipStream_t st
 
 // Head slots [slot0, slot0 + n_slots) in q|k|v numbering: Q heads, then K heads, then V
 // heads (slot >= NH + NKV).  The launch's blocks come in two parts: the first handles the
-// Q/K slots, one wave per (sequence, row m, slot); the rest the V slots, one workgroup per
-// (sequence, V slot, 64 rows).  Below QKR_V_TILE_MIN rows (a decode step's few context rows)
-// the 64-row V workgroups would mostly idle: there the per-row waves take the V slots too.
+// Q/K slots, one item (sequence, row m, slot) per quarter wave (16 items per block); the
+// rest the V slots, one workgroup per (sequence, V slot, 64 rows).  Below QKR_V_TILE_MIN rows
+// (a decode step's few context rows) the 64-row V workgroups would mostly idle: there the
+// Q/K part takes the V slots too, with one item per wave (4 per block), so that a small
+// launch still spreads over the CUs and each lane computes one angle.
 constexpr int QKR_V_TILE_MIN = 64;
 struct QkRopeGrid {
   int qk0, nqk, v0, nv;      // first Q/K slot and count, first V slot and count
-  long long qk_blocks;       // blocks of the Q/K part (4 waves each)
+  int items;                 // Q/K items per block: 16 (quarter waves) or 4 (waves)
+  long long qk_blocks;       // blocks of the Q/K part
   int v_tiles;               // 64-row tiles per sequence
 };
 __host__ __device__ inline QkRopeGrid qk_rope_grid(const QKRopeArgs& a) {
@@ -292,7 +295,8 @@ __host__ __device__ inline QkRopeGrid qk_rope_grid(const QKRopeArgs& a) {
     gr.nv = end - gr.v0;
     if (gr.nv < 0) gr.nv = 0;
   }
-  gr.qk_blocks = ((long long)a.M * gr.nqk * a.n_seq + 3) / 4;
+  gr.items = a.M < QKR_V_TILE_MIN ? 4 : 16;
+  gr.qk_blocks = ((long long)a.M * gr.nqk * a.n_seq + gr.items - 1) / gr.items;
   gr.v_tiles = (a.M + 63) / 64;
   return gr;
 }
@@ -303,15 +307,140 @@ DFL_DEV void qk_rope_src(const QKRopeArgs& a, int sidx, int m, int slot, size_t&
   c0 = (a.layer_cols ? sidx * a.layer_cols : 0) + (slot - a.col_slot0) * 128;
 }
 
-// Projection value (fp16 Linear output, as float) of row `row`, column c: rounded by the GEMM
-// epilogue (qkv16), or here from the fp32 GEMM rows and the per-column scales (qkv32).
-DFL_DEV float qk_rope_value(const QKRopeArgs& a, size_t row, int c) {
-  return a.qkv32 ? h2f(f2h(a.qkv32[row * a.N + c] * h2f(a.oscale[c]))) : h2f(a.qkv16[row * a.N + c]);
+// Projection values (fp16 Linear output, as float) of row `row`, columns c .. c+E-1 (c % E ==
+// 0, E = 1 or 4): rounded by the GEMM epilogue (qkv16), or here from the fp32 GEMM rows and
+// the per-column scales (qkv32); for E = 4 one 8- or 16-byte load (and an 8-byte scale load).
+template <int E>
+DFL_DEV void qk_rope_values(const QKRopeArgs& a, size_t row, int c, float v[E]) {
+  if constexpr (E == 4) {
+    if (a.qkv32) {
+      const floatx4 x = *reinterpret_cast<const floatx4*>(a.qkv32 + row * a.N + c);
+      const half4_t sc = *reinterpret_cast<const half4_t*>(a.oscale + c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = h2f(mul_f16_once(x[i], sc[i]));
+    } else {
+      const half4_t h = *reinterpret_cast<const half4_t*>(a.qkv16 + row * a.N + c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = h2f(h[i]);
+    }
+  } else {
+    v[0] = a.qkv32 ? h2f(mul_f16_once(a.qkv32[row * a.N + c], a.oscale[c])) : h2f(a.qkv16[row * a.N + c]);
+  }
 }
 
-// Q/K part: lane j holds head elements j and j + 64, which are exactly the neox RoPE pair
-// (dflash.py:263-275, split-half rotation), so the rotation is lane-local.  Angles are
-// computed in fp64 (pos * theta^(-j/64), or the scaled frequency table).
+// Q/K item (sequence sidx, row m, slot) on a group of 64/E lanes, lane L holding head
+// elements E*L .. E*L+E-1 and 64+E*L .. 64+E*L+E-1: exactly the neox RoPE pairs (d, d + 64)
+// (dflash.py:263-275, split-half rotation), so the rotation is lane-local.  The row's sum
+// of squares is the sum tree of a 64-lane butterfly over one pair per lane (lane d:
+// v_d^2 + v_(d+64)^2, pairs combined across lane bits 5, 4, ..., 0) for either E: with E = 4
+// bits 5..2 of d are the group's lane bits (xor 8, 4, 2, 1), bits 1..0 the lane's four pairs.
+// Angles are computed in fp64 (pos * theta^(-j/64), or the scaled frequency table) or taken
+// from the angle table.
+template <int E>
+DFL_DEV void qk_rope_item(const QKRopeArgs& a, int sidx, int m, int slot, int L) {
+  const RopeSeq& sq = a.sq[sidx];
+  const int crow = slot >= a.NH ? cache_slot(sq, a.M, m) : 0;
+  if (crow < 0) return;   // the whole group: one (row, head slot) per group
+  size_t row;
+  int c0;
+  qk_rope_src(a, sidx, m, slot, row, c0);
+  const int j0 = E * L;
+  float v0[E], v1[E];
+  qk_rope_values<E>(a, row, c0 + j0, v0);
+  qk_rope_values<E>(a, row, c0 + j0 + 64, v1);
+  if (slot >= a.NH + a.NKV) {   // V head (few rows): down its Vt column, no norm or rotation
+    half_t* vt = sq.Vt + (size_t)(slot - a.NH - a.NKV) * 128 * a.cap + crow;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      vt[(size_t)(j0 + i) * a.cap] = f2h(v0[i]);
+      vt[(size_t)(j0 + i + 64) * a.cap] = f2h(v1[i]);
+    }
+    return;
+  }
+  const bool is_q = slot < a.NH;
+  const half_t* gn = is_q ? a.q_norm : (a.layer_cols ? a.k_norm_s[sidx] : a.k_norm);
+  float t[E];
+#pragma unroll
+  for (int i = 0; i < E; ++i) t[i] = __builtin_fmaf(v0[i], v0[i], v1[i] * v1[i]);
+#pragma unroll
+  for (int o = 32 / E; o > 0; o >>= 1)
+#pragma unroll
+    for (int i = 0; i < E; ++i) t[i] += __shfl_xor(t[i], o, 64);
+  float ss = t[0];
+  if constexpr (E == 4) ss = (t[0] + t[2]) + (t[1] + t[3]);
+  const float r = 1.0f / sqrtf(ss * (1.0f / 128.0f) + a.eps);
+  float c[E], sn[E];
+  if (a.cs) {   // (cos, sin) pairs of j0 .. j0 + E - 1: 8 E contiguous bytes
+    const float* csp = a.cs + 2 * (m * 64 + j0);
+    float w[2 * E];
+    if constexpr (E == 4) {
+      const floatx4 q0 = reinterpret_cast<const floatx4*>(csp)[0];
+      const floatx4 q1 = reinterpret_cast<const floatx4*>(csp)[1];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        w[i] = q0[i];
+        w[4 + i] = q1[i];
+      }
+    } else {
+      w[0] = csp[0];
+      w[1] = csp[1];
+    }
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      c[i] = w[2 * i];
+      sn[i] = w[2 * i + 1];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      const double inv_freq =
+          a.inv_freq ? a.inv_freq[j0 + i] : exp2(-(double)(j0 + i) * (1.0 / 64.0) * a.log2_theta);
+      const double ang = (double)(sq.pos0 + m) * inv_freq;
+      double sd, cd;
+      sincos(ang, &sd, &cd);
+      c[i] = (float)cd;
+      sn[i] = (float)sd;
+    }
+  }
+  half_t* dst;
+  if (is_q) {
+    dst = a.Q + (((size_t)sidx * a.NH + slot) * a.M + m) * 128;
+  } else {
+    const int gk = slot - a.NH;
+    dst = sq.Kc + ((size_t)gk * a.cap + crow) * 128;
+  }
+  half_t g0[E], g1[E], o0[E], o1[E];
+  if constexpr (E == 4) {
+    const half4_t h0 = *reinterpret_cast<const half4_t*>(gn + j0);
+    const half4_t h1 = *reinterpret_cast<const half4_t*>(gn + j0 + 64);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      g0[i] = h0[i];
+      g1[i] = h1[i];
+    }
+  } else {
+    g0[0] = gn[j0];
+    g1[0] = gn[j0 + 64];
+  }
+#pragma unroll
+  for (int i = 0; i < E; ++i) {
+    const float y0 = h2f(rms_out_once(v0[i], r, g0[i]));
+    const float y1 = h2f(rms_out_once(v1[i], r, g1[i]));
+    // the rotation written out (the y * c products fused and rounded once to fp16 with the
+    // rounded y * sn products), so that the result does not depend on the compiler's choices
+    o0[i] = fma_f16_once(y0, c[i], -(y1 * sn[i]));
+    o1[i] = fma_f16_once(y1, c[i], y0 * sn[i]);
+  }
+  if constexpr (E == 4) {
+    *reinterpret_cast<half4_t*>(dst + j0) = (half4_t){o0[0], o0[1], o0[2], o0[3]};
+    *reinterpret_cast<half4_t*>(dst + j0 + 64) = (half4_t){o1[0], o1[1], o1[2], o1[3]};
+  } else {
+    dst[j0] = o0[0];
+    dst[j0 + 64] = o1[0];
+  }
+}
+
+// Q/K part: qk_rope_item per (sequence, row, slot).
 // V part: the workgroup reads its 64 rows x 128 values row by row (coalesced), transposes
 // them through LDS and writes each Vt row d as 64 consecutive cache columns, so the
 // transposed cache layout costs no scattered 2-byte stores.
@@ -325,16 +454,17 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(QKRopeArgs a) {
     const int sidx = (int)(sv / gr.nv), slot = gr.v0 + (int)(sv % gr.nv);
     const RopeSeq& sq = a.sq[sidx];
     const int m0 = tile * 64;
-    for (int i = threadIdx.x; i < 64 * 128; i += 256) {
-      const int r = i >> 7, d = i & 127;
-      half_t v = (half_t)0.0f;
+    for (int i = threadIdx.x; i < 64 * 32; i += 256) {
+      const int r = i >> 5, d = (i & 31) * 4;
+      float v[4] = {0.f, 0.f, 0.f, 0.f};
       if (m0 + r < a.M) {
         size_t row;
         int c0;
         qk_rope_src(a, sidx, m0 + r, slot, row, c0);
-        v = f2h(qk_rope_value(a, row, c0 + d));
+        qk_rope_values<4>(a, row, c0 + d, v);
       }
-      vt_s[d][r] = v;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) vt_s[d + k][r] = f2h(v[k]);
     }
     __syncthreads();
     const int gk = slot - (a.NH + a.NKV);
@@ -347,60 +477,23 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(QKRopeArgs a) {
     }
     return;
   }
-  const int lane = threadIdx.x & 63;
-  const long long p = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
   const long long per_seq = (long long)a.M * gr.nqk;
-  if (p >= per_seq * a.n_seq) return;
+  long long p;
+  int L;
+  if (gr.items == 16) {   // prompt-sized: a quarter wave per item
+    p = (long long)blockIdx.x * 16 + (threadIdx.x >> 4);
+    L = threadIdx.x & 15;
+  } else {                // few rows: a wave per item
+    p = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    L = threadIdx.x & 63;
+  }
+  if (p >= per_seq * a.n_seq) return;   // a whole group (its shuffles stay inside it)
   const int sidx = (int)(p / per_seq);
   const long long pr = p - (long long)sidx * per_seq;
   const int m = (int)(pr / gr.nqk);
   const int slot = gr.qk0 + (int)(pr - (long long)m * gr.nqk);
-  const RopeSeq& sq = a.sq[sidx];
-  const int crow = slot >= a.NH ? cache_slot(sq, a.M, m) : 0;
-  if (crow < 0) return;   // whole wave: one (row, head slot) per wave
-  size_t row;
-  int c0;
-  qk_rope_src(a, sidx, m, slot, row, c0);
-  const float v0 = qk_rope_value(a, row, c0 + lane);
-  const float v1 = qk_rope_value(a, row, c0 + lane + 64);
-  if (slot >= a.NH + a.NKV) {   // V head (few rows): down its Vt column, no norm or rotation
-    half_t* vt = sq.Vt + (size_t)(slot - a.NH - a.NKV) * 128 * a.cap + crow;
-    vt[(size_t)lane * a.cap] = f2h(v0);
-    vt[(size_t)(lane + 64) * a.cap] = f2h(v1);
-    return;
-  }
-  const bool is_q = slot < a.NH;
-  const half_t* gn = is_q ? a.q_norm : (a.layer_cols ? a.k_norm_s[sidx] : a.k_norm);
-  const float ss = wave_sum(v0 * v0 + v1 * v1);
-  const float r = 1.0f / sqrtf(ss * (1.0f / 128.0f) + a.eps);
-  const float y0 = h2f(rms_out(v0, r, gn[lane]));
-  const float y1 = h2f(rms_out(v1, r, gn[lane + 64]));
-  float c, sn;
-  if (a.cs) {
-    c = a.cs[2 * (m * 64 + lane)];
-    sn = a.cs[2 * (m * 64 + lane) + 1];
-  } else {
-    const double inv_freq =
-        a.inv_freq ? a.inv_freq[lane] : exp2(-(double)lane * (1.0 / 64.0) * a.log2_theta);
-    const double ang = (double)(sq.pos0 + m) * inv_freq;
-    double sd, cd;
-    sincos(ang, &sd, &cd);
-    c = (float)cd;
-    sn = (float)sd;
-  }
-  // the rotation's contraction written out (the y * c products fused, the y * sn products
-  // rounded), so that the result does not depend on the compiler's choice of fma
-  const half_t o0 = f2h(__builtin_fmaf(y0, c, -(y1 * sn)));
-  const half_t o1 = f2h(__builtin_fmaf(y1, c, y0 * sn));
-  half_t* dst;
-  if (is_q) {
-    dst = a.Q + (((size_t)sidx * a.NH + slot) * a.M + m) * 128;
-  } else {
-    const int gk = slot - a.NH;
-    dst = sq.Kc + ((size_t)gk * a.cap + crow) * 128;
-  }
-  dst[lane] = o0;
-  dst[lane + 64] = o1;
+  if (gr.items == 16) qk_rope_item<4>(a, sidx, m, slot, L);
+  else qk_rope_item<1>(a, sidx, m, slot, L);
 }
 
 __global__ __launch_bounds__(256) void rope_table_kernel(int M, long long pos0, double log2_theta,
