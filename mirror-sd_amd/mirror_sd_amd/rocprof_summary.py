@@ -73,17 +73,23 @@ def read_stats(path):
     return rows
 
 
-def read_trace(path, skip_blocks, block_rx, from_rx=None, from_index=0):
+def read_trace(path, skip_blocks, block_rx, from_rx=None, from_index=0, until_rx=None,
+               until_back=0):
     """(calls, total ns) per kernel name from a kernel trace, leaving out the dispatches
     from the first draft block's start (a dispatch matching block_rx) to the start of
     block skip_blocks + 1; dispatches before the first block (context ingest) are kept.
     With from_rx, every dispatch before the from_index-th (0-based) one matching from_rx
-    is left out first."""
+    is left out first; with until_rx, the first dispatch after that point matching until_rx,
+    the until_back dispatches before it and everything after it are left out too."""
     with open(path) as f:
         rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
     if from_rx:
         hits = [i for i, r in enumerate(rows) if re.search(from_rx, r["Kernel_Name"])]
         rows = rows[hits[from_index]:] if from_index < len(hits) else []
+    if until_rx:
+        hits = [i for i, r in enumerate(rows) if re.search(until_rx, r["Kernel_Name"])]
+        if hits:
+            rows = rows[:max(0, hits[0] - until_back)]
     starts = [i for i, r in enumerate(rows) if re.search(block_rx, r["Kernel_Name"])]
     lo = hi = 0
     if skip_blocks > 0 and starts:
@@ -135,6 +141,11 @@ def main(argv=None):
                     help="trace mode: drop every dispatch before the --from-index-th one "
                          "whose name matches this regex")
     ap.add_argument("--from-index", type=int, default=0)
+    ap.add_argument("--until-kernel", default=None,
+                    help="trace mode: drop the first dispatch (after --from-kernel's) whose "
+                         "name matches this regex, the --until-back dispatches before it and "
+                         "everything after it")
+    ap.add_argument("--until-back", type=int, default=0)
     ap.add_argument("--fetch")
     ap.add_argument("--write")
     ap.add_argument("--mfma")
@@ -150,7 +161,8 @@ def main(argv=None):
         print("pass exactly one of --stats / --trace", file=sys.stderr)
         return 2
     stats = read_stats(a.stats) if a.stats else read_trace(a.trace, a.skip_blocks, a.block_start,
-                                                             a.from_kernel, a.from_index)
+                                                             a.from_kernel, a.from_index,
+                                                             a.until_kernel, a.until_back)
     out = [f"# rocprofv3 summary: {a.workload} draft block", ""]
     if a.note:
         out += [a.note, ""]
@@ -160,7 +172,8 @@ def main(argv=None):
             f"## Kernel durations (--kernel-trace; the {a.skip_blocks} warmup blocks left out)"
             if not a.from_kernel else
             f"## Kernel durations (--kernel-trace; from dispatch {a.from_index} of "
-            f"{a.from_kernel} on)")
+            f"{a.from_kernel} on" + (f", up to the first {a.until_kernel} less "
+                                      f"{a.until_back}" if a.until_kernel else "") + ")")
     out += [head, "",
             "| group | calls | avg us | total ms |", "|---|---:|---:|---:|"]
     for label, rx in GROUPS:

@@ -268,6 +268,14 @@ def test_rocprof_summary_trace_skips_warmup_blocks(tmp_path):
     # from the 3rd gemm_k dispatch on (blocks 2 and 3), nothing else skipped
     assert rs.read_trace(str(path), 0, r"embed_norm", r"gemm_k", 2) == {
         "embed_norm_kernel": (1, 13.0), "gemm_k": (2, 52.0 + 53.0)}
+    # from the 2nd gemm_k on, up to the first embed_norm after it less one more dispatch:
+    # gemm_k of blocks 1 and 2 and embed_norm of block 2 ... up to block 3's embed_norm
+    assert rs.read_trace(str(path), 0, r"embed_norm", r"gemm_k", 1, r"embed_norm_kernel", 0) == {
+        "gemm_k": (1, 51.0)}
+    assert rs.read_trace(str(path), 0, r"embed_norm", r"gemm_k", 0, r"gemm_k_none", 0) == {
+        "gemm_k": (4, 50.0 + 51 + 52 + 53), "embed_norm_kernel": (3, 11.0 + 12 + 13)}
+    assert rs.read_trace(str(path), 0, r"embed_norm", r"ingest_k", 0, r"gemm_k", 1) == {
+        "ingest_k": (1, 100.0)}
 
 
 def test_argmax_agreement_rule():
