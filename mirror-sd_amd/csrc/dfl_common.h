@@ -88,10 +88,10 @@ DFL_DEV float h2f(half_t h) { return (float)h; }
 DFL_DEV half_t f2h(float f) { return (half_t)f; }   // round-to-nearest-even
 // RMSNorm output expression: fp16(fp16(x * r) * g)  (nn.RMSNorm, dflash.py:338-339).
 DFL_DEV half_t rms_out(float x, float r, half_t g) { return f2h(h2f(f2h(x * r)) * h2f(g)); }
-// rms_out with fp16(x * r) rounded once from the exact product (v_fma_mix, +0 addend).  The
-// compiler turns f2h(x * r) into either that or an fp32 product and a conversion (two
-// roundings, now and then a different fp16) depending on the surrounding code; a kernel
-// whose results must not depend on that choice uses this form.
+// rms_out with fp16(x * r) rounded once from the exact product (v_fma_mix with a +0 addend,
+// so a zero product comes out +0).  The compiler turns f2h(x * r) into either that or an fp32
+// product and a conversion (two roundings, now and then a different fp16) depending on the
+// surrounding code; a kernel whose results must not depend on that choice uses this form.
 DFL_DEV half_t rms_out_once(float x, float r, half_t g) {
   uint32_t d = 0;
   asm("v_fma_mixlo_f16 %0, %1, %2, 0" : "+v"(d) : "v"(x), "v"(r));
