@@ -18,7 +18,20 @@ inline const char* check_stream_args(int wt, int epi, bool norm, const StreamArg
   if (!a.W) return "null weight matrix";
   if (a.N <= 0 || a.N % 64) return "N must be a positive multiple of 64";
   if (a.KB < CHECK_WG_WAVES) return "fewer k-blocks than streaming waves";
-  if (!a.X) return "null activations";
+  if (a.xr_n < 0 || a.xr_n > MAX_FEATS) return "row-major activations: feature count out of range";
+  if (a.xr_n > 0) {
+    if (wt != WT_F16 || epi != EPI_RESID || norm || m_split)
+      return "row-major activations are read by the one-tile fp16 RESID kernel only";
+    if (a.xr_h < 64 || a.xr_h % 16 || (long long)a.xr_n * a.xr_h != (long long)a.KB * 16)
+      return "row-major activations: features do not tile the K axis in 16-column blocks";
+    if (a.xr_ld < a.xr_h || a.xr_ld % 8)
+      return "row-major activations: row stride below the feature width or not a multiple of 8";
+    for (int j = 0; j < a.xr_n; ++j)
+      if (!a.xr_p[j] || (reinterpret_cast<uintptr_t>(a.xr_p[j]) & 15))
+        return "row-major activations: feature rows null or not 16-byte aligned";
+  } else if (!a.X) {
+    return "null activations";
+  }
   if (a.M < 1) return "no activation rows";
   if (m_split ? (a.MT < 2 || a.MT > 8 || a.M > 32 * a.MT) : (a.M > 32))
     return "activation rows exceed the kernel's m-tiles";

@@ -36,12 +36,21 @@ struct RopeEpi {
 
 
 // ---- stream-K weight-streaming GEMM for M <= 32 rows (dfl_stream.hip) ----
+constexpr int MAX_FEATS = 16;   // tapped target layers (FeatPtrs, StreamArgs::xr_p)
+
 struct StreamArgs {
   const uint4* W;           // packed weight blocks, N rows (multiple of 64)
   const half_t* scale;      // [N] per packed row (int8) or nullptr
   int N, KB;                // KB = K/32 (int8) or K/16 (fp16)
   const half_t* X;          // activations: one 32-row tile in the fragment layout (afl_offset)
   int ldx, M;
+  // Row-major activations instead of X (xr_n > 0: the per-step ingest fc, fp16 weights,
+  // one m-tile): element (m, k) is xr_p[k / xr_h][m * xr_ld + k % xr_h], i.e. feature j of
+  // the tapped layers gives columns [j * xr_h, (j + 1) * xr_h), read in place; rows >= M
+  // are zero.  Every xr_p[j] 16-byte aligned, xr_ld % 8 == 0, xr_h % 16 == 0, xr_h >= 64.
+  const half_t* xr_p[MAX_FEATS];
+  long long xr_ld;
+  int xr_n, xr_h;
   int MT;                   // M-split kernel: 32-row m-tiles of X (M <= 32 * MT)
   const float* rnorm;       // NORM: per-row 1/rms of X (used when ss_in is null)
   const float* ss_in;       // NORM: [ss_tiles][32] row sums of squares of X (RESID output)
@@ -182,7 +191,6 @@ void launch_embed_block(const int32_t* ids, int B, const half_t* embed, int Vemb
                         unsigned long long* cand, half_t* out, int* err, hipStream_t st);
 // Feature tensors of the tapped target layers: p[j] -> [rows][ld] fp16 (first H columns
 // used), 16-byte aligned, ld % 8 == 0.
-constexpr int MAX_FEATS = 16;
 struct FeatPtrs {
   const half_t* p[MAX_FEATS];
   int n;

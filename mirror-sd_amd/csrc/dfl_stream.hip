@@ -37,6 +37,8 @@
 
 #include <hip/hip_ext.h>
 
+#include <climits>
+
 namespace dfl {
 
 namespace {
@@ -160,7 +162,10 @@ DFL_DEV float rn_from_ss(const float* ss, int tiles, int n, float eps, int lane)
 // reducer wave through LDS slot set (segment & 1), while the next units' loads are already
 // in flight.
 // ---------------------------------------------------------------------------------------
-template <int WT, bool NORM, int P>
+// XRM (fp16 only): the activations are row-major feature rows (StreamArgs::xr_p) instead of
+// the fragment-layout tile X; lane (m, g) of k-block kb loads X[m][16 kb + 8 g .. + 7], the
+// same eight values its fragment-layout record entry holds.
+template <int WT, bool NORM, int P, bool XRM = false>
 DFL_DEV void stream_range(const StreamArgs& a, const half_t* gsh, const float* rn_lds,
                           int* ready, float (*red)[WG_WAVES][2048], int* arrived, int* reduced,
                           long long u0, long long u1, long long v0, long long v1, int w,
@@ -220,6 +225,23 @@ DFL_DEV void stream_range(const StreamArgs& a, const half_t* gsh, const float* r
       }
     }
     int issued = 0;
+    // XRM: feature xr_j covers k-blocks from xr_k0 / 16; xr_row is this lane's row in it
+    // (offset 8 g), moved only when the walk enters another feature (a tile change, the
+    // second range, or every xr_h / 64 of the wave's units)
+    [[maybe_unused]] int xr_j = 0, xr_k0 = INT_MIN / 2;
+    [[maybe_unused]] const half_t* xr_row = nullptr;
+    [[maybe_unused]] const size_t xr_lane = XRM ? (size_t)m * a.xr_ld + 8 * g : 0;
+    auto xr_track = [&](int kb) {
+      if constexpr (XRM) {
+        const int k = 16 * kb;
+        if (k < xr_k0 || k >= xr_k0 + a.xr_h) {
+          xr_j = k / a.xr_h;
+          xr_k0 = xr_j * a.xr_h;
+          xr_row = a.xr_p[xr_j] + xr_lane;
+        }
+      }
+    };
+    xr_track(ikb);
     struct Stage {
       u32x4 w0[P], w1[P], x[P][NX];
       int kb[P], sg[P];
@@ -234,6 +256,10 @@ DFL_DEV void stream_range(const StreamArgs& a, const half_t* gsh, const float* r
         if constexpr (WT == WT_INT8) {
           st.x[s][0] = xf[(size_t)(2 * ikb) * 64 + lane];
           st.x[s][NX - 1] = xf[(size_t)(2 * ikb + 1) * 64 + lane];
+        } else if constexpr (XRM) {
+          u32x4 v = {0u, 0u, 0u, 0u};
+          if (m < a.M) v = *reinterpret_cast<const u32x4*>(xr_row + (16 * ikb - xr_k0));
+          st.x[s][0] = v;
         } else {
           st.x[s][0] = xf[(size_t)((ikb >> 1) * 2 + g) * 64 + m + 32 * (ikb & 1)];
         }
@@ -250,6 +276,7 @@ DFL_DEV void stream_range(const StreamArgs& a, const half_t* gsh, const float* r
               ++isg;
             }
           }
+          xr_track(ikb);
         }
       });
     };
@@ -892,7 +919,7 @@ DFL_DEV StreamArgs mtile_view(const StreamArgs& a, int mt) {
 // ---------------------------------------------------------------------------------------
 // The stream-K kernel: one workgroup per CU, 4 streaming waves + 1 reducer wave.
 // ---------------------------------------------------------------------------------------
-template <int WT, int EPI, bool NORM, int P>
+template <int WT, int EPI, bool NORM, int P, bool XRM = false>
 __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_gemm_kernel(StreamArgs a) {
   __shared__ float red[2][WG_WAVES][2048];     // partial slots, two sets
   __shared__ half_t gsh[NORM ? 8192 : 8];
@@ -929,8 +956,8 @@ __global__ __launch_bounds__(64 * (WG_WAVES + 1)) void gsk_gemm_kernel(StreamArg
 
   if (w < WG_WAVES) {
     int si = 0;
-    stream_range<WT, NORM, P>(a, gsh, rn_s, &ready, red, arrived, &reduced, u0, u1, v0, v1, w,
-                              lane, si);
+    stream_range<WT, NORM, P, XRM>(a, gsh, rn_s, &ready, red, arrived, &reduced, u0, u1, v0, v1,
+                                   w, lane, si);
     return;
   }
 
@@ -1243,14 +1270,15 @@ static void launch_dyn_t(const StreamArgs& a, const SKPlan& p, hipStream_t st, h
 
 // With events, the dispatch itself records its start / end time into them (the same
 // timestamps a kernel trace reports); no marker packets are added to the stream.
-template <int WT, int EPI, bool NORM>
+template <int WT, int EPI, bool NORM, bool XRM = false>
 static void launch_t(const StreamArgs& a, const SKPlan& p, hipStream_t st, hipEvent_t e0,
                      hipEvent_t e1) {
   const dim3 grid(p.workers), block(64 * (WG_WAVES + 1));
   if (e0 || e1)
-    hipExtLaunchKernelGGL((gsk_gemm_kernel<WT, EPI, NORM, 4>), grid, block, 0, st, e0, e1, 0, a);
+    hipExtLaunchKernelGGL((gsk_gemm_kernel<WT, EPI, NORM, 4, XRM>), grid, block, 0, st, e0, e1, 0,
+                          a);
   else
-    hipLaunchKernelGGL((gsk_gemm_kernel<WT, EPI, NORM, 4>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((gsk_gemm_kernel<WT, EPI, NORM, 4, XRM>), grid, block, 0, st, a);
 }
 
 template <int WT, int EPI, bool NORM, int MTW>
@@ -1316,7 +1344,8 @@ bool launch_streamk_gemm(int wt, int epi, bool norm, const StreamArgs& a, const 
   DFL_SK_CASE(WT_F16, EPI_ARGMAX)
   DFL_SK_CASE(WT_F16, EPI_STORE)
   if (wt == WT_F16 && epi == EPI_RESID && !norm) {   // the per-step ingest's fc (x_zero)
-    launch_t<WT_F16, EPI_RESID, false>(a, p, st, ev_start, ev_stop);
+    if (a.xr_n > 0) launch_t<WT_F16, EPI_RESID, false, true>(a, p, st, ev_start, ev_stop);
+    else launch_t<WT_F16, EPI_RESID, false>(a, p, st, ev_start, ev_stop);
     return true;
   }
   if (wt == WT_INT8 && epi == EPI_QKROPE && norm && a.M <= 32) {   // one sequence, one m-tile

@@ -51,6 +51,23 @@ int main() {
   { StreamArgs b = a; b.ws = nullptr; expect(check_stream_args(WT_INT8, EPI_RESID, false, b, p, false), "workspace", "ws"); }
   { StreamArgs b = a; b.x_zero = 1; expect(check_stream_args(WT_F16, EPI_RESID, false, b, p, false), nullptr, "x_zero RESID"); }
   { StreamArgs b = a; b.x_zero = 1; expect(check_stream_args(WT_INT8, EPI_STORE, false, b, p, false), "x_zero", "x_zero STORE"); }
+  {   // the per-step ingest fc reading row-major feature rows in place (5 features x 5120
+      // columns = KB 1600 of 16 columns)
+    StreamArgs r = a;
+    r.X = nullptr; r.KB = 1600; r.x_zero = 1; r.xr_n = 5; r.xr_h = 5120; r.xr_ld = 5120;
+    for (int j = 0; j < 5; ++j) r.xr_p[j] = (const half_t*)P;
+    expect(check_stream_args(WT_F16, EPI_RESID, false, r, p, false), nullptr, "row-major fc");
+    { StreamArgs b = r; b.xr_n = 0; expect(check_stream_args(WT_F16, EPI_RESID, false, b, p, false), "null activations", "row-major off, no X"); }
+    { StreamArgs b = r; b.xr_n = MAX_FEATS + 1; expect(check_stream_args(WT_F16, EPI_RESID, false, b, p, false), "count", "xr_n range"); }
+    { StreamArgs b = r; expect(check_stream_args(WT_F16, EPI_STORE, false, b, p, false), "one-tile fp16 RESID", "row-major STORE"); }
+    { StreamArgs b = r; expect(check_stream_args(WT_F16, EPI_RESID, true, b, p, false), "one-tile fp16 RESID", "row-major norm"); }
+    { StreamArgs b = r; b.M = 64; b.MT = 2; expect(check_stream_args(WT_F16, EPI_RESID, false, b, p, true), "one-tile fp16 RESID", "row-major m-split"); }
+    { StreamArgs b = r; b.xr_h = 5112; expect(check_stream_args(WT_F16, EPI_RESID, false, b, p, false), "tile the K axis", "xr_h % 16"); }
+    { StreamArgs b = r; b.xr_n = 4; expect(check_stream_args(WT_F16, EPI_RESID, false, b, p, false), "tile the K axis", "features short of K"); }
+    { StreamArgs b = r; b.xr_ld = 5116; expect(check_stream_args(WT_F16, EPI_RESID, false, b, p, false), "row stride", "xr_ld"); }
+    { StreamArgs b = r; b.xr_p[3] = (const half_t*)(dummy + 2); expect(check_stream_args(WT_F16, EPI_RESID, false, b, p, false), "aligned", "xr_p alignment"); }
+    { StreamArgs b = r; b.xr_p[4] = nullptr; expect(check_stream_args(WT_F16, EPI_RESID, false, b, p, false), "aligned", "xr_p null"); }
+  }
   { StreamArgs b = a; expect(check_stream_args(7, EPI_RESID, false, b, p, false), "weight type", "wt"); }
   { StreamArgs b = a; expect(check_stream_args(WT_INT8, 42, false, b, p, false), "epilogue", "epi"); }
 

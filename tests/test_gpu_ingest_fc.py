@@ -88,3 +88,47 @@ def test_prompt_fc_unaligned_rows(case):
     # the feature-list ABI takes aligned rows only: the wrapper copies unaligned ones
     feats = [_misaligned(th[:, j * H:(j + 1) * H].contiguous())[None] for j in range(nf)]
     _check(case, feats, "unaligned tapped layers (copied by the wrapper)", h0)
+
+
+@pytest.mark.parametrize("k", [1, 5, 16, 17, 32])
+def test_step_fc_rows_read_in_place_match_gathered(k):
+    """Per-step ingest (at most 64 rows: the stream-K fc).  Up to 16 rows whose data is
+    16-byte aligned are read in place, row-major, by the fc; unaligned rows (and more than
+    16) are gathered into fragment layout first.  The same values reach the same products,
+    so the K/V caches of every layer and the next block's hidden states agree bit for bit;
+    the tapped-layer list (strided, aligned) takes the in-place path too."""
+    from mirror_sd_amd.dflash import DFlashDraftModel
+    cfg = _draft_cfg(256, 4, 2, 512, 2, vocab=1024, block=8)
+    H, nf, C0 = cfg.hidden_size, 5, 40
+    t = synth.make_weights_numpy(cfg, seed=13)
+    th0 = torch.from_numpy(synth.np_normal(13, "step.ctx", (C0, nf * H), 1.0, np.float16)).cuda()
+    th1 = torch.from_numpy(synth.np_normal(13, f"step.rows{k}", (k, nf * H), 1.0, np.float16)).cuda()
+    wide = torch.zeros((nf, k, 3 * H), dtype=torch.float16, device="cuda")
+    for j in range(nf):
+        wide[j, :, H:2 * H] = th1[:, j * H:(j + 1) * H]
+    srcs = {"aligned": th1[None], "unaligned": _misaligned(th1)[None],
+            "strided tapped layers": [wide[j, :, H:2 * H][None] for j in range(nf)]}
+    ids = np.array([7] + [cfg.mask_token_id] * (cfg.block_size - 1), dtype=np.int32)
+    res = {}
+    for name, src in srcs.items():
+        print(f"step ingest of {k} rows: {name}", flush=True)
+        m = DFlashDraftModel(cfg, max_ctx=C0 + 64)
+        m.load_weights(torch_tensors(t, "cuda"))
+        cache = m.make_cache(0, 0)
+        noise = m.embed_block(torch.from_numpy(ids).cuda())
+        noise = noise if noise.dim() == 3 else noise[None]
+        m(noise, th0[None], cache=cache)
+        for c in cache:
+            c.trim(cfg.block_size)
+        out = m(noise, src, cache=cache)
+        torch.cuda.synchronize()
+        kv = [(kk[:, :C0 + k].float().cpu().numpy(), vt[:, :, :C0 + k].float().cpu().numpy())
+              for kk, vt in m._cache_tensors]
+        res[name] = (kv, out.float().cpu().numpy())
+    base_kv, base_out = res["unaligned"]
+    for name in ("aligned", "strided tapped layers"):
+        kv, out = res[name]
+        for l, ((k1, v1), (k2, v2)) in enumerate(zip(kv, base_kv)):
+            np.testing.assert_array_equal(k1.view(np.uint32), k2.view(np.uint32), err_msg=f"{name} K layer {l}")
+            np.testing.assert_array_equal(v1.view(np.uint32), v2.view(np.uint32), err_msg=f"{name} Vt layer {l}")
+        np.testing.assert_array_equal(out.view(np.uint32), base_out.view(np.uint32), err_msg=f"{name} hidden")
