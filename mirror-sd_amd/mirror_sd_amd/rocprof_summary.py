@@ -32,17 +32,19 @@ import sys
 
 # kernel groups: (label, regex on the kernel name)
 GROUPS = [
-    ("proj_gemm_w8a16", r"gsk_gemm_kernel<0, [145], (true|false), 4>"),
+    ("proj_gemm_w8a16", r"gsk_gemm_kernel<0, [145], (true|false), 4, false>"),
     ("qkv (norm-on-load; Q/K norm + RoPE + cache scatter in the epilogue)",
-     r"gsk_gemm_kernel<0, 5, true, 4>"),
-    ("o / down (RESID)", r"gsk_gemm_kernel<0, 4, false, 4>"),
-    ("gate|up (SWIGLU, norm-on-load)", r"gsk_gemm_kernel<0, 1, true, 4>"),
-    ("lm_head (fp16, ARGMAX, norm-on-load)", r"gsk_(gemm|dyn)_kernel<1, 2, true, 4>"),
+     r"gsk_gemm_kernel<0, 5, true, 4, false>"),
+    ("o / down (RESID)", r"gsk_gemm_kernel<0, 4, false, 4, false>"),
+    ("gate|up (SWIGLU, norm-on-load)", r"gsk_gemm_kernel<0, 1, true, 4, false>"),
+    ("lm_head (fp16, ARGMAX, norm-on-load)", r"gsk_(gemm_kernel<1, 2, true, 4, false|dyn_kernel<1, 2, true, 4)>"),
     ("M-split stream-K (stacked rows up to 64)", r"gsk_gemm_m_kernel"),
-    ("per-step ingest fc (fp16, zero-residual RESID: rows + row sums)",
-     r"gsk_gemm_kernel<1, 4, false, 4>"),
+    ("per-step ingest fc (fp16, zero-residual RESID: rows + row sums), up to 16 rows read in "
+     "place", r"gsk_gemm_kernel<1, 4, false, 4, true>"),
+    ("per-step ingest fc, rows gathered into fragment layout first (17-32, or unaligned)",
+     r"gsk_gemm_kernel<1, 4, false, 4, false>"),
     ("per-step ingest K|V, all layers (int8 STORE, hidden_norm on load)",
-     r"gsk_gemm_kernel<0, 3, true, 4>"),
+     r"gsk_gemm_kernel<0, 3, true, 4, false>"),
     ("tile GEMM int8, fp32 rows (stacked qkv; split-K planes of o, down; prompt-sized ingest K|V)",
      r"tile_gemm_kernel<0, 0,"),
     ("tile GEMM int8, RESID (stacked o, down without split-K)", r"tile_gemm_kernel<0, 1,"),
