@@ -20,6 +20,7 @@ __global__ __launch_bounds__(ROW_THREADS) void embed_norm_kernel(
     int* __restrict__ err, float* __restrict__ rope_cs, long long pos0, double log2_theta,
     const double* __restrict__ inv_freq_tab) {
   __shared__ float sm[16];
+  __shared__ __attribute__((aligned(16))) half_t row_s[ROW_MAXV * ROW_THREADS];
   const int b = blockIdx.x;
   const half_t* src = noise + (size_t)b * H;
   bool bad = false;
@@ -54,12 +55,16 @@ __global__ __launch_bounds__(ROW_THREADS) void embed_norm_kernel(
     const int k = threadIdx.x + i * ROW_THREADS;
     v[i] = 0.f;
     if (k < H) {
-      x[afl_index(b, k, H)] = e[i];   // residual stream in the activation fragment layout
+      row_s[k] = e[i];
       v[i] = h2f(e[i]);
       ss += v[i] * v[i];
     }
   }
-  ss = block_sum(ss, sm);
+  ss = block_sum(ss, sm);   // (its barriers also complete row_s)
+  // residual stream in the activation fragment layout, 16-byte entries of 8 columns
+  for (int c = threadIdx.x; c < H / 8; c += ROW_THREADS)
+    *reinterpret_cast<u32x4*>(x + afl_index(b, 8 * c, H)) =
+        *reinterpret_cast<const u32x4*>(row_s + 8 * c);
   const float r = 1.0f / sqrtf(ss / (float)H + eps);
   if (rnorm && threadIdx.x == 0) rnorm[b] = r;
   if (!h) return;
