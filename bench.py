@@ -6,8 +6,10 @@ FFN 17408, W8A16 projections, fp16 lm_head [151936, 5120], block 32, context 409
 
 A step is one draft block: embedding of the block ids -> 5 decoder layers attending to
 the resident context K/V plus the block -> final norm -> lm_head -> argmax ids.  The
-context (fc fusion + per-layer K/V of 4096 rows) is ingested once before timing and
-reported as its own phase.  Weights and inputs are synthetic (seeded, random-init).
+context (fc fusion + per-layer K/V of 4096 rows) is ingested before timing; the ingest is
+reported as its own phase (``context_ingest_ms``: the median of 5 ingests of the same
+context run after the timed blocks, each listed in ``context_ingest_runs_ms``).  Weights
+and inputs are synthetic (seeded, random-init).
 
 ``steady_step`` times the decode-loop step: 16 or 32 new context rows ingested (the
 per-step path) and then the block, next to the ingest alone.
@@ -251,8 +253,8 @@ def run_workload(wl, args, sweep, want_cpu):
     sh = stream.cuda_stream
     out_ids = torch.empty((n_seq * wl.block,), dtype=torch.int32, device="cuda")
 
-    # context ingest (fc fusion + per-layer K/V), timed as its own phase after one untimed
-    # ingest (the first launches load the kernels' code objects)
+    # context ingest (fc fusion + per-layer K/V): one untimed ingest here (the first
+    # launches load the kernels' code objects); the timed ones run after the headline
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     def ingest_all():
         for i, t in enumerate(ths):
@@ -266,12 +268,6 @@ def run_workload(wl, args, sweep, want_cpu):
     ingest_all()
     torch.cuda.synchronize()
     first_ingest_s = time.perf_counter() - t_first
-    torch.cuda.synchronize()
-    ev0.record(stream)
-    ingest_all()
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    ingest_ms = ev0.elapsed_time(ev1)
 
     def step():
         if batched:
@@ -307,6 +303,18 @@ def run_workload(wl, args, sweep, want_cpu):
 
     ms_per_step, wall_s, _ = timed(args.steps, False)
     first_ids = out_ids.cpu().tolist()
+    # The context ingest as its own phase, on the GPU warmed up by the blocks (as a drafting
+    # loop's prompt ingest follows the target's prefill): 5 ingests of the same context
+    # (cache reset, then the rows again), the median reported and each run listed.
+    ingest_runs = []
+    for _ in range(5):
+        torch.cuda.synchronize()
+        ev0.record(stream)
+        ingest_all()
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        ingest_runs.append(ev0.elapsed_time(ev1))
+    ingest_ms = sorted(ingest_runs)[len(ingest_runs) // 2]
     # The same K steps again with dispatch-timestamp events on the GEMM launches: the
     # kernel durations they give match a kernel trace, but attaching them lengthens the
     # gaps between dispatches, so the headline latency comes from the plain run above.
@@ -464,7 +472,8 @@ def run_workload(wl, args, sweep, want_cpu):
     torch.cuda.empty_cache()
     return {"lat_us": lat_us, "ms_per_step": ms_per_step, "wall_s": wall_s, "gbs": gbs,
             "nbytes": nbytes, "roofline": roofline, "kernels": kernels, "cpu": cpu,
-            "ingest_ms": ingest_ms, "first_ingest_s": first_ingest_s, "setup_s": setup_s,
+            "ingest_ms": ingest_ms, "ingest_runs": ingest_runs, "first_ingest_s": first_ingest_s,
+            "setup_s": setup_s,
             "ms_events": ms_events, "context_sweep": context_sweep, "steady": steady,
             "python_path": python_path, "first_ids": first_ids,
             "n_seq": n_seq, "batched": batched}
@@ -548,7 +557,8 @@ def main():
                  "hbm_gbps": round(x["gbs"], 1),
                  "algorithmic_bytes_per_block": x["nbytes"]["total"],
                  "roofline": x["roofline"], "kernels": x["kernels"],
-                 "context_ingest_ms": round(x["ingest_ms"], 3)}
+                 "context_ingest_ms": round(x["ingest_ms"], 3),
+                 "context_ingest_runs_ms": [round(v, 3) for v in x["ingest_runs"]]}
         print(f"{xw.name}: block {x['lat_us']:.1f} us", file=sys.stderr, flush=True)
 
     metric = METRIC if headline else \
@@ -568,6 +578,7 @@ def main():
         "roofline": r["roofline"],
         "cpu_baseline": r["cpu"],
         "phases": {"context_ingest_ms": round(r["ingest_ms"], 3),
+                   "context_ingest_runs_ms": [round(v, 3) for v in r["ingest_runs"]],
                    "first_ingest_s": round(r["first_ingest_s"], 3), "setup_s": round(r["setup_s"], 1),
                    "ms_per_step_with_gemm_events": (round(r["ms_events"], 5) if r["ms_events"]
                                                     else None),
