@@ -5,7 +5,8 @@ runs on the tile GEMM over the packed fp16 fc weight.  Every variant matches the
 within the draft tolerance, its argmax ids pass the suite's agreement rule (check_argmax:
 a row may differ only where the oracle's fp32 and fp64 runs disagree), and the variants
 agree with each other within
-SAME_TOL."""
+SAME_TOL.  The per-step ingest's fc (at most 64 rows, the stream-K kernel) reads up to 16
+aligned rows in place and gathers the rest first: both give the same bits."""
 
 import numpy as np
 import pytest
