@@ -351,3 +351,38 @@ def _argmax_rule_cases(P):
         P.check_argmax(ids4, lg4, ref, ref, "listed", ti, tv2, 5.0)
     with pytest.raises(AssertionError):   # ids must be the argmax of the logits
         P.check_argmax(ids, lg2, ref, alts, "not argmax", ti, tv, 5.0)
+
+
+def test_rocprof_summary_groups_match_the_built_kernels():
+    """The profile summariser's kernel groups match the stream-K instantiations the build
+    records (names demangled as a kernel trace shows them), each in the intended group:
+    the projection row takes qkv, o / down and gate|up and nothing else."""
+    import json
+    import shutil
+    import subprocess
+    from mirror_sd_amd import rocprof_summary as rs
+    groups = dict(rs.GROUPS)
+    expect = {
+        "void dfl::gsk_gemm_kernel<0, 5, true, 4, false>(dfl::StreamArgs)": "qkv (",
+        "void dfl::gsk_gemm_kernel<0, 4, false, 4, false>(dfl::StreamArgs)": "o / down",
+        "void dfl::gsk_gemm_kernel<0, 1, true, 4, false>(dfl::StreamArgs)": "gate|up",
+        "void dfl::gsk_dyn_kernel<1, 2, true, 4>(dfl::StreamArgs)": "lm_head",
+        "void dfl::gsk_gemm_kernel<1, 4, false, 4, true>(dfl::StreamArgs)": "read in place",
+        "void dfl::gsk_gemm_kernel<1, 4, false, 4, false>(dfl::StreamArgs)": "gathered",
+        "void dfl::gsk_gemm_kernel<0, 3, true, 4, false>(dfl::StreamArgs)": "K|V, all layers",
+    }
+    for name, label in expect.items():
+        hits = [g for g, rx in groups.items() if re.search(rx, name) and g != "proj_gemm_w8a16"]
+        assert len(hits) == 1 and label in hits[0], (name, hits)
+        in_proj = bool(re.search(groups["proj_gemm_w8a16"], name))
+        assert in_proj == (label in ("qkv (", "o / down", "gate|up")), name
+    res = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                       "mirror-sd_amd", "_build", "kernel_resources.json")
+    if not (os.path.exists(res) and shutil.which("c++filt")):
+        pytest.skip("no build record or c++filt")
+    with open(res) as f:
+        mangled = [k for k in json.load(f) if "gsk_" in k]
+    out = subprocess.run(["c++filt"], input="\n".join(mangled), capture_output=True, text=True,
+                         check=True).stdout.split("\n")
+    built = {n.strip() for n in out if n.strip()}
+    assert set(expect) <= built, sorted(set(expect) - built)
